@@ -1,0 +1,315 @@
+"""Python binding of libmeshgpt.so, the MI355X Mesh GPT generate path.
+
+A thin ctypes layer over the C ABI in include/meshgpt.h, mirroring the
+reference's inference API (src/gpt/gpu.rs:1693-2092: ``SpecializedMeshGpt``)
+and its host types (``GptConfig``, ``Checkpoint``).  The product is the native
+library; this module only marshals arrays.  Importing it fails loudly when the
+library has not been built: there is no fallback implementation.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+PACKAGE_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(PACKAGE_DIR, "libmeshgpt.so")
+CLI_PATH = os.path.join(PACKAGE_DIR, "mesh-gpt")
+
+MG_OK, MG_INVALID_ARGUMENT, MG_OUT_OF_MEMORY, MG_DEVICE_ERROR, MG_NONFINITE, MG_IO, MG_UNSUPPORTED = range(7)
+
+# Every function include/meshgpt.h declares.
+EXPORTS = (
+    "mg_last_error", "mg_config_default", "mg_config_validate", "mg_parameter_count",
+    "mg_initial_parameters", "mg_token_codes", "mg_model_create", "mg_model_destroy",
+    "mg_model_config", "mg_parameters", "mg_set_parameters", "mg_logits", "mg_token_embeddings",
+    "mg_hidden_states", "mg_generate", "mg_generate_text", "mg_prefill", "mg_decode",
+    "mg_decode_profiled", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
+    "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
+    "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save",
+)
+
+
+class GptConfig(ctypes.Structure):
+    """mg_config: GptConfig (src/gpt/config.rs:21-56) in checkpoint field order."""
+
+    _fields_ = [(name, ctypes.c_uint32) for name in (
+        "vocab_size", "context", "width", "heads", "layers", "attention_mesh_depth",
+        "ffn_mesh_depth", "embedding", "connectivity", "long_context")]
+
+    def __init__(self, **overrides):
+        super().__init__()
+        lib().mg_config_default(ctypes.byref(self))
+        for key, value in overrides.items():
+            if key not in dict(self._fields_):
+                raise TypeError(f"unknown GptConfig field {key}")
+            setattr(self, key, int(value))
+
+    def as_dict(self):
+        return {name: getattr(self, name) for name, _ in self._fields_}
+
+    def __repr__(self):
+        return "GptConfig(" + ", ".join(f"{k}={v}" for k, v in self.as_dict().items()) + ")"
+
+    def __eq__(self, other):
+        return isinstance(other, GptConfig) and self.as_dict() == other.as_dict()
+
+
+class MeshGptError(RuntimeError):
+    def __init__(self, status, message):
+        super().__init__(message)
+        self.status = status
+        self.message = message
+
+
+_u32p = ctypes.POINTER(ctypes.c_uint32)
+_f32p = ctypes.POINTER(ctypes.c_float)
+_szp = ctypes.POINTER(ctypes.c_size_t)
+_cfgp = ctypes.POINTER(GptConfig)
+_lib = None
+
+
+def lib():
+    """The loaded libmeshgpt.so; raises ImportError when it was never built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(f"{LIB_PATH} is missing: build it with __graft_entry__.build() "
+                          "(or make -C grokking_abmod_amd/csrc)")
+    L = ctypes.CDLL(LIB_PATH)
+    vp, sz, i, u64, f = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int, ctypes.c_uint64, ctypes.c_float
+    sigs = {
+        "mg_last_error": (ctypes.c_char_p, []),
+        "mg_config_default": (None, [_cfgp]),
+        "mg_config_validate": (i, [_cfgp]),
+        "mg_parameter_count": (i, [_cfgp, _szp]),
+        "mg_initial_parameters": (i, [_cfgp, u64, _f32p, sz]),
+        "mg_token_codes": (i, [_cfgp, _f32p, sz]),
+        "mg_model_create": (i, [i, _cfgp, u64, sz, ctypes.POINTER(vp)]),
+        "mg_model_destroy": (None, [vp]),
+        "mg_model_config": (i, [vp, _cfgp]),
+        "mg_parameters": (i, [vp, _f32p, sz]),
+        "mg_set_parameters": (i, [vp, _f32p, sz]),
+        "mg_logits": (i, [vp, _u32p, sz, sz, i, _f32p, sz]),
+        "mg_token_embeddings": (i, [vp, _f32p, sz]),
+        "mg_hidden_states": (i, [vp, _u32p, sz, sz, _f32p, sz]),
+        "mg_generate": (i, [vp, _u32p, sz, sz, sz, f, u64, _u32p]),
+        "mg_generate_text": (i, [vp, _u32p, sz, ctypes.c_char_p, sz, f, u64, ctypes.c_char_p, sz, _szp]),
+        "mg_prefill": (i, [vp, _u32p, sz, sz, f, u64, sz]),
+        "mg_decode": (i, [vp, sz]),
+        "mg_decode_profiled": (i, [vp, sz, _f32p, sz]),
+        "mg_sequence_length": (i, [vp, _szp]),
+        "mg_read_tokens": (i, [vp, _u32p, sz, sz]),
+        "mg_last_logits": (i, [vp, _f32p, sz]),
+        "mg_model_stream": (vp, [vp]),
+        "mg_checkpoint_load": (i, [ctypes.c_char_p, ctypes.POINTER(vp)]),
+        "mg_checkpoint_info": (i, [vp, _cfgp, _szp, _szp]),
+        "mg_checkpoint_characters": (i, [vp, _u32p, sz]),
+        "mg_checkpoint_parameters": (i, [vp, _f32p, sz]),
+        "mg_checkpoint_free": (None, [vp]),
+        "mg_checkpoint_save": (i, [ctypes.c_char_p, _cfgp, _u32p, sz, _f32p, sz]),
+    }
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name)
+        fn.restype = res
+        fn.argtypes = args
+    _lib = L
+    return L
+
+
+def _check(status):
+    if status != MG_OK:
+        raise MeshGptError(status, lib().mg_last_error().decode("utf-8", "replace"))
+
+
+def _u32(a):
+    return np.ascontiguousarray(a, dtype=np.uint32)
+
+
+def _f32(a):
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a, kind):
+    return a.ctypes.data_as(kind)
+
+
+def validate(config):
+    _check(lib().mg_config_validate(ctypes.byref(config)))
+
+
+def parameter_count(config):
+    n = ctypes.c_size_t()
+    _check(lib().mg_parameter_count(ctypes.byref(config), ctypes.byref(n)))
+    return n.value
+
+
+def initial_parameters(config, seed):
+    out = np.empty(parameter_count(config), dtype=np.float32)
+    _check(lib().mg_initial_parameters(ctypes.byref(config), seed, _p(out, _f32p), out.size))
+    return out
+
+
+def token_codes(config):
+    out = np.empty((config.vocab_size, config.width), dtype=np.float32)
+    _check(lib().mg_token_codes(ctypes.byref(config), _p(out, _f32p), out.size))
+    return out
+
+
+class MeshGpt:
+    """SpecializedMeshGpt (src/gpt/gpu.rs:1693-2092) on one MI355X."""
+
+    def __init__(self, device, config, seed, max_batch=1):
+        handle = ctypes.c_void_p()
+        _check(lib().mg_model_create(device, ctypes.byref(config), seed, max_batch, ctypes.byref(handle)))
+        self._h = handle
+        self._config = GptConfig(**config.as_dict())
+
+    def close(self):
+        if getattr(self, "_h", None):
+            lib().mg_model_destroy(self._h)
+            self._h = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    def config(self):
+        out = GptConfig()
+        _check(lib().mg_model_config(self._h, ctypes.byref(out)))
+        return out
+
+    def parameters(self):
+        out = np.empty(parameter_count(self._config), dtype=np.float32)
+        _check(lib().mg_parameters(self._h, _p(out, _f32p), out.size))
+        return out
+
+    def set_parameters(self, values):
+        values = _f32(values)
+        _check(lib().mg_set_parameters(self._h, _p(values, _f32p), values.size))
+
+    def logits(self, tokens, sequence, last_only=False):
+        tokens = _u32(tokens).reshape(-1)
+        rows = tokens.size // sequence if (last_only and sequence) else tokens.size
+        out = np.empty((max(rows, 1), self._config.vocab_size), dtype=np.float32)
+        _check(lib().mg_logits(self._h, _p(tokens, _u32p), tokens.size, sequence, int(last_only),
+                               _p(out, _f32p), out.size))
+        return out[:rows]
+
+    def token_embeddings(self):
+        out = np.empty((self._config.vocab_size, self._config.width), dtype=np.float32)
+        _check(lib().mg_token_embeddings(self._h, _p(out, _f32p), out.size))
+        return out
+
+    def hidden_states(self, tokens, sequence):
+        tokens = _u32(tokens).reshape(-1)
+        out = np.empty((max(tokens.size, 1), self._config.width), dtype=np.float32)
+        _check(lib().mg_hidden_states(self._h, _p(tokens, _u32p), tokens.size, sequence,
+                                      _p(out, _f32p), out.size))
+        return out[:tokens.size]
+
+    def generate_tokens(self, prompts, count, temperature, seed):
+        prompts = _u32(np.atleast_2d(prompts))
+        batch, length = prompts.shape
+        out = np.empty((batch, length + count), dtype=np.uint32)
+        _check(lib().mg_generate(self._h, _p(prompts, _u32p), batch, length, count, temperature, seed,
+                                 _p(out, _u32p)))
+        return out
+
+    def generate(self, characters, prompt, count, temperature, seed):
+        chars = _u32([ord(c) if isinstance(c, str) else c for c in characters])
+        data = prompt.encode("utf-8")
+        capacity = 4 * (len(prompt) + count) + 16
+        buf = ctypes.create_string_buffer(capacity)
+        written = ctypes.c_size_t()
+        _check(lib().mg_generate_text(self._h, _p(chars, _u32p), chars.size, data, count, temperature,
+                                      seed, buf, capacity, ctypes.byref(written)))
+        return buf.raw[:written.value].decode("utf-8")
+
+    def prefill(self, prompts, temperature, seed, reserve=0):
+        prompts = _u32(np.atleast_2d(prompts))
+        batch, length = prompts.shape
+        _check(lib().mg_prefill(self._h, _p(prompts, _u32p), batch, length, temperature, seed, reserve))
+
+    def decode(self, steps):
+        _check(lib().mg_decode(self._h, steps))
+
+    def decode_profiled(self, steps):
+        out = np.empty(steps * self._config.layers, dtype=np.float32)
+        _check(lib().mg_decode_profiled(self._h, steps, _p(out, _f32p), out.size))
+        return out
+
+    def sequence_length(self):
+        n = ctypes.c_size_t()
+        _check(lib().mg_sequence_length(self._h, ctypes.byref(n)))
+        return n.value
+
+    def read_tokens(self, batch, length=None):
+        length = self.sequence_length() if length is None else length
+        out = np.empty((batch, length), dtype=np.uint32)
+        _check(lib().mg_read_tokens(self._h, _p(out, _u32p), batch, length))
+        return out
+
+    def last_logits(self, batch):
+        out = np.empty((batch, self._config.vocab_size), dtype=np.float32)
+        _check(lib().mg_last_logits(self._h, _p(out, _f32p), out.size))
+        return out
+
+    def stream(self):
+        return lib().mg_model_stream(self._h)
+
+
+class Checkpoint:
+    """Checkpoint (src/gpt/checkpoint.rs:14-192): config, tokenizer characters, weights."""
+
+    def __init__(self, config, characters, parameters):
+        self.config = config
+        self.characters = list(characters)
+        self.parameters = _f32(parameters)
+
+    @staticmethod
+    def load(path):
+        handle = ctypes.c_void_p()
+        _check(lib().mg_checkpoint_load(os.fsencode(path), ctypes.byref(handle)))
+        try:
+            config = GptConfig()
+            vocab, count = ctypes.c_size_t(), ctypes.c_size_t()
+            _check(lib().mg_checkpoint_info(handle, ctypes.byref(config), ctypes.byref(vocab),
+                                            ctypes.byref(count)))
+            chars = np.empty(vocab.value, dtype=np.uint32)
+            params = np.empty(count.value, dtype=np.float32)
+            _check(lib().mg_checkpoint_characters(handle, _p(chars, _u32p), chars.size))
+            _check(lib().mg_checkpoint_parameters(handle, _p(params, _f32p), params.size))
+        finally:
+            lib().mg_checkpoint_free(handle)
+        return Checkpoint(config, [int(c) for c in chars], params)
+
+    def save(self, path):
+        chars = _u32([ord(c) if isinstance(c, str) else c for c in self.characters])
+        _check(lib().mg_checkpoint_save(os.fsencode(path), ctypes.byref(self.config), _p(chars, _u32p),
+                                        chars.size, _p(self.parameters, _f32p), self.parameters.size))
+
+
+def named_config(name):
+    """The synthetic workloads of the benchmark (butterfly meshes, defaults otherwise)."""
+    table = {
+        "tiny": dict(vocab_size=64, width=128, heads=4, layers=2, attention_mesh_depth=7,
+                     ffn_mesh_depth=7, context=256, connectivity=1),
+        "symbolic": dict(vocab_size=99, width=128, heads=4, layers=2, attention_mesh_depth=4,
+                         ffn_mesh_depth=6, context=4, connectivity=0),
+        "mid": dict(vocab_size=256, width=512, heads=8, layers=6, attention_mesh_depth=9,
+                    ffn_mesh_depth=9, context=1024, connectivity=1),
+        "long": dict(vocab_size=256, width=512, heads=8, layers=4, attention_mesh_depth=9,
+                     ffn_mesh_depth=9, context=8448, connectivity=1, long_context=1),
+        "high": dict(vocab_size=256, width=1024, heads=16, layers=12, attention_mesh_depth=10,
+                     ffn_mesh_depth=10, context=2048, connectivity=1),
+    }
+    return GptConfig(**table[name])

@@ -1,0 +1,151 @@
+// Host-side model types of the Mesh GPT generate path: configuration and its
+// validation, the parameter layout and seeded initialisation, fixed token codes,
+// the character tokenizer and the weights-only checkpoint format.  These mirror
+// the reference's Rust types one for one (names, argument meaning, error text).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+namespace meshgpt {
+
+// Status codes shared with the C ABI (include/meshgpt.h).
+enum Status : int {
+    kOk = 0,
+    kInvalidArgument = 1,
+    kOutOfMemory = 2,
+    kDeviceError = 3,
+    kNonfinite = 4,
+    kIo = 5,
+    kUnsupported = 6,
+};
+
+// Every failure carries the reference's message text and a C ABI status.
+struct Error : std::runtime_error {
+    int status;
+    explicit Error(const std::string &message, int code = kInvalidArgument)
+        : std::runtime_error(message), status(code) {}
+};
+
+constexpr size_t kMaxRows = 131072;        // src/gpt/mod.rs:31
+constexpr size_t kModelMaxWidth = 4096;    // src/gpt/mod.rs:33
+constexpr size_t kModelMaxContext = 4096;  // src/gpt/mod.rs:34
+constexpr size_t kModelMaxHeads = 64;      // src/gpt/mod.rs:35
+constexpr size_t kModelMaxVocab = 65536;   // src/gpt/mod.rs:36
+constexpr float kRopeBase = 10000.0f;      // src/gpt/mod.rs:37
+constexpr float kRmsEpsilon = 1e-5f;       // src/gpt/mod.rs:38
+constexpr float kXsaEpsilon = 1e-12f;      // src/gpt/mod.rs:40
+// Long-context extension: contexts beyond 4096 are accepted only when a config
+// sets long_context (the reference caps context at 4096, config.rs:148).
+constexpr size_t kExtendedMaxContext = 65536;
+
+enum class TokenEmbedding : uint32_t { Mesh = 0, Table = 1 };        // config.rs:58-67
+enum class MeshConnectivity : uint32_t { Neighbor = 0, Butterfly = 1 };  // config.rs:96-106
+
+const char *name(TokenEmbedding e);
+const char *name(MeshConnectivity c);
+TokenEmbedding parse_embedding(const std::string &text);     // config.rs:84-94
+MeshConnectivity parse_connectivity(const std::string &text);  // config.rs:131-141
+
+// Distance from a neuron's own channel to its second parent (config.rs:116-122).
+size_t stride(MeshConnectivity connectivity, size_t width, size_t layer);
+
+// GptConfig (config.rs:21-56).  Geometry is fixed at its defaults and RoPE,
+// QK-Norm and XSA are always on; checkpoints that change them are rejected.
+struct GptConfig {
+    size_t vocab_size = 32;
+    size_t context = 32;
+    size_t width = 32;
+    size_t heads = 4;
+    size_t layers = 2;
+    size_t attention_mesh_depth = 4;
+    size_t ffn_mesh_depth = 6;
+    TokenEmbedding embedding = TokenEmbedding::Mesh;
+    MeshConnectivity connectivity = MeshConnectivity::Neighbor;
+    bool long_context = false;  // extension flag, never stored in checkpoints
+
+    bool operator==(const GptConfig &o) const;
+    void validate() const;                                                // config.rs:144-172
+    size_t parameter_count() const;                                       // config.rs:174-176
+    size_t embedding_parameter_count() const;                             // config.rs:179-184
+    std::vector<float> initial_parameters(uint64_t seed) const;           // config.rs:187-190
+    void validate_tokens(const uint32_t *tokens, size_t n, size_t sequence) const;  // 210-228
+    size_t head_width() const { return width / heads; }
+};
+
+struct Group {
+    size_t offset, size, depth;
+};
+struct Block {
+    size_t query, key, value, projection, ffn;
+};
+
+// Layout (config.rs:351-459): the embedding group, then q, k, v, projection and
+// ffn meshes of every block; each mesh layer stores [self, partner] per channel.
+struct Layout {
+    std::vector<Group> groups;
+    std::vector<Block> blocks;
+    size_t embedding = 0;
+
+    static Layout build(const GptConfig &config);
+    size_t count() const;
+    std::vector<float> initialize(const GptConfig &config, uint64_t seed) const;
+};
+
+// Fixed token codes, vocab x width (config.rs:552-591).
+std::vector<float> token_codes(const GptConfig &config);
+// Table parameters of a mesh-embedding model (config.rs:505-547).
+std::vector<float> tabulate_embedding(const GptConfig &config, const std::vector<float> &parameters);
+
+// SplitMix64 (src/mesh.rs:256-288).
+class Random {
+  public:
+    explicit Random(uint64_t seed) : state_(seed) {}
+    uint64_t next_u64();
+    float unit();
+    size_t index(size_t bound);
+
+  private:
+    uint64_t state_;
+};
+
+// "{name} must contain only finite values" (src/mesh.rs:239-246).
+void validate_finite(const float *values, size_t n, const char *name);
+
+// CharacterTokenizer (src/gpt/text.rs:7-56): sorted unique Unicode scalars.
+class CharacterTokenizer {
+  public:
+    static CharacterTokenizer from_text(const std::string &utf8);
+    static CharacterTokenizer from_characters(std::vector<uint32_t> characters);
+    size_t vocab_size() const { return characters_.size(); }
+    std::vector<uint32_t> encode(const std::string &utf8) const;
+    std::string decode(const uint32_t *tokens, size_t n) const;
+    const std::vector<uint32_t> &characters() const { return characters_; }
+    bool operator==(const CharacterTokenizer &o) const { return characters_ == o.characters_; }
+
+  private:
+    std::vector<uint32_t> characters_;
+};
+
+std::vector<uint32_t> utf8_decode(const std::string &text);
+std::string utf8_encode(const uint32_t *scalars, size_t n);
+
+// Weights-only checkpoint (src/gpt/checkpoint.rs:14-201): MSHGPT07 for the
+// default architecture, MSHGPT08 with embedding/connectivity codes.  MSHGPT09
+// files are parsed and validated like the reference, then rejected as
+// unsupported when they change geometry or switch an operator off.
+struct Checkpoint {
+    GptConfig config;
+    CharacterTokenizer tokenizer;
+    std::vector<float> parameters;
+
+    std::vector<uint8_t> serialize() const;
+    void save(const std::string &path) const;
+    static Checkpoint read(const uint8_t *bytes, size_t n);
+    static Checkpoint load(const std::string &path);
+};
+
+}  // namespace meshgpt

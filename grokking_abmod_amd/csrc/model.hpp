@@ -1,0 +1,59 @@
+// MeshGpt: the device-resident Mesh GPT used by generate, mirroring the
+// reference's SpecializedMeshGpt inference API (src/gpt/gpu.rs:1693-2092) with
+// run-time dimensions instead of compile-time capacities, a KV cache, batched
+// sequences and on-device sampling.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "meshgpt_types.hpp"
+
+namespace meshgpt {
+
+class MeshGpt {
+  public:
+    // gpu.rs:1718-1771: validates the config, seeds the weights with `seed` and
+    // keeps decode state for up to max_batch sequences (grown on demand).
+    MeshGpt(int device, const GptConfig &config, uint64_t seed, size_t max_batch = 1);
+    ~MeshGpt();
+    MeshGpt(const MeshGpt &) = delete;
+    MeshGpt &operator=(const MeshGpt &) = delete;
+
+    const GptConfig &config() const;
+    std::vector<float> parameters() const;                  // gpu.rs:1846-1853
+    void set_parameters(const float *values, size_t n);     // gpu.rs:1856-1872
+    // gpu.rs:1875-1887: logits of every row (or only each sequence's last row)
+    std::vector<float> logits(const uint32_t *tokens, size_t n, size_t sequence, bool last_only = false);
+    std::vector<float> token_embeddings();                  // gpu.rs:2056-2068, V x W
+    std::vector<float> hidden_states(const uint32_t *tokens, size_t n, size_t sequence);  // gpu.rs:2070
+    // gpu.rs:2006-2053 on text; batch rows b use seed + b.
+    std::string generate(const CharacterTokenizer &tokenizer, const std::string &prompt, size_t count,
+                         float temperature, uint64_t seed);
+    // Token-level batched generate: prompts[B][P] -> out[B][P+count].
+    void generate_tokens(const uint32_t *prompts, size_t batch, size_t prompt_len, size_t count,
+                         float temperature, uint64_t seed, uint32_t *out);
+
+    // Step-wise decode surface used by the benchmark: prefill samples the first
+    // token; decode(k) runs k more on-device steps (KV path only).
+    void prefill(const uint32_t *prompts, size_t batch, size_t prompt_len, float temperature,
+                 uint64_t seed, size_t reserve);
+    void decode(size_t steps);
+    // Same steps without graph replay, timing every decode-attention launch
+    // with HIP events; returns milliseconds per launch (steps x layers).
+    std::vector<float> decode_profiled(size_t steps);
+    size_t sequence_length() const;
+    void read_tokens(uint32_t *out, size_t batch, size_t length);
+    std::vector<float> last_logits();
+    hipStream_t stream() const;
+    void synchronize();
+
+  private:
+    struct Impl;
+    std::unique_ptr<Impl> impl_;
+};
+
+}  // namespace meshgpt

@@ -1,0 +1,137 @@
+/*
+ * meshgpt.h — C ABI of the MI355X Mesh GPT generate path (libmeshgpt.so).
+ *
+ * This is the seam that replaces the reference's cuda-oxide launcher and the
+ * Rust `SpecializedMeshGpt` inference API (src/gpt/gpu.rs:21-1392 kernels and
+ * launcher, 1693-2092 public API).  Plain C types only: an opaque model handle,
+ * caller-owned host buffers, an int status and a thread-local message that
+ * carries the reference's error text.  Every call returns after its work is
+ * complete on the device; calls on one handle must not overlap (the caller
+ * serialises them, as the reference's &self / &mut self borrows do);
+ * distinct handles are independent.  All host pointers are borrowed for the
+ * duration of the call only.
+ */
+#ifndef MESHGPT_H
+#define MESHGPT_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  The message of the last failure on the calling thread is
+ * returned by mg_last_error(). */
+enum {
+    MG_OK = 0,
+    MG_INVALID_ARGUMENT = 1, /* the reference's Err(...) on validation */
+    MG_OUT_OF_MEMORY = 2,
+    MG_DEVICE_ERROR = 3,
+    MG_NONFINITE = 4, /* "... must contain only finite values" (src/mesh.rs:239-246) */
+    MG_IO = 5,        /* checkpoint files */
+    MG_UNSUPPORTED = 6 /* MSHGPT09 geometry/operator ablations */
+};
+
+/* GptConfig (src/gpt/config.rs:21-56) in checkpoint field order
+ * (src/gpt/checkpoint.rs:51-63,129-138).  Geometry stays at its defaults and
+ * RoPE, QK-Norm and XSA are on, as in every checkpoint the reference writes
+ * as MSHGPT07/08. */
+typedef struct {
+    uint32_t vocab_size;
+    uint32_t context;
+    uint32_t width;
+    uint32_t heads;
+    uint32_t layers;
+    uint32_t attention_mesh_depth;
+    uint32_t ffn_mesh_depth;
+    uint32_t embedding;    /* 0 mesh, 1 table (config.rs:58-67) */
+    uint32_t connectivity; /* 0 neighbor, 1 butterfly (config.rs:96-106) */
+    uint32_t long_context; /* extension: 1 accepts context up to 65536 (reference cap 4096,
+                              config.rs:148); such configs cannot be checkpointed */
+} mg_config;
+
+typedef struct mg_model mg_model;
+
+/* Message of the last failed call on this thread ("" if none). */
+const char *mg_last_error(void);
+
+/* GptConfig::default() (config.rs:38-55). */
+void mg_config_default(mg_config *out);
+/* GptConfig::validate (config.rs:144-172). */
+int mg_config_validate(const mg_config *config);
+/* GptConfig::parameter_count (config.rs:174-176). */
+int mg_parameter_count(const mg_config *config, size_t *out);
+/* GptConfig::initial_parameters (config.rs:187-190); out holds parameter_count floats. */
+int mg_initial_parameters(const mg_config *config, uint64_t seed, float *out, size_t n);
+/* GptConfig::fixed_token_codes (config.rs:205-208); out is vocab_size x width. */
+int mg_token_codes(const mg_config *config, float *out, size_t n);
+
+/* SpecializedMeshGpt::new (gpu.rs:1718-1771): seeded weights on `device`, decode
+ * state for max_batch sequences (grown on demand). */
+int mg_model_create(int device, const mg_config *config, uint64_t seed, size_t max_batch, mg_model **out);
+void mg_model_destroy(mg_model *model);
+/* SpecializedMeshGpt::config (gpu.rs:1773-1775). */
+int mg_model_config(const mg_model *model, mg_config *out);
+/* SpecializedMeshGpt::parameters (gpu.rs:1846-1853). */
+int mg_parameters(mg_model *model, float *out, size_t n);
+/* SpecializedMeshGpt::set_parameters (gpu.rs:1856-1872). */
+int mg_set_parameters(mg_model *model, const float *values, size_t n);
+/* SpecializedMeshGpt::logits / cached_logits (gpu.rs:1875-1901): n tokens in
+ * sequences of `sequence`; out is n x vocab_size, or (n/sequence) x vocab_size of
+ * each sequence's last row when last_only != 0. */
+int mg_logits(mg_model *model, const uint32_t *tokens, size_t n, size_t sequence, int last_only,
+              float *out, size_t out_len);
+/* SpecializedMeshGpt::token_embeddings (gpu.rs:2056-2068): vocab_size x width. */
+int mg_token_embeddings(mg_model *model, float *out, size_t n);
+/* SpecializedMeshGpt::hidden_states (gpu.rs:2070-2092): n x width. */
+int mg_hidden_states(mg_model *model, const uint32_t *tokens, size_t n, size_t sequence, float *out,
+                     size_t out_len);
+
+/* SpecializedMeshGpt::generate (gpu.rs:2006-2053) on token ids, batched:
+ * prompts is batch x prompt_len, out is batch x (prompt_len + count).  Row b
+ * samples with Random::new(seed + b); row 0 is exactly the reference's call. */
+int mg_generate(mg_model *model, const uint32_t *prompts, size_t batch, size_t prompt_len, size_t count,
+                float temperature, uint64_t seed, uint32_t *out);
+/* The same on text: the tokenizer is given as its characters (Unicode scalar
+ * values, CharacterTokenizer, src/gpt/text.rs:7-56); prompt is UTF-8.  Writes the
+ * UTF-8 result (prompt + generated, no terminator) and its byte length. */
+int mg_generate_text(mg_model *model, const uint32_t *characters, size_t vocab, const char *prompt,
+                     size_t count, float temperature, uint64_t seed, char *out, size_t capacity,
+                     size_t *written);
+
+/* Step-wise decode for benchmarks (no reference counterpart: the reference
+ * recomputes the window per token).  mg_prefill runs the prompts and samples
+ * the first token; mg_decode runs `steps` more on-device decode steps. */
+int mg_prefill(mg_model *model, const uint32_t *prompts, size_t batch, size_t prompt_len, float temperature,
+               uint64_t seed, size_t reserve);
+int mg_decode(mg_model *model, size_t steps);
+/* As mg_decode, without graph replay, timing each decode-attention launch with
+ * HIP events on the model's stream: ms has steps x layers entries. */
+int mg_decode_profiled(mg_model *model, size_t steps, float *ms, size_t n);
+/* Current tokens per sequence (prompt + generated). */
+int mg_sequence_length(const mg_model *model, size_t *out);
+int mg_read_tokens(mg_model *model, uint32_t *out, size_t batch, size_t length);
+/* Logits of the last sampled step, batch x vocab_size. */
+int mg_last_logits(mg_model *model, float *out, size_t n);
+/* The hipStream_t every call of this model runs on. */
+void *mg_model_stream(mg_model *model);
+
+/* Checkpoint (src/gpt/checkpoint.rs:24-192).  mg_checkpoint_load reads the file
+ * into a handle; query its parts, then free it. */
+typedef struct mg_checkpoint mg_checkpoint;
+int mg_checkpoint_load(const char *path, mg_checkpoint **out);
+int mg_checkpoint_info(const mg_checkpoint *checkpoint, mg_config *config, size_t *vocab,
+                       size_t *parameters);
+int mg_checkpoint_characters(const mg_checkpoint *checkpoint, uint32_t *out, size_t n);
+int mg_checkpoint_parameters(const mg_checkpoint *checkpoint, float *out, size_t n);
+void mg_checkpoint_free(mg_checkpoint *checkpoint);
+/* Checkpoint::save (checkpoint.rs:25-94). */
+int mg_checkpoint_save(const char *path, const mg_config *config, const uint32_t *characters, size_t vocab,
+                       const float *parameters, size_t n);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

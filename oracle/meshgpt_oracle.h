@@ -1,0 +1,113 @@
+/*
+ * TEST INFRASTRUCTURE ONLY — not part of the product.
+ *
+ * CPU restatement of the reference Mesh GPT forward pass and its `generate`
+ * loop, in plain C with f64 arithmetic.  Only tests/, __graft_entry__.smoke()
+ * and the cpu_baseline leg of bench.py may load this library, and only as the
+ * checker or the timed CPU baseline; the product library never links it.
+ *
+ * The reference is pure Rust (/root/reference/src/gpt/); no Rust toolchain
+ * exists in this image, so nothing of it can be built (oracle/_ref stays empty).
+ * Each function below names the reference lines it restates.  How each one is
+ * pinned (reference KATs, published whole-model numbers, closed forms) is
+ * recorded in tests/test_oracle_*.py.
+ */
+#ifndef MESHGPT_ORACLE_H
+#define MESHGPT_ORACLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* GptConfig (reference src/gpt/config.rs:21-56); geometry fields are fixed at
+ * their defaults (parity codes, token order, no normalisation) and rope, qk_norm,
+ * xsa are always on (config.rs:38-55). */
+typedef struct {
+    uint32_t vocab_size;
+    uint32_t context;
+    uint32_t width;
+    uint32_t heads;
+    uint32_t layers;
+    uint32_t attention_mesh_depth;
+    uint32_t ffn_mesh_depth;
+    uint32_t embedding;    /* 0 = mesh (default), 1 = table (config.rs:58-67) */
+    uint32_t connectivity; /* 0 = neighbor (default), 1 = butterfly (config.rs:96-106) */
+} og_config;
+
+/* ---- SplitMix64 (reference src/mesh.rs:256-288) ---- */
+uint64_t og_rng_next(uint64_t *state);
+float og_rng_unit(uint64_t *state);
+uint64_t og_rng_index(uint64_t *state, uint64_t bound);
+
+/* ---- configuration, layout, initialisation (config.rs:117-122,144-172,358-459) ---- */
+/* Returns 0 when valid, else writes the reference's message into err (may be NULL). */
+int og_validate(const og_config *c, int allow_long_context, char *err, size_t err_len);
+size_t og_parameter_count(const og_config *c);
+size_t og_embedding_parameter_count(const og_config *c);
+/* offset of each parameter group: [0] embedding, then per block q,k,v,proj,ffn */
+void og_group_offsets(const og_config *c, size_t *offsets /* 1+5L */);
+uint32_t og_stride(const og_config *c, uint32_t layer);
+void og_initialize(const og_config *c, uint64_t seed, float *out);
+/* fixed token codes, V x W (config.rs:552-591) */
+void og_token_codes(const og_config *c, float *out);
+
+/* ---- per-op references used by the reference's own KATs (reference.rs:392-603) ---- */
+void og_rmsnorm(const double *in, size_t width, size_t heads, double *out);
+void og_rotary(const double *in, size_t width, size_t heads, size_t position, double *out);
+void og_exclusive(const double *y, const double *v, size_t width, size_t heads, double *out);
+/* rows x width q,k,v; causal attention inside consecutive sequences of `sequence` rows */
+void og_attention(const double *q, const double *k, const double *v, size_t rows, size_t width,
+                  size_t heads, size_t sequence, double *out);
+/* a mesh stack over rows x width; params points at the group's first weight */
+void og_mesh(const double *in, size_t rows, size_t width, const float *params, size_t depth,
+             uint32_t connectivity, double *out);
+
+/* ---- whole model (reference.rs:49-59,90-102,104-228) ---- */
+/* effective token vectors, V x W */
+int og_token_embeddings(const og_config *c, const float *params, double *out);
+/* logits for every row, n x V (f64, before the f32 cast of reference.rs:54) */
+int og_logits(const og_config *c, const float *params, const uint32_t *tokens, size_t n,
+              size_t sequence, double *out);
+/* residual stream before the final RMSNorm, n x W */
+int og_hidden_states(const og_config *c, const float *params, const uint32_t *tokens, size_t n,
+                     size_t sequence, double *out);
+/* next-token cross-entropy, mean over rows whose target != UINT32_MAX, computed on the
+ * f32-cast logits like the reference's loss kernel (gpu.rs:949-994,2296-2313) */
+int og_cross_entropy(const og_config *c, const float *params, const uint32_t *inputs,
+                     const uint32_t *targets, size_t n, size_t sequence, double *loss);
+
+/* ---- generate (reference src/gpt/gpu.rs:2006-2053) ----
+ * prompt of P tokens; writes P+count tokens into out.  Every step recomputes the
+ * window of at most `context` tokens, exactly as the reference does. */
+int og_generate(const og_config *c, const float *params, const uint32_t *prompt, size_t P,
+                size_t count, float temperature, uint64_t seed, uint32_t *out);
+/* the f32 sampler of gpu.rs:2028-2049 on one row of f32 logits; returns the token and
+ * advances *rng only when temperature > 0 */
+uint32_t og_sample(const float *logits, size_t vocab, float temperature, uint64_t *rng);
+
+/* ---- KV-cached incremental decode (same math, used as the CPU baseline) ----
+ * Valid while P+count <= context; returns -1 otherwise. */
+int og_generate_cached(const og_config *c, const float *params, const uint32_t *prompt, size_t P,
+                       size_t count, float temperature, uint64_t seed, uint32_t *out,
+                       float *last_logits /* V, may be NULL */);
+
+/* ---- datasets used by the published-number pins ---- */
+/* TextDataset::batch (src/gpt/text.rs:63-108) over an already tokenised corpus */
+int og_text_batch(const uint32_t *tokens, size_t len, int validation, size_t sequence,
+                  size_t batch, uint64_t seed, uint32_t *inputs, uint32_t *targets);
+/* EquationDataset (src/gpt/grokking.rs:116-186,228-271): writes the residue permutation
+ * (p entries) and both splits as (a,b,answer) triples; returns the training count. */
+int og_equations(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed,
+                 uint32_t *residue_tokens, uint32_t *train /* 3*n */, uint32_t *valid /* 3*n */,
+                 size_t *n_train, size_t *n_valid);
+/* row_metrics of src/bin/mesh-gpt/grokking.rs:544-557 on one f32 row */
+double og_row_metrics(const float *row, size_t vocab, size_t target, size_t *prediction);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif
