@@ -25,7 +25,7 @@ EXPORTS = (
     "mg_hidden_states", "mg_generate", "mg_generate_text", "mg_prefill", "mg_decode",
     "mg_decode_profiled", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
-    "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save",
+    "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
 )
 
 
@@ -108,6 +108,7 @@ def lib():
         "mg_checkpoint_parameters": (i, [vp, _f32p, sz]),
         "mg_checkpoint_free": (None, [vp]),
         "mg_checkpoint_save": (i, [ctypes.c_char_p, _cfgp, _u32p, sz, _f32p, sz]),
+        "mg_copy_bandwidth": (i, [i, sz, i, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -154,6 +155,18 @@ def token_codes(config):
     out = np.empty((config.vocab_size, config.width), dtype=np.float32)
     _check(lib().mg_token_codes(ctypes.byref(config), _p(out, _f32p), out.size))
     return out
+
+
+def copy_bandwidth(nbytes, iters=20, device=0):
+    """Read+write GB/s of the library's plain copy kernel (calibration_copy)."""
+    gbps = ctypes.c_double()
+    _check(lib().mg_copy_bandwidth(device, nbytes, iters, ctypes.byref(gbps)))
+    return gbps.value
+
+
+def calibration_copy(nbytes, device=0):
+    """One warm-up and one timed launch of calibration_copy over nbytes."""
+    return copy_bandwidth(nbytes, 1, device)
 
 
 class MeshGpt:

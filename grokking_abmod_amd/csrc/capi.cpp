@@ -230,6 +230,13 @@ int mg_last_logits(mg_model *model, float *out, size_t n) {
 
 void *mg_model_stream(mg_model *model) { return model ? static_cast<void *>(model->model.stream()) : nullptr; }
 
+int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps) {
+    return guarded([&] {
+        require(gbps != nullptr && bytes >= 16 && iters >= 1, "bytes >= 16, iters >= 1 and output required");
+        *gbps = copy_bandwidth(device, bytes, iters);
+    });
+}
+
 int mg_checkpoint_load(const char *path, mg_checkpoint **out) {
     return guarded([&] {
         require(path != nullptr && out != nullptr, "path and output must not be null");

@@ -48,47 +48,68 @@ struct KvView {
     int cap;
 };
 
-// Rows per workgroup and how many mesh layers of weights are staged in LDS at
-// once (0: weights are read straight from global memory).
-struct Tiling {
-    int rpw;
-    int stage_layers;
+// One block_kernel launch: the post-attention half of block l-1 (when wproj
+// is set) followed by the pre-attention half of block l (when wq is set).
+struct BlockArgs {
+    Shape s;
+    Rows ro;
+    float *x;  // residual rows, read and written
+    // post half: weights, attention output (split partials or rows), block l-1's cache
+    const float *wproj, *wffn;
+    const float *part;
+    int nsplit;
+    const float *ybuf;
+    KvView kv_post;
+    // pre half: weights, token vectors when embed, query rows out, block l's cache
+    const float *wq, *wk, *wv;
+    const float *E;
+    int embed;
+    float *q;
+    KvView kv_pre;
+    const float2 *rope;
+    float *xn;  // when set: the final RMSNorm of x for the head
+    int rpw;    // rows per workgroup
+    int teams;  // 3: Q, K, V meshes run concurrently; 1: one after another
 };
 
-size_t qkv_lds_bytes(const Shape &s, const Tiling &t);
-size_t post_lds_bytes(const Shape &s, const Tiling &t);
-size_t mesh_lds_bytes(const Shape &s, const Tiling &t);
-size_t head_lds_bytes(const Shape &s, int rt);
+// Threads per mesh team and channels per thread for width W.
+int team_threads(int W);
+int channels_per_thread(int W);
 
-// Allows dynamic LDS above the 64 KiB default on every kernel that needs it.
+size_t block_lds_bytes(const Shape &s, int rpw, int teams, int nsplit);
+size_t mesh_lds_bytes(const Shape &s, int rpw);
+size_t head_lds_bytes(const Shape &s, int rt);
+size_t head_sample_lds_bytes(const Shape &s);  // size_t(-1) when V is too large
+
+// Allows dynamic LDS up to max_bytes on every kernel that uses it.
 void configure_lds(size_t max_bytes);
 
 // out = mesh(in) for rows x W (the embedding table from token codes).
-void mesh_rows(const Shape &s, const float *in, float *out, int rows, const float *w, int depth,
-               Tiling t, hipStream_t stream);
-// Et[c][t] = E[t][c]
-void transpose(const float *E, float *Et, int V, int W, hipStream_t stream);
-// Pre-attention half of a block for `rows`: (embed), RMSNorm, one of the Q/K/V
-// meshes per grid.y, QK-Norm + RoPE, then q rows or the KV-cache append.
-void qkv(const Shape &s, const Rows &r, const float *wq, const float *wk, const float *wv,
-         const float *E, float *x, float *q, KvView kv, const float2 *rope, int embed, Tiling t,
-         hipStream_t stream);
-// Split-KV decode attention: one query row per sequence, partial softmax states
-// per split of `ks` keys written to part[((b*H+h)*smax+split)*(hdp+2)].
-void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int ks,
-                 int smax, float *part, hipStream_t stream);
+void mesh_rows(const Shape &s, const float *in, float *out, int rows, const float *w, int depth, int rpw,
+               hipStream_t stream);
+// Et[c][t] = E[t][c], rows of Vp >= V floats with zero padding.
+void transpose(const float *E, float *Et, int V, int Vp, int W, hipStream_t stream);
+void block(const BlockArgs &a, hipStream_t stream);
+// Split-KV decode attention: one query row per sequence; the len[b] keys are
+// cut into nsplit equal shares whose partial softmax states (acc[hdp], m, l)
+// go to part[((b*H+h)*nsplit+split)*(hdp+2)].
+void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit,
+                 float *part, hipStream_t stream);
 // Causal flash attention over whole sequences already appended to the cache.
 void attn_prefill(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y,
                   hipStream_t stream);
-// Post-attention half of a block: (split combine), XSA, projection mesh +
-// residual, RMSNorm, FFN mesh + residual; updates x in place.
-void post(const Shape &s, const Rows &r, const float *part, int ks, int smax, const float *y,
-          KvView kv, const float *wproj, const float *wffn, float *x, Tiling t, hipStream_t stream);
-// logits[i][t] = rmsnorm(x[i*row_mul+row_add]) . E[t]
-void head(const Shape &s, const float *x, int nrows, int row_mul, int row_add, const float *Et,
+// logits[i][t] = xn[i*row_mul+row_add] . E[t] (xn already RMS-normalised).
+void head(const Shape &s, const float *xn, int nrows, int row_mul, int row_add, const float *Et, int Vp,
           float *logits, int rt, hipStream_t stream);
-// Greedy / temperature sampling per sequence; appends the token and bumps len.
-void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng,
-            uint32_t *tokens, int tok_stride, int *len, int *flags, hipStream_t stream);
+// Decode head fused with sampling: logits of each sequence's row, then the
+// next token appended at len[b].
+void head_sample(const Shape &s, const float *xn, int batch, const float *Et, int Vp, float *logits,
+                 float temperature, uint64_t *rng, uint32_t *tokens, int tok_stride, int *len, int *flags,
+                 hipStream_t stream);
+// Greedy / temperature sampling from logits rows; appends the token and bumps len.
+void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng, uint32_t *tokens,
+            int tok_stride, int *len, int *flags, hipStream_t stream);
+// dst[i] = src[i] for n float4 elements (bandwidth calibration).
+void calibration_copy(const float4 *src, float4 *dst, size_t n, hipStream_t stream);
 
 }  // namespace meshgpt::kern

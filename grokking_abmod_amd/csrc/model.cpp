@@ -72,6 +72,7 @@ struct MeshGpt::Impl {
     GptConfig cfg;
     Layout layout;
     kern::Shape shape{};
+    int vpad = 0;  // vocabulary rounded up to a multiple of 4: the row stride of Et
     size_t lds_limit = 65536;
 
     DevBuf params, codes, E, Et, rope;
@@ -79,13 +80,12 @@ struct MeshGpt::Impl {
     // Decode state: KV cache [L][batch_cap][H][context][hdp], per-sequence
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
     size_t batch_cap = 0, tcap = 0;
-    int ks = 64, smax = 1;
-    DevBuf kc, vc, dx, dq, part, dtokens, dlen, drng, dlogits, dflags;
+    DevBuf kc, vc, dx, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
     size_t batch = 0, length = 0, cached = kNoCache;
     float temperature = 0.0f;
 
     // Prefill / logits workspace, grown on demand.
-    DevBuf wx, wq, wy, wtok, wlogits, wk, wv;
+    DevBuf wx, wxn, wq, wy, wtok, wlogits, wk, wv;
 
     hipGraph_t graph = nullptr;
     hipGraphExec_t exec = nullptr;
@@ -112,33 +112,45 @@ struct MeshGpt::Impl {
         return batch_cap * size_t(shape.H) * cfg.context * size_t(shape.hdp);
     }
 
-    // Rows per workgroup and staged mesh layers for a row kernel.
-    kern::Tiling tiling(int kind, size_t rows, bool decode) const {
-        const int depth = kind == 2 ? int(std::max(cfg.attention_mesh_depth, cfg.ffn_mesh_depth))
-                                    : int(cfg.attention_mesh_depth);
-        const size_t budget = decode ? lds_limit : std::min<size_t>(lds_limit, 40960);
-        auto bytes = [&](kern::Tiling t) {
-            return kind == 2 ? kern::post_lds_bytes(shape, t)
-                             : (kind == 1 ? kern::qkv_lds_bytes(shape, t) : kern::mesh_lds_bytes(shape, t));
-        };
-        kern::Tiling t{1, 0};
-        if (!decode) {
-            t.rpw = std::max(1, std::min(16, 2048 / shape.W));
-            while (t.rpw > 1 && (rows + t.rpw - 1) / t.rpw < 512) t.rpw /= 2;
+    // Splits per (sequence, head) of decode attention: enough workgroups to
+    // cover the chip (about 2048 for the batch) without tiny shares.
+    int splits_for(size_t b) const {
+        const int forced = env_int("MG_DECODE_SPLITS", 0);
+        if (forced > 0) return std::min(forced, 256);
+        const size_t want = 2048 / std::max<size_t>(b * cfg.heads, 1);
+        return int(std::max<size_t>(1, std::min<size_t>({want, 64, cfg.context})));
+    }
+
+    // Rows per workgroup and team count of block_kernel.  Decode runs one row
+    // per workgroup with the Q/K/V meshes in three concurrent teams; prefill
+    // packs rows so mesh weights are reused, keeping at least 256 workgroups.
+    struct BlockTiling {
+        int rpw, teams;
+    };
+    BlockTiling block_tiling(size_t rows, bool decode, int nsplit) const {
+        const size_t budget = decode ? lds_limit : std::min<size_t>(lds_limit, 49152);
+        for (int teams : {3, 1}) {
+            int rpw = decode ? 1 : 16;
+            while (rpw > 1 && ((rows + rpw - 1) / rpw < 256 ||
+                               kern::block_lds_bytes(shape, rpw, teams, nsplit) > budget))
+                rpw /= 2;
+            if (kern::block_lds_bytes(shape, rpw, teams, nsplit) <= budget) return {rpw, teams};
         }
-        while (t.rpw > 1 && bytes(t) > budget) t.rpw /= 2;
-        const size_t base = bytes(t);
-        if (base > lds_limit) throw Error("model width exceeds the workgroup LDS budget", kUnsupported);
-        const size_t per_layer = size_t(shape.W) * 8;
-        t.stage_layers = base + per_layer + 16 <= budget ? int((budget - base - 16) / per_layer) : 0;
-        t.stage_layers = std::min(t.stage_layers, depth);
-        return t;
+        throw Error("model width exceeds the workgroup LDS budget", kUnsupported);
+    }
+
+    int mesh_rows_per_group(size_t rows) const {
+        int rpw = 16;
+        while (rpw > 1 && ((rows + rpw - 1) / rpw < 64 || kern::mesh_lds_bytes(shape, rpw) > 49152)) rpw /= 2;
+        if (kern::mesh_lds_bytes(shape, rpw) > lds_limit)
+            throw Error("model width exceeds the workgroup LDS budget", kUnsupported);
+        return rpw;
     }
 
     int head_rows() const {
-        size_t rt = 16;
-        while (rt > 1 && kern::head_lds_bytes(shape, int(rt)) > lds_limit) rt /= 2;
-        return int(rt);
+        int rt = 8;
+        while (rt > 1 && kern::head_lds_bytes(shape, rt) > lds_limit) rt /= 2;
+        return rt;
     }
 
     void init(int dev, const GptConfig &config, uint64_t seed, size_t max_batch) {
@@ -172,9 +184,6 @@ struct MeshGpt::Impl {
         shape.F = int(cfg.ffn_mesh_depth);
 
         const size_t C = cfg.context;
-        ks = env_int("MG_DECODE_KS", C <= 512 ? 64 : (C <= 2048 ? 128 : 256));
-        ks = std::max(1, ks);
-        smax = int((C + ks - 1) / ks);
 
         // RoPE angles pos / 10000^(i / half) in f64 (reference.rs:468-470), stored as f32.
         std::vector<float> table(C * shape.half * 2);
@@ -192,7 +201,8 @@ struct MeshGpt::Impl {
         codes.ensure(c.size() * 4);
         check(hipMemcpy(codes.p, c.data(), c.size() * 4, hipMemcpyHostToDevice), "upload codes");
         E.ensure(W * cfg.vocab_size * 4);
-        Et.ensure(W * cfg.vocab_size * 4);
+        vpad = int((cfg.vocab_size + 3) / 4 * 4);
+        Et.ensure(W * size_t(vpad) * 4);
         params.ensure(layout.count() * 4);
         std::vector<float> initial = layout.initialize(cfg, seed);
         set_parameters(initial.data(), initial.size());
@@ -207,13 +217,13 @@ struct MeshGpt::Impl {
         // The token vectors depend only on the weights: computed once here, not per token.
         if (cfg.embedding == TokenEmbedding::Mesh) {
             kern::mesh_rows(shape, codes.as<float>(), E.as<float>(), shape.V, params.as<float>(), shape.A,
-                            tiling(0, cfg.vocab_size, false), stream);
+                            mesh_rows_per_group(cfg.vocab_size), stream);
         } else {
             check(hipMemcpyAsync(E.p, params.p, cfg.vocab_size * cfg.width * 4, hipMemcpyDeviceToDevice,
                                  stream),
                   "copy table");
         }
-        kern::transpose(E.as<float>(), Et.as<float>(), shape.V, shape.W, stream);
+        kern::transpose(E.as<float>(), Et.as<float>(), shape.V, vpad, shape.W, stream);
         sync();
     }
 
@@ -236,28 +246,28 @@ struct MeshGpt::Impl {
             check(hipMemsetAsync(kc.p, 0, cache, stream), "zero cache");
             check(hipMemsetAsync(vc.p, 0, cache, stream), "zero cache");
             dx.ensure(batch_cap * cfg.width * 4);
+            dxn.ensure(batch_cap * cfg.width * 4);
             dq.ensure(batch_cap * cfg.width * 4);
-            part.ensure(batch_cap * cfg.heads * size_t(smax) * (shape.hdp + 2) * 4);
+            size_t slots = 0;
+            for (size_t k = 1; k <= batch_cap; ++k) slots = std::max(slots, k * size_t(splits_for(k)));
+            part.ensure(slots * cfg.heads * (shape.hdp + 2) * 4);
             dlen.ensure(batch_cap * 4);
             drng.ensure(batch_cap * 8);
             dlogits.ensure(batch_cap * cfg.vocab_size * 4);
             dflags.ensure(4);
-            cached = kNoCache;
         }
-        if (grow_t || grow_b) {
-            tcap = std::max(t, tcap);
-            std::vector<uint32_t> keep;
-            dtokens.release();
-            dtokens.ensure(batch_cap * tcap * 4);
-            cached = kNoCache;
-            length = 0;
-        }
+        tcap = std::max(t, tcap);
+        dtokens.release();
+        dtokens.ensure(batch_cap * tcap * 4);
+        cached = kNoCache;
+        length = 0;
         sync();
     }
 
     void ensure_workspace(size_t rows, size_t out_rows, bool kv) {
         const size_t W = cfg.width;
         wx.ensure(rows * W * 4);
+        wxn.ensure(rows * W * 4);
         wq.ensure(rows * W * 4);
         wy.ensure(rows * W * 4);
         wtok.ensure(rows * 4);
@@ -271,24 +281,53 @@ struct MeshGpt::Impl {
 
     const float *group(size_t id) const { return params.as<float>() + layout.groups[id].offset; }
 
-    // All blocks over `rows`; kv(l) gives each layer's cache view.
+    // Every block over `rows`: L+1 block_kernel launches (the first also embeds
+    // the tokens, the last writes the final RMSNorm rows to xn) with each
+    // block's attention between them.  kv_of(l) is block l's cache view.  With
+    // `events`, each decode-attention launch is bracketed by a pair of events.
     template <class KvOf>
-    void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *q, float *y, bool decode) {
-        const kern::Tiling tq = tiling(1, size_t(rows.rows), decode);
-        const kern::Tiling tp = tiling(2, size_t(rows.rows), decode);
-        for (size_t l = 0; l < cfg.layers; ++l) {
-            const Block &blk = layout.blocks[l];
-            const kern::KvView kv = kv_of(l);
-            kern::qkv(shape, rows, group(blk.query), group(blk.key), group(blk.value), E.as<float>(), x, q, kv,
-                      rope.as<float2>(), l == 0, tq, stream);
-            if (decode) {
-                kern::attn_decode(shape, q, kv, rows.len, rows.rows, ks, smax, part.as<float>(), stream);
-                kern::post(shape, rows, part.as<float>(), ks, smax, nullptr, kv, group(blk.projection),
-                           group(blk.ffn), x, tp, stream);
+    void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *q, float *y, float *xn,
+                    bool decode, hipEvent_t *events = nullptr) {
+        const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
+        const BlockTiling t = block_tiling(size_t(rows.rows), decode, nsplit);
+        const size_t L = cfg.layers;
+        for (size_t l = 0; l <= L; ++l) {
+            kern::BlockArgs a{};
+            a.s = shape;
+            a.ro = rows;
+            a.x = x;
+            a.rpw = t.rpw;
+            a.teams = t.teams;
+            if (l > 0) {
+                const Block &prev = layout.blocks[l - 1];
+                a.wproj = group(prev.projection);
+                a.wffn = group(prev.ffn);
+                a.part = decode ? part.as<float>() : nullptr;
+                a.nsplit = nsplit;
+                a.ybuf = decode ? nullptr : y;
+                a.kv_post = kv_of(l - 1);
+            }
+            if (l < L) {
+                const Block &blk = layout.blocks[l];
+                a.wq = group(blk.query);
+                a.wk = group(blk.key);
+                a.wv = group(blk.value);
+                a.E = E.as<float>();
+                a.embed = l == 0;
+                a.q = q;
+                a.kv_pre = kv_of(l);
+                a.rope = rope.as<float2>();
             } else {
-                kern::attn_prefill(shape, q, kv, nseq, rows.rows_per_seq, y, stream);
-                kern::post(shape, rows, nullptr, ks, smax, y, kv, group(blk.projection), group(blk.ffn), x, tp,
-                           stream);
+                a.xn = xn;
+            }
+            kern::block(a, stream);
+            if (l == L) break;
+            if (decode) {
+                if (events) check(hipEventRecord(events[2 * l], stream), "event");
+                kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream);
+                if (events) check(hipEventRecord(events[2 * l + 1], stream), "event");
+            } else {
+                kern::attn_prefill(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, stream);
             }
         }
     }
@@ -298,14 +337,15 @@ struct MeshGpt::Impl {
         return kern::KvView{kc.as<float>() + off, vc.as<float>() + off, int(cfg.context)};
     }
 
-    // Forward over a flat batch of sequences with a per-call KV workspace.
+    // Forward over a flat batch of sequences with a one-layer KV workspace
+    // (each block's keys are consumed before the next block overwrites them).
     void forward_rows(const uint32_t *tokens, size_t n, size_t sequence, size_t out_rows) {
         ensure_workspace(n, out_rows, true);
         check(hipMemcpyAsync(wtok.p, tokens, n * 4, hipMemcpyHostToDevice, stream), "upload tokens");
         kern::Rows rows{int(n), int(sequence), nullptr, wtok.as<uint32_t>(), int(sequence), 0};
         const kern::KvView kv{wk.as<float>(), wv.as<float>(), int(sequence)};
         run_blocks(rows, int(n / sequence), [&](size_t) { return kv; }, wx.as<float>(), wq.as<float>(),
-                   wy.as<float>(), false);
+                   wy.as<float>(), wxn.as<float>(), false);
     }
 
     std::vector<float> logits(const uint32_t *tokens, size_t n, size_t sequence, bool last_only) {
@@ -313,8 +353,9 @@ struct MeshGpt::Impl {
         activate();
         const size_t out_rows = last_only ? n / sequence : n;
         forward_rows(tokens, n, sequence, out_rows);
-        kern::head(shape, wx.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
-                   last_only ? int(sequence) - 1 : 0, Et.as<float>(), wlogits.as<float>(), head_rows(), stream);
+        kern::head(shape, wxn.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
+                   last_only ? int(sequence) - 1 : 0, Et.as<float>(), vpad, wlogits.as<float>(), head_rows(),
+                   stream);
         std::vector<float> out(out_rows * cfg.vocab_size);
         check(hipMemcpyAsync(out.data(), wlogits.p, out.size() * 4, hipMemcpyDeviceToHost, stream),
               "download logits");
@@ -359,14 +400,25 @@ struct MeshGpt::Impl {
         temperature = t;
     }
 
-    void launch_decode_step() {
-        const kern::Rows rows{int(batch), 1, dlen.as<int>(), dtokens.as<uint32_t>(), int(tcap), 0};
-        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, dx.as<float>(), dq.as<float>(),
-                   nullptr, true);
-        kern::head(shape, dx.as<float>(), int(batch), 1, 0, Et.as<float>(), dlogits.as<float>(), head_rows(),
-                   stream);
+    // The head and sampler for `n` sequence rows of xn (row i at i*row_mul+row_add).
+    void head_and_sample(const float *xn, int row_mul, int row_add) {
+        if (row_mul == 1 && row_add == 0 && kern::head_sample_lds_bytes(shape) <= lds_limit) {
+            kern::head_sample(shape, xn, int(batch), Et.as<float>(), vpad, dlogits.as<float>(), temperature,
+                              drng.as<uint64_t>(), dtokens.as<uint32_t>(), int(tcap), dlen.as<int>(),
+                              dflags.as<int>(), stream);
+            return;
+        }
+        kern::head(shape, xn, int(batch), row_mul, row_add, Et.as<float>(), vpad, dlogits.as<float>(),
+                   head_rows(), stream);
         kern::sample(shape.V, int(batch), dlogits.as<float>(), temperature, drng.as<uint64_t>(),
                      dtokens.as<uint32_t>(), int(tcap), dlen.as<int>(), dflags.as<int>(), stream);
+    }
+
+    void launch_decode_step(hipEvent_t *events = nullptr) {
+        const kern::Rows rows{int(batch), 1, dlen.as<int>(), dtokens.as<uint32_t>(), int(tcap), 0};
+        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, dx.as<float>(), dq.as<float>(),
+                   nullptr, dxn.as<float>(), true, events);
+        head_and_sample(dxn.as<float>(), 1, 0);
     }
 
     void decode_step() {
@@ -392,11 +444,8 @@ struct MeshGpt::Impl {
         ensure_workspace(batch * n, 1, false);
         const kern::Rows rows{int(batch * n), int(n), nullptr, dtokens.as<uint32_t>(), int(tcap), int(start)};
         run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, wx.as<float>(), wq.as<float>(),
-                   wy.as<float>(), false);
-        kern::head(shape, wx.as<float>(), int(batch), int(n), int(n) - 1, Et.as<float>(), dlogits.as<float>(),
-                   head_rows(), stream);
-        kern::sample(shape.V, int(batch), dlogits.as<float>(), temperature, drng.as<uint64_t>(),
-                     dtokens.as<uint32_t>(), int(tcap), dlen.as<int>(), dflags.as<int>(), stream);
+                   wy.as<float>(), wxn.as<float>(), false);
+        head_and_sample(wxn.as<float>(), int(n), int(n) - 1);
     }
 
     // One generated token for every sequence (gpu.rs:2025-2050).
@@ -430,6 +479,10 @@ struct MeshGpt::Impl {
         check(hipMemcpy2DAsync(out, len * 4, dtokens.p, tcap * 4, len * 4, b, hipMemcpyDeviceToHost, stream),
               "download tokens");
         sync();
+    }
+
+    bool decodable(size_t steps) const {
+        return batch > 0 && cached == length - 1 && length - 1 + steps <= cfg.context && length + steps <= tcap;
     }
 };
 
@@ -500,8 +553,7 @@ void MeshGpt::prefill(const uint32_t *prompts, size_t batch, size_t prompt_len, 
 
 void MeshGpt::decode(size_t steps) {
     Impl &m = *impl_;
-    if (m.batch == 0 || m.cached != m.length - 1 || m.length - 1 + steps > m.cfg.context ||
-        m.length + steps > m.tcap)
+    if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
     for (size_t i = 0; i < steps; ++i) m.step();
@@ -510,40 +562,20 @@ void MeshGpt::decode(size_t steps) {
 
 std::vector<float> MeshGpt::decode_profiled(size_t steps) {
     Impl &m = *impl_;
-    if (m.batch == 0 || m.cached != m.length - 1 || m.length - 1 + steps > m.cfg.context ||
-        m.length + steps > m.tcap)
+    if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
-    const size_t launches = steps * m.cfg.layers;
-    std::vector<hipEvent_t> ev(2 * launches);
+    const size_t L = m.cfg.layers;
+    std::vector<hipEvent_t> ev(2 * L * steps);
     for (auto &e : ev) check(hipEventCreate(&e), "hipEventCreate");
-    const kern::Rows rows{int(m.batch), 1, m.dlen.as<int>(), m.dtokens.as<uint32_t>(), int(m.tcap), 0};
-    const kern::Tiling tq = m.tiling(1, m.batch, true), tp = m.tiling(2, m.batch, true);
-    size_t at = 0;
     for (size_t s = 0; s < steps; ++s) {
-        for (size_t l = 0; l < m.cfg.layers; ++l) {
-            const Block &blk = m.layout.blocks[l];
-            const kern::KvView kv = m.cache_layer(l);
-            kern::qkv(m.shape, rows, m.group(blk.query), m.group(blk.key), m.group(blk.value), m.E.as<float>(),
-                      m.dx.as<float>(), m.dq.as<float>(), kv, m.rope.as<float2>(), l == 0, tq, m.stream);
-            check(hipEventRecord(ev[2 * at], m.stream), "event");
-            kern::attn_decode(m.shape, m.dq.as<float>(), kv, rows.len, rows.rows, m.ks, m.smax,
-                              m.part.as<float>(), m.stream);
-            check(hipEventRecord(ev[2 * at + 1], m.stream), "event");
-            ++at;
-            kern::post(m.shape, rows, m.part.as<float>(), m.ks, m.smax, nullptr, kv, m.group(blk.projection),
-                       m.group(blk.ffn), m.dx.as<float>(), tp, m.stream);
-        }
-        kern::head(m.shape, m.dx.as<float>(), int(m.batch), 1, 0, m.Et.as<float>(), m.dlogits.as<float>(),
-                   m.head_rows(), m.stream);
-        kern::sample(m.shape.V, int(m.batch), m.dlogits.as<float>(), m.temperature, m.drng.as<uint64_t>(),
-                     m.dtokens.as<uint32_t>(), int(m.tcap), m.dlen.as<int>(), m.dflags.as<int>(), m.stream);
+        m.launch_decode_step(ev.data() + 2 * L * s);
         m.cached = m.length;
         ++m.length;
     }
     m.finish();
-    std::vector<float> ms(launches);
-    for (size_t i = 0; i < launches; ++i) check(hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]), "elapsed");
+    std::vector<float> ms(L * steps);
+    for (size_t i = 0; i < ms.size(); ++i) check(hipEventElapsedTime(&ms[i], ev[2 * i], ev[2 * i + 1]), "elapsed");
     for (auto &e : ev) (void)hipEventDestroy(e);
     return ms;
 }
@@ -561,6 +593,32 @@ std::vector<float> MeshGpt::last_logits() {
 }
 
 hipStream_t MeshGpt::stream() const { return impl_->stream; }
+
+double copy_bandwidth(int device, size_t bytes, int iters) {
+    int count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count) throw Error("invalid device ordinal", kDeviceError);
+    check(hipSetDevice(device), "hipSetDevice");
+    const size_t n = bytes / 16;
+    DevBuf src, dst;
+    src.ensure(n * 16);
+    dst.ensure(n * 16);
+    check(hipMemset(src.p, 0, n * 16), "hipMemset");
+    hipEvent_t start, stop;
+    check(hipEventCreate(&start), "hipEventCreate");
+    check(hipEventCreate(&stop), "hipEventCreate");
+    kern::calibration_copy(src.as<float4>(), dst.as<float4>(), n, nullptr);
+    check(hipEventRecord(start, nullptr), "event");
+    for (int i = 0; i < iters; ++i) kern::calibration_copy(src.as<float4>(), dst.as<float4>(), n, nullptr);
+    check(hipEventRecord(stop, nullptr), "event");
+    check(hipEventSynchronize(stop), "event sync");
+    float ms = 0.0f;
+    check(hipEventElapsedTime(&ms, start, stop), "elapsed");
+    (void)hipEventDestroy(start);
+    (void)hipEventDestroy(stop);
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    return 2.0 * double(n * 16) * iters / (double(ms) / 1000.0) / 1e9;
+}
 
 void MeshGpt::synchronize() { impl_->sync(); }
 

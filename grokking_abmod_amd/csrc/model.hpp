@@ -56,4 +56,8 @@ class MeshGpt {
     std::unique_ptr<Impl> impl_;
 };
 
+// Mean bandwidth (read + write bytes / s / 1e9) of a plain device copy of
+// `bytes`, repeated `iters` times on `device`.
+double copy_bandwidth(int device, size_t bytes, int iters);
+
 }  // namespace meshgpt

@@ -117,6 +117,12 @@ int mg_last_logits(mg_model *model, float *out, size_t n);
 /* The hipStream_t every call of this model runs on. */
 void *mg_model_stream(mg_model *model);
 
+/* A plain device-to-device copy of `bytes` (a float4 grid-stride kernel named
+ * calibration_copy) run `iters` times on `device`; writes the mean bandwidth
+ * counting read plus write bytes.  No reference counterpart: it calibrates the
+ * HBM byte counters and gives the measured copy roofline of the box. */
+int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps);
+
 /* Checkpoint (src/gpt/checkpoint.rs:24-192).  mg_checkpoint_load reads the file
  * into a handle; query its parts, then free it. */
 typedef struct mg_checkpoint mg_checkpoint;
