@@ -9,7 +9,8 @@ steps starting right after the prompt (K = 512 is the full config-3 run), with
 every input already resident in HBM.
 
 Prints one JSON line with the roofline of the dominant kernel (split-KV decode
-attention, timed per launch with HIP events on the model's stream), the
+attention, timed per launch with HIP events that hipExtLaunchKernel stamps with
+the dispatch's own begin and end on the model's stream), the
 step-level fraction of the HBM roofline, the batch-1 (config 1) figure and the
 CPU baseline (the f64 oracle on one core, a bounded sample of the workload).
 """
@@ -174,7 +175,7 @@ def pmc_traffic(args, config, batch):
         out = tempfile.mkdtemp(prefix="mg_pmc_")
         cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
                "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe",
-               "--steps", "8"]
+               "--steps", str(args.steps), "--prompt", str(args.prompt), "--batch", str(batch)]
         res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
         files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
         if not files:
@@ -204,8 +205,9 @@ PROBE_COPY_BYTES = 256 << 20
 
 
 def probe(args):
-    """Child process under rocprofv3 --pmc: a few decode steps of the workload and
-    one plain copy kernel of known size for calibration."""
+    """Child process under rocprofv3 --pmc: the timed region's decode steps (same
+    positions, so per-launch means compare with the algorithmic bytes) and one
+    plain copy kernel of known size for calibration."""
     config = G.named_config("mid")
     prompts = prompts_for(config, args.batch, args.prompt)
     with G.MeshGpt(0, config, 7, max_batch=args.batch) as model:
@@ -260,8 +262,9 @@ def main():
             model.decode(args.warmup)
         hip.synchronize()
         ms, wall_ms = run_decode(hip, model, prompts, args.steps, temperature, 7)
-        # Roofline pass: the same steps without graph replay, each decode-attention
-        # launch bracketed by HIP events on the model's stream.
+        # Roofline pass: the same steps (same positions) without graph replay; each
+        # decode-attention launch goes through hipExtLaunchKernel with a pair of HIP
+        # events on the model's stream that take the dispatch's begin and end.
         model.prefill(prompts, temperature, 7, reserve=args.prompt + 1 + args.steps)
         per_launch = model.decode_profiled(args.steps).reshape(args.steps, config.layers)
 
@@ -273,6 +276,7 @@ def main():
     step_gbps = total_step_bytes / (ms / 1000.0) / 1e9
 
     traffic = None
+    pmc = None
     if not args.no_pmc:
         try:
             pmc = pmc_traffic(args, config, args.batch)
@@ -311,6 +315,9 @@ def main():
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
+            "traffic_calibration": None if not pmc else {
+                "fetch_factor": round(pmc["FETCH_SIZE_factor"], 4), "write_factor": round(pmc["WRITE_SIZE_factor"], 4),
+                "fetch_bytes": round(pmc["FETCH_SIZE"]), "write_bytes": round(pmc["WRITE_SIZE"])},
             "algorithmic_bytes_per_launch": round(float(attn_bytes.mean())),
             "avg_launch_us": round(float(per_launch.mean()) * 1000.0, 3),
         },

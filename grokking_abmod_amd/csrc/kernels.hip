@@ -15,11 +15,14 @@
 // register ring three layers ahead, and every kernel issues its independent
 // global loads before its first wait.  All arithmetic is FP32.
 // Reference semantics: src/gpt/reference.rs:104-228, src/gpt/gpu.rs:2006-2053.
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <climits>
 #include <cmath>
+#include <type_traits>
+#include <utility>
 
 #include "kernels.hpp"
 
@@ -32,16 +35,34 @@ constexpr float kXsaFloor = float(double(1e-12f) * double(1e-12f));
 
 #define HIP_LAUNCH_CHECK() (void)hipGetLastError()
 
+// Wave-wide reductions through DPP lane moves (no LDS round trips): quad
+// swaps, half-row and row mirrors, then the row broadcasts of GFX9; the total
+// lands in lane 63 and is read back to every lane.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ float dpp_move(float old, float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, old),
+                                                                 __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                                 0xf, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
+    v += dpp_move<0xB1>(0.0f, v);       // quad_perm [1,0,3,2]
+    v += dpp_move<0x4E>(0.0f, v);       // quad_perm [2,3,0,1]
+    v += dpp_move<0x141>(0.0f, v);      // row_half_mirror
+    v += dpp_move<0x140>(0.0f, v);      // row_mirror
+    v += dpp_move<0x142, 0xa>(0.0f, v); // row_bcast:15
+    v += dpp_move<0x143, 0xc>(0.0f, v); // row_bcast:31
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-    return v;
+    v = fmaxf(v, dpp_move<0xB1>(v, v));
+    v = fmaxf(v, dpp_move<0x4E>(v, v));
+    v = fmaxf(v, dpp_move<0x141>(v, v));
+    v = fmaxf(v, dpp_move<0x140>(v, v));
+    v = fmaxf(v, dpp_move<0x142, 0xa>(v, v));
+    v = fmaxf(v, dpp_move<0x143, 0xc>(v, v));
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
 __device__ __forceinline__ int wave_min_int(int v) {
@@ -56,8 +77,27 @@ __device__ __forceinline__ int wave_or_int(int v) {
     return v;
 }
 
-// ELU of reference.rs:325-332 (expm1 for negative inputs).
-__device__ __forceinline__ float elu(float z) { return z >= 0.0f ? z : expm1f(z); }
+// Sum over aligned groups of N lanes (N a power of two <= 64), left in every
+// lane of the group: DPP quad swaps and row mirrors inside a 16-lane row, then
+// lane shuffles across rows.
+template <int N>
+__device__ __forceinline__ float group_sum(float v) {
+    if constexpr (N >= 2) v += dpp_move<0xB1>(0.0f, v);   // quad_perm [1,0,3,2]
+    if constexpr (N >= 4) v += dpp_move<0x4E>(0.0f, v);   // quad_perm [2,3,0,1]
+    if constexpr (N >= 8) v += dpp_move<0x141>(0.0f, v);  // row_half_mirror
+    if constexpr (N >= 16) v += dpp_move<0x140>(0.0f, v); // row_mirror
+    if constexpr (N >= 32) v += __shfl_xor(v, 16, 64);
+    if constexpr (N >= 64) v += __shfl_xor(v, 32, 64);
+    return v;
+}
+
+// ELU of reference.rs:325-332.  The negative branch is exp(z) - 1 from the
+// hardware exp2: its absolute error (~1e-7 for z near 0) is that of one f32
+// rounding of the row values, far below the logit tolerance; the library
+// expm1 costs a long dependent chain on every mesh layer.
+__device__ __forceinline__ float elu(float z) {
+    return z >= 0.0f ? z : __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f;
+}
 
 // Flat LDS index -> (row, column) for rows of length W.
 __device__ __forceinline__ void split_row(int idx, const Shape &s, int &r, int &c) {
@@ -96,7 +136,7 @@ __device__ void segment_inv_rms(const float *buf, int nseg, int len, float *inv)
         float acc = 0.0f;
         for (int i = lane; i < len; i += 64) acc = fmaf(p[i], p[i], acc);
         acc = wave_sum(acc);
-        if (lane == 0) inv[sg] = 1.0f / sqrtf(acc * scale + kRmsEps);
+        if (lane == 0) inv[sg] = rsqrtf(acc * scale + kRmsEps);
     }
 }
 
@@ -136,70 +176,62 @@ size_t align16(size_t x) { return (x + 15) & ~size_t(15); }
 
 // ------------------------------------------------------------- mesh stacks
 
-// The [self, partner] weights of a thread's CPT channels for the next three
-// layers of a mesh; a slot is refilled three layers ahead of its use.
-template <int CPT>
-struct MeshRing {
-    float2 w[3][CPT];
-};
-
-template <int CPT>
-__device__ __forceinline__ void ring_load(float2 (&slot)[CPT], const float2 *__restrict__ wp, int layer, int W,
-                                          int tt, int T) {
-#pragma unroll
-    for (int k = 0; k < CPT; ++k) slot[k] = wp[size_t(layer) * W + min(tt + k * T, W - 1)];
-}
-
-template <int CPT>
-__device__ __forceinline__ void ring_prime(MeshRing<CPT> &ring, const float *w, int depth, int W, int tt, int T,
-                                           bool active) {
-    if (!active) return;
-    const float2 *wp = reinterpret_cast<const float2 *>(w);
-#pragma unroll
-    for (int u = 0; u < 3; ++u)
-        if (u < depth) ring_load<CPT>(ring.w[u], wp, u, W, tt, T);
-}
-
 // A mesh stack (reference.rs:422-453) over the nr rows in LDS `in`, computed by
 // the team of T threads whose `active` flag is set (thread tt of the team owns
-// channels tt + k*T).  Every thread of the block calls it: one barrier per
-// layer.  Layer outputs alternate between a and b; returns the last one.
+// channels tt + k*T).  `w` holds the [self, partner] pairs of every layer, in
+// LDS (staged) or global memory.  Every thread of the block calls it: one
+// barrier per layer.  Outputs alternate between a and b; returns the last.
 template <int CPT>
-__device__ const float *mesh_team(MeshRing<CPT> &ring, const float *in, float *a, float *b, int nr,
-                                  const Shape &s, const float *__restrict__ w, int depth, int tt, int T,
-                                  bool active) {
+__device__ const float *mesh_team(const float *in, float *a, float *b, int nr, const Shape &s,
+                                  const float2 *w, int depth, int tt, int T, bool active) {
     const int W = s.W;
-    const float2 *wp = reinterpret_cast<const float2 *>(w);
     const float *cur = in;
     float *nxt = a;
-    for (int l0 = 0; l0 < depth; l0 += 3) {
+    for (int l = 0; l < depth; ++l) {
+        if (active) {
+            const int st = s.butterfly ? (1 << (l % s.log2w)) : 1;
+            const bool last = l + 1 == depth;
+            const float2 *wl = w + size_t(l) * W;
+            if (nr == 1) {
+                // One row (decode): the CPT channels' loads, then their
+                // arithmetic, interleaved.
+                float xs[CPT], xp[CPT];
+                float2 ww[CPT];
 #pragma unroll
-        for (int u = 0; u < 3; ++u) {
-            const int l = l0 + u;
-            if (l < depth) {
-                if (active) {
-                    const int st = s.butterfly ? (1 << (l % s.log2w)) : 1;
-                    const bool last = l + 1 == depth;
+                for (int k = 0; k < CPT; ++k) {
+                    const int c = min(tt + k * T, W - 1);
+                    int p = c + st;
+                    if (p >= W) p -= W;
+                    xs[k] = cur[c];
+                    xp[k] = cur[p];
+                    ww[k] = wl[c];
+                }
+                // Buffers are padded to CPT*T floats, so lanes past W store
+                // (ignored) values without a branch.
 #pragma unroll
-                    for (int k = 0; k < CPT; ++k) {
-                        const int c = tt + k * T;
-                        if (c < W) {
-                            int p = c + st;
-                            if (p >= W) p -= W;
-                            const float2 ww = ring.w[u][k];
-                            for (int r = 0; r < nr; ++r) {
-                                const float z = cur[r * W + c] * ww.x + cur[r * W + p] * ww.y;
-                                nxt[r * W + c] = last ? z : elu(z);
-                            }
+                for (int k = 0; k < CPT; ++k) {
+                    const float z = xs[k] * ww[k].x + xp[k] * ww[k].y;
+                    nxt[tt + k * T] = last ? z : elu(z);
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < CPT; ++k) {
+                    const int c = tt + k * T;
+                    if (c < W) {
+                        int p = c + st;
+                        if (p >= W) p -= W;
+                        const float2 ww = wl[c];
+                        for (int r = 0; r < nr; ++r) {
+                            const float z = cur[r * W + c] * ww.x + cur[r * W + p] * ww.y;
+                            nxt[r * W + c] = last ? z : elu(z);
                         }
                     }
-                    if (l + 3 < depth) ring_load<CPT>(ring.w[u], wp, l + 3, W, tt, T);
                 }
-                __syncthreads();
-                cur = nxt;
-                nxt = nxt == a ? b : a;
             }
         }
+        __syncthreads();
+        cur = nxt;
+        nxt = nxt == a ? b : a;
     }
     return cur;
 }
@@ -207,123 +239,137 @@ __device__ const float *mesh_team(MeshRing<CPT> &ring, const float *in, float *a
 // Buffer holding the result of a depth-layer mesh_team run with (a, b).
 __device__ __forceinline__ float *mesh_result(float *a, float *b, int depth) { return (depth & 1) ? a : b; }
 
+// Floats of one mesh buffer: rpw rows, at least `sweep` channels, 16-byte rows.
+__host__ __device__ inline size_t mesh_buffer_floats(int W, int rpw, int sweep1, int sweep2) {
+    const size_t n = std::max<size_t>(size_t(rpw) * W, size_t(std::max(sweep1, sweep2)));
+    return (n + 3) / 4 * 4;
+}
+
+// Per-thread register capacity (float2) for weights loaded at kernel start:
+// the projection + FFN meshes, and the Q/K/V meshes held until LDS frees up.
+constexpr int kHoldPF = 16, kHoldQKV = 24;
+
+template <int HOLD>
+__device__ __forceinline__ void hold_load(float2 (&h)[HOLD], const float2 *__restrict__ src, int n) {
+#pragma unroll
+    for (int k = 0; k < HOLD; ++k) h[k] = src[min(k * int(blockDim.x) + int(threadIdx.x), n - 1)];
+}
+
+template <int HOLD>
+__device__ __forceinline__ void hold_store(const float2 (&h)[HOLD], float2 *dst, int n) {
+#pragma unroll
+    for (int k = 0; k < HOLD; ++k) {
+        const int i = k * int(blockDim.x) + int(threadIdx.x);
+        if (i < n) dst[i] = h[k];
+    }
+}
+
 // ------------------------------------------------------------ block kernel
 
 // Post-attention half of block l-1 (reference.rs:194-216) fused with the
 // pre-attention half of block l (reference.rs:164-193) for a tile of rows.
-// Launch: one workgroup per `rpw` rows, teams x T threads.
-template <int CPT>
+// One workgroup per `rpw` rows, teams x T threads.  STAGED: all mesh weights
+// are read from global memory once at kernel start (the projection + FFN pair
+// straight into LDS, the Q/K/V triple into registers until the post half has
+// released LDS); otherwise the meshes read their weights from global memory.
+template <int CPT, bool STAGED, int TEAMS>
 __global__ void __launch_bounds__(768)
 block_kernel(BlockArgs a) {
+    // The projection and FFN meshes run on every thread of the block.
+    constexpr int CPTW = TEAMS == 3 ? (CPT + 2) / 3 : CPT;
     extern __shared__ __align__(16) char smem[];
     LdsCarve lds{smem};
     const Shape &s = a.s;
     const int W = s.W, rpw = a.rpw;
-    const int T = int(blockDim.x) / a.teams, team = int(threadIdx.x) / T, tt = int(threadIdx.x) - team * T;
+    const int T = int(blockDim.x) / TEAMS, team = int(threadIdx.x) / T, tt = int(threadIdx.x) - team * T;
     const bool post = a.wproj != nullptr, pre = a.wq != nullptr;
+    const int n_pf = (s.A + s.F) * W, n_qkv = 3 * s.A * W;
+    float2 *S = lds.take<float2>(STAGED ? size_t(max(post ? n_pf : 0, pre ? n_qkv : 0)) : 0);
     float *X = lds.take<float>(size_t(rpw) * W);
-    float *N = lds.take<float>(size_t(rpw) * W);
-    // 2*teams ping-pong buffers of rpw rows each, addressed by index (no
-    // pointer arrays: those would live in scratch memory).
-    const size_t bstride = (size_t(rpw) * W * 4 + 15) / 16 * 4;
-    float *bufs = lds.take<float>(bstride * 2 * a.teams);
+    // Mesh buffers hold rpw rows, padded to the widest channel sweep so the
+    // one-row path stores without bounds checks.  The 2*teams ping-pong buffers
+    // are addressed by index (a pointer array would live in scratch memory).
+    const size_t bstride = mesh_buffer_floats(W, rpw, CPT * T, CPTW * int(blockDim.x));
+    float *N = lds.take<float>(bstride);
+    float *bufs = lds.take<float>(bstride * 2 * TEAMS);
     auto buf = [bufs, bstride](int i) { return bufs + size_t(i) * bstride; };
     float *inv1 = lds.take<float>(size_t(rpw) * s.H);
     float *inv2 = lds.take<float>(size_t(rpw) * s.H);
     float *rinv = lds.take<float>(size_t(rpw));
-    float *wsplit = lds.take<float>(a.part ? size_t(rpw) * s.H * a.nsplit : 0);
     const int r0 = blockIdx.x * rpw, nr = min(rpw, a.ro.rows - r0);
+    float *Y = buf(0), *Vs = buf(1);
 
-    // Weight rings first: their loads overlap the row loads below.
-    MeshRing<CPT> rp, rf, rq;
-    if (post) {
-        ring_prime<CPT>(rp, a.wproj, s.A, W, tt, T, team == 0);
-        ring_prime<CPT>(rf, a.wffn, s.F, W, tt, T, team == 0);
+    // 1. Every independent global load first: weights, rows, attention output.
+    float2 hpf[STAGED ? kHoldPF : 1], hqkv[STAGED ? kHoldQKV : 1];
+    if constexpr (STAGED) {
+        if (post) hold_load<kHoldPF>(hpf, reinterpret_cast<const float2 *>(a.wproj), n_pf);
+        else if (pre) hold_load<kHoldQKV>(hqkv, reinterpret_cast<const float2 *>(a.wq), n_qkv);
     }
-    const float *wmine = team == 0 ? a.wq : (team == 1 ? a.wk : a.wv);
-    if (pre) ring_prime<CPT>(rq, a.teams == 3 ? wmine : a.wq, s.A, W, tt, T, true);
-
-    // Residual rows: the token vectors (first block) or x.
     for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
-        int r, c;
+        int r, c, h, d, seq, pos;
         split_row(idx, s, r, c);
         const int row = r0 + r;
-        float v;
+        row_position(a.ro, row, seq, pos);
+        float xv;
         if (a.embed) {
-            int seq, pos;
-            row_position(a.ro, row, seq, pos);
             const uint32_t tok = a.ro.tokens[size_t(seq) * a.ro.tok_stride + a.ro.tok_offset + pos];
-            v = a.E[size_t(tok) * W + c];
-            a.x[size_t(row) * W + c] = v;
+            xv = a.E[size_t(tok) * W + c];
+            a.x[size_t(row) * W + c] = xv;
         } else {
-            v = a.x[size_t(row) * W + c];
+            xv = a.x[size_t(row) * W + c];
         }
-        X[idx] = v;
-    }
-
-    if (post) {
-        const int stride = s.hdp + 2;
-        float *Y = buf(0), *Vs = buf(1);
-        if (a.part) {
-            // Split combine, step 1: every (row, head, split) softmax maximum in one
-            // pass, then per (row, head) the weights exp2(m_s - M) / L.
-            const int hs = s.H * a.nsplit;
-            for (int i = threadIdx.x; i < nr * hs; i += blockDim.x) {
-                const int r = i / hs, rem = i - r * hs;
-                int seq, pos;
-                row_position(a.ro, r0 + r, seq, pos);
-                wsplit[i] = a.part[(size_t(seq) * hs + rem) * stride + s.hdp];
-            }
-            __syncthreads();
-            for (int i = threadIdx.x; i < nr * s.H; i += blockDim.x) {
-                const int r = i / s.H, h = i - r * s.H;
-                int seq, pos;
-                row_position(a.ro, r0 + r, seq, pos);
-                const float *pp = a.part + (size_t(seq * s.H + h) * a.nsplit) * stride;
-                float *wv = wsplit + size_t(i) * a.nsplit;
-                float M = -INFINITY;
-                for (int k = 0; k < a.nsplit; ++k) M = fmaxf(M, wv[k]);
-                float L = 0.0f;
-                for (int k = 0; k < a.nsplit; ++k) {
-                    wv[k] = exp2f(wv[k] - M);
-                    L = fmaf(wv[k], pp[k * stride + s.hdp + 1], L);
-                }
-                const float il = 1.0f / L;
-                for (int k = 0; k < a.nsplit; ++k) wv[k] *= il;
-            }
-            __syncthreads();
-        }
-        // Attention output y and the row's own value v.
-        for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
-            int r, c, h, d, seq, pos;
-            split_row(idx, s, r, c);
+        if (post) {
             split_head(c, s, h, d);
-            const int row = r0 + r;
-            row_position(a.ro, row, seq, pos);
-            float yval;
+            float yv;
             if (a.part) {
-                // Step 2: y = sum_s w_s acc_s with four splits' loads in flight.
-                const float *pp = a.part + (size_t(seq * s.H + h) * a.nsplit) * stride + d;
-                const float *wv = wsplit + size_t(r * s.H + h) * a.nsplit;
-                float acc = 0.0f;
-                int k = 0;
-                for (; k + 4 <= a.nsplit; k += 4) {
-                    const float a0 = pp[(k + 0) * stride], a1 = pp[(k + 1) * stride];
-                    const float a2 = pp[(k + 2) * stride], a3 = pp[(k + 3) * stride];
-                    acc = fmaf(wv[k], a0, acc);
-                    acc = fmaf(wv[k + 1], a1, acc);
-                    acc = fmaf(wv[k + 2], a2, acc);
-                    acc = fmaf(wv[k + 3], a3, acc);
+                // Merge the split softmax states (m_s, l_s, acc_s) of this head.
+                // Branch-free, so all 24 loads of a group of 8 splits stay in
+                // flight together; an empty split (m = -inf) gets weight 0 and
+                // the running maximum starts at a finite floor.
+                const int stride = s.hdp + 2;
+                const float *pp = a.part + (size_t(seq * s.H + h) * a.nsplit) * stride;
+                float M = -1e30f, num = 0.0f, den = 0.0f;
+                for (int k0 = 0; k0 < a.nsplit; k0 += 8) {
+                    float m8[8], l8[8], a8[8];
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const float *q = pp + size_t(min(k0 + u, a.nsplit - 1)) * stride;
+                        m8[u] = q[s.hdp];
+                        l8[u] = q[s.hdp + 1];
+                        a8[u] = q[d];
+                    }
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const float mu = k0 + u < a.nsplit ? m8[u] : -INFINITY;
+                        const float mn = fmaxf(M, mu);
+                        const float sold = exp2f(M - mn), snew = exp2f(mu - mn);
+                        num = num * sold + a8[u] * snew;
+                        den = den * sold + l8[u] * snew;
+                        M = mn;
+                    }
                 }
-                for (; k < a.nsplit; ++k) acc = fmaf(wv[k], pp[k * stride], acc);
-                yval = acc;
+                yv = num / den;
             } else {
-                yval = a.ybuf[size_t(row) * W + c];
+                yv = a.ybuf[size_t(row) * W + c];
             }
-            Y[idx] = yval;
+            Y[idx] = yv;
             Vs[idx] = a.kv_post.v[(size_t(seq * s.H + h) * a.kv_post.cap + pos) * s.hdp + d];
         }
-        __syncthreads();
+        X[idx] = xv;
+    }
+    if constexpr (STAGED) {
+        if (post) hold_store<kHoldPF>(hpf, S, n_pf);
+        else if (pre) hold_store<kHoldQKV>(hqkv, S, n_qkv);
+    }
+    __syncthreads();
+
+    if (post) {
+        // The Q/K/V weights load while the post half computes.
+        if constexpr (STAGED) {
+            if (pre) hold_load<kHoldQKV>(hqkv, reinterpret_cast<const float2 *>(a.wq), n_qkv);
+        }
+        const float2 *wp = STAGED ? S : reinterpret_cast<const float2 *>(a.wproj);
+        const float2 *wf = wp + size_t(s.A) * W;
         // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
         segment_dots(Y, Vs, nr * s.H, s.hd, inv1, inv2);
         __syncthreads();
@@ -332,11 +378,11 @@ block_kernel(BlockArgs a) {
             split_row(idx, s, r, c);
             split_head(c, s, h, d);
             const int sg = r * s.H + h;
-            const float iv = 1.0f / sqrtf(fmaxf(inv1[sg], kXsaFloor));
+            const float iv = rsqrtf(fmaxf(inv1[sg], kXsaFloor));
             Y[idx] = Y[idx] - (inv2[sg] * iv) * (Vs[idx] * iv);
         }
         __syncthreads();
-        const float *proj = mesh_team<CPT>(rp, Y, buf(1), N, nr, s, a.wproj, s.A, tt, T, team == 0);
+        const float *proj = mesh_team<CPTW>(Y, buf(1), N, nr, s, wp, s.A, threadIdx.x, blockDim.x, true);
         for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) X[idx] += proj[idx];
         __syncthreads();
         segment_inv_rms(X, nr, W, rinv);
@@ -349,13 +395,17 @@ block_kernel(BlockArgs a) {
         }
         __syncthreads();
         float *fa = Nf == N ? buf(0) : N, *fb = Nf == buf(1) ? buf(0) : buf(1);
-        const float *ffn = mesh_team<CPT>(rf, Nf, fa, fb, nr, s, a.wffn, s.F, tt, T, team == 0);
+        const float *ffn = mesh_team<CPTW>(Nf, fa, fb, nr, s, wf, s.F, threadIdx.x, blockDim.x, true);
         for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
             int r, c;
             split_row(idx, s, r, c);
             const float v = X[idx] + ffn[idx];
             X[idx] = v;
             a.x[size_t(r0 + r) * W + c] = v;
+        }
+        // The Q/K/V weights held since kernel start replace the post weights.
+        if constexpr (STAGED) {
+            if (pre) hold_store<kHoldQKV>(hqkv, S, n_qkv);
         }
     }
     __syncthreads();
@@ -376,9 +426,11 @@ block_kernel(BlockArgs a) {
     if (!pre) return;
 
     // Q, K and V meshes: concurrently with three teams, else one after another.
+    const float2 *wqkv = STAGED ? S : reinterpret_cast<const float2 *>(a.wq);
+    const size_t mesh = size_t(s.A) * W;
     const float *res0, *res1, *res2;
-    if (a.teams == 3) {
-        mesh_team<CPT>(rq, N, buf(2 * team), buf(2 * team + 1), nr, s, wmine, s.A, tt, T, true);
+    if constexpr (TEAMS == 3) {
+        mesh_team<CPT>(N, buf(2 * team), buf(2 * team + 1), nr, s, wqkv + team * mesh, s.A, tt, T, true);
         res0 = mesh_result(buf(0), buf(1), s.A);
         res1 = mesh_result(buf(2), buf(3), s.A);
         res2 = mesh_result(buf(4), buf(5), s.A);
@@ -386,18 +438,15 @@ block_kernel(BlockArgs a) {
         // One team: Q's result is copied into X (free once x is normalised), K
         // stays in its buffer, and V alternates between the other buffer and N
         // (N is read only by V's first layer).
-        const float *q = mesh_team<CPT>(rq, N, buf(0), buf(1), nr, s, a.wq, s.A, tt, T, true);
+        const float *q = mesh_team<CPT>(N, buf(0), buf(1), nr, s, wqkv, s.A, tt, T, true);
         for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) X[idx] = q[idx];
         __syncthreads();
-        ring_prime<CPT>(rq, a.wk, s.A, W, tt, T, true);
-        const float *k = mesh_team<CPT>(rq, N, buf(0), buf(1), nr, s, a.wk, s.A, tt, T, true);
-        ring_prime<CPT>(rq, a.wv, s.A, W, tt, T, true);
+        const float *k = mesh_team<CPT>(N, buf(0), buf(1), nr, s, wqkv + mesh, s.A, tt, T, true);
         float *kres = const_cast<float *>(k);
         float *other = kres == buf(0) ? buf(1) : buf(0);
-        const float *v = mesh_team<CPT>(rq, N, other, N, nr, s, a.wv, s.A, tt, T, true);
+        res2 = mesh_team<CPT>(N, other, N, nr, s, wqkv + 2 * mesh, s.A, tt, T, true);
         res0 = X;
         res1 = kres;
-        res2 = v;
     }
     // QK-Norm per head, split-half RoPE at each row's position, cache append.
     segment_inv_rms(res0, nr * s.H, s.hd, inv1);
@@ -433,6 +482,444 @@ block_kernel(BlockArgs a) {
         split_head(c, s, h, d);
         row_position(a.ro, r0 + r, seq, pos);
         a.kv_pre.v[(size_t(seq * s.H + h) * a.kv_pre.cap + pos) * s.hdp + d] = res2[idx];
+    }
+}
+
+// ------------------------------------------------- decode block kernel
+//
+// Decode has one row per sequence, and a row's meshes are chains of dependent
+// layers: latency, not bandwidth, bounds them.  Here each mesh of a row runs
+// on ONE wavefront that keeps the whole row in registers (channel c = j*64 +
+// lane sits in register j of lane `lane`, CPL = W/64 registers) and its layer
+// weights in registers loaded at kernel start, so a layer is a few lane
+// permutes and FMAs with no workgroup barrier.  Four waves per row, one per
+// SIMD, so each may use the SIMD's whole register file (arch VGPRs + AGPRs):
+//   wave 0    split merge, XSA, projection mesh, residual, RMSNorm, FFN mesh,
+//             residual, next RMSNorm -> LDS N
+//   wave 1-3  Q, K, V meshes from N; QK-Norm + RoPE; q row and cache append
+// with one workgroup barrier between the two stages.
+
+constexpr int kDecodeThreads = 256;
+
+// Mesh layers whose weights one wave holds in registers at a time (2*D*CPL
+// registers, sized so the kernel needs no scratch: 9 covers the depth-9
+// meshes of width 512).
+template <int CPL>
+constexpr int wave_mesh_hold() {
+    return CPL >= 16 ? 5 : (CPL >= 8 ? 9 : 16);
+}
+
+// w[u] = weights of layer l0 + u for the layers below depth.
+template <int CPL, int D>
+__device__ __forceinline__ void load_mesh_chunk(float2 (&w)[D][CPL], const float2 *__restrict__ wg, int l0,
+                                                int depth, int lane) {
+#pragma unroll
+    for (int u = 0; u < D; ++u) {
+        if (l0 + u < depth) {
+            const float2 *wl = wg + size_t(l0 + u) * (CPL * 64);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) w[u][j] = wl[j * 64 + lane];
+        }
+    }
+}
+
+__device__ __forceinline__ float lane_read(float v, int byte_addr) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(byte_addr, __builtin_bit_cast(int, v)));
+}
+
+// f(integral_constant<int, I>) for I = 0..N-1, expanded by the front end:
+// register-array indices built from I are constants before any optimisation
+// pass runs, so a select between two elements never becomes a select of the
+// index (which would turn the array into dynamically indexed memory).
+template <class F, int... I>
+__device__ __forceinline__ void static_for_impl(F &f, std::integer_sequence<int, I...>) {
+    (f(std::integral_constant<int, I>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F &&f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// p[j] = value of channel (c + st) mod W for c = j*64 + lane.  For st < 64
+// each lane offers register j, or j+1 when it is one of the first st lanes
+// (their readers wrapped past lane 63), and the readers take lane (lane+st)
+// mod 64; for st = 64k it is register (j + k) mod CPL of the same lane.
+template <int CPL>
+__device__ __forceinline__ void mesh_partner(const float (&x)[CPL], float (&p)[CPL], int st, int lane) {
+    if (st < 64) {
+        const int addr = ((lane + st) & 63) << 2;
+        const bool next = lane < st;
+        static_for<CPL>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            const float offer = next ? x[(j + 1) % CPL] : x[j];
+            p[j] = lane_read(offer, addr);
+        });
+        return;
+    }
+    const int k = st >> 6;
+    static_for<CPL>([&](auto K) {
+        constexpr int kk = decltype(K)::value;
+        if (kk > 0 && (kk & (kk - 1)) == 0 && k == kk) {
+            static_for<CPL>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                p[j] = x[(j + kk) % CPL];
+            });
+        }
+    });
+}
+
+// A mesh stack (reference.rs:422-453) over one row held by one wave.  w holds
+// the first D layers' weights (loaded by the caller ahead of time); deeper
+// stacks reload it D layers at a time.  With `next`, w is left holding the
+// first layers of the next mesh (depth next_depth): when this stack fits in w,
+// each slot is refilled right after its layer has run, so those loads overlap
+// the rest of this stack.
+template <int CPL, int D>
+__device__ void wave_mesh(float (&x)[CPL], float2 (&w)[D][CPL], const float2 *__restrict__ wg, int depth,
+                          const Shape &s, int lane, const float2 *__restrict__ next = nullptr,
+                          int next_depth = 0) {
+    const int W = CPL * 64;
+    const bool refill = next != nullptr && depth <= D;
+    int st = 1;
+    for (int l0 = 0;; l0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            if (l0 + u < depth) {
+                float p[CPL];
+                mesh_partner<CPL>(x, p, st, lane);
+                const bool last = l0 + u + 1 == depth;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const float z = x[j] * w[u][j].x + p[j] * w[u][j].y;
+                    x[j] = last ? z : elu(z);
+                }
+                if (s.butterfly) {
+                    st <<= 1;
+                    if (st >= W) st = 1;
+                }
+                if (refill && u < next_depth) {
+                    const float2 *wl = next + size_t(u) * W;
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) w[u][j] = wl[j * 64 + lane];
+                }
+            }
+        }
+        if (l0 + D >= depth) break;
+        load_mesh_chunk<CPL, D>(w, wg, l0 + D, depth, lane);
+    }
+    if (next != nullptr) {
+        if (refill) {
+            // Slots past this stack's depth.
+#pragma unroll
+            for (int u = 0; u < D; ++u) {
+                if (u >= depth && u < next_depth) {
+                    const float2 *wl = next + size_t(u) * W;
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) w[u][j] = wl[j * 64 + lane];
+                }
+            }
+        } else {
+            load_mesh_chunk<CPL, D>(w, next, 0, next_depth, lane);
+        }
+    }
+}
+
+// Fixed-depth form for butterfly meshes: all DEPTH layers unrolled into one
+// straight-line block (no per-layer branch, so the scheduler overlaps a
+// layer's lane permutes with the previous layer's tail), with each layer's
+// stride a constant: strides >= 64 are register renames.
+template <int CPL, int ST>
+__device__ __forceinline__ void mesh_partner_c(const float (&x)[CPL], float (&p)[CPL], int lane) {
+    if constexpr (ST < 64) {
+        const int addr = ((lane + ST) & 63) << 2;
+        const bool next = lane < ST;
+        static_for<CPL>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            p[j] = lane_read(next ? x[(j + 1) % CPL] : x[j], addr);
+        });
+    } else {
+        static_for<CPL>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            p[j] = x[(j + ST / 64) % CPL];
+        });
+    }
+}
+
+template <int CPL, int DEPTH>
+__device__ __forceinline__ void load_mesh_all(float2 (&w)[DEPTH][CPL], const float2 *__restrict__ wg, int lane) {
+    static_for<DEPTH>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) w[u][j] = wg[u * (CPL * 64) + j * 64 + lane];
+    });
+}
+
+template <int CPL, int DEPTH>
+__device__ __forceinline__ void wave_mesh_fixed(float (&x)[CPL], const float2 (&w)[DEPTH][CPL], int lane) {
+    constexpr int LOG2W = CPL == 1 ? 6 : CPL == 2 ? 7 : CPL == 4 ? 8 : CPL == 8 ? 9 : 10;
+    static_for<DEPTH>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        constexpr int ST = 1 << (u % LOG2W);
+        float p[CPL];
+        mesh_partner_c<CPL, ST>(x, p, lane);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float z = x[j] * w[u][j].x + p[j] * w[u][j].y;
+            x[j] = u + 1 == DEPTH ? z : elu(z);
+        }
+    });
+}
+
+// out[j] = sum of v over the head holding channel j*64 + lane: HSEG lanes of
+// one register (head width <= 64), or `rph` whole registers (64*rph wide).
+template <int CPL, int HSEG>
+__device__ __forceinline__ void head_sum(const float (&v)[CPL], float (&out)[CPL], int rph) {
+    float t[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) t[j] = group_sum<HSEG>(v[j]);
+    if (HSEG < 64 || rph == 1) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) out[j] = t[j];
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int g = j / rph;
+        float acc = 0.0f;
+#pragma unroll
+        for (int k = 0; k < CPL; ++k)
+            if (k / rph == g) acc += t[k];
+        out[j] = acc;
+    }
+}
+
+// Merge of the split softmax states (m_s, l_s, acc_s) of one channel, G splits
+// per round with clamped (branch-free) loads; an empty split (m = -inf) gets
+// weight 0 and the running maximum starts at a finite floor.
+template <int G>
+__device__ __forceinline__ float merge_splits(const float *__restrict__ pp, int nsplit, int stride, int hdp,
+                                              int d) {
+    float M = -1e30f, num = 0.0f, den = 0.0f;
+    for (int k0 = 0; k0 < nsplit; k0 += G) {
+        float m8[G], l8[G], a8[G];
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const float *q = pp + size_t(min(k0 + u, nsplit - 1)) * stride;
+            m8[u] = q[hdp];
+            l8[u] = q[hdp + 1];
+            a8[u] = q[d];
+        }
+#pragma unroll
+        for (int u = 0; u < G; ++u) {
+            const float mu = k0 + u < nsplit ? m8[u] : -INFINITY;
+            const float mn = fmaxf(M, mu);
+            const float sold = exp2f(M - mn), snew = exp2f(mu - mn);
+            num = num * sold + a8[u] * snew;
+            den = den * sold + l8[u] * snew;
+            M = mn;
+        }
+    }
+    return num / den;
+}
+
+// 1/sqrt(mean(x^2) + eps) of the wave's row (reference.rs:392-409).
+template <int CPL>
+__device__ __forceinline__ float row_inv_rms(const float (&x)[CPL]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
+    return rsqrtf(wave_sum(acc) * (1.0f / float(CPL * 64)) + kRmsEps);
+}
+
+// One decode row per workgroup (Rows.rows_per_seq == 1); block semantics as
+// block_kernel.  Requires W = 64*CPL and head width HSEG (<= 64) or a
+// multiple of 64 (HSEG = 64).  DEPTH > 0: butterfly meshes with A = F =
+// DEPTH (fixed-depth straight-line meshes, the FFN weights in registers of
+// their own); DEPTH = 0: any depth and connectivity.
+template <int CPL, int HSEG, int DEPTH>
+__global__ void __launch_bounds__(kDecodeThreads) __attribute__((amdgpu_waves_per_eu(1, 1)))
+block_decode_kernel(BlockArgs a) {
+    constexpr int W = CPL * 64;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : wave_mesh_hold<CPL>();
+    static_assert(!FIXED || 4 * DEPTH * CPL <= 320, "two fixed meshes must fit the register file");
+    __shared__ float N[W];
+    const Shape &s = a.s;
+    const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
+    const int row = blockIdx.x;
+    int seq, pos;
+    row_position(a.ro, row, seq, pos);
+    const bool post = a.wproj != nullptr, pre = a.wq != nullptr;
+    const int rph = HSEG < 64 ? 1 : s.hd >> 6;
+    // Head and in-head dim of register j's channel.
+    auto head_of = [&](int j) { return HSEG < 64 ? j * (64 / HSEG) + lane / HSEG : j / rph; };
+    auto dim_of = [&](int j) { return HSEG < 64 ? lane % HSEG : (j % rph) * 64 + lane; };
+    auto load_weights = [&](float2 (&w)[D][CPL], const float *wg, int depth) {
+        if constexpr (FIXED) load_mesh_all<CPL, DEPTH>(w, reinterpret_cast<const float2 *>(wg), lane);
+        else load_mesh_chunk<CPL, D>(w, reinterpret_cast<const float2 *>(wg), 0, depth, lane);
+    };
+    float2 w[D][CPL];
+    float x[CPL];
+    float2 cs[CPL];  // RoPE (cos, sin) of each channel's pair at this position (Q and K waves)
+
+    if (wave == 0) {
+        // Every load first: the row, the attention state, the meshes' weights.
+        if (a.embed) {
+            const uint32_t tok = a.ro.tokens[size_t(seq) * a.ro.tok_stride + a.ro.tok_offset + pos];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                x[j] = a.E[size_t(tok) * W + j * 64 + lane];
+                a.x[size_t(row) * W + j * 64 + lane] = x[j];
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[j] = a.x[size_t(row) * W + j * 64 + lane];
+        }
+        if (post) {
+            float y[CPL], v[CPL];
+            float2 wf[FIXED ? D : 1][CPL];
+            const int stride = s.hdp + 2;
+            const float *part0 = a.part + size_t(seq * s.H) * a.nsplit * stride;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                v[j] = a.kv_post.v[(size_t(seq * s.H + head_of(j)) * a.kv_post.cap + pos) * s.hdp + dim_of(j)];
+            if (a.nsplit <= 2) {
+                float m2[CPL][2], l2[CPL][2], a2[CPL][2];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const float *pp = part0 + size_t(head_of(j)) * a.nsplit * stride;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float *q = pp + size_t(min(u, a.nsplit - 1)) * stride;
+                        m2[j][u] = q[s.hdp];
+                        l2[j][u] = q[s.hdp + 1];
+                        a2[j][u] = q[dim_of(j)];
+                    }
+                }
+                load_weights(w, a.wproj, s.A);
+                if constexpr (FIXED) load_mesh_all<CPL, DEPTH>(wf, reinterpret_cast<const float2 *>(a.wffn), lane);
+                // Merge of the two split softmax states (see merge_splits).
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    float M = -1e30f, num = 0.0f, den = 0.0f;
+#pragma unroll
+                    for (int u = 0; u < 2; ++u) {
+                        const float mu = u < a.nsplit ? m2[j][u] : -INFINITY;
+                        const float mn = fmaxf(M, mu);
+                        const float sold = exp2f(M - mn), snew = exp2f(mu - mn);
+                        num = num * sold + a2[j][u] * snew;
+                        den = den * sold + l2[j][u] * snew;
+                        M = mn;
+                    }
+                    y[j] = num / den;
+                }
+            } else {
+                load_weights(w, a.wproj, s.A);
+                if constexpr (FIXED) load_mesh_all<CPL, DEPTH>(wf, reinterpret_cast<const float2 *>(a.wffn), lane);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                    y[j] = merge_splits<8>(part0 + size_t(head_of(j)) * a.nsplit * stride, a.nsplit, stride,
+                                           s.hdp, dim_of(j));
+            }
+            // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
+            float vv[CPL], yv[CPL], t[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
+            head_sum<CPL, HSEG>(t, vv, rph);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
+            head_sum<CPL, HSEG>(t, yv, rph);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
+                y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
+            }
+            if constexpr (FIXED) wave_mesh_fixed<CPL, DEPTH>(y, w, lane);
+            else
+                wave_mesh<CPL, D>(y, w, reinterpret_cast<const float2 *>(a.wproj), s.A, s, lane,
+                                  reinterpret_cast<const float2 *>(a.wffn), s.F);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[j] += y[j];
+            const float inv = row_inv_rms<CPL>(x);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
+            if constexpr (FIXED) wave_mesh_fixed<CPL, DEPTH>(y, wf, lane);
+            else wave_mesh<CPL, D>(y, w, reinterpret_cast<const float2 *>(a.wffn), s.F, s, lane);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                x[j] += y[j];
+                a.x[size_t(row) * W + j * 64 + lane] = x[j];
+            }
+        }
+        if (a.xn || pre) {
+            // The next RMSNorm: the final one for the head, or the block's pre-norm.
+            const float inv = row_inv_rms<CPL>(x);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const float v = x[j] * inv;
+                N[j * 64 + lane] = v;
+                if (a.xn) a.xn[size_t(row) * W + j * 64 + lane] = v;
+            }
+        }
+    } else if (pre) {
+        load_weights(w, wave == 1 ? a.wq : (wave == 2 ? a.wk : a.wv), s.A);
+        if (wave < 3) {
+            const float2 *rope = a.rope + size_t(pos) * s.half;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int d = dim_of(j);
+                cs[j] = rope[d < s.half ? d : d - s.half];
+            }
+        }
+    }
+    __syncthreads();
+    if (wave == 0 || !pre) return;
+
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = N[j * 64 + lane];
+    if constexpr (FIXED) wave_mesh_fixed<CPL, DEPTH>(x, w, lane);
+    else
+        wave_mesh<CPL, D>(x, w, reinterpret_cast<const float2 *>(wave == 1 ? a.wq : (wave == 2 ? a.wk : a.wv)), s.A,
+                          s, lane);
+    const size_t cache_row = size_t(seq * s.H) * a.kv_pre.cap + pos;  // + head * cap, then * hdp
+    if (wave == 3) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            a.kv_pre.v[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + dim_of(j)] = x[j];
+        return;
+    }
+    // QK-Norm per head, then split-half RoPE at the row's position.
+    float sq[CPL], ss[CPL], other[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) sq[j] = x[j] * x[j];
+    head_sum<CPL, HSEG>(sq, ss, rph);
+    const int half = s.half;
+    if (HSEG < 64 || rph == 1) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) other[j] = __shfl_xor(x[j], half, 64);
+    } else {
+        const int m = half >> 6;  // partner register offset j ^ m
+        static_for<CPL>([&](auto M) {
+            constexpr int mm = decltype(M)::value;
+            if (mm > 0 && (mm & (mm - 1)) == 0 && m == mm) {
+                static_for<CPL>([&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    other[j] = x[j ^ mm];
+                });
+            }
+        });
+    }
+    const float scale = 1.0f / float(s.hd);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int d = dim_of(j);
+        const float sc = rsqrtf(ss[j] * scale + kRmsEps);
+        const float self = x[j] * sc, oth = other[j] * sc;
+        const float r = d < half ? self * cs[j].x - oth * cs[j].y : self * cs[j].x + oth * cs[j].y;
+        if (wave == 1)
+            a.q[size_t(row) * W + j * 64 + lane] = r;
+        else
+            a.kv_pre.k[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + d] = r;
     }
 }
 
@@ -526,8 +1013,7 @@ attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *_
             float p = 0.0f;
 #pragma unroll
             for (int e = 0; e < VEC; ++e) p = fmaf(qr[e], kk[u][e], p);
-#pragma unroll
-            for (int o = 1; o < LPK; o <<= 1) p += __shfl_xor(p, o, 64);
+            p = group_sum<LPK>(p);
             sc[u] = (j0 + u * G + g < end) ? p * scale_log2 : -INFINITY;
         }
         float cm = sc[0];
@@ -640,8 +1126,7 @@ attn_prefill_kernel(Shape s, const float *__restrict__ q, KvView kv, int rows_pe
 #pragma unroll
                     for (int e = 0; e < DPT; ++e) p = fmaf(qr[e], kr[e], p);
                 }
-#pragma unroll
-                for (int o = 1; o < TPQ; o <<= 1) p += __shfl_xor(p, o, 64);
+                p = group_sum<TPQ>(p);
                 sc[u] = (j < nk && k0 + j <= qpos) ? p : -INFINITY;
             }
             float cm = sc[0];
@@ -953,7 +1438,8 @@ transpose_kernel(const float *__restrict__ E, float *__restrict__ Et, int V, int
     }
 }
 
-// out = mesh(in) for rows x W with one team (the embedding table from codes).
+// out = mesh(in) for rows x W with one team (the embedding table from codes;
+// runs once per weight upload, so its weights are read from global memory).
 template <int CPT>
 __global__ void __launch_bounds__(256)
 mesh_rows_kernel(Shape s, const float *__restrict__ in, float *__restrict__ out, int rows,
@@ -961,15 +1447,15 @@ mesh_rows_kernel(Shape s, const float *__restrict__ in, float *__restrict__ out,
     extern __shared__ __align__(16) char smem[];
     LdsCarve lds{smem};
     const int W = s.W, T = blockDim.x;
-    float *A = lds.take<float>(size_t(rpw) * W);
-    float *B = lds.take<float>(size_t(rpw) * W);
-    float *C = lds.take<float>(size_t(rpw) * W);
+    const size_t n = mesh_buffer_floats(W, rpw, CPT * T, 0);
+    float *A = lds.take<float>(n);
+    float *B = lds.take<float>(n);
+    float *C = lds.take<float>(n);
     const int r0 = blockIdx.x * rpw, nr = min(rpw, rows - r0);
-    MeshRing<CPT> ring;
-    ring_prime<CPT>(ring, w, depth, W, threadIdx.x, T, true);
     for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) A[idx] = in[size_t(r0) * W + idx];
     __syncthreads();
-    const float *res = mesh_team<CPT>(ring, A, B, C, nr, s, w, depth, threadIdx.x, T, true);
+    const float *res = mesh_team<CPT>(A, B, C, nr, s, reinterpret_cast<const float2 *>(w), depth, threadIdx.x, T,
+                                      true);
     for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) out[size_t(r0) * W + idx] = res[idx];
 }
 
@@ -981,11 +1467,17 @@ calibration_copy_kernel(const float4 *__restrict__ src, float4 *__restrict__ dst
 
 template <int HDP>
 void launch_decode_t(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit,
-                     float *part, hipStream_t stream) {
+                     float *part, hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     const float scale_log2 = float(1.4426950408889634 / std::sqrt(double(s.hd)));
     dim3 grid(nsplit * batch, s.H);
-    hipLaunchKernelGGL(attn_decode_kernel<HDP>, grid, dim3(DecodeCfg<HDP>::THREADS), 0, stream, s, q, kv,
-                       len, nsplit, part, scale_log2);
+    if (start || stop) {
+        // The events take the dispatch's own begin and end timestamps.
+        hipExtLaunchKernelGGL(attn_decode_kernel<HDP>, grid, dim3(DecodeCfg<HDP>::THREADS), 0, stream, start,
+                              stop, 0, s, q, kv, len, nsplit, part, scale_log2);
+    } else {
+        hipLaunchKernelGGL(attn_decode_kernel<HDP>, grid, dim3(DecodeCfg<HDP>::THREADS), 0, stream, s, q, kv,
+                           len, nsplit, part, scale_log2);
+    }
     HIP_LAUNCH_CHECK();
 }
 
@@ -1022,13 +1514,27 @@ int channels_per_thread(int W) {
     return cpt;
 }
 
-size_t block_lds_bytes(const Shape &s, int rpw, int teams, int nsplit) {
-    const size_t row = align16(size_t(rpw) * s.W * 4);
-    return (2 + 2 * size_t(teams)) * row + 2 * align16(size_t(rpw) * s.H * 4) + align16(size_t(rpw) * 4) +
-           align16(size_t(rpw) * s.H * nsplit * 4);
+size_t block_stage_bytes(const Shape &s, bool post, bool pre) {
+    const size_t pf = post ? size_t(s.A + s.F) * s.W * 8 : 0, qkv = pre ? size_t(3 * s.A) * s.W * 8 : 0;
+    return align16(std::max(pf, qkv));
 }
 
-size_t mesh_lds_bytes(const Shape &s, int rpw) { return 3 * align16(size_t(rpw) * s.W * 4); }
+size_t block_lds_bytes(const Shape &s, int rpw, int teams, bool staged, bool post, bool pre) {
+    const int T = team_threads(s.W), cpt = channels_per_thread(s.W);
+    const int cptw = teams == 3 ? (cpt + 2) / 3 : cpt;
+    const size_t mesh = mesh_buffer_floats(s.W, rpw, cpt * T, cptw * teams * T) * 4;
+    return (staged ? block_stage_bytes(s, post, pre) : 0) + align16(size_t(rpw) * s.W * 4) +
+           (1 + 2 * size_t(teams)) * mesh + 2 * align16(size_t(rpw) * s.H * 4) + align16(size_t(rpw) * 4);
+}
+
+bool block_can_stage(const Shape &s, int teams, bool post, bool pre) {
+    const int threads = teams * team_threads(s.W);
+    return (!post || (s.A + s.F) * s.W <= kHoldPF * threads) && (!pre || 3 * s.A * s.W <= kHoldQKV * threads);
+}
+
+size_t mesh_lds_bytes(const Shape &s, int rpw) {
+    return 3 * align16(mesh_buffer_floats(s.W, rpw, channels_per_thread(s.W) * team_threads(s.W), 0) * 4);
+}
 
 size_t head_lds_bytes(const Shape &s, int rt) {
     return align16(size_t(rt) * s.W * 4) + align16(size_t(kHeadGroups) * kHeadMaxRows * kHeadTokens * 4);
@@ -1047,7 +1553,10 @@ void configure_lds(size_t max_bytes) {
     };
     for (int cpt : {1, 2, 4, 8, 16})
         with_cpt(cpt, [&](auto c) {
-            allow(reinterpret_cast<const void *>(&block_kernel<decltype(c)::value>));
+            allow(reinterpret_cast<const void *>(&block_kernel<decltype(c)::value, true, 3>));
+            allow(reinterpret_cast<const void *>(&block_kernel<decltype(c)::value, false, 3>));
+            allow(reinterpret_cast<const void *>(&block_kernel<decltype(c)::value, true, 1>));
+            allow(reinterpret_cast<const void *>(&block_kernel<decltype(c)::value, false, 1>));
             allow(reinterpret_cast<const void *>(&mesh_rows_kernel<decltype(c)::value>));
         });
     allow(reinterpret_cast<const void *>(&head_kernel));
@@ -1070,31 +1579,65 @@ void transpose(const float *E, float *Et, int V, int Vp, int W, hipStream_t stre
     HIP_LAUNCH_CHECK();
 }
 
-void block(const BlockArgs &a, hipStream_t stream) {
+void block(const BlockArgs &a, bool staged, hipStream_t stream) {
     dim3 grid((a.ro.rows + a.rpw - 1) / a.rpw);
-    const size_t lds = block_lds_bytes(a.s, a.rpw, a.teams, a.part ? a.nsplit : 0);
+    const size_t lds = block_lds_bytes(a.s, a.rpw, a.teams, staged, a.wproj != nullptr, a.wq != nullptr);
+    const dim3 threads(a.teams * team_threads(a.s.W));
     with_cpt(channels_per_thread(a.s.W), [&](auto c) {
-        hipLaunchKernelGGL(block_kernel<decltype(c)::value>, grid, dim3(a.teams * team_threads(a.s.W)), lds,
-                           stream, a);
+        constexpr int C = decltype(c)::value;
+        if (a.teams == 3) {
+            if (staged) hipLaunchKernelGGL((block_kernel<C, true, 3>), grid, threads, lds, stream, a);
+            else hipLaunchKernelGGL((block_kernel<C, false, 3>), grid, threads, lds, stream, a);
+        } else {
+            if (staged) hipLaunchKernelGGL((block_kernel<C, true, 1>), grid, threads, lds, stream, a);
+            else hipLaunchKernelGGL((block_kernel<C, false, 1>), grid, threads, lds, stream, a);
+        }
     });
     HIP_LAUNCH_CHECK();
 }
 
+bool block_decode_supported(const Shape &s) {
+    return s.wshift >= 6 && s.W <= 1024 && s.hdshift >= 3;
+}
+
+void block_decode(const BlockArgs &a, hipStream_t stream) {
+    const Shape &s = a.s;
+    const dim3 grid(a.ro.rows), threads(kDecodeThreads);
+    // Fixed-depth instantiations for the shipped configurations' shapes.
+    const bool fixed = s.butterfly && s.A == s.F;
+    if (fixed && s.W == 512 && s.hd == 64 && s.A == 9) {
+        hipLaunchKernelGGL((block_decode_kernel<8, 64, 9>), grid, threads, 0, stream, a);
+    } else if (fixed && s.W == 128 && s.hd == 32 && s.A == 7) {
+        hipLaunchKernelGGL((block_decode_kernel<2, 32, 7>), grid, threads, 0, stream, a);
+    } else {
+        with_cpt(s.W / 64, [&](auto c) {
+            constexpr int C = decltype(c)::value;
+            switch (std::min(s.hd, 64)) {
+            case 8: hipLaunchKernelGGL((block_decode_kernel<C, 8, 0>), grid, threads, 0, stream, a); break;
+            case 16: hipLaunchKernelGGL((block_decode_kernel<C, 16, 0>), grid, threads, 0, stream, a); break;
+            case 32: hipLaunchKernelGGL((block_decode_kernel<C, 32, 0>), grid, threads, 0, stream, a); break;
+            default: hipLaunchKernelGGL((block_decode_kernel<C, 64, 0>), grid, threads, 0, stream, a); break;
+            }
+        });
+    }
+    HIP_LAUNCH_CHECK();
+}
+
 void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit, float *part,
-                 hipStream_t stream) {
+                 hipStream_t stream, hipEvent_t start, hipEvent_t stop) {
     switch (s.hdp) {
-    case 2: return launch_decode_t<2>(s, q, kv, len, batch, nsplit, part, stream);
-    case 4: return launch_decode_t<4>(s, q, kv, len, batch, nsplit, part, stream);
-    case 8: return launch_decode_t<8>(s, q, kv, len, batch, nsplit, part, stream);
-    case 16: return launch_decode_t<16>(s, q, kv, len, batch, nsplit, part, stream);
-    case 32: return launch_decode_t<32>(s, q, kv, len, batch, nsplit, part, stream);
-    case 64: return launch_decode_t<64>(s, q, kv, len, batch, nsplit, part, stream);
-    case 128: return launch_decode_t<128>(s, q, kv, len, batch, nsplit, part, stream);
-    case 256: return launch_decode_t<256>(s, q, kv, len, batch, nsplit, part, stream);
-    case 512: return launch_decode_t<512>(s, q, kv, len, batch, nsplit, part, stream);
-    case 1024: return launch_decode_t<1024>(s, q, kv, len, batch, nsplit, part, stream);
-    case 2048: return launch_decode_t<2048>(s, q, kv, len, batch, nsplit, part, stream);
-    case 4096: return launch_decode_t<4096>(s, q, kv, len, batch, nsplit, part, stream);
+    case 2: return launch_decode_t<2>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 4: return launch_decode_t<4>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 8: return launch_decode_t<8>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 16: return launch_decode_t<16>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 32: return launch_decode_t<32>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 64: return launch_decode_t<64>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 128: return launch_decode_t<128>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 256: return launch_decode_t<256>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 512: return launch_decode_t<512>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 1024: return launch_decode_t<1024>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 2048: return launch_decode_t<2048>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
+    case 4096: return launch_decode_t<4096>(s, q, kv, len, batch, nsplit, part, stream, start, stop);
     default: break;
     }
 }

@@ -58,7 +58,7 @@ struct BlockArgs {
     const float *wproj, *wffn;
     const float *part;
     int nsplit;
-    const float *ybuf;
+    const float *ybuf;  // attention rows when part is null
     KvView kv_post;
     // pre half: weights, token vectors when embed, query rows out, block l's cache
     const float *wq, *wk, *wv;
@@ -76,7 +76,10 @@ struct BlockArgs {
 int team_threads(int W);
 int channels_per_thread(int W);
 
-size_t block_lds_bytes(const Shape &s, int rpw, int teams, int nsplit);
+// LDS of one block_kernel launch; staged adds the weight stage, which needs
+// block_can_stage (the weights fit the per-thread register hold).
+size_t block_lds_bytes(const Shape &s, int rpw, int teams, bool staged, bool post, bool pre);
+bool block_can_stage(const Shape &s, int teams, bool post, bool pre);
 size_t mesh_lds_bytes(const Shape &s, int rpw);
 size_t head_lds_bytes(const Shape &s, int rt);
 size_t head_sample_lds_bytes(const Shape &s);  // size_t(-1) when V is too large
@@ -89,12 +92,19 @@ void mesh_rows(const Shape &s, const float *in, float *out, int rows, const floa
                hipStream_t stream);
 // Et[c][t] = E[t][c], rows of Vp >= V floats with zero padding.
 void transpose(const float *E, float *Et, int V, int Vp, int W, hipStream_t stream);
-void block(const BlockArgs &a, hipStream_t stream);
+void block(const BlockArgs &a, bool staged, hipStream_t stream);
+// Decode variant of block(): one row per sequence (rows_per_seq == 1), each
+// mesh of a row on one wavefront.  Supported for W a power of two in
+// [64, 1024] and a power-of-two head width >= 8.
+bool block_decode_supported(const Shape &s);
+void block_decode(const BlockArgs &a, hipStream_t stream);
 // Split-KV decode attention: one query row per sequence; the len[b] keys are
 // cut into nsplit equal shares whose partial softmax states (acc[hdp], m, l)
-// go to part[((b*H+h)*nsplit+split)*(hdp+2)].
+// go to part[((b*H+h)*nsplit+split)*(hdp+2)].  When start/stop are given the
+// launch goes through hipExtLaunchKernel and the events receive the kernel's
+// own begin and end timestamps.
 void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit,
-                 float *part, hipStream_t stream);
+                 float *part, hipStream_t stream, hipEvent_t start = nullptr, hipEvent_t stop = nullptr);
 // Causal flash attention over whole sequences already appended to the cache.
 void attn_prefill(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y,
                   hipStream_t stream);

@@ -87,11 +87,16 @@ struct MeshGpt::Impl {
     // Prefill / logits workspace, grown on demand.
     DevBuf wx, wxn, wq, wy, wtok, wlogits, wk, wv;
 
-    hipGraph_t graph = nullptr;
-    hipGraphExec_t exec = nullptr;
+    // Decode graphs replaying 1 and kGraphSteps steps.
+    static constexpr size_t kGraphSteps = 8;
+    hipGraph_t graph[2] = {nullptr, nullptr};
+    hipGraphExec_t exec[2] = {nullptr, nullptr};
     size_t graph_batch = 0;
     float graph_temperature = -1.0f;
     bool use_graph = true;
+    // Decode blocks on the one-wave-per-mesh kernel (MG_DISABLE_WAVE_DECODE=1
+    // selects the general block kernel instead).
+    bool wave_decode = false;
 
     ~Impl() {
         drop_graph();
@@ -101,10 +106,12 @@ struct MeshGpt::Impl {
     void activate() const { check(hipSetDevice(device), "hipSetDevice"); }
 
     void drop_graph() {
-        if (exec) (void)hipGraphExecDestroy(exec);
-        if (graph) (void)hipGraphDestroy(graph);
-        exec = nullptr;
-        graph = nullptr;
+        for (int i = 0; i < 2; ++i) {
+            if (exec[i]) (void)hipGraphExecDestroy(exec[i]);
+            if (graph[i]) (void)hipGraphDestroy(graph[i]);
+            exec[i] = nullptr;
+            graph[i] = nullptr;
+        }
         graph_batch = 0;
     }
 
@@ -112,31 +119,40 @@ struct MeshGpt::Impl {
         return batch_cap * size_t(shape.H) * cfg.context * size_t(shape.hdp);
     }
 
-    // Splits per (sequence, head) of decode attention: enough workgroups to
-    // cover the chip (about 2048 for the batch) without tiny shares.
+    // Splits per (sequence, head) of decode attention: about 512 workgroups
+    // for the batch (two per CU).  More, shorter shares measured slower at
+    // B=32 H=8: each workgroup's first loads are latency-bound, and the merge
+    // in the next block launch grows with the split count.
     int splits_for(size_t b) const {
         const int forced = env_int("MG_DECODE_SPLITS", 0);
         if (forced > 0) return std::min(forced, 256);
-        const size_t want = 2048 / std::max<size_t>(b * cfg.heads, 1);
+        const size_t want = 512 / std::max<size_t>(b * cfg.heads, 1);
         return int(std::max<size_t>(1, std::min<size_t>({want, 64, cfg.context})));
     }
 
     // Rows per workgroup and team count of block_kernel.  Decode runs one row
     // per workgroup with the Q/K/V meshes in three concurrent teams; prefill
     // packs rows so mesh weights are reused, keeping at least 256 workgroups.
+    // Row buffers are sized without the weight stage, which each launch adds
+    // when it fits (staged()).
     struct BlockTiling {
         int rpw, teams;
     };
-    BlockTiling block_tiling(size_t rows, bool decode, int nsplit) const {
+    BlockTiling block_tiling(size_t rows, bool decode) const {
         const size_t budget = decode ? lds_limit : std::min<size_t>(lds_limit, 49152);
         for (int teams : {3, 1}) {
             int rpw = decode ? 1 : 16;
             while (rpw > 1 && ((rows + rpw - 1) / rpw < 256 ||
-                               kern::block_lds_bytes(shape, rpw, teams, nsplit) > budget))
+                               kern::block_lds_bytes(shape, rpw, teams, false, true, true) > budget))
                 rpw /= 2;
-            if (kern::block_lds_bytes(shape, rpw, teams, nsplit) <= budget) return {rpw, teams};
+            if (kern::block_lds_bytes(shape, rpw, teams, false, true, true) <= budget) return {rpw, teams};
         }
         throw Error("model width exceeds the workgroup LDS budget", kUnsupported);
+    }
+
+    bool staged(const BlockTiling &t, bool post, bool pre) const {
+        return env_int("MG_DISABLE_STAGING", 0) == 0 && kern::block_can_stage(shape, t.teams, post, pre) &&
+               kern::block_lds_bytes(shape, t.rpw, t.teams, true, post, pre) <= lds_limit;
     }
 
     int mesh_rows_per_group(size_t rows) const {
@@ -164,7 +180,7 @@ struct MeshGpt::Impl {
         activate();
         int lds = 0;
         check(hipDeviceGetAttribute(&lds, hipDeviceAttributeMaxSharedMemoryPerBlock, dev), "LDS query");
-        lds_limit = std::min<size_t>(size_t(lds), 65536);
+        lds_limit = size_t(lds);
         kern::configure_lds(lds_limit);
         check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
         use_graph = env_int("MG_DISABLE_GRAPH", 0) == 0;
@@ -182,6 +198,7 @@ struct MeshGpt::Impl {
         shape.butterfly = cfg.connectivity == MeshConnectivity::Butterfly ? 1 : 0;
         shape.A = int(cfg.attention_mesh_depth);
         shape.F = int(cfg.ffn_mesh_depth);
+        wave_decode = env_int("MG_DISABLE_WAVE_DECODE", 0) == 0 && kern::block_decode_supported(shape);
 
         const size_t C = cfg.context;
 
@@ -284,12 +301,13 @@ struct MeshGpt::Impl {
     // Every block over `rows`: L+1 block_kernel launches (the first also embeds
     // the tokens, the last writes the final RMSNorm rows to xn) with each
     // block's attention between them.  kv_of(l) is block l's cache view.  With
-    // `events`, each decode-attention launch is bracketed by a pair of events.
+    // `events`, each decode-attention launch stamps its own begin and end into
+    // events[2l] and events[2l+1].
     template <class KvOf>
     void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *q, float *y, float *xn,
                     bool decode, hipEvent_t *events = nullptr) {
         const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
-        const BlockTiling t = block_tiling(size_t(rows.rows), decode, nsplit);
+        const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
         for (size_t l = 0; l <= L; ++l) {
             kern::BlockArgs a{};
@@ -320,12 +338,14 @@ struct MeshGpt::Impl {
             } else {
                 a.xn = xn;
             }
-            kern::block(a, stream);
+            if (decode && wave_decode)
+                kern::block_decode(a, stream);
+            else
+                kern::block(a, staged(t, a.wproj != nullptr, a.wq != nullptr), stream);
             if (l == L) break;
             if (decode) {
-                if (events) check(hipEventRecord(events[2 * l], stream), "event");
-                kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream);
-                if (events) check(hipEventRecord(events[2 * l + 1], stream), "event");
+                kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream,
+                                  events ? events[2 * l] : nullptr, events ? events[2 * l + 1] : nullptr);
             } else {
                 kern::attn_prefill(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, stream);
             }
@@ -421,22 +441,27 @@ struct MeshGpt::Impl {
         head_and_sample(dxn.as<float>(), 1, 0);
     }
 
-    void decode_step() {
+    // `n` decode steps (1 or kGraphSteps) as one graph replay; the graphs are
+    // captured on first use for the current batch and temperature.
+    void decode_steps(size_t n) {
         if (!use_graph) {
-            launch_decode_step();
+            for (size_t i = 0; i < n; ++i) launch_decode_step();
             return;
         }
-        if (!exec || graph_batch != batch || graph_temperature != temperature) {
-            drop_graph();
+        if (graph_batch != batch || graph_temperature != temperature) drop_graph();
+        const int g = n == 1 ? 0 : 1;
+        if (!exec[g]) {
             check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "begin capture");
-            launch_decode_step();
-            check(hipStreamEndCapture(stream, &graph), "end capture");
-            check(hipGraphInstantiate(&exec, graph, nullptr, nullptr, 0), "instantiate graph");
+            for (size_t i = 0; i < n; ++i) launch_decode_step();
+            check(hipStreamEndCapture(stream, &graph[g]), "end capture");
+            check(hipGraphInstantiate(&exec[g], graph[g], nullptr, nullptr, 0), "instantiate graph");
             graph_batch = batch;
             graph_temperature = temperature;
         }
-        check(hipGraphLaunch(exec, stream), "graph launch");
+        check(hipGraphLaunch(exec[g], stream), "graph launch");
     }
+
+    void decode_step() { decode_steps(1); }
 
     // Prefill over positions [start, start+n) of every sequence into the cache
     // (positions rebased to 0), then the head on each sequence's last row.
@@ -556,7 +581,14 @@ void MeshGpt::decode(size_t steps) {
     if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
-    for (size_t i = 0; i < steps; ++i) m.step();
+    size_t done = 0;
+    // Whole graphs of kGraphSteps steps, then single steps.
+    for (; done + Impl::kGraphSteps <= steps; done += Impl::kGraphSteps) {
+        m.decode_steps(Impl::kGraphSteps);
+        m.cached = m.length + Impl::kGraphSteps - 1;
+        m.length += Impl::kGraphSteps;
+    }
+    for (; done < steps; ++done) m.step();
     m.finish();
 }
 
