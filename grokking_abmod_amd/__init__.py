@@ -26,6 +26,7 @@ EXPORTS = (
     "mg_decode_profiled", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
+    "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode",
 )
 
 
@@ -109,6 +110,9 @@ def lib():
         "mg_checkpoint_free": (None, [vp]),
         "mg_checkpoint_save": (i, [ctypes.c_char_p, _cfgp, _u32p, sz, _f32p, sz]),
         "mg_copy_bandwidth": (i, [i, sz, i, ctypes.POINTER(ctypes.c_double)]),
+        "mg_tokenizer_from_text": (i, [ctypes.c_char_p, sz, _u32p, sz, _szp]),
+        "mg_tokenizer_encode": (i, [_u32p, sz, ctypes.c_char_p, sz, _u32p, sz, _szp]),
+        "mg_tokenizer_decode": (i, [_u32p, sz, _u32p, sz, ctypes.c_char_p, sz, _szp]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -278,6 +282,47 @@ class MeshGpt:
 
     def stream(self):
         return lib().mg_model_stream(self._h)
+
+
+class CharacterTokenizer:
+    """CharacterTokenizer (src/gpt/text.rs:7-56): token id = index into the sorted
+    unique characters of a text."""
+
+    def __init__(self, characters):
+        self.characters = [c if isinstance(c, str) else chr(c) for c in characters]
+        self._chars = _u32([ord(c) for c in self.characters])
+
+    @staticmethod
+    def from_text(text):
+        data = text.encode("utf-8")
+        n = ctypes.c_size_t()
+        _check(lib().mg_tokenizer_from_text(data, len(data), None, 0, ctypes.byref(n)))
+        out = np.empty(n.value, dtype=np.uint32)
+        _check(lib().mg_tokenizer_from_text(data, len(data), _p(out, _u32p), out.size, ctypes.byref(n)))
+        return CharacterTokenizer([int(c) for c in out])
+
+    def vocab_size(self):
+        return len(self.characters)
+
+    def encode(self, text):
+        data = text.encode("utf-8")
+        out = np.empty(max(len(data), 1), dtype=np.uint32)
+        n = ctypes.c_size_t()
+        _check(lib().mg_tokenizer_encode(_p(self._chars, _u32p), self._chars.size, data, len(data),
+                                         _p(out, _u32p), out.size, ctypes.byref(n)))
+        return out[:n.value]
+
+    def decode(self, tokens):
+        tokens = _u32(tokens).reshape(-1)
+        capacity = 4 * tokens.size + 1
+        buf = ctypes.create_string_buffer(capacity)
+        written = ctypes.c_size_t()
+        _check(lib().mg_tokenizer_decode(_p(self._chars, _u32p), self._chars.size, _p(tokens, _u32p),
+                                         tokens.size, buf, capacity, ctypes.byref(written)))
+        return buf.raw[:written.value].decode("utf-8")
+
+    def __eq__(self, other):
+        return isinstance(other, CharacterTokenizer) and self.characters == other.characters
 
 
 class Checkpoint:

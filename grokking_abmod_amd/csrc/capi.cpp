@@ -237,6 +237,47 @@ int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps) {
     });
 }
 
+int mg_tokenizer_from_text(const char *text, size_t length, uint32_t *characters, size_t capacity, size_t *n) {
+    return guarded([&] {
+        require(text != nullptr || length == 0, "text must not be null");
+        require(n != nullptr, "output must not be null");
+        const auto t = CharacterTokenizer::from_text(std::string(text ? text : "", length));
+        *n = t.vocab_size();
+        if (characters) {
+            require(capacity >= t.vocab_size(), "output buffer is too small");
+            std::memcpy(characters, t.characters().data(), t.vocab_size() * 4);
+        }
+    });
+}
+
+int mg_tokenizer_encode(const uint32_t *characters, size_t vocab, const char *text, size_t length,
+                        uint32_t *tokens, size_t capacity, size_t *n) {
+    return guarded([&] {
+        require(characters != nullptr && (text != nullptr || length == 0) && n != nullptr,
+                "characters, text and output must not be null");
+        const auto t = CharacterTokenizer::from_characters(std::vector<uint32_t>(characters, characters + vocab));
+        const auto ids = t.encode(std::string(text ? text : "", length));
+        require(tokens != nullptr || ids.empty(), "output must not be null");
+        require(capacity >= ids.size(), "output buffer is too small");
+        if (!ids.empty()) std::memcpy(tokens, ids.data(), ids.size() * 4);
+        *n = ids.size();
+    });
+}
+
+int mg_tokenizer_decode(const uint32_t *characters, size_t vocab, const uint32_t *tokens, size_t n, char *out,
+                        size_t capacity, size_t *written) {
+    return guarded([&] {
+        require(characters != nullptr && (tokens != nullptr || n == 0) && written != nullptr,
+                "characters, tokens and output must not be null");
+        const auto t = CharacterTokenizer::from_characters(std::vector<uint32_t>(characters, characters + vocab));
+        const std::string text = t.decode(tokens, n);
+        require(out != nullptr || text.empty(), "output must not be null");
+        require(capacity >= text.size(), "output buffer is too small");
+        if (!text.empty()) std::memcpy(out, text.data(), text.size());
+        *written = text.size();
+    });
+}
+
 int mg_checkpoint_load(const char *path, mg_checkpoint **out) {
     return guarded([&] {
         require(path != nullptr && out != nullptr, "path and output must not be null");

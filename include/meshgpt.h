@@ -123,6 +123,19 @@ void *mg_model_stream(mg_model *model);
  * HBM byte counters and gives the measured copy roofline of the box. */
 int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps);
 
+/* CharacterTokenizer (src/gpt/text.rs:7-56).  A tokenizer is passed as its
+ * characters (Unicode scalar values, token id = index).
+ * mg_tokenizer_from_text (text.rs:13-15): the sorted unique characters of the
+ * UTF-8 text; *n receives their count, and characters may be NULL to query it.
+ * mg_tokenizer_encode (text.rs:30-43): UTF-8 text -> token ids, *n = count.
+ * mg_tokenizer_decode (text.rs:45-55): token ids -> UTF-8 (no terminator),
+ * *written = bytes. */
+int mg_tokenizer_from_text(const char *text, size_t length, uint32_t *characters, size_t capacity, size_t *n);
+int mg_tokenizer_encode(const uint32_t *characters, size_t vocab, const char *text, size_t length,
+                        uint32_t *tokens, size_t capacity, size_t *n);
+int mg_tokenizer_decode(const uint32_t *characters, size_t vocab, const uint32_t *tokens, size_t n, char *out,
+                        size_t capacity, size_t *written);
+
 /* Checkpoint (src/gpt/checkpoint.rs:24-192).  mg_checkpoint_load reads the file
  * into a handle; query its parts, then free it. */
 typedef struct mg_checkpoint mg_checkpoint;
