@@ -923,6 +923,320 @@ block_decode_kernel(BlockArgs a) {
     }
 }
 
+// --------------------------------------------------- row decode kernel
+//
+// A faster decode block: the channels of a row are spread over NW waves,
+// channel c = wave + NW*(lane + 64*j) for j < CPL (W = 64*NW*CPL).  With this
+// map a butterfly stride st < NW crosses waves (one LDS exchange and barrier),
+// NW <= st < 64*NW rotates lanes inside every wave (ds_bpermute, no barrier),
+// and larger strides only rename registers, so most layers of a width-512
+// mesh never wait on a barrier.  Each row runs on three workgroups (teams):
+// all three compute the post-attention half of block l-1 (the projection and
+// FFN meshes are short, serial and cheap to repeat), then team 0 computes Q
+// (and owns the residual row), team 1 K and team 2 V of block l, so the three
+// meshes run on three CUs at once.  Mesh weights, token vectors and the
+// residual rows are stored pre-permuted into this map ("row order": element
+// (j*NW + wave)*64 + lane holds channel c), so every wave's loads are
+// contiguous.
+
+// LDS exchange with the channel st < NW further on.  Double-buffered: the
+// write of exchange k+2 follows the barrier of exchange k+1, which every wave
+// reaches only after its reads of exchange k.
+template <int NW, int CPL>
+__device__ __forceinline__ void row_partner(const float (&x)[CPL], float (&p)[CPL], int st, int lane, int wave,
+                                            float *xch, int &parity) {
+    if (st < NW) {
+        float *b = xch + (parity & 1) * (NW * CPL * 64);
+        ++parity;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) b[(j * NW + wave) * 64 + lane] = x[j];
+        __syncthreads();
+        int w2 = wave + st, l2 = lane, jc = 0;
+        if (w2 >= NW) {
+            w2 -= NW;
+            ++l2;
+        }
+        if (l2 >= 64) {
+            l2 -= 64;
+            jc = 1;
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int j2 = j + jc < CPL ? j + jc : 0;
+            p[j] = b[(j2 * NW + w2) * 64 + l2];
+        }
+    } else if (st < 64 * NW) {
+        // Reader lane l takes lane (l + k) mod 64; readers that wrap past lane
+        // 63 need the next register, and they read exactly the lanes < k.
+        const int k = st / NW;
+        const int addr = ((lane + k) & 63) << 2;
+        const bool next = lane < k;
+        static_for<CPL>([&](auto J) {
+            constexpr int j = decltype(J)::value;
+            p[j] = lane_read(next ? x[(j + 1) % CPL] : x[j], addr);
+        });
+    } else {
+        const int m = st / (64 * NW);
+        static_for<CPL>([&](auto M) {
+            constexpr int mm = decltype(M)::value;
+            if (mm > 0 && m == mm) {
+                static_for<CPL>([&](auto J) {
+                    constexpr int j = decltype(J)::value;
+                    p[j] = x[(j + mm) % CPL];
+                });
+            }
+        });
+    }
+}
+
+template <int NW, int CPL>
+__device__ __forceinline__ void row_layer(float (&x)[CPL], const float2 (&w)[CPL], int st, bool last, int lane,
+                                          int wave, float *xch, int &parity) {
+    float p[CPL];
+    row_partner<NW, CPL>(x, p, st, lane, wave, xch, parity);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const float z = x[j] * w[j].x + p[j] * w[j].y;
+        x[j] = last ? z : elu(z);
+    }
+}
+
+// Weights of mesh layer u in row order: float2 (u*CPL + j)*NW*64 + wave*64 + lane.
+template <int NW, int CPL, int D>
+__device__ __forceinline__ void row_load_weights(float2 (&w)[D][CPL], const float *wg, int lane, int wave) {
+    const float2 *g = reinterpret_cast<const float2 *>(wg) + wave * 64 + lane;
+#pragma unroll
+    for (int u = 0; u < D; ++u)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) w[u][j] = g[(u * CPL + j) * NW * 64];
+}
+
+// A butterfly mesh stack of compile-time depth D (reference.rs:422-453): all
+// layers unrolled, each stride a constant.
+template <int NW, int CPL, int D>
+__device__ __forceinline__ void row_mesh_fixed(float (&x)[CPL], const float2 (&w)[D][CPL], int lane, int wave,
+                                               float *xch, int &parity) {
+    constexpr int W = 64 * NW * CPL;
+    constexpr int LOG2W = W == 128 ? 7 : W == 256 ? 8 : W == 512 ? 9 : 10;
+    static_for<D>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        row_layer<NW, CPL>(x, w[u], 1 << (u % LOG2W), u + 1 == D, lane, wave, xch, parity);
+    });
+}
+
+// Any depth and connectivity: weights stream from global memory one layer ahead.
+template <int NW, int CPL>
+__device__ void row_mesh(float (&x)[CPL], const float *wg, int depth, const Shape &s, int lane, int wave,
+                         float *xch, int &parity) {
+    const float2 *g = reinterpret_cast<const float2 *>(wg) + wave * 64 + lane;
+    float2 wn[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) wn[j] = g[j * NW * 64];
+    for (int u = 0; u < depth; ++u) {
+        float2 wc[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) wc[j] = wn[j];
+        if (u + 1 < depth) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) wn[j] = g[((u + 1) * CPL + j) * NW * 64];
+        }
+        const int st = s.butterfly ? (1 << (u % s.log2w)) : 1;
+        row_layer<NW, CPL>(x, wc, st, u + 1 == depth, lane, wave, xch, parity);
+    }
+}
+
+// Sum over the whole row, in every lane (fixed order: waves 0..NW-1).
+template <int NW>
+__device__ __forceinline__ float row_total(float v, int lane, int wave, float *red) {
+    v = wave_sum(v);
+    if constexpr (NW == 1) return v;
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int w = 0; w < NW; ++w) t += red[w];
+    return t;
+}
+
+// Per-head sums: register j of lane `lane` holds head lane/GL + (64/GL)*j at
+// dim NW*(lane % GL) + wave, so a head is GL lanes of every wave.
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ void row_head_sums(const float (&v)[CPL], float (&out)[CPL], int lane, int wave,
+                                              float *red) {
+    constexpr int G = 64 / GL;
+    float t[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) t[j] = group_sum<GL>(v[j]);
+    if constexpr (NW == 1) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) out[j] = t[j];
+        return;
+    }
+    if (lane % GL == 0) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) red[(j * NW + wave) * G + lane / GL] = t[j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        float a = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) a += red[(j * NW + w) * G + lane / GL];
+        out[j] = a;
+    }
+}
+
+// One decode row (Rows.rows_per_seq == 1) per `teams` workgroups of 64*NW
+// threads; block semantics as block_kernel.  DEPTH > 0: butterfly meshes with
+// A = F = DEPTH held in registers; DEPTH = 0: any depth and connectivity.
+// Requires hd = GL*NW with GL <= 64 (a head is GL lanes of every wave).
+template <int NW, int CPL, int GL, int DEPTH>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
+row_block_kernel(BlockArgs a) {
+    constexpr int W = 64 * NW * CPL, G = 64 / GL;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : 1;
+    __shared__ float xch[2 * W];
+    __shared__ float red[8][CPL * NW * G];
+    const Shape &s = a.s;
+    const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
+    const bool pre = a.wq != nullptr, post = a.wproj != nullptr;
+    const int teams = pre ? 3 : 1;
+    const int row = int(blockIdx.x) / teams, team = int(blockIdx.x) - row * teams;
+    int seq, pos;
+    row_position(a.ro, row, seq, pos);
+    int parity = 0;
+    auto head_of = [&](int j) { return lane / GL + G * j; };
+    const int dim = NW * (lane % GL) + wave;  // in-head dim of every register
+    auto ridx = [&](int j) { return (j * NW + wave) * 64 + lane; };  // row-order index
+    auto chan = [&](int j) { return wave + NW * (lane + 64 * j); };  // channel
+
+    // Every independent load first: row, attention state, weights.
+    float x[CPL];
+    if (a.embed) {
+        const uint32_t tok = a.ro.tokens[size_t(seq) * a.ro.tok_stride + a.ro.tok_offset + pos];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + ridx(j)];
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[j] = a.x[size_t(row) * W + ridx(j)];
+    }
+    const float *wmine = pre ? (team == 0 ? a.wq : team == 1 ? a.wk : a.wv) : nullptr;
+    float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
+    if constexpr (FIXED) {
+        if (post) {
+            row_load_weights<NW, CPL, D>(wp, a.wproj, lane, wave);
+            row_load_weights<NW, CPL, D>(wf, a.wffn, lane, wave);
+        }
+        if (pre) row_load_weights<NW, CPL, D>(wm, wmine, lane, wave);
+    }
+
+    if (post) {
+        float y[CPL], v[CPL];
+        const int stride = s.hdp + 2;
+        const float *part0 = a.part + size_t(seq * s.H) * a.nsplit * stride;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            v[j] = a.kv_post.v[(size_t(seq * s.H + head_of(j)) * a.kv_post.cap + pos) * s.hdp + dim];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float *pp = part0 + size_t(head_of(j)) * a.nsplit * stride;
+            y[j] = a.nsplit <= 2 ? merge_splits<2>(pp, a.nsplit, stride, s.hdp, dim)
+                                 : merge_splits<8>(pp, a.nsplit, stride, s.hdp, dim);
+        }
+        // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
+        float vv[CPL], yv[CPL], t[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
+        row_head_sums<NW, CPL, GL>(t, vv, lane, wave, red[0]);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
+        row_head_sums<NW, CPL, GL>(t, yv, lane, wave, red[1]);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
+            y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
+        }
+        if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(y, wp, lane, wave, xch, parity);
+        else row_mesh<NW, CPL>(y, a.wproj, s.A, s, lane, wave, xch, parity);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            x[j] += y[j];
+            acc = fmaf(x[j], x[j], acc);
+        }
+        const float inv = rsqrtf(row_total<NW>(acc, lane, wave, red[2]) * (1.0f / float(W)) + kRmsEps);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
+        if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(y, wf, lane, wave, xch, parity);
+        else row_mesh<NW, CPL>(y, a.wffn, s.F, s, lane, wave, xch, parity);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[j] += y[j];
+    }
+    if (team == 0 && (post || a.embed)) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) a.x[size_t(row) * W + ridx(j)] = x[j];
+    }
+    if (!a.xn && !pre) return;
+
+    // The next RMSNorm: the final one for the head, or the block's pre-norm.
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
+    const float inv = rsqrtf(row_total<NW>(acc, lane, wave, red[3]) * (1.0f / float(W)) + kRmsEps);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] *= inv;
+    if (a.xn) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) a.xn[size_t(row) * W + chan(j)] = x[j];
+    }
+    if (!pre) return;
+
+    if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(x, wm, lane, wave, xch, parity);
+    else row_mesh<NW, CPL>(x, wmine, s.A, s, lane, wave, xch, parity);
+    const size_t cache_row = size_t(seq * s.H) * a.kv_pre.cap + pos;  // + head * cap, then * hdp
+    if (team == 2) {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            a.kv_pre.v[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[j];
+        return;
+    }
+    // QK-Norm per head, then split-half RoPE at the row's position: the pair
+    // partner (dim +- hd/2) is GL/2 lanes away in the same wave and register.
+    float sq[CPL], ss[CPL], other[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) sq[j] = x[j] * x[j];
+    row_head_sums<NW, CPL, GL>(sq, ss, lane, wave, red[4]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) other[j] = __shfl_xor(x[j], GL / 2, 64);
+    const int half = s.half;
+    const float2 cs = a.rope[size_t(pos) * half + (dim < half ? dim : dim - half)];
+    const float scale = 1.0f / float(s.hd);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const float sc = rsqrtf(ss[j] * scale + kRmsEps);
+        const float self = x[j] * sc, oth = other[j] * sc;
+        const float r = dim < half ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
+        if (team == 0)
+            a.q[size_t(row) * W + chan(j)] = r;
+        else
+            a.kv_pre.k[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = r;
+    }
+}
+
+// dst[r][(j*NW + wave)*64 + lane] = src[r][wave + NW*(lane + 64*j)] for rows of W
+// elements of T (float: token vectors; float2: mesh weight pairs).
+template <class T>
+__global__ void __launch_bounds__(kThreads)
+row_order_kernel(const T *__restrict__ src, T *__restrict__ dst, int rows, int W, int NW) {
+    const size_t n = size_t(rows) * W;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += size_t(gridDim.x) * blockDim.x) {
+        const int r = int(i / W), k = int(i - size_t(r) * W);
+        const int lane = k & 63, jw = k >> 6, wave = jw % NW, j = jw / NW;
+        dst[i] = src[size_t(r) * W + wave + NW * (lane + 64 * j)];
+    }
+}
+
 template <int N>
 __device__ __forceinline__ void load_vec(const float *__restrict__ p, float (&o)[N]) {
     if constexpr (N % 4 == 0) {
@@ -1620,6 +1934,70 @@ void block_decode(const BlockArgs &a, hipStream_t stream) {
             }
         });
     }
+    HIP_LAUNCH_CHECK();
+}
+
+int row_waves(int W) { return W >= 256 ? 4 : 2; }
+
+bool row_block_supported(const Shape &s) {
+    if (s.wshift < 7 || s.wshift > 10) return false;
+    const int nw = row_waves(s.W);
+    if (s.hd % nw != 0) return false;
+    const int gl = s.hd / nw;
+    return gl == 8 || gl == 16 || gl == 32;
+}
+
+template <int NW, int CPL>
+void launch_row_block(const BlockArgs &a, dim3 grid, hipStream_t stream) {
+    const Shape &s = a.s;
+    const dim3 threads(64 * NW);
+    const bool fixed = s.butterfly && s.A == s.F;
+    if constexpr (NW == 4 && CPL == 2) {
+        if (fixed && s.A == 9 && s.hd == 64) {
+            hipLaunchKernelGGL((row_block_kernel<4, 2, 16, 9>), grid, threads, 0, stream, a);
+            return;
+        }
+    }
+    if constexpr (NW == 2 && CPL == 1) {
+        if (fixed && s.A == 7 && s.hd == 32) {
+            hipLaunchKernelGGL((row_block_kernel<2, 1, 16, 7>), grid, threads, 0, stream, a);
+            return;
+        }
+    }
+    if constexpr (NW == 4 && CPL == 4) {
+        if (fixed && s.A == 10 && s.hd == 64) {
+            hipLaunchKernelGGL((row_block_kernel<4, 4, 16, 10>), grid, threads, 0, stream, a);
+            return;
+        }
+    }
+    switch (s.hd / NW) {
+    case 8: hipLaunchKernelGGL((row_block_kernel<NW, CPL, 8, 0>), grid, threads, 0, stream, a); break;
+    case 16: hipLaunchKernelGGL((row_block_kernel<NW, CPL, 16, 0>), grid, threads, 0, stream, a); break;
+    default: hipLaunchKernelGGL((row_block_kernel<NW, CPL, 32, 0>), grid, threads, 0, stream, a); break;
+    }
+}
+
+void row_block(const BlockArgs &a, hipStream_t stream) {
+    const dim3 grid(a.ro.rows * (a.wq != nullptr ? 3 : 1));
+    switch (a.s.W) {
+    case 128: launch_row_block<2, 1>(a, grid, stream); break;
+    case 256: launch_row_block<4, 1>(a, grid, stream); break;
+    case 512: launch_row_block<4, 2>(a, grid, stream); break;
+    default: launch_row_block<4, 4>(a, grid, stream); break;
+    }
+    HIP_LAUNCH_CHECK();
+}
+
+void row_order(const float *src, float *dst, int rows, int W, bool pairs, hipStream_t stream) {
+    const size_t n = size_t(rows) * W;
+    const unsigned blocks = unsigned(std::min<size_t>((n + kThreads - 1) / kThreads, 4096));
+    if (pairs)
+        hipLaunchKernelGGL(row_order_kernel<float2>, dim3(blocks), dim3(kThreads), 0, stream,
+                           reinterpret_cast<const float2 *>(src), reinterpret_cast<float2 *>(dst), rows, W,
+                           row_waves(W));
+    else
+        hipLaunchKernelGGL(row_order_kernel<float>, dim3(blocks), dim3(kThreads), 0, stream, src, dst, rows, W,
+                           row_waves(W));
     HIP_LAUNCH_CHECK();
 }
 

@@ -98,6 +98,16 @@ void block(const BlockArgs &a, bool staged, hipStream_t stream);
 // [64, 1024] and a power-of-two head width >= 8.
 bool block_decode_supported(const Shape &s);
 void block_decode(const BlockArgs &a, hipStream_t stream);
+// Row-order decode block (three workgroups per row, channels spread over
+// row_waves(W) waves: channel c = wave + NW*(lane + 64*j)).  Needs W in
+// {128, 256, 512, 1024} and hd / NW in {8, 16, 32}.  Its E, x and mesh weights
+// are in row order (row_order()); xn, q and the cache stay in channel order.
+int row_waves(int W);
+bool row_block_supported(const Shape &s);
+void row_block(const BlockArgs &a, hipStream_t stream);
+// dst = src with each row of W channels (floats, or float2 weight pairs when
+// `pairs`) permuted into row order.
+void row_order(const float *src, float *dst, int rows, int W, bool pairs, hipStream_t stream);
 // Split-KV decode attention: one query row per sequence; the len[b] keys are
 // cut into nsplit equal shares whose partial softmax states (acc[hdp], m, l)
 // go to part[((b*H+h)*nsplit+split)*(hdp+2)].  When start/stop are given the

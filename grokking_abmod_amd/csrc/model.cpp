@@ -76,6 +76,9 @@ struct MeshGpt::Impl {
     size_t lds_limit = 65536;
 
     DevBuf params, codes, E, Et, rope;
+    // Row-order copies of the block weights and token vectors for the row
+    // decode kernel (kern::row_order).
+    DevBuf wdec, Edec;
 
     // Decode state: KV cache [L][batch_cap][H][context][hdp], per-sequence
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
@@ -94,8 +97,10 @@ struct MeshGpt::Impl {
     size_t graph_batch = 0;
     float graph_temperature = -1.0f;
     bool use_graph = true;
-    // Decode blocks on the one-wave-per-mesh kernel (MG_DISABLE_WAVE_DECODE=1
-    // selects the general block kernel instead).
+    // Decode blocks run on the row-order kernel when the shape allows it, else
+    // on the one-wave-per-mesh kernel, else on the general block kernel
+    // (MG_DISABLE_ROW_DECODE=1 / MG_DISABLE_WAVE_DECODE=1 skip the first two).
+    bool row_decode = false;
     bool wave_decode = false;
 
     ~Impl() {
@@ -199,6 +204,7 @@ struct MeshGpt::Impl {
         shape.A = int(cfg.attention_mesh_depth);
         shape.F = int(cfg.ffn_mesh_depth);
         wave_decode = env_int("MG_DISABLE_WAVE_DECODE", 0) == 0 && kern::block_decode_supported(shape);
+        row_decode = env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
 
         const size_t C = cfg.context;
 
@@ -241,6 +247,15 @@ struct MeshGpt::Impl {
                   "copy table");
         }
         kern::transpose(E.as<float>(), Et.as<float>(), shape.V, vpad, shape.W, stream);
+        if (row_decode) {
+            const size_t emb = cfg.embedding_parameter_count();
+            const size_t block_rows = cfg.layers * (4 * cfg.attention_mesh_depth + cfg.ffn_mesh_depth);
+            wdec.ensure(n * 4);
+            Edec.ensure(cfg.vocab_size * cfg.width * 4);
+            kern::row_order(E.as<float>(), Edec.as<float>(), shape.V, shape.W, false, stream);
+            kern::row_order(params.as<float>() + emb, wdec.as<float>() + emb, int(block_rows), shape.W, true,
+                            stream);
+        }
         sync();
     }
 
@@ -297,6 +312,7 @@ struct MeshGpt::Impl {
     }
 
     const float *group(size_t id) const { return params.as<float>() + layout.groups[id].offset; }
+    const float *group_rows(size_t id) const { return wdec.as<float>() + layout.groups[id].offset; }
 
     // Every block over `rows`: L+1 block_kernel launches (the first also embeds
     // the tokens, the last writes the final RMSNorm rows to xn) with each
@@ -309,6 +325,8 @@ struct MeshGpt::Impl {
         const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
         const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
+        const bool rows_order = decode && row_decode;
+        auto weights = [&](size_t id) { return rows_order ? group_rows(id) : group(id); };
         for (size_t l = 0; l <= L; ++l) {
             kern::BlockArgs a{};
             a.s = shape;
@@ -318,8 +336,8 @@ struct MeshGpt::Impl {
             a.teams = t.teams;
             if (l > 0) {
                 const Block &prev = layout.blocks[l - 1];
-                a.wproj = group(prev.projection);
-                a.wffn = group(prev.ffn);
+                a.wproj = weights(prev.projection);
+                a.wffn = weights(prev.ffn);
                 a.part = decode ? part.as<float>() : nullptr;
                 a.nsplit = nsplit;
                 a.ybuf = decode ? nullptr : y;
@@ -327,10 +345,10 @@ struct MeshGpt::Impl {
             }
             if (l < L) {
                 const Block &blk = layout.blocks[l];
-                a.wq = group(blk.query);
-                a.wk = group(blk.key);
-                a.wv = group(blk.value);
-                a.E = E.as<float>();
+                a.wq = weights(blk.query);
+                a.wk = weights(blk.key);
+                a.wv = weights(blk.value);
+                a.E = rows_order ? Edec.as<float>() : E.as<float>();
                 a.embed = l == 0;
                 a.q = q;
                 a.kv_pre = kv_of(l);
@@ -338,7 +356,9 @@ struct MeshGpt::Impl {
             } else {
                 a.xn = xn;
             }
-            if (decode && wave_decode)
+            if (rows_order)
+                kern::row_block(a, stream);
+            else if (decode && wave_decode)
                 kern::block_decode(a, stream);
             else
                 kern::block(a, staged(t, a.wproj != nullptr, a.wq != nullptr), stream);

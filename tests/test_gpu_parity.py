@@ -280,3 +280,52 @@ def test_mid_config3_decode_parity_subset():
         for b in range(2):
             ref = O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1]
             assert_close(last[b], ref, what=f"config-3 logits seq {b}")
+
+
+# Decode shapes that exercise each row-order kernel instantiation: the
+# fixed-depth ones of the benchmark configs above, and the any-depth form for
+# neighbor meshes (every layer crosses waves), head groups of 8 and 32 lanes,
+# and widths 256 and 1024.
+ROW_DECODE = [
+    dict(vocab_size=64, context=32, width=128, heads=4, layers=2, attention_mesh_depth=3, ffn_mesh_depth=5),
+    dict(vocab_size=32, context=32, width=256, heads=8, layers=1, attention_mesh_depth=4, ffn_mesh_depth=4,
+         connectivity=1),
+    dict(vocab_size=32, context=32, width=512, heads=4, layers=2, attention_mesh_depth=9, ffn_mesh_depth=8,
+         connectivity=1),
+    dict(vocab_size=16, context=16, width=1024, heads=16, layers=1, attention_mesh_depth=2, ffn_mesh_depth=3,
+         connectivity=1),
+    dict(vocab_size=16, context=16, width=1024, heads=16, layers=1, attention_mesh_depth=10, ffn_mesh_depth=10,
+         connectivity=1),
+]
+
+
+@pytest.mark.parametrize("cfg", ROW_DECODE, ids=[_ids(c) for c in ROW_DECODE])
+def test_row_decode_shapes_match_oracle(cfg):
+    g, o = configs_for(**cfg)
+    params = O.initialize(o, 5)
+    prompts = (np.arange(2 * 5).reshape(2, 5) * 3 % cfg["vocab_size"]).astype(np.uint32)
+    with G.MeshGpt(0, g, 5, max_batch=2) as model:
+        got = model.generate_tokens(prompts, 6, 0.0, 9)
+        last = model.last_logits(2)
+    for b in range(2):
+        expected = O.generate(o, params, prompts[b], 6, 0.0, 9 + b, cached=True)
+        _check_trajectory(o, params, prompts[b], got[b], expected, 0.0, 9 + b)
+        ref = O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1]
+        assert_close(last[b], ref, what=f"decode logits seq {b}")
+
+
+@pytest.mark.parametrize("name", ["tiny", "mid"])
+def test_decode_kernels_agree(name, monkeypatch):
+    # The row-order decode kernel and the one-wave-per-mesh kernel decode the
+    # same tokens, with last-step logits within the tolerance of each other.
+    config = G.named_config(name)
+    prompts = (np.arange(4 * 24).reshape(4, 24) * 7 % config.vocab_size).astype(np.uint32)
+    results = []
+    for disable in ("0", "1"):
+        monkeypatch.setenv("MG_DISABLE_ROW_DECODE", disable)
+        with G.MeshGpt(0, config, 7, max_batch=4) as model:
+            tokens = model.generate_tokens(prompts, 24, 0.0, 7)
+            results.append((tokens, model.last_logits(4)))
+    (t0, l0), (t1, l1) = results
+    assert np.array_equal(t0, t1)
+    assert_close(l0, l1, what="row vs wave decode logits")
