@@ -23,10 +23,10 @@ EXPORTS = (
     "mg_initial_parameters", "mg_token_codes", "mg_model_create", "mg_model_destroy",
     "mg_model_config", "mg_parameters", "mg_set_parameters", "mg_logits", "mg_token_embeddings",
     "mg_hidden_states", "mg_generate", "mg_generate_text", "mg_prefill", "mg_decode",
-    "mg_decode_profiled", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
+    "mg_decode_profiled", "mg_decode_traced", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
-    "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode",
+    "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits",
 )
 
 
@@ -99,6 +99,7 @@ def lib():
         "mg_prefill": (i, [vp, _u32p, sz, sz, f, u64, sz]),
         "mg_decode": (i, [vp, sz]),
         "mg_decode_profiled": (i, [vp, sz, _f32p, sz]),
+        "mg_decode_traced": (i, [vp, sz, ctypes.POINTER(ctypes.c_uint64), sz]),
         "mg_sequence_length": (i, [vp, _szp]),
         "mg_read_tokens": (i, [vp, _u32p, sz, sz]),
         "mg_last_logits": (i, [vp, _f32p, sz]),
@@ -113,6 +114,7 @@ def lib():
         "mg_tokenizer_from_text": (i, [ctypes.c_char_p, sz, _u32p, sz, _szp]),
         "mg_tokenizer_encode": (i, [_u32p, sz, ctypes.c_char_p, sz, _u32p, sz, _szp]),
         "mg_tokenizer_decode": (i, [_u32p, sz, _u32p, sz, ctypes.c_char_p, sz, _szp]),
+        "mg_sample_logits": (i, [i, _f32p, sz, sz, f, ctypes.POINTER(ctypes.c_uint64), _u32p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -168,6 +170,18 @@ def copy_bandwidth(nbytes, iters=20, device=0):
     return gbps.value
 
 
+def sample_logits(logits, temperature, rng_states, device=0):
+    """generate's sampler on the device for rows of f32 logits; returns
+    (tokens, advanced rng states)."""
+    logits = _f32(np.atleast_2d(logits))
+    states = np.ascontiguousarray(rng_states, dtype=np.uint64).copy()
+    rows, vocab = logits.shape
+    out = np.empty(rows, dtype=np.uint32)
+    _check(lib().mg_sample_logits(device, _p(logits, _f32p), rows, vocab, temperature,
+                                  states.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), _p(out, _u32p)))
+    return out, states
+
+
 def calibration_copy(nbytes, device=0):
     """One warm-up and one timed launch of calibration_copy over nbytes."""
     return copy_bandwidth(nbytes, 1, device)
@@ -181,6 +195,7 @@ class MeshGpt:
         _check(lib().mg_model_create(device, ctypes.byref(config), seed, max_batch, ctypes.byref(handle)))
         self._h = handle
         self._config = GptConfig(**config.as_dict())
+        self._batch = 0
 
     def close(self):
         if getattr(self, "_h", None):
@@ -236,6 +251,7 @@ class MeshGpt:
     def generate_tokens(self, prompts, count, temperature, seed):
         prompts = _u32(np.atleast_2d(prompts))
         batch, length = prompts.shape
+        self._batch = batch
         out = np.empty((batch, length + count), dtype=np.uint32)
         _check(lib().mg_generate(self._h, _p(prompts, _u32p), batch, length, count, temperature, seed,
                                  _p(out, _u32p)))
@@ -254,6 +270,7 @@ class MeshGpt:
     def prefill(self, prompts, temperature, seed, reserve=0):
         prompts = _u32(np.atleast_2d(prompts))
         batch, length = prompts.shape
+        self._batch = batch
         _check(lib().mg_prefill(self._h, _p(prompts, _u32p), batch, length, temperature, seed, reserve))
 
     def decode(self, steps):
@@ -262,6 +279,18 @@ class MeshGpt:
     def decode_profiled(self, steps):
         out = np.empty(steps * self._config.layers, dtype=np.float32)
         _check(lib().mg_decode_profiled(self._h, steps, _p(out, _f32p), out.size))
+        return out
+
+    def decode_traced(self, steps):
+        """Persistent decode of `steps` steps with its timeline: an array
+        [blocks, steps, layers + 1, 2] of 100 MHz wall-clock stamps (ready,
+        published); blocks are 3*batch mesh teams, then batch*heads attention
+        blocks."""
+        c = self._config
+        batch = self._batch
+        blocks = 3 * batch + batch * c.heads
+        out = np.zeros((blocks, steps, c.layers + 1, 2), dtype=np.uint64)
+        _check(lib().mg_decode_traced(self._h, steps, out.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), out.size))
         return out
 
     def sequence_length(self):

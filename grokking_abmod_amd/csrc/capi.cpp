@@ -210,6 +210,14 @@ int mg_decode_profiled(mg_model *model, size_t steps, float *ms, size_t n) {
     return guarded([&] { copy_out(model_of(model).decode_profiled(steps), ms, n); });
 }
 
+int mg_decode_traced(mg_model *model, size_t steps, uint64_t *stamps, size_t n) {
+    return guarded([&] {
+        const std::vector<uint64_t> t = model_of(model).decode_traced(steps);
+        require(stamps != nullptr && n >= t.size(), "output buffer is too small");
+        std::memcpy(stamps, t.data(), t.size() * 8);
+    });
+}
+
 int mg_sequence_length(const mg_model *model, size_t *out) {
     return guarded([&] {
         require(model != nullptr && out != nullptr, "model and output must not be null");
@@ -229,6 +237,16 @@ int mg_last_logits(mg_model *model, float *out, size_t n) {
 }
 
 void *mg_model_stream(mg_model *model) { return model ? static_cast<void *>(model->model.stream()) : nullptr; }
+
+int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                     uint64_t *rng_states, uint32_t *tokens) {
+    return guarded([&] {
+        require((logits != nullptr && rng_states != nullptr && tokens != nullptr) || rows == 0,
+                "logits, states and tokens must not be null");
+        if (sample_logits(device, logits, rows, vocab, temperature, rng_states, tokens))
+            throw Error("logits must contain only finite values", kNonfinite);
+    });
+}
 
 int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps) {
     return guarded([&] {

@@ -1086,6 +1086,101 @@ __device__ __forceinline__ void row_head_sums(const float (&v)[CPL], float (&out
     }
 }
 
+// Lane geometry and LDS of one row held by NW waves (see row_partner).
+template <int NW, int CPL, int GL>
+struct RowCtx {
+    static constexpr int W = 64 * NW * CPL, G = 64 / GL, SLOT = CPL * NW * G;
+    int lane, wave, parity;
+    float *xch;  // 2*W floats: mesh exchange buffers
+    float *red;  // reduction slots of SLOT floats each
+    __device__ RowCtx(float *x, float *r)
+        : lane(int(threadIdx.x) & 63), wave(int(threadIdx.x) >> 6), parity(0), xch(x), red(r) {}
+    // Head and in-head dim of register j: a head is GL lanes of every wave.
+    __device__ int head_of(int j) const { return lane / GL + G * j; }
+    __device__ int dim() const { return NW * (lane % GL) + wave; }
+    __device__ int ridx(int j) const { return (j * NW + wave) * 64 + lane; }  // row-order index
+    __device__ int chan(int j) const { return wave + NW * (lane + 64 * j); }   // channel
+    __device__ float *slot(int k) const { return red + k * SLOT; }
+};
+
+// A mesh stack on the row: fixed depth (weights in registers) or any depth.
+template <int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void row_run_mesh(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], const float2 (&w)[D][CPL],
+                                             const float *wg, int depth, const Shape &s, bool fixed) {
+    if (fixed) row_mesh_fixed<NW, CPL, D>(x, w, c.lane, c.wave, c.xch, c.parity);
+    else row_mesh<NW, CPL>(x, wg, depth, s, c.lane, c.wave, c.xch, c.parity);
+}
+
+// XSA (reference.rs:577-603): y <- y - (y.u)u with u = v / max(|v|, eps) per head.
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ void row_xsa(RowCtx<NW, CPL, GL> &c, float (&y)[CPL], const float (&v)[CPL]) {
+    float vv[CPL], yv[CPL], t[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
+    row_head_sums<NW, CPL, GL>(t, vv, c.lane, c.wave, c.slot(0));
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
+    row_head_sums<NW, CPL, GL>(t, yv, c.lane, c.wave, c.slot(1));
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
+        y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
+    }
+}
+
+// 1/sqrt(mean(x^2) + eps) over the row (reference.rs:392-409).
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ float row_inv_rms(RowCtx<NW, CPL, GL> &c, const float (&x)[CPL], int k) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
+    return rsqrtf(row_total<NW>(acc, c.lane, c.wave, c.slot(k)) * (1.0f / float(c.W)) + kRmsEps);
+}
+
+// Post-attention half of a block (reference.rs:194-216) on the residual row x,
+// given the attention output y and the row's own value vector v.
+template <int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void row_post(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], float (&y)[CPL],
+                                         const float (&v)[CPL], const float2 (&wp)[D][CPL],
+                                         const float2 (&wf)[D][CPL], const float *gp, const float *gf,
+                                         const Shape &s, bool fixed) {
+    row_xsa(c, y, v);
+    row_run_mesh(c, y, wp, gp, s.A, s, fixed);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] += y[j];
+    const float inv = row_inv_rms(c, x, 2);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
+    row_run_mesh(c, y, wf, gf, s.F, s, fixed);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] += y[j];
+}
+
+// QK-Norm per head, then split-half RoPE (reference.rs:462-482) at the position
+// whose (cos, sin) pair for this lane's dim is cs: the pair partner (dim +-
+// hd/2) is GL/2 lanes away in the same wave and register.
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ void row_qk_rope(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], float2 cs, const Shape &s) {
+    float sq[CPL], ss[CPL], other[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) sq[j] = x[j] * x[j];
+    row_head_sums<NW, CPL, GL>(sq, ss, c.lane, c.wave, c.slot(4));
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) other[j] = __shfl_xor(x[j], GL / 2, 64);
+    const float scale = 1.0f / float(s.hd);
+    const bool low = c.dim() < s.half;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const float sc = rsqrtf(ss[j] * scale + kRmsEps);
+        const float self = x[j] * sc, oth = other[j] * sc;
+        x[j] = low ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
+    }
+}
+
+__device__ __forceinline__ float2 rope_pair(const float2 *rope, int pos, int dim, int half) {
+    return rope[size_t(pos) * half + (dim < half ? dim : dim - half)];
+}
+
 // One decode row (Rows.rows_per_seq == 1) per `teams` workgroups of 64*NW
 // threads; block semantics as block_kernel.  DEPTH > 0: butterfly meshes with
 // A = F = DEPTH held in registers; DEPTH = 0: any depth and connectivity.
@@ -1093,42 +1188,39 @@ __device__ __forceinline__ void row_head_sums(const float (&v)[CPL], float (&out
 template <int NW, int CPL, int GL, int DEPTH>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
 row_block_kernel(BlockArgs a) {
-    constexpr int W = 64 * NW * CPL, G = 64 / GL;
+    using Ctx = RowCtx<NW, CPL, GL>;
+    constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
     constexpr int D = FIXED ? DEPTH : 1;
     __shared__ float xch[2 * W];
-    __shared__ float red[8][CPL * NW * G];
+    __shared__ float red[8 * Ctx::SLOT];
+    Ctx c(xch, red);
     const Shape &s = a.s;
-    const int lane = int(threadIdx.x) & 63, wave = int(threadIdx.x) >> 6;
     const bool pre = a.wq != nullptr, post = a.wproj != nullptr;
     const int teams = pre ? 3 : 1;
     const int row = int(blockIdx.x) / teams, team = int(blockIdx.x) - row * teams;
     int seq, pos;
     row_position(a.ro, row, seq, pos);
-    int parity = 0;
-    auto head_of = [&](int j) { return lane / GL + G * j; };
-    const int dim = NW * (lane % GL) + wave;  // in-head dim of every register
-    auto ridx = [&](int j) { return (j * NW + wave) * 64 + lane; };  // row-order index
-    auto chan = [&](int j) { return wave + NW * (lane + 64 * j); };  // channel
+    const int dim = c.dim();
 
     // Every independent load first: row, attention state, weights.
     float x[CPL];
     if (a.embed) {
         const uint32_t tok = a.ro.tokens[size_t(seq) * a.ro.tok_stride + a.ro.tok_offset + pos];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + ridx(j)];
+        for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
     } else {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x[j] = a.x[size_t(row) * W + ridx(j)];
+        for (int j = 0; j < CPL; ++j) x[j] = a.x[size_t(row) * W + c.ridx(j)];
     }
     const float *wmine = pre ? (team == 0 ? a.wq : team == 1 ? a.wk : a.wv) : nullptr;
     float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
     if constexpr (FIXED) {
         if (post) {
-            row_load_weights<NW, CPL, D>(wp, a.wproj, lane, wave);
-            row_load_weights<NW, CPL, D>(wf, a.wffn, lane, wave);
+            row_load_weights<NW, CPL, D>(wp, a.wproj, c.lane, c.wave);
+            row_load_weights<NW, CPL, D>(wf, a.wffn, c.lane, c.wave);
         }
-        if (pre) row_load_weights<NW, CPL, D>(wm, wmine, lane, wave);
+        if (pre) row_load_weights<NW, CPL, D>(wm, wmine, c.lane, c.wave);
     }
 
     if (post) {
@@ -1137,90 +1229,46 @@ row_block_kernel(BlockArgs a) {
         const float *part0 = a.part + size_t(seq * s.H) * a.nsplit * stride;
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
-            v[j] = a.kv_post.v[(size_t(seq * s.H + head_of(j)) * a.kv_post.cap + pos) * s.hdp + dim];
+            v[j] = a.kv_post.v[(size_t(seq * s.H + c.head_of(j)) * a.kv_post.cap + pos) * s.hdp + dim];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-            const float *pp = part0 + size_t(head_of(j)) * a.nsplit * stride;
+            const float *pp = part0 + size_t(c.head_of(j)) * a.nsplit * stride;
             y[j] = a.nsplit <= 2 ? merge_splits<2>(pp, a.nsplit, stride, s.hdp, dim)
                                  : merge_splits<8>(pp, a.nsplit, stride, s.hdp, dim);
         }
-        // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
-        float vv[CPL], yv[CPL], t[CPL];
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
-        row_head_sums<NW, CPL, GL>(t, vv, lane, wave, red[0]);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
-        row_head_sums<NW, CPL, GL>(t, yv, lane, wave, red[1]);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
-            y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
-        }
-        if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(y, wp, lane, wave, xch, parity);
-        else row_mesh<NW, CPL>(y, a.wproj, s.A, s, lane, wave, xch, parity);
-        float acc = 0.0f;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            x[j] += y[j];
-            acc = fmaf(x[j], x[j], acc);
-        }
-        const float inv = rsqrtf(row_total<NW>(acc, lane, wave, red[2]) * (1.0f / float(W)) + kRmsEps);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
-        if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(y, wf, lane, wave, xch, parity);
-        else row_mesh<NW, CPL>(y, a.wffn, s.F, s, lane, wave, xch, parity);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) x[j] += y[j];
+        row_post(c, x, y, v, wp, wf, a.wproj, a.wffn, s, FIXED);
     }
     if (team == 0 && (post || a.embed)) {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) a.x[size_t(row) * W + ridx(j)] = x[j];
+        for (int j = 0; j < CPL; ++j) a.x[size_t(row) * W + c.ridx(j)] = x[j];
     }
     if (!a.xn && !pre) return;
 
     // The next RMSNorm: the final one for the head, or the block's pre-norm.
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
-    const float inv = rsqrtf(row_total<NW>(acc, lane, wave, red[3]) * (1.0f / float(W)) + kRmsEps);
+    const float inv = row_inv_rms(c, x, 3);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) x[j] *= inv;
     if (a.xn) {
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) a.xn[size_t(row) * W + chan(j)] = x[j];
+        for (int j = 0; j < CPL; ++j) a.xn[size_t(row) * W + c.chan(j)] = x[j];
     }
     if (!pre) return;
 
-    if constexpr (FIXED) row_mesh_fixed<NW, CPL, D>(x, wm, lane, wave, xch, parity);
-    else row_mesh<NW, CPL>(x, wmine, s.A, s, lane, wave, xch, parity);
+    row_run_mesh(c, x, wm, wmine, s.A, s, FIXED);
     const size_t cache_row = size_t(seq * s.H) * a.kv_pre.cap + pos;  // + head * cap, then * hdp
     if (team == 2) {
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
-            a.kv_pre.v[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[j];
+            a.kv_pre.v[(cache_row + size_t(c.head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[j];
         return;
     }
-    // QK-Norm per head, then split-half RoPE at the row's position: the pair
-    // partner (dim +- hd/2) is GL/2 lanes away in the same wave and register.
-    float sq[CPL], ss[CPL], other[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) sq[j] = x[j] * x[j];
-    row_head_sums<NW, CPL, GL>(sq, ss, lane, wave, red[4]);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) other[j] = __shfl_xor(x[j], GL / 2, 64);
-    const int half = s.half;
-    const float2 cs = a.rope[size_t(pos) * half + (dim < half ? dim : dim - half)];
-    const float scale = 1.0f / float(s.hd);
+    row_qk_rope(c, x, rope_pair(a.rope, pos, dim, s.half), s);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const float sc = rsqrtf(ss[j] * scale + kRmsEps);
-        const float self = x[j] * sc, oth = other[j] * sc;
-        const float r = dim < half ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
         if (team == 0)
-            a.q[size_t(row) * W + chan(j)] = r;
+            a.q[size_t(row) * W + c.chan(j)] = x[j];
         else
-            a.kv_pre.k[(cache_row + size_t(head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = r;
+            a.kv_pre.k[(cache_row + size_t(c.head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[j];
     }
 }
 
@@ -1256,70 +1304,98 @@ __device__ __forceinline__ void load_vec(const float *__restrict__ p, float (&o)
     }
 }
 
-template <int HDP>
+template <int HDP, int TH = 0>
 struct DecodeCfg {
     static constexpr int VEC = HDP <= 4 ? HDP : (HDP / 64 > 4 ? HDP / 64 : 4);  // dims per lane
     static constexpr int LPK = HDP / VEC;                                      // lanes per key (<= 64)
-    static constexpr int THREADS = HDP >= 4096 ? 128 : 256;
+    static constexpr int THREADS = TH > 0 ? TH : (HDP >= 4096 ? 128 : 256);
     static constexpr int G = THREADS / LPK;                                    // key groups
     static constexpr int U = VEC >= 32 ? 1 : (VEC >= 16 ? 2 : (VEC >= 8 ? 4 : 8));  // keys per group per step
 };
 
-// Split-KV decode attention (reference.rs:510-554 for one query row).  Block
-// (seq * nsplit + split, head) streams an equal share of the len[seq] keys of
-// the cache; each group of LPK lanes owns one key at a time, so every K/V row
-// is one coalesced VEC-wide load per lane, and U keys' loads are issued before
-// any is consumed.  Scores live in the log2 domain.  An empty share writes the
-// neutral partial (m = -inf, l = 0).
-template <int HDP>
-__global__ void __launch_bounds__(DecodeCfg<HDP>::THREADS)
-attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *__restrict__ len, int nsplit,
-                   float *__restrict__ part, float scale_log2) {
-    using C = DecodeCfg<HDP>;
-    constexpr int VEC = C::VEC, LPK = C::LPK, G = C::G, U = C::U;
+__device__ __forceinline__ float load_coherent(const float *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void store_coherent(float *p, float v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Online-softmax attention (reference.rs:510-554) of one query head over keys
+// [start, end) of one (sequence, head) cache slab kb/vb (position-major rows of
+// HDP floats); the block's partial state (acc[HDP], m, l) goes to out[0..HDP+1].
+// Each group of LPK lanes owns one key at a time, so every K/V row is one
+// coalesced VEC-wide load per lane, and U keys' loads are issued before any is
+// consumed.  Scores live in the log2 domain; q stays unscaled (the score is
+// scaled instead) so its load does not hold back the first K/V loads.  An
+// empty share writes the neutral partial (m = -inf, l = 0).  COHERENT: q is
+// read and out written with agent-scope accesses (for the persistent kernel,
+// where both cross workgroups inside one launch).
+template <int HDP, bool COHERENT, int TH = 0, bool PIPE = false>
+__device__ void attn_share(const float *__restrict__ qh, int hd, const float *__restrict__ kslab,
+                           const float *__restrict__ vslab, int start, int end, float scale_log2,
+                           float *__restrict__ out) {
+    using C = DecodeCfg<HDP, TH>;
+    // PIPE holds two rounds of keys, so each round takes half as many.
+    constexpr int VEC = C::VEC, LPK = C::LPK, G = C::G, U = PIPE && C::U > 1 ? C::U / 2 : C::U;
     __shared__ float sm[G], sl[G];
     __shared__ __align__(16) float sacc[G * HDP];
-    const int b = int(blockIdx.x) / nsplit, split = int(blockIdx.x) - b * nsplit, h = blockIdx.y;
-    const int keys = len[b];
-    const int chunk = (keys + nsplit - 1) / nsplit;
-    const int start = split * chunk;
-    const int end = min(start + chunk, keys);
-    float *out = part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2);
     if (start >= end) {
-        for (int d = threadIdx.x; d < HDP; d += blockDim.x) out[d] = 0.0f;
+        for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
+            if (COHERENT) store_coherent(out + d, 0.0f);
+            else out[d] = 0.0f;
+        }
         if (threadIdx.x == 0) {
-            out[HDP] = -INFINITY;
-            out[HDP + 1] = 0.0f;
+            if (COHERENT) {
+                store_coherent(out + HDP, -INFINITY);
+                store_coherent(out + HDP + 1, 0.0f);
+            } else {
+                out[HDP] = -INFINITY;
+                out[HDP + 1] = 0.0f;
+            }
         }
         return;
     }
     const int g = threadIdx.x / LPK, li = threadIdx.x % LPK, d0 = li * VEC;
-    // q stays unscaled (the score is scaled instead), so its load does not hold
-    // back the first K/V loads.
     float qr[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
-        const int d = min(d0 + e, s.hd - 1);
-        qr[e] = q[size_t(b) * s.W + h * s.hd + d];
+        const int d = min(d0 + e, hd - 1);
+        qr[e] = COHERENT ? load_coherent(qh + d) : qh[d];
     }
 #pragma unroll
     for (int e = 0; e < VEC; ++e)
-        if (d0 + e >= s.hd) qr[e] = 0.0f;
-    const size_t head = size_t(b * s.H + h) * kv.cap;
-    const float *kb = kv.k + head * HDP + d0;
-    const float *vb = kv.v + head * HDP + d0;
+        if (d0 + e >= hd) qr[e] = 0.0f;
+    const float *kb = kslab + d0;
+    const float *vb = vslab + d0;
     float m = -INFINITY, l = 0.0f, acc[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-    for (int j0 = start; j0 < end; j0 += G * U) {
-        float kk[U][VEC], vv[U][VEC];
+    // Clamped rows keep every load in bounds and branch-free; keys past `end`
+    // are masked out of the softmax below.
+    auto load_keys = [&](int j0, float (&kk)[U][VEC], float (&vv)[U][VEC]) {
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            // Clamped rows keep every load in bounds and branch-free; keys past
-            // `end` are masked out of the softmax below.
             const int j = min(j0 + u * G + g, end - 1);
             load_vec<VEC>(kb + size_t(j) * HDP, kk[u]);
             load_vec<VEC>(vb + size_t(j) * HDP, vv[u]);
+        }
+    };
+    // PIPE: the next round's keys load while this round's are consumed.
+    float kn[PIPE ? U : 1][VEC], vn[PIPE ? U : 1][VEC];
+    if constexpr (PIPE) load_keys(start, kn, vn);
+    for (int j0 = start; j0 < end; j0 += G * U) {
+        float kk[U][VEC], vv[U][VEC];
+        if constexpr (PIPE) {
+#pragma unroll
+            for (int u = 0; u < U; ++u)
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    kk[u][e] = kn[u][e];
+                    vv[u][e] = vn[u][e];
+                }
+            if (j0 + G * U < end) load_keys(j0 + G * U, kn, vn);
+        } else {
+            load_keys(j0, kk, vv);
         }
         float sc[U];
 #pragma unroll
@@ -1365,14 +1441,37 @@ attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *_
     for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
         float a = 0.0f;
         for (int k = 0; k < G; ++k) a += exp2f(sm[k] - M) * sacc[k * HDP + d];
-        out[d] = a;
+        if (COHERENT) store_coherent(out + d, a);
+        else out[d] = a;
     }
     if (threadIdx.x == 0) {
         float L = 0.0f;
         for (int k = 0; k < G; ++k) L += exp2f(sm[k] - M) * sl[k];
-        out[HDP] = M;
-        out[HDP + 1] = L;
+        if (COHERENT) {
+            store_coherent(out + HDP, M);
+            store_coherent(out + HDP + 1, L);
+        } else {
+            out[HDP] = M;
+            out[HDP + 1] = L;
+        }
     }
+}
+
+// Split-KV decode attention for one query row per sequence.  Block
+// (seq * nsplit + split, head) runs attn_share over an equal share of the
+// len[seq] keys of the cache.
+template <int HDP>
+__global__ void __launch_bounds__(DecodeCfg<HDP>::THREADS)
+attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *__restrict__ len, int nsplit,
+                   float *__restrict__ part, float scale_log2) {
+    const int b = int(blockIdx.x) / nsplit, split = int(blockIdx.x) - b * nsplit, h = blockIdx.y;
+    const int keys = len[b];
+    const int chunk = (keys + nsplit - 1) / nsplit;
+    const int start = split * chunk;
+    const int end = min(start + chunk, keys);
+    const size_t slab = size_t(b * s.H + h) * kv.cap * HDP;
+    attn_share<HDP, false>(q + size_t(b) * s.W + h * s.hd, s.hd, kv.k + slab, kv.v + slab, start, end, scale_log2,
+                           part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2));
 }
 
 template <int HDP>
@@ -1547,55 +1646,95 @@ __device__ __forceinline__ uint64_t splitmix_next(uint64_t &state) {
     return bits ^ (bits >> 31);
 }
 
-// The reference's sequential f32 sampler (gpu.rs:2034-2048) in one lane: a
-// token-order sum, one SplitMix64 draw, and a token-order scan that stops at
-// the first negative remainder; no multiply-add fusion.  Values come sixteen at
-// a time so only the additions form the serial chain.  CACHED: p holds the
-// exponentials; otherwise they are recomputed from the logits row.
-template <bool CACHED>
-__device__ int sequential_sample(const float *p, const float *row, int V, float mx,
-                                              float temperature, uint64_t *rng) {
+// exp(x) rounded once to f32 from an f64 evaluation: the correctly rounded
+// value except within about 2^-29 ulp of a rounding midpoint, which is what
+// host libm expf returns (the reference's f32::exp).  The device's f32 expf
+// can differ by an ulp, and a near-tie draw then picks another token.
+__device__ __forceinline__ float expf_rounded(float x) { return float(exp(double(x))); }
+
+// The reference's sequential f32 sampler (gpu.rs:2034-2048) in one lane, for
+// a given draw u: a token-order f32 sum of p_i = exp((l_i - max)/T), then a
+// token-order scan of u*sum - p_0 - p_1 - ... that stops at the first negative
+// remainder (default: the last token); no multiply-add fusion.  The next
+// sixteen values load while the current sixteen are added.
+__device__ __forceinline__ int sequential_pick(const float *row, int V, float mx, float temperature, float u) {
 #pragma clang fp contract(off)
     constexpr int kBatch = 16;
+    auto fetch = [&](float (&v)[kBatch], int t) {
+#pragma unroll
+        for (int k = 0; k < kBatch; ++k) v[k] = expf_rounded((row[min(t + k, V - 1)] - mx) / temperature);
+    };
+    const int full = V / kBatch * kBatch;
     float sum = 0.0f;
-    int t = 0;
-    for (; t + kBatch <= V; t += kBatch) {
-        float v[kBatch];
+    float cur[kBatch], nxt[kBatch];
+    if (full) fetch(nxt, 0);
+    for (int t = 0; t < full; t += kBatch) {
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) v[k] = CACHED ? p[t + k] : expf((row[t + k] - mx) / temperature);
+        for (int k = 0; k < kBatch; ++k) cur[k] = nxt[k];
+        if (t + kBatch < full) fetch(nxt, t + kBatch);
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) sum = sum + v[k];
+        for (int k = 0; k < kBatch; ++k) sum = sum + cur[k];
     }
-    for (; t < V; ++t) sum = sum + (CACHED ? p[t] : expf((row[t] - mx) / temperature));
-    uint64_t state = *rng;
-    const float u = float(uint32_t(splitmix_next(state) >> 40)) / 16777216.0f;
-    *rng = state;
+    for (int t = full; t < V; ++t) sum = sum + expf_rounded((row[t] - mx) / temperature);
     float sample = u * sum;
-    for (t = 0; t + kBatch <= V; t += kBatch) {
-        float v[kBatch], left[kBatch];
+    if (full) fetch(nxt, 0);
+    for (int t = 0; t < full; t += kBatch) {
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) v[k] = CACHED ? p[t + k] : expf((row[t + k] - mx) / temperature);
+        for (int k = 0; k < kBatch; ++k) cur[k] = nxt[k];
+        if (t + kBatch < full) fetch(nxt, t + kBatch);
+        float left[kBatch];
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) {
-            sample = sample - v[k];
+            sample = sample - cur[k];
             left[k] = sample;
         }
 #pragma unroll
         for (int k = 0; k < kBatch; ++k)
             if (left[k] < 0.0f) return t + k;
     }
-    for (; t < V; ++t) {
-        sample = sample - (CACHED ? p[t] : expf((row[t] - mx) / temperature));
+    for (int t = full; t < V; ++t) {
+        sample = sample - expf_rounded((row[t] - mx) / temperature);
         if (sample < 0.0f) return t;
     }
     return V - 1;
 }
 
+// LDS scratch of choose_token: a float, an int and a double per wave, and one
+// more double.
+struct SampleLds {
+    float *redf;
+    int *redi;
+    double *redd;
+};
+
+__device__ __forceinline__ int block_min_int(int v, const SampleLds &m) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    v = wave_min_int(v);
+    if (lane == 0) m.redi[wave] = v;
+    __syncthreads();
+    v = INT_MAX;
+    for (int w = 0; w < nw; ++w) v = min(v, m.redi[w]);
+    __syncthreads();
+    return v;
+}
+
 // Block-wide choice of the next token from a logits row (gpu.rs:2028-2049):
-// greedy = the first maximal logit; T > 0 = the sequential sampler.  `p` is
-// LDS scratch of `cap` floats; red holds one float and one int per wave.
-__device__ int choose_token(const float *row, int V, float temperature, uint64_t *rng, int *flags, float *p,
-                            int cap, float *redf, int *redi) {
+// greedy = the first maximal logit; T > 0 = the reference's sampler.  Sets
+// bit 0 of *flags when the row holds a non-finite value.
+//
+// Temperature sampling is decided in parallel with the same result as the
+// sequential f32 process: with p_i = exp((l_i - max)/T) in f32, the reference
+// sums them in token order in f32 (S32), draws u, and returns the first i
+// whose sequential f32 remainder u*S32 - p_0 - ... - p_i is negative.  With
+// unit roundoff e = 2^-24 and all p_i >= 0, |S32 - S| <= (V+2) e S for the
+// exact sum S, and every remainder is within beta = (V+2) e S32 of the exact
+// u*S32 - P_i (P_i the exact prefix sums, here in f64).  So an index is
+// surely non-negative when P_i < u*S_lo - beta and surely negative when
+// P_i > u*S_hi + beta; the first index that is not surely non-negative is the
+// answer when it is surely negative.  Otherwise (a near-tie, or a non-finite
+// row) thread 0 runs the sequential f32 process itself with the same u.
+__device__ __forceinline__ int choose_token(const float *row, int V, float temperature, uint64_t *rng, int *flags,
+                                            const SampleLds &m) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     float mx = -INFINITY;
     int bad = 0;
@@ -1607,15 +1746,15 @@ __device__ int choose_token(const float *row, int V, float temperature, uint64_t
     mx = wave_max(mx);
     bad = wave_or_int(bad);
     if (lane == 0) {
-        redf[wave] = mx;
-        redi[wave] = bad;
+        m.redf[wave] = mx;
+        m.redi[wave] = bad;
     }
     __syncthreads();
     mx = -INFINITY;
     bad = 0;
     for (int w = 0; w < nw; ++w) {
-        mx = fmaxf(mx, redf[w]);
-        bad |= redi[w];
+        mx = fmaxf(mx, m.redf[w]);
+        bad |= m.redi[w];
     }
     __syncthreads();
     if (bad && threadIdx.x == 0) atomicOr(flags, 1);
@@ -1623,24 +1762,62 @@ __device__ int choose_token(const float *row, int V, float temperature, uint64_t
         int best = INT_MAX;
         for (int t = threadIdx.x; t < V; t += blockDim.x)
             if (row[t] == mx) best = min(best, t);
-        best = wave_min_int(best);
-        if (lane == 0) redi[wave] = best;
-        __syncthreads();
-        best = INT_MAX;
-        for (int w = 0; w < nw; ++w) best = min(best, redi[w]);
-        __syncthreads();
+        best = block_min_int(best, m);
         return best == INT_MAX ? 0 : best;
     }
-    const bool cached = V <= cap;
-    if (cached)
-        for (int t = threadIdx.x; t < V; t += blockDim.x) p[t] = expf((row[t] - mx) / temperature);
+    // Each thread takes a contiguous run [i0, i1) of the tokens.
+    const int run = (V + int(blockDim.x) - 1) / int(blockDim.x);
+    const int i0 = min(int(threadIdx.x) * run, V), i1 = min(i0 + run, V);
+    auto pexp = [&](int i) { return expf_rounded((row[i] - mx) / temperature); };
+    double mine = 0.0;
+    for (int i = i0; i < i1; ++i) mine += double(pexp(i));
+    double incl = mine;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        const double n = __shfl_up(incl, o, 64);
+        if (lane >= o) incl += n;
+    }
+    if (lane == 63) m.redd[wave] = incl;
+    if (threadIdx.x == 0) {
+        // One SplitMix64 draw per sampled token, as Random::unit (src/mesh.rs:263-265).
+        uint64_t state = *rng;
+        m.redd[nw] = double(float(uint32_t(splitmix_next(state) >> 40)) / 16777216.0f);
+        *rng = state;
+    }
     __syncthreads();
-    if (threadIdx.x == 0)
-        redi[0] = cached ? sequential_sample<true>(p, row, V, mx, temperature, rng)
-                         : sequential_sample<false>(p, row, V, mx, temperature, rng);
+    double before = 0.0, S = 0.0;
+    for (int w = 0; w < nw; ++w) {
+        if (w < wave) before += m.redd[w];
+        S += m.redd[w];
+    }
+    const float u = float(m.redd[nw]);
+    const double e = 0x1p-24, slack = 1e-12 * S;
+    const double g = double(V + 2) * e * 1.01;
+    const double s_lo = S * (1.0 - g) - slack, s_hi = S * (1.0 + g) + slack;
+    const double beta = double(V + 2) * e * s_hi * 1.01 + slack;
+    const double lo = double(u) * s_lo - beta, hi = double(u) * s_hi + beta;
+    double prefix = before + incl - mine;
+    int first = INT_MAX, decided = 0;
+    for (int i = i0; i < i1; ++i) {
+        prefix += double(pexp(i));
+        if (!(prefix < lo)) {
+            first = i;
+            decided = prefix > hi;
+            break;
+        }
+    }
+    first = block_min_int(first, m);
+    if (first == INT_MAX) return V - 1;
+    if (first >= i0 && first < i1) m.redi[0] = decided ? first : -1;
     __syncthreads();
-    const int token = redi[0];
+    int token = m.redi[0];
     __syncthreads();
+    if (token < 0) {
+        if (threadIdx.x == 0) m.redi[0] = sequential_pick(row, V, mx, temperature, u);
+        __syncthreads();
+        token = m.redi[0];
+        __syncthreads();
+    }
     return token;
 }
 
@@ -1660,16 +1837,16 @@ __global__ void __launch_bounds__(kThreads)
 sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64_t *rng, uint32_t *tokens,
               int tok_stride, int *len, int *flags) {
     __shared__ __align__(16) float row[kSampleCap];
-    __shared__ __align__(16) float p[kSampleCap];
     __shared__ float redf[kThreads / 64];
     __shared__ int redi[kThreads / 64];
+    __shared__ double redd[kThreads / 64 + 1];
     const int b = blockIdx.x;
     const float *src = logits + size_t(b) * V;
     const bool staged = V <= kSampleCap;
     if (staged)
         for (int t = threadIdx.x; t < V; t += blockDim.x) row[t] = src[t];
     __syncthreads();
-    const int token = choose_token(staged ? row : src, V, temperature, rng + b, flags, p, kSampleCap, redf, redi);
+    const int token = choose_token(staged ? row : src, V, temperature, rng + b, flags, SampleLds{redf, redi, redd});
     append_token(tokens, tok_stride, len, b, token);
 }
 
@@ -1688,10 +1865,10 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
     const int W = s.W, V = s.V, b = blockIdx.x;
     float *N = lds.take<float>(size_t(W));
     float *L = lds.take<float>(size_t(kHeadSampleCap));
-    float *P = lds.take<float>(size_t(kHeadSampleCap));
     float4 *red = lds.take<float4>(size_t(kHsGroups) * 64);
     float *redf = lds.take<float>(kHsThreads / 64);
     int *redi = lds.take<int>(kHsThreads / 64);
+    double *redd = lds.take<double>(kHsThreads / 64 + 1);
     for (int c = threadIdx.x; c < W; c += blockDim.x) N[c] = xn[size_t(b) * W + c];
     __syncthreads();
     const int q = threadIdx.x & 63, g = threadIdx.x >> 6, quads = Vp / 4;
@@ -1732,8 +1909,320 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
         }
         __syncthreads();
     }
-    const int token = choose_token(L, V, temperature, rng + b, flags, P, kHeadSampleCap, redf, redi);
+    const int token = choose_token(L, V, temperature, rng + b, flags, SampleLds{redf, redi, redd});
     append_token(tokens, tok_stride, len, b, token);
+}
+
+// ------------------------------------------------ persistent decode kernel
+//
+// Every decode step of a batch in one launch, as a dataflow between
+// workgroups that stay resident for the whole launch:
+//   mesh teams   three per sequence (the row decode kernel's teams): the
+//                residual row lives in their registers across layers; each
+//                team repeats the post-attention meshes of block l-1, then runs
+//                its Q, K or V mesh of block l.  After the last block they take
+//                the logits, and all three sample the same next token;
+//   attention    one per (sequence, head): the head's whole key range each
+//                layer (attn_share).  After the last block's attention the
+//                sequence's H attention blocks each repeat its post-attention
+//                half and compute 1/H of the logits.
+// Rows advance independently, so one sequence's meshes overlap another's KV
+// stream.  A hand-off is a flag word per producer: the producer writes its
+// data with agent-scope (coherent) stores, drains them with s_waitcnt, then
+// stores the sequence number of the phase into its flag; the consumer polls
+// the producers' flags (one lane each) and reads the data with agent-scope
+// loads.  No cache-wide release/acquire fence is needed, as no cached copy of
+// the exchanged lines can exist.  The KV rows appended during the launch are
+// read with ordinary loads: their cache lines are never read before they are
+// written (rows are whole 128-byte lines, hdp >= 32, and a launch starts with
+// invalidated caches).  Every wait is bounded: after kWaitTicks of wall clock
+// it raises *abort, and every other wait gives up as soon as it sees the flag,
+// so a broken hand-off ends the launch with an error instead of a hang.
+
+constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
+constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
+
+__device__ __forceinline__ int load_flag(const int *p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits (wave 0 polls, one lane per flag; the block meets at a barrier) until
+// all n <= 64 flags are >= target.  Returns false when the launch was aborted.
+__device__ bool wait_flags(const int *flags, int n, int target, int *abort) {
+    __shared__ int ok;
+    if (threadIdx.x < 64) {
+        const int lane = threadIdx.x;
+        int good = 1;
+        const uint64_t t0 = wall_clock64();
+        while (!__all(lane >= n || load_flag(flags + lane) >= target)) {
+            if (load_flag(abort) != 0) {
+                good = 0;
+                break;
+            }
+            if (wall_clock64() - t0 > kWaitTicks) {
+                if (lane == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                good = 0;
+                break;
+            }
+            __builtin_amdgcn_s_sleep(1);
+        }
+        if (lane == 0) ok = good;
+    }
+    __syncthreads();
+    return ok != 0;
+}
+
+// Publishes the block's coherent stores, then sets its flag to `value`.
+__device__ __forceinline__ void publish(int *flag, int value) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Records one trace timestamp (thread 0) when a timeline is requested.
+__device__ __forceinline__ void trace_mark(const PersistArgs &a, int step, int l, int which) {
+    if (a.trace && threadIdx.x == 0)
+        a.trace[((size_t(blockIdx.x) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = wall_clock64();
+}
+
+// Flag words: per sequence 3 team flags (q/k/v of a layer published), H
+// attention flags (a layer's attention state published) and H head flags
+// (a step's logit slice published).
+struct PersistFlags {
+    int *team, *attn, *head;
+    __device__ PersistFlags(const PersistArgs &a, int b)
+        : team(a.sync + size_t(b) * 3), attn(a.sync + size_t(a.batch) * 3 + size_t(b) * a.s.H),
+          head(a.sync + size_t(a.batch) * (3 + a.s.H) + size_t(b) * a.s.H) {}
+};
+
+// Logits of tokens [t0, t1) for the row-order normalised row xn (in LDS):
+// wave w takes tokens t0 + w, t0 + w + NW, ...; each lane a contiguous W/64
+// channels of the row-order token vectors E.  Eight tokens' loads are in
+// flight before their dot products and wave sums.
+template <int NW, int W>
+__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, float *out, int t0,
+                                                      int t1, int lane, int wave) {
+    constexpr int CW = W / 64, T8 = 8;
+    float xr[CW];
+#pragma unroll
+    for (int k = 0; k < CW; ++k) xr[k] = xn[lane * CW + k];
+    for (int base = t0 + wave; base < t1; base += T8 * NW) {
+        float e[T8][CW];
+#pragma unroll
+        for (int u = 0; u < T8; ++u) {
+            const int t = min(base + u * NW, t1 - 1);
+            const float *row = E + size_t(t) * W + lane * CW;
+            if constexpr (CW % 4 == 0) {
+#pragma unroll
+                for (int k = 0; k < CW; k += 4) {
+                    const float4 v = *reinterpret_cast<const float4 *>(row + k);
+                    e[u][k] = v.x;
+                    e[u][k + 1] = v.y;
+                    e[u][k + 2] = v.z;
+                    e[u][k + 3] = v.w;
+                }
+            } else {
+#pragma unroll
+                for (int k = 0; k < CW; ++k) e[u][k] = row[k];
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < T8; ++u) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CW; ++k) acc = fmaf(xr[k], e[u][k], acc);
+            acc = wave_sum(acc);
+            const int t = base + u * NW;
+            if (lane == 0 && t < t1) store_coherent(out + t, acc);
+        }
+    }
+}
+
+template <int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const float *g, bool fixed, int lane,
+                                                   int wave) {
+    if (fixed) row_load_weights<NW, CPL, D>(w, g, lane, wave);
+}
+
+struct PersistLds {
+    float *xch, *red, *xn, *row, *redf;
+    int *redi;
+    double *redd;
+    uint64_t *rng;
+};
+
+// Mesh team `team` of sequence b.
+template <int NW, int CPL, int GL, int DEPTH, int HDP>
+__device__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m) {
+    using Ctx = RowCtx<NW, CPL, GL>;
+    constexpr int W = Ctx::W;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : 1;
+    const Shape &s = a.s;
+    Ctx c(m.xch, m.red);
+    const int dim = c.dim(), H = s.H, L = a.layers, V = s.V;
+    const PersistFlags f(a, b);
+    int len = a.len[b];
+    uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
+    if (threadIdx.x == 0) *m.rng = a.rng[b];
+    const size_t gA = 2 * size_t(W) * s.A;           // floats of one attention-depth mesh
+    const size_t blk = 4 * gA + 2 * size_t(W) * s.F;  // floats of one block: q, k, v, proj, ffn
+    auto block = [&](int l) { return a.w + a.block0 + size_t(l) * blk; };
+    float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
+    bool alive = true;
+    for (int step = 0; step < a.steps && alive; ++step) {
+        const int pos = len - 1;
+        float x[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
+        trace_mark(a, step, 0, 0);
+        for (int l = 0; l < L; ++l) {
+            const float *wb = block(l);
+            load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
+            if (l > 0) {
+                // Post-attention half of block l-1, its weights loading during the wait.
+                const float *wq = block(l - 1);
+                load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
+                load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
+                if (!wait_flags(f.attn, H, step * L + l, a.abort)) {
+                    alive = false;
+                    break;
+                }
+                trace_mark(a, step, l, 0);
+                float y[CPL], v[CPL];
+                const float *dvb = a.dv + (size_t((l - 1) & 1) * a.batch + b) * W;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const float *pp = a.part + size_t(b * H + c.head_of(j)) * (HDP + 2);
+                    v[j] = load_coherent(dvb + c.ridx(j));
+                    y[j] = load_coherent(pp + dim) / load_coherent(pp + HDP + 1);
+                }
+                row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
+            }
+            if (l + 1 == L && team == 0) {
+                // The attention blocks finish the last block from this row.
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) store_coherent(a.xrow + size_t(b) * W + c.ridx(j), x[j]);
+            }
+            const float inv = row_inv_rms(c, x, 3);
+            float n[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
+            row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
+            float *kl = a.kc + size_t(l) * a.layer_elems, *vl = a.vc + size_t(l) * a.layer_elems;
+            if (team == 2) {
+                float *dvb = a.dv + (size_t(l & 1) * a.batch + b) * W;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    store_coherent(vl + (size_t(b * H + c.head_of(j)) * a.cap + pos) * HDP + dim, n[j]);
+                    store_coherent(dvb + c.ridx(j), n[j]);
+                }
+            } else {
+                row_qk_rope(c, n, rope_pair(a.rope, pos, dim, s.half), s);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    if (team == 0)
+                        store_coherent(a.q + size_t(b) * W + c.chan(j), n[j]);
+                    else
+                        store_coherent(kl + (size_t(b * H + c.head_of(j)) * a.cap + pos) * HDP + dim, n[j]);
+                }
+            }
+            publish(f.team + team, step * L + l + 1);
+            trace_mark(a, step, l, 1);
+        }
+        if (!alive) break;
+        // The logits, then every team draws the same token from the same
+        // logits and state.
+        if (!wait_flags(f.head, H, step + 1, a.abort)) break;
+        trace_mark(a, step, L, 0);
+        for (int t = threadIdx.x; t < V; t += blockDim.x) m.row[t] = load_coherent(a.logits + size_t(b) * V + t);
+        __syncthreads();
+        tok = uint32_t(choose_token(m.row, V, a.temperature, m.rng, a.flags, SampleLds{m.redf, m.redi, m.redd}));
+        if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
+        ++len;
+        trace_mark(a, step, L, 1);
+    }
+    if (team == 0 && threadIdx.x == 0) {
+        a.len[b] = len;
+        a.rng[b] = *m.rng;
+    }
+}
+
+// Attention block of (sequence b, head h); after the last block's attention
+// it finishes that block from the published residual row and computes the
+// logits of tokens [h*V/H, (h+1)*V/H).
+template <int NW, int CPL, int GL, int DEPTH, int HDP>
+__device__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
+    using Ctx = RowCtx<NW, CPL, GL>;
+    constexpr int W = Ctx::W;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : 1;
+    const Shape &s = a.s;
+    const int len0 = a.len[b], L = a.layers, H = s.H, V = s.V;
+    const PersistFlags f(a, b);
+    const size_t slab = size_t(b * H + h) * a.cap * HDP;
+    const size_t gA = 2 * size_t(W) * s.A;
+    const float *wlast = a.w + a.block0 + size_t(L - 1) * (4 * gA + 2 * size_t(W) * s.F);
+    Ctx c(m.xch, m.red);
+    const int dim = c.dim();
+    float2 wp[D][CPL], wf[D][CPL];
+    for (int step = 0; step < a.steps; ++step) {
+        for (int l = 0; l < L; ++l) {
+            if (!wait_flags(f.team, 3, step * L + l + 1, a.abort)) return;
+            trace_mark(a, step, l, 0);
+            attn_share<HDP, true, 64 * NW, true>(a.q + size_t(b) * s.W + h * s.hd, s.hd,
+                                                 a.kc + size_t(l) * a.layer_elems + slab,
+                                                 a.vc + size_t(l) * a.layer_elems + slab, 0, len0 + step,
+                                                 a.scale_log2, a.part + size_t(b * H + h) * (HDP + 2));
+            publish(f.attn + h, step * L + l + 1);
+            trace_mark(a, step, l, 1);
+        }
+        // Post-attention half of the last block, then this block's logits.
+        load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
+        load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
+        if (!wait_flags(f.attn, H, step * L + L, a.abort)) return;
+        float x[CPL], y[CPL], v[CPL];
+        const float *dvb = a.dv + (size_t((L - 1) & 1) * a.batch + b) * W;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const float *pp = a.part + size_t(b * H + c.head_of(j)) * (HDP + 2);
+            x[j] = load_coherent(a.xrow + size_t(b) * W + c.ridx(j));
+            v[j] = load_coherent(dvb + c.ridx(j));
+            y[j] = load_coherent(pp + dim) / load_coherent(pp + HDP + 1);
+        }
+        row_post(c, x, y, v, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
+        const float inv = row_inv_rms(c, x, 3);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
+        __syncthreads();
+        persistent_head_slice<NW, W>(m.xn, a.E, a.logits + size_t(b) * V, h * V / H, (h + 1) * V / H, c.lane, c.wave);
+        publish(f.head + h, step + 1);
+        trace_mark(a, step, L, 1);
+    }
+}
+
+// Blocks [0, 3*batch): mesh teams (sequence, team); then (sequence, head)
+// attention blocks.  Needs every block resident at once (cooperative launch).
+template <int NW, int CPL, int GL, int DEPTH, int HDP>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
+persistent_decode_kernel(PersistArgs a) {
+    constexpr int W = 64 * NW * CPL;
+    __shared__ float xch[2 * W];
+    __shared__ float red[8 * RowCtx<NW, CPL, GL>::SLOT];
+    __shared__ __align__(16) float xn[W];
+    __shared__ __align__(16) float row[kPersistVocab];
+    __shared__ float redf[NW];
+    __shared__ int redi[NW];
+    __shared__ double redd[NW + 1];
+    __shared__ uint64_t rng;
+    const PersistLds m{xch, red, xn, row, redf, redi, redd, &rng};
+    const int blk = blockIdx.x;
+    if (blk < 3 * a.batch) {
+        persistent_team<NW, CPL, GL, DEPTH, HDP>(a, blk / 3, blk % 3, m);
+    } else {
+        const int i = blk - 3 * a.batch;
+        persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, i / a.s.H, i % a.s.H, m);
+    }
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -1856,8 +2345,8 @@ size_t head_lds_bytes(const Shape &s, int rt) {
 
 size_t head_sample_lds_bytes(const Shape &s) {
     if (s.V > kHeadSampleCap) return size_t(-1);
-    return align16(size_t(s.W) * 4) + 2 * align16(kHeadSampleCap * 4) + align16(size_t(kHsGroups) * 64 * 16) +
-           2 * align16(kHsThreads / 64 * 4);
+    return align16(size_t(s.W) * 4) + align16(kHeadSampleCap * 4) + align16(size_t(kHsGroups) * 64 * 16) +
+           2 * align16(kHsThreads / 64 * 4) + align16((kHsThreads / 64 + 1) * 8);
 }
 
 void configure_lds(size_t max_bytes) {
@@ -1999,6 +2488,56 @@ void row_order(const float *src, float *dst, int rows, int W, bool pairs, hipStr
         hipLaunchKernelGGL(row_order_kernel<float>, dim3(blocks), dim3(kThreads), 0, stream, src, dst, rows, W,
                            row_waves(W));
     HIP_LAUNCH_CHECK();
+}
+
+// The persistent kernel instantiation for a shape, or nullptr.
+template <int NW, int CPL, int HDP>
+const void *persistent_pick(const Shape &s) {
+    constexpr int GL = HDP / NW;
+    const bool fixed = s.butterfly && s.A == s.F;
+    if constexpr (NW == 4 && CPL == 2 && HDP == 64) {
+        if (fixed && s.A == 9) return reinterpret_cast<const void *>(&persistent_decode_kernel<4, 2, 16, 9, 64>);
+    }
+    if constexpr (NW == 2 && CPL == 1 && HDP == 32) {
+        if (fixed && s.A == 7) return reinterpret_cast<const void *>(&persistent_decode_kernel<2, 1, 16, 7, 32>);
+    }
+    return reinterpret_cast<const void *>(&persistent_decode_kernel<NW, CPL, GL, 0, HDP>);
+}
+
+const void *persistent_kernel(const Shape &s) {
+    if (!row_block_supported(s) || s.hd != s.hdp || s.V > kPersistVocab) return nullptr;
+    const int nw = row_waves(s.W);
+    if (s.hd / nw != 8 && s.hd / nw != 16) return nullptr;
+    switch (s.W * 10000 + s.hd) {
+    case 1280032: return persistent_pick<2, 1, 32>(s);
+    case 2560032: return persistent_pick<4, 1, 32>(s);
+    case 2560064: return persistent_pick<4, 1, 64>(s);
+    case 5120032: return persistent_pick<4, 2, 32>(s);
+    case 5120064: return persistent_pick<4, 2, 64>(s);
+    case 10240064: return persistent_pick<4, 4, 64>(s);
+    default: return nullptr;
+    }
+}
+
+int persistent_blocks(const Shape &s, int batch) { return 3 * batch + batch * s.H; }
+
+bool persistent_fits(const Shape &s, int batch, int device) {
+    const void *f = persistent_kernel(s);
+    if (!f) return false;
+    int per_cu = 0, cus = 0;
+    if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * row_waves(s.W), 0) != hipSuccess) return false;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return false;
+    return persistent_blocks(s, batch) <= per_cu * cus;
+}
+
+hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream) {
+    const void *f = persistent_kernel(a.s);
+    if (!f) return hipErrorInvalidValue;
+    PersistArgs args = a;
+    args.scale_log2 = float(1.4426950408889634 / std::sqrt(double(a.s.hd)));
+    void *params[] = {&args};
+    return hipLaunchCooperativeKernel(f, dim3(persistent_blocks(a.s, a.batch)), dim3(64 * row_waves(a.s.W)), params, 0,
+                                      stream);
 }
 
 void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit, float *part,

@@ -108,6 +108,44 @@ void row_block(const BlockArgs &a, hipStream_t stream);
 // dst = src with each row of W channels (floats, or float2 weight pairs when
 // `pairs`) permuted into row order.
 void row_order(const float *src, float *dst, int rows, int W, bool pairs, hipStream_t stream);
+// One launch of the persistent decode kernel: `steps` decode steps of `batch`
+// sequences (each with its last token not yet run through the blocks), every
+// mesh and attention phase inside the launch.  Needs persistent_fits().
+struct PersistArgs {
+    Shape s;
+    int batch, layers, steps;
+    const float *E;       // token vectors in row order (V x W)
+    const float *w;       // mesh weights in row order, at their parameter offsets
+    size_t block0;        // offset of block 0's first mesh
+    float *kc, *vc;       // KV cache, layer-major
+    size_t layer_elems;   // floats of one layer of the cache
+    int cap;              // positions per (sequence, head) slab
+    float *q;             // [batch][W] queries
+    float *dv;            // [2][batch][W] value rows in row order, by layer parity
+    float *xrow;          // [batch][W] residual rows (row order) entering the last block
+    float *part;          // [batch][H][hdp + 2] attention states
+    float *logits;        // [batch][V]
+    const float2 *rope;
+    uint32_t *tokens;
+    int tok_stride;
+    int *len;
+    uint64_t *rng;
+    float temperature;
+    int *flags;           // bit 0: non-finite logits
+    int *sync;            // [batch][3 + 2*H] hand-off flags, zero at launch
+    int *abort;           // zero at launch; set when a wait times out
+    float scale_log2;     // set by persistent_decode
+    // Optional timeline (nullptr: none): for block k, step t and phase l,
+    // trace[((k * steps + t) * (layers + 1) + l) * 2 + {0, 1}] receive the
+    // wall clock (100 MHz) when the phase's inputs were ready and when its
+    // outputs were published.  Mesh teams: l = 0..layers (l = layers: logits
+    // ready, token drawn); attention blocks: l = 0..layers-1, and l = layers
+    // (slot 1) when their logit slice is published.
+    uint64_t *trace;
+};
+bool persistent_fits(const Shape &s, int batch, int device);
+hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream);
+
 // Split-KV decode attention: one query row per sequence; the len[b] keys are
 // cut into nsplit equal shares whose partial softmax states (acc[hdp], m, l)
 // go to part[((b*H+h)*nsplit+split)*(hdp+2)].  When start/stop are given the

@@ -84,6 +84,9 @@ struct MeshGpt::Impl {
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
     size_t batch_cap = 0, tcap = 0;
     DevBuf kc, vc, dx, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
+    // Persistent decode kernel state: value rows by layer parity, hand-off
+    // counters and the abort flag.
+    DevBuf pdv, pxrow, psync, pabort;
     size_t batch = 0, length = 0, cached = kNoCache;
     float temperature = 0.0f;
 
@@ -102,6 +105,9 @@ struct MeshGpt::Impl {
     // (MG_DISABLE_ROW_DECODE=1 / MG_DISABLE_WAVE_DECODE=1 skip the first two).
     bool row_decode = false;
     bool wave_decode = false;
+    // Decode steps run in one persistent launch when the shape and batch allow
+    // it (MG_DISABLE_PERSISTENT=1 keeps the per-phase kernels).
+    bool persistent_ok = false;
 
     ~Impl() {
         drop_graph();
@@ -205,6 +211,7 @@ struct MeshGpt::Impl {
         shape.F = int(cfg.ffn_mesh_depth);
         wave_decode = env_int("MG_DISABLE_WAVE_DECODE", 0) == 0 && kern::block_decode_supported(shape);
         row_decode = env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
+        persistent_ok = row_decode && env_int("MG_DISABLE_PERSISTENT", 0) == 0;
 
         const size_t C = cfg.context;
 
@@ -287,6 +294,12 @@ struct MeshGpt::Impl {
             drng.ensure(batch_cap * 8);
             dlogits.ensure(batch_cap * cfg.vocab_size * 4);
             dflags.ensure(4);
+            if (persistent_ok) {
+                pdv.ensure(2 * batch_cap * cfg.width * 4);
+                pxrow.ensure(batch_cap * cfg.width * 4);
+                psync.ensure(persist_flag_words(batch_cap) * 4);
+                pabort.ensure(4);
+            }
         }
         tcap = std::max(t, tcap);
         dtokens.release();
@@ -529,6 +542,56 @@ struct MeshGpt::Impl {
     bool decodable(size_t steps) const {
         return batch > 0 && cached == length - 1 && length - 1 + steps <= cfg.context && length + steps <= tcap;
     }
+
+    size_t persist_flag_words(size_t b) const { return b * (3 + 2 * cfg.heads); }
+
+    bool persistent_usable() const {
+        return persistent_ok && row_decode && kern::persistent_fits(shape, int(batch), device);
+    }
+
+    // `steps` decode steps in one launch of the persistent kernel (the caller
+    // checked decodable(steps) and persistent_usable()).
+    void persistent(size_t steps, uint64_t *trace = nullptr) {
+        check(hipMemsetAsync(psync.p, 0, persist_flag_words(batch) * 4, stream), "clear flags");
+        check(hipMemsetAsync(pabort.p, 0, 4, stream), "clear abort");
+        kern::PersistArgs a{};
+        a.s = shape;
+        a.batch = int(batch);
+        a.layers = int(cfg.layers);
+        a.steps = int(steps);
+        a.E = Edec.as<float>();
+        a.w = wdec.as<float>();
+        a.block0 = layout.groups[layout.blocks[0].query].offset;
+        a.kc = kc.as<float>();
+        a.vc = vc.as<float>();
+        a.layer_elems = layer_cache_elems();
+        a.cap = int(cfg.context);
+        a.q = dq.as<float>();
+        a.dv = pdv.as<float>();
+        a.xrow = pxrow.as<float>();
+        a.part = part.as<float>();
+        a.logits = dlogits.as<float>();
+        a.rope = rope.as<float2>();
+        a.tokens = dtokens.as<uint32_t>();
+        a.tok_stride = int(tcap);
+        a.len = dlen.as<int>();
+        a.rng = drng.as<uint64_t>();
+        a.temperature = temperature;
+        a.flags = dflags.as<int>();
+        a.sync = psync.as<int>();
+        a.abort = pabort.as<int>();
+        a.trace = trace;
+        check(kern::persistent_decode(a, stream), "persistent decode launch");
+        sync();
+        int aborted = 0;
+        check(hipMemcpy(&aborted, pabort.p, 4, hipMemcpyDeviceToHost), "download abort flag");
+        if (aborted) {
+            cached = kNoCache;
+            throw Error("persistent decode kernel timed out waiting on a hand-off", kDeviceError);
+        }
+        cached = length + steps - 1;
+        length += steps;
+    }
 };
 
 MeshGpt::MeshGpt(int device, const GptConfig &config, uint64_t seed, size_t max_batch)
@@ -570,7 +633,16 @@ void MeshGpt::generate_tokens(const uint32_t *prompts, size_t batch, size_t prom
                               float temperature, uint64_t seed, uint32_t *out) {
     Impl &m = *impl_;
     m.start(prompts, batch, prompt_len, temperature, seed, prompt_len + count);
-    for (size_t i = 0; i < count; ++i) m.step();
+    size_t done = 0;
+    if (count > 0) {
+        m.step();  // the prompt's prefill and the first token
+        ++done;
+    }
+    if (done < count && m.decodable(count - done) && m.persistent_usable()) {
+        m.persistent(count - done);
+        done = count;
+    }
+    for (; done < count; ++done) m.step();
     m.finish();
     m.read_tokens(out, batch, prompt_len + count);
 }
@@ -601,6 +673,11 @@ void MeshGpt::decode(size_t steps) {
     if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
+    if (m.persistent_usable()) {
+        m.persistent(steps);
+        m.finish();
+        return;
+    }
     size_t done = 0;
     // Whole graphs of kGraphSteps steps, then single steps.
     for (; done + Impl::kGraphSteps <= steps; done += Impl::kGraphSteps) {
@@ -632,6 +709,25 @@ std::vector<float> MeshGpt::decode_profiled(size_t steps) {
     return ms;
 }
 
+std::vector<uint64_t> MeshGpt::decode_traced(size_t steps) {
+    Impl &m = *impl_;
+    if (!m.decodable(steps))
+        throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
+    m.activate();
+    if (!m.persistent_usable()) throw Error("the persistent decode kernel does not support this model and batch",
+                                            kUnsupported);
+    const size_t blocks = 3 * m.batch + m.batch * m.cfg.heads;
+    const size_t n = blocks * steps * (m.cfg.layers + 1) * 2;
+    DevBuf trace;
+    trace.ensure(n * 8);
+    check(hipMemsetAsync(trace.p, 0, n * 8, m.stream), "clear trace");
+    m.persistent(steps, trace.as<uint64_t>());
+    m.finish();
+    std::vector<uint64_t> out(n);
+    check(hipMemcpy(out.data(), trace.p, n * 8, hipMemcpyDeviceToHost), "download trace");
+    return out;
+}
+
 size_t MeshGpt::sequence_length() const { return impl_->length; }
 
 void MeshGpt::read_tokens(uint32_t *out, size_t batch, size_t length) { impl_->read_tokens(out, batch, length); }
@@ -645,6 +741,37 @@ std::vector<float> MeshGpt::last_logits() {
 }
 
 hipStream_t MeshGpt::stream() const { return impl_->stream; }
+
+bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                   uint64_t *rng_states, uint32_t *tokens) {
+    if (rows == 0) return false;
+    if (vocab == 0 || vocab > size_t(1) << 24) throw Error("vocabulary must hold 1..2^24 tokens");
+    if (!std::isfinite(temperature) || temperature < 0.0f)
+        throw Error("temperature must be finite and nonnegative (0 is greedy)");
+    int count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count) throw Error("invalid device ordinal", kDeviceError);
+    check(hipSetDevice(device), "hipSetDevice");
+    DevBuf dl, drng, dtok, dlen, dflags;
+    dl.ensure(rows * vocab * 4);
+    drng.ensure(rows * 8);
+    dtok.ensure(rows * 4);
+    dlen.ensure(rows * 4);
+    dflags.ensure(4);
+    check(hipMemcpy(dl.p, logits, rows * vocab * 4, hipMemcpyHostToDevice), "upload logits");
+    check(hipMemcpy(drng.p, rng_states, rows * 8, hipMemcpyHostToDevice), "upload rng");
+    check(hipMemset(dlen.p, 0, rows * 4), "clear lengths");
+    check(hipMemset(dflags.p, 0, 4), "clear flags");
+    kern::sample(int(vocab), int(rows), dl.as<float>(), temperature, drng.as<uint64_t>(), dtok.as<uint32_t>(), 1,
+                 dlen.as<int>(), dflags.as<int>(), nullptr);
+    check(hipGetLastError(), "sample launch");
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    check(hipMemcpy(tokens, dtok.p, rows * 4, hipMemcpyDeviceToHost), "download tokens");
+    check(hipMemcpy(rng_states, drng.p, rows * 8, hipMemcpyDeviceToHost), "download rng");
+    int flags = 0;
+    check(hipMemcpy(&flags, dflags.p, 4, hipMemcpyDeviceToHost), "download flags");
+    return flags != 0;
+}
 
 double copy_bandwidth(int device, size_t bytes, int iters) {
     int count = 0;

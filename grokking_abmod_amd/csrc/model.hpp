@@ -45,6 +45,11 @@ class MeshGpt {
     // Same steps without graph replay, timing every decode-attention launch
     // with HIP events; returns milliseconds per launch (steps x layers).
     std::vector<float> decode_profiled(size_t steps);
+    // Same steps in one persistent launch that records its timeline: blocks x
+    // steps x (layers + 1) x 2 wall-clock stamps (100 MHz), layout as
+    // kern::PersistArgs::trace; blocks are 3*batch mesh teams then
+    // batch*heads attention blocks.
+    std::vector<uint64_t> decode_traced(size_t steps);
     size_t sequence_length() const;
     void read_tokens(uint32_t *out, size_t batch, size_t length);
     std::vector<float> last_logits();
@@ -55,6 +60,12 @@ class MeshGpt {
     struct Impl;
     std::unique_ptr<Impl> impl_;
 };
+
+// The generate sampler on device for `rows` rows of `vocab` logits: greedy
+// when temperature == 0, else one draw from rng_states[r] per row (advanced in
+// place).  Returns whether any row held a non-finite logit.
+bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                   uint64_t *rng_states, uint32_t *tokens);
 
 // Mean bandwidth (read + write bytes / s / 1e9) of a plain device copy of
 // `bytes`, repeated `iters` times on `device`.

@@ -109,6 +109,13 @@ int mg_decode(mg_model *model, size_t steps);
 /* As mg_decode, without graph replay, timing each decode-attention launch with
  * HIP events on the model's stream: ms has steps x layers entries. */
 int mg_decode_profiled(mg_model *model, size_t steps, float *ms, size_t n);
+/* As mg_decode, in one persistent launch that records its timeline (no
+ * reference counterpart: a profiling aid).  stamps receives blocks x steps x
+ * (layers + 1) x 2 wall-clock values at 100 MHz: for each block (3*batch mesh
+ * teams, then batch*heads attention blocks), step and phase, when the phase's
+ * inputs were ready and when its outputs were published.  Fails with
+ * MG_UNSUPPORTED when the persistent kernel cannot run this model and batch. */
+int mg_decode_traced(mg_model *model, size_t steps, uint64_t *stamps, size_t n);
 /* Current tokens per sequence (prompt + generated). */
 int mg_sequence_length(const mg_model *model, size_t *out);
 int mg_read_tokens(mg_model *model, uint32_t *out, size_t batch, size_t length);
@@ -116,6 +123,15 @@ int mg_read_tokens(mg_model *model, uint32_t *out, size_t batch, size_t length);
 int mg_last_logits(mg_model *model, float *out, size_t n);
 /* The hipStream_t every call of this model runs on. */
 void *mg_model_stream(mg_model *model);
+
+/* The sampler of mg_generate (gpu.rs:2028-2049) on `device`, for `rows` rows
+ * of `vocab` f32 logits: the first maximal logit when temperature == 0, else
+ * one Random::unit() draw from rng_states[r] per row (states advanced in place)
+ * and the reference's sequential f32 CDF scan.  Returns MG_NONFINITE (tokens
+ * still written) when a row holds a non-finite logit.  No separate reference
+ * call: it exposes generate's sampling step to tests. */
+int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                     uint64_t *rng_states, uint32_t *tokens);
 
 /* A plain device-to-device copy of `bytes` (a float4 grid-stride kernel named
  * calibration_copy) run `iters` times on `device`; writes the mean bandwidth

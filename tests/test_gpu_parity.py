@@ -329,3 +329,35 @@ def test_decode_kernels_agree(name, monkeypatch):
     (t0, l0), (t1, l1) = results
     assert np.array_equal(t0, t1)
     assert_close(l0, l1, what="row vs wave decode logits")
+
+
+@pytest.mark.parametrize("name,temperature", [("tiny", 0.0), ("tiny", 0.8), ("mid", 0.0), ("mid", 1.0)])
+def test_persistent_decode_matches_per_phase_kernels(name, temperature, monkeypatch):
+    # The persistent decode launch (all steps in one kernel) and the per-phase
+    # kernels decode the same tokens from the same prompts and seeds, with
+    # last-step logits within the tolerance of each other.
+    config = G.named_config(name)
+    prompts = (np.arange(6 * 20).reshape(6, 20) * 5 % config.vocab_size).astype(np.uint32)
+    results = []
+    for disable in ("0", "1"):
+        monkeypatch.setenv("MG_DISABLE_PERSISTENT", disable)
+        with G.MeshGpt(0, config, 7, max_batch=6) as model:
+            tokens = model.generate_tokens(prompts, 40, temperature, 11)
+            results.append((tokens, model.last_logits(6)))
+    (t0, l0), (t1, l1) = results
+    assert np.array_equal(t0, t1)
+    assert_close(l0, l1, what="persistent vs per-phase decode logits")
+
+
+def test_persistent_decode_steps_continue_a_generation():
+    # decode(k) after prefill appends exactly the tokens a single generate call
+    # produces (the persistent launch picks up the sampler state and lengths).
+    config = G.named_config("tiny")
+    prompts = (np.arange(3 * 16).reshape(3, 16) * 11 % config.vocab_size).astype(np.uint32)
+    with G.MeshGpt(0, config, 7, max_batch=3) as model:
+        whole = model.generate_tokens(prompts, 33, 0.9, 5)
+        model.prefill(prompts, 0.9, 5, reserve=16 + 33)
+        model.decode(12)
+        model.decode(20)
+        assert model.sequence_length() == 16 + 33
+        assert np.array_equal(model.read_tokens(3), whole)
