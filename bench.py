@@ -8,11 +8,13 @@ batch (32 tokens).  Prompts are prefilled untimed; the timed region is K decode
 steps starting right after the prompt (K = 512 is the full config-3 run), with
 every input already resident in HBM.
 
-Prints one JSON line with the roofline of the dominant kernel (split-KV decode
-attention, timed per launch with HIP events that hipExtLaunchKernel stamps with
-the dispatch's own begin and end on the model's stream), the
-step-level fraction of the HBM roofline, the batch-1 (config 1) figure and the
-CPU baseline (the f64 oracle on one core, a bounded sample of the workload).
+The K steps run as one launch of the persistent decode kernel, so the timed
+region is that kernel: HIP events recorded on the model's stream right
+before and after the launch give its duration, and the roofline divides the
+steps' algorithmic HBM bytes (KV-cache reads and appends, mesh weights, tied
+head table, token ids) by it.  Prints one JSON line with that roofline, the
+batch-1 (config 1) figure and the CPU baseline (the f64 oracle on one core, a
+bounded sample of the workload).
 """
 import argparse
 import ctypes
@@ -90,14 +92,6 @@ def prompts_for(config, batch, length, seed=7):
     return out
 
 
-def attention_bytes(config, batch, position):
-    """Algorithmic HBM bytes of one decode-attention launch processing the token at
-    `position`: K and V rows of all position+1 keys for every sequence (2*W*4
-    bytes per key per sequence), plus the query read and the output write."""
-    w = config.width
-    return batch * ((position + 1) * 2 * w * 4 + 2 * w * 4)
-
-
 def step_bytes(config, batch, position):
     """Algorithmic HBM bytes of a whole decode step (all layers): KV reads and
     appends, mesh weights, the tied head table and the token ids."""
@@ -108,7 +102,8 @@ def step_bytes(config, batch, position):
 
 
 def run_decode(hip, model, prompts, steps, temperature, seed):
-    """Prefill (untimed) then `steps` timed decode steps; returns milliseconds."""
+    """Prefill (untimed) then `steps` timed decode steps (one persistent launch
+    when the model supports it); returns (event ms, wall ms)."""
     model.prefill(prompts, temperature, seed, reserve=prompts.shape[1] + 1 + steps)
     hip.synchronize()
     stream = model.stream()
@@ -163,40 +158,52 @@ def cpu_baseline(config, prompts, steps, temperature, budget_s):
     }
 
 
+KERNEL = "persistent_decode_kernel"
+
+
 def pmc_traffic(args, config, batch):
-    """HBM bytes per decode-attention launch from two rocprofv3 --pmc runs of a
-    child process (FETCH_SIZE, then WRITE_SIZE), each scaled by the same counter
-    on a plain copy kernel of known size.  Returns None when unavailable."""
+    """HBM bytes of the persistent decode launch of the timed steps, from two
+    rocprofv3 --pmc runs of a child process (FETCH_SIZE, then WRITE_SIZE), each
+    scaled by the same counter on a plain copy kernel of known size.  Returns
+    None when unavailable."""
     rocprof = "/opt/rocm/bin/rocprofv3"
     if not os.path.exists(rocprof):
         return None
-    per_counter = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+    import csv
+
+    def collect(counter):
+        # rocprofv3 may exit with a segmentation fault after the program ends
+        # (cooperative launches); the counter file is complete by then.
         out = tempfile.mkdtemp(prefix="mg_pmc_")
         cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
                "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe",
                "--steps", str(args.steps), "--prompt", str(args.prompt), "--batch", str(batch)]
         res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
-        files = glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True)
-        if not files:
-            sys.stderr.write(f"pmc {counter}: no counter file (rc={res.returncode})\n{res.stderr[-2000:]}\n")
-            return None
-        import csv
+        hits, copy = [], []
+        for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    name = row.get("Kernel_Name", "")
+                    value = float(row.get("Counter_Value", "nan"))
+                    if KERNEL in name:
+                        hits.append(value)
+                    elif "calibration_copy" in name:
+                        copy.append(value)
+        if not hits or not copy:
+            sys.stderr.write(f"pmc {counter}: kernel rows {len(hits)}, copy rows {len(copy)} "
+                             f"(rc={res.returncode})\n{res.stderr[-1500:]}\n")
+        return hits, copy
 
-        attn, copy = [], []
-        with open(files[0]) as f:
-            for row in csv.DictReader(f):
-                name = row.get("Kernel_Name", "")
-                value = float(row.get("Counter_Value", "nan"))
-                if "attn_decode_kernel" in name:
-                    attn.append(value)
-                elif "calibration_copy" in name:
-                    copy.append(value)
-        if not attn or not copy:
+    per_counter = {}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        hits, copy = collect(counter)
+        if not hits or not copy:
+            hits, copy = collect(counter)
+        if not hits or not copy:
             return None
         copy_kib = PROBE_COPY_BYTES / 1024.0
         factor = copy_kib / float(np.mean(copy))
-        per_counter[counter] = float(np.mean(attn)) * factor * 1024.0
+        per_counter[counter] = float(np.mean(hits)) * factor * 1024.0
         per_counter[counter + "_factor"] = factor
     return per_counter
 
@@ -206,8 +213,8 @@ PROBE_COPY_BYTES = 256 << 20
 
 def probe(args):
     """Child process under rocprofv3 --pmc: the timed region's decode steps (same
-    positions, so per-launch means compare with the algorithmic bytes) and one
-    plain copy kernel of known size for calibration."""
+    positions, one persistent launch) and one plain copy kernel of known size
+    for calibration."""
     config = G.named_config("mid")
     prompts = prompts_for(config, args.batch, args.prompt)
     with G.MeshGpt(0, config, 7, max_batch=args.batch) as model:
@@ -246,7 +253,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
-              "decode would shard by sequence with no per-step exchange (see DESIGN.md).", file=sys.stderr)
+              "decode would shard by sequence with no per-step exchange between GPUs.", file=sys.stderr)
         sys.exit(2)
 
     config = G.named_config("mid")
@@ -256,24 +263,16 @@ def main():
     prompts = prompts_for(config, args.batch, args.prompt)
     hip = Hip()
     with G.MeshGpt(0, config, 7, max_batch=args.batch) as model:
-        # Warm-up: a full prefill and W decode steps (graph capture happens here).
-        model.prefill(prompts, temperature, 7, reserve=args.prompt + 1 + max(args.steps, args.warmup))
+        # Warm-up: a full prefill and W decode steps.
         if args.warmup:
+            model.prefill(prompts, temperature, 7, reserve=args.prompt + 1 + max(args.steps, args.warmup))
             model.decode(args.warmup)
-        hip.synchronize()
+            hip.synchronize()
         ms, wall_ms = run_decode(hip, model, prompts, args.steps, temperature, 7)
-        # Roofline pass: the same steps (same positions) without graph replay; each
-        # decode-attention launch goes through hipExtLaunchKernel with a pair of HIP
-        # events on the model's stream that take the dispatch's begin and end.
-        model.prefill(prompts, temperature, 7, reserve=args.prompt + 1 + args.steps)
-        per_launch = model.decode_profiled(args.steps).reshape(args.steps, config.layers)
 
     positions = args.prompt + np.arange(args.steps)
-    attn_bytes = np.array([attention_bytes(config, args.batch, p) for p in positions], dtype=np.float64)
-    attn_s = per_launch.astype(np.float64) / 1000.0
-    achieved = float((attn_bytes[:, None] * np.ones((1, config.layers))).sum() / attn_s.sum() / 1e9)
-    total_step_bytes = float(sum(step_bytes(config, args.batch, p) for p in positions))
-    step_gbps = total_step_bytes / (ms / 1000.0) / 1e9
+    total_bytes = float(sum(step_bytes(config, args.batch, p) for p in positions))
+    gbps = total_bytes / (ms / 1000.0) / 1e9
 
     traffic = None
     pmc = None
@@ -309,22 +308,18 @@ def main():
         },
         "roofline": {
             "bound": "hbm",
-            "kernel": "attn_decode_kernel<64>",
-            "achieved": round(achieved, 1),
+            "kernel": "persistent_decode_kernel<4, 2, 16, 9, 64> (one launch = all timed steps)",
+            "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
-            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
             "traffic_calibration": None if not pmc else {
                 "fetch_factor": round(pmc["FETCH_SIZE_factor"], 4), "write_factor": round(pmc["WRITE_SIZE_factor"], 4),
                 "fetch_bytes": round(pmc["FETCH_SIZE"]), "write_bytes": round(pmc["WRITE_SIZE"])},
-            "algorithmic_bytes_per_launch": round(float(attn_bytes.mean())),
-            "avg_launch_us": round(float(per_launch.mean()) * 1000.0, 3),
-        },
-        "step_roofline": {
-            "achieved": round(step_gbps, 1), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-            "frac": round(step_gbps / HBM_PEAK_GBPS, 4),
-            "algorithmic_bytes_per_step": round(total_step_bytes / args.steps),
+            "algorithmic_bytes_per_launch": round(total_bytes),
+            "algorithmic_bytes_per_step": round(total_bytes / args.steps),
+            "avg_launch_us": round(ms * 1000.0, 1),
         },
         "wall_ms_timed_region": round(wall_ms, 3),
     }

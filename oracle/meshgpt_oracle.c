@@ -12,7 +12,7 @@
  * never contracts multiply-add pairs, and its f32 initialisation and sampler
  * are bit-exact only without contraction.
  *
- * Pinning: every function here is checked in tests/test_oracle_*.py against
+ * Pinning: every function here is checked in tests/test_oracle.py against
  * the reference's KATs (reference.rs:627-998, config.rs:660-807,
  * text.rs:115-155, grokking.rs:391-393), against the two published step-0
  * cross-entropies (docs/mesh-gpt.md:269, docs/cuda-performance.md:238-240), and

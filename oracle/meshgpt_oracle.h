@@ -9,8 +9,10 @@
  * The reference is pure Rust (/root/reference/src/gpt/); no Rust toolchain
  * exists in this image, so nothing of it can be built (oracle/_ref stays empty).
  * Each function below names the reference lines it restates.  How each one is
- * pinned (reference KATs, published whole-model numbers, closed forms) is
- * recorded in tests/test_oracle_*.py.
+ * pinned (reference KATs, published whole-model numbers, closed forms,
+ * independent numpy restatements) is recorded in tests/test_oracle.py.
+ * og_sample with temperature > 0 is parity unpinned: the reference holds no
+ * sampler vector, so it is checked only against an independent restatement.
  */
 #ifndef MESHGPT_ORACLE_H
 #define MESHGPT_ORACLE_H
@@ -85,7 +87,7 @@ int og_cross_entropy(const og_config *c, const float *params, const uint32_t *in
 int og_generate(const og_config *c, const float *params, const uint32_t *prompt, size_t P,
                 size_t count, float temperature, uint64_t seed, uint32_t *out);
 /* the f32 sampler of gpu.rs:2028-2049 on one row of f32 logits; returns the token and
- * advances *rng only when temperature > 0 */
+ * advances *rng only when temperature > 0 (T > 0: parity unpinned, see above) */
 uint32_t og_sample(const float *logits, size_t vocab, float temperature, uint64_t *rng);
 
 /* ---- KV-cached incremental decode (same math, used as the CPU baseline) ----
