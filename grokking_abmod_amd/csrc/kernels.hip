@@ -1004,11 +1004,14 @@ __device__ __forceinline__ void row_layer(float (&x)[CPL], const float2 (&w)[CPL
 // Weights of mesh layer u in row order: float2 (u*CPL + j)*NW*64 + wave*64 + lane.
 template <int NW, int CPL, int D>
 __device__ __forceinline__ void row_load_weights(float2 (&w)[D][CPL], const float *wg, int lane, int wave) {
-    const float2 *g = reinterpret_cast<const float2 *>(wg) + wave * 64 + lane;
+    // A uniform base and 32-bit lane offsets: one address register for all
+    // the loads instead of a 64-bit address per load.
+    const float2 *g = reinterpret_cast<const float2 *>(wg);
+    const uint32_t at = uint32_t(wave * 64 + lane);
 #pragma unroll
     for (int u = 0; u < D; ++u)
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) w[u][j] = g[(u * CPL + j) * NW * 64];
+        for (int j = 0; j < CPL; ++j) w[u][j] = g[at + uint32_t((u * CPL + j) * NW * 64)];
 }
 
 // A butterfly mesh stack of compile-time depth D (reference.rs:422-453): all
@@ -1313,96 +1316,45 @@ struct DecodeCfg {
     static constexpr int U = VEC >= 32 ? 1 : (VEC >= 16 ? 2 : (VEC >= 8 ? 4 : 8));  // keys per group per step
 };
 
-__device__ __forceinline__ float load_coherent(const float *p) {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-__device__ __forceinline__ void store_coherent(float *p, float v) {
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Online-softmax attention (reference.rs:510-554) of one query head over keys
-// [start, end) of one (sequence, head) cache slab kb/vb (position-major rows of
-// HDP floats); the block's partial state (acc[HDP], m, l) goes to out[0..HDP+1].
-// Each group of LPK lanes owns one key at a time, so every K/V row is one
-// coalesced VEC-wide load per lane, and U keys' loads are issued before any is
-// consumed.  Scores live in the log2 domain; q stays unscaled (the score is
-// scaled instead) so its load does not hold back the first K/V loads.  An
-// empty share writes the neutral partial (m = -inf, l = 0).  COHERENT: q is
-// read and out written with agent-scope accesses (for the persistent kernel,
-// where both cross workgroups inside one launch).
-template <int HDP, bool COHERENT, int TH = 0, bool PIPE = false>
-__device__ void attn_share(const float *__restrict__ qh, int hd, const float *__restrict__ kslab,
-                           const float *__restrict__ vslab, int start, int end, float scale_log2,
-                           float *__restrict__ out) {
+// One round of K/V rows of an attention share: each group of LPK lanes owns
+// one key at a time, so every K/V row is one coalesced VEC-wide load per lane,
+// and U keys per group load at once.  Rows past `end` are clamped to end - 1
+// (in bounds and branch-free) and masked out of the softmax.  UK > 0
+// overrides the keys per group.
+template <int HDP, int TH, int UK = 0>
+struct AttnRound {
     using C = DecodeCfg<HDP, TH>;
-    // PIPE holds two rounds of keys, so each round takes half as many.
-    constexpr int VEC = C::VEC, LPK = C::LPK, G = C::G, U = PIPE && C::U > 1 ? C::U / 2 : C::U;
-    __shared__ float sm[G], sl[G];
-    __shared__ __align__(16) float sacc[G * HDP];
-    if (start >= end) {
-        for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
-            if (COHERENT) store_coherent(out + d, 0.0f);
-            else out[d] = 0.0f;
-        }
-        if (threadIdx.x == 0) {
-            if (COHERENT) {
-                store_coherent(out + HDP, -INFINITY);
-                store_coherent(out + HDP + 1, 0.0f);
-            } else {
-                out[HDP] = -INFINITY;
-                out[HDP + 1] = 0.0f;
-            }
-        }
-        return;
-    }
-    const int g = threadIdx.x / LPK, li = threadIdx.x % LPK, d0 = li * VEC;
-    float qr[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-        const int d = min(d0 + e, hd - 1);
-        qr[e] = COHERENT ? load_coherent(qh + d) : qh[d];
-    }
-#pragma unroll
-    for (int e = 0; e < VEC; ++e)
-        if (d0 + e >= hd) qr[e] = 0.0f;
-    const float *kb = kslab + d0;
-    const float *vb = vslab + d0;
-    float m = -INFINITY, l = 0.0f, acc[VEC];
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) acc[e] = 0.0f;
-    // Clamped rows keep every load in bounds and branch-free; keys past `end`
-    // are masked out of the softmax below.
-    auto load_keys = [&](int j0, float (&kk)[U][VEC], float (&vv)[U][VEC]) {
+    static constexpr int VEC = C::VEC, LPK = C::LPK, G = C::G, U = UK > 0 ? UK : C::U;
+    float k[U][VEC], v[U][VEC];
+    __device__ __forceinline__ void load(const float *__restrict__ kslab, const float *__restrict__ vslab, int j0,
+                                         int end) {
+        const int g = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             const int j = min(j0 + u * G + g, end - 1);
-            load_vec<VEC>(kb + size_t(j) * HDP, kk[u]);
-            load_vec<VEC>(vb + size_t(j) * HDP, vv[u]);
+            load_vec<VEC>(kslab + size_t(j) * HDP + d0, k[u]);
+            load_vec<VEC>(vslab + size_t(j) * HDP + d0, v[u]);
         }
-    };
-    // PIPE: the next round's keys load while this round's are consumed.
-    float kn[PIPE ? U : 1][VEC], vn[PIPE ? U : 1][VEC];
-    if constexpr (PIPE) load_keys(start, kn, vn);
-    for (int j0 = start; j0 < end; j0 += G * U) {
-        float kk[U][VEC], vv[U][VEC];
-        if constexpr (PIPE) {
-#pragma unroll
-            for (int u = 0; u < U; ++u)
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    kk[u][e] = kn[u][e];
-                    vv[u][e] = vn[u][e];
-                }
-            if (j0 + G * U < end) load_keys(j0 + G * U, kn, vn);
-        } else {
-            load_keys(j0, kk, vv);
-        }
+    }
+};
+
+// Online-softmax state (reference.rs:510-554) of one key group: scores live in
+// the log2 domain, and q stays unscaled (each score is scaled instead) so its
+// load does not hold back the first K/V loads.
+template <int HDP, int TH, int UK = 0>
+struct AttnState {
+    using R = AttnRound<HDP, TH, UK>;
+    static constexpr int VEC = R::VEC, LPK = R::LPK, G = R::G, U = R::U;
+    float m = -INFINITY, l = 0.0f, acc[VEC] = {};
+    // Folds in the round loaded at j0 (keys at or past `end` are masked).
+    __device__ __forceinline__ void add(const float (&qr)[VEC], const R &cur, int j0, int end, float scale_log2) {
+        const int g = threadIdx.x / LPK;
         float sc[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) {
             float p = 0.0f;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) p = fmaf(qr[e], kk[u][e], p);
+            for (int e = 0; e < VEC; ++e) p = fmaf(qr[e], cur.k[u][e], p);
             p = group_sum<LPK>(p);
             sc[u] = (j0 + u * G + g < end) ? p * scale_log2 : -INFINITY;
         }
@@ -1423,38 +1375,85 @@ __device__ void attn_share(const float *__restrict__ qh, int hd, const float *__
             for (int e = 0; e < VEC; ++e) {
                 float a = acc[e] * alpha;
 #pragma unroll
-                for (int u = 0; u < U; ++u) a = fmaf(pu[u], vv[u][e], a);
+                for (int u = 0; u < U; ++u) a = fmaf(pu[u], cur.v[u][e], a);
                 acc[e] = a;
             }
             m = mn;
         }
     }
+    // Folds in one key whose (log2-domain) score is sc and value row v.
+    __device__ __forceinline__ void add_one(float sc, const float (&v)[VEC]) {
+        const float mn = fmaxf(m, sc);
+        const float alpha = exp2f(m - mn), p = exp2f(sc - mn);
+        l = l * alpha + p;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) sacc[g * HDP + d0 + e] = acc[e];
-    if (li == 0) {
-        sm[g] = m;
-        sl[g] = l;
+        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(p, v[e], acc[e] * alpha);
+        m = mn;
     }
-    __syncthreads();
-    float M = -INFINITY;
-    for (int k = 0; k < G; ++k) M = fmaxf(M, sm[k]);
-    for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
-        float a = 0.0f;
-        for (int k = 0; k < G; ++k) a += exp2f(sm[k] - M) * sacc[k * HDP + d];
-        if (COHERENT) store_coherent(out + d, a);
-        else out[d] = a;
-    }
-    if (threadIdx.x == 0) {
+    // Merges the G groups' states of the block: emit(d, a, M, L) for each
+    // d < HDP with a = sum of the rescaled accumulators, M the block maximum
+    // and L the rescaled denominator.
+    template <class Emit>
+    __device__ __forceinline__ void combine(Emit emit) const {
+        __shared__ float sm[G], sl[G];
+        __shared__ __align__(16) float sacc[G * HDP];
+        const int g = threadIdx.x / LPK, li = threadIdx.x % LPK;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sacc[g * HDP + li * VEC + e] = acc[e];
+        if (li == 0) {
+            sm[g] = m;
+            sl[g] = l;
+        }
+        __syncthreads();
+        float M = -INFINITY;
+        for (int k = 0; k < G; ++k) M = fmaxf(M, sm[k]);
         float L = 0.0f;
         for (int k = 0; k < G; ++k) L += exp2f(sm[k] - M) * sl[k];
-        if (COHERENT) {
-            store_coherent(out + HDP, M);
-            store_coherent(out + HDP + 1, L);
-        } else {
+        for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
+            float a = 0.0f;
+            for (int k = 0; k < G; ++k) a += exp2f(sm[k] - M) * sacc[k * HDP + d];
+            emit(d, a, M, L);
+        }
+        __syncthreads();
+    }
+};
+
+// Online-softmax attention of one query head over keys [start, end) of one
+// (sequence, head) cache slab kslab/vslab (position-major rows of HDP floats);
+// the block's partial state (acc[HDP], m, l) goes to out[0..HDP+1].  An empty
+// share writes the neutral partial (m = -inf, l = 0).
+template <int HDP>
+__device__ __forceinline__ void attn_share(const float *__restrict__ qh, int hd, const float *__restrict__ kslab,
+                                           const float *__restrict__ vslab, int start, int end, float scale_log2,
+                                           float *__restrict__ out) {
+    using S = AttnState<HDP, 0>;
+    using R = typename S::R;
+    constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U;
+    if (start >= end) {
+        for (int d = threadIdx.x; d < HDP; d += blockDim.x) out[d] = 0.0f;
+        if (threadIdx.x == 0) {
+            out[HDP] = -INFINITY;
+            out[HDP + 1] = 0.0f;
+        }
+        return;
+    }
+    const int d0 = (threadIdx.x % LPK) * VEC;
+    float qr[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) qr[e] = d0 + e < hd ? qh[d0 + e] : 0.0f;
+    S st;
+    for (int j0 = start; j0 < end; j0 += G * U) {
+        R cur;
+        cur.load(kslab, vslab, j0, end);
+        st.add(qr, cur, j0, end, scale_log2);
+    }
+    st.combine([&](int d, float a, float M, float L) {
+        out[d] = a;
+        if (d == 0) {
             out[HDP] = M;
             out[HDP + 1] = L;
         }
-    }
+    });
 }
 
 // Split-KV decode attention for one query row per sequence.  Block
@@ -1470,8 +1469,8 @@ attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *_
     const int start = split * chunk;
     const int end = min(start + chunk, keys);
     const size_t slab = size_t(b * s.H + h) * kv.cap * HDP;
-    attn_share<HDP, false>(q + size_t(b) * s.W + h * s.hd, s.hd, kv.k + slab, kv.v + slab, start, end, scale_log2,
-                           part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2));
+    attn_share<HDP>(q + size_t(b) * s.W + h * s.hd, s.hd, kv.k + slab, kv.v + slab, start, end, scale_log2,
+                    part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2));
 }
 
 template <int HDP>
@@ -1919,64 +1918,75 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 // workgroups that stay resident for the whole launch:
 //   mesh teams   three per sequence (the row decode kernel's teams): the
 //                residual row lives in their registers across layers; each
-//                team repeats the post-attention meshes of block l-1, then runs
-//                its Q, K or V mesh of block l.  After the last block they take
-//                the logits, and all three sample the same next token;
-//   attention    one per (sequence, head): the head's whole key range each
-//                layer (attn_share).  After the last block's attention the
-//                sequence's H attention blocks each repeat its post-attention
-//                half and compute 1/H of the logits.
-// Rows advance independently, so one sequence's meshes overlap another's KV
-// stream.  A hand-off is a flag word per producer: the producer writes its
-// data with agent-scope (coherent) stores, drains them with s_waitcnt, then
-// stores the sequence number of the phase into its flag; the consumer polls
-// the producers' flags (one lane each) and reads the data with agent-scope
-// loads.  No cache-wide release/acquire fence is needed, as no cached copy of
-// the exchanged lines can exist.  The KV rows appended during the launch are
-// read with ordinary loads: their cache lines are never read before they are
-// written (rows are whole 128-byte lines, hdp >= 32, and a launch starts with
-// invalidated caches).  Every wait is bounded: after kWaitTicks of wall clock
-// it raises *abort, and every other wait gives up as soon as it sees the flag,
-// so a broken hand-off ends the launch with an error instead of a hang.
+//                team repeats the post-attention meshes of block l-1, then
+//                runs its Q, K or V mesh of block l;
+//   attention    one per (sequence, head): appends the head's new K/V row to
+//                the cache and attends over the head's keys, each layer.
+// After the last block's attention all 3 + H workgroups of a sequence repeat
+// its post-attention half and each computes 1/(3 + H) of the logits; the
+// three teams then draw the same next token from the same logits and state.
+// Sequences advance independently, so one sequence's meshes overlap another's
+// KV stream.
+//
+// Hand-offs are tagged words: every exchanged float travels in a 64-bit word
+// whose high half holds the sequence number of the phase that wrote it,
+// stored and loaded with single-copy-atomic agent-scope accesses.  A consumer
+// polls exactly the words it needs until their tags match, so data and
+// readiness arrive together; no flag, fence or store drain sits on the
+// chain.  The exchange buffers are zeroed before a launch (tag 0 is never
+// waited for), and a word is rewritten only after every reader of its
+// previous value has read it (each rewrite depends, through the chain, on
+// those reads).  The cache rows of a (sequence, head) are written and later
+// read only by that pair's attention workgroup, so its own barriers order
+// them.  Every poll is bounded: after kWaitTicks of wall clock it raises
+// *abort, a poll that sees *abort gives up at once, and the launch then runs
+// to its end on whatever it read (trip counts are fixed and tokens stay in
+// range), so a broken hand-off ends the launch with an error, not a hang.
 
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
 constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
+constexpr int kPersistKeys = 4;            // keys per lane group in one round of attention loads
 
-__device__ __forceinline__ int load_flag(const int *p) {
+__device__ __forceinline__ void put_word(uint64_t *p, float v, int tag) {
+    __hip_atomic_store(p, (uint64_t(uint32_t(tag)) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
+                       __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ uint64_t get_word(const uint64_t *p) {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Waits (wave 0 polls, one lane per flag; the block meets at a barrier) until
-// all n <= 64 flags are >= target.  Returns false when the launch was aborted.
-__device__ bool wait_flags(const int *flags, int n, int target, int *abort) {
-    __shared__ int ok;
-    if (threadIdx.x < 64) {
-        const int lane = threadIdx.x;
-        int good = 1;
+// out[i] = the float of the word at addr(i), i < N, once every such word of
+// the wave carries `tag`.
+template <int N, class Addr>
+__device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], int *abort) {
+    const uint32_t want = uint32_t(tag);
+    uint64_t w[N];
+#pragma unroll
+    for (int i = 0; i < N; ++i) w[i] = get_word(addr(i));
+    auto ready = [&] {
+        bool r = true;
+#pragma unroll
+        for (int i = 0; i < N; ++i) r = r && uint32_t(w[i] >> 32) == want;
+        return r;
+    };
+    if (!__all(ready())) {
         const uint64_t t0 = wall_clock64();
-        while (!__all(lane >= n || load_flag(flags + lane) >= target)) {
-            if (load_flag(abort) != 0) {
-                good = 0;
-                break;
-            }
-            if (wall_clock64() - t0 > kWaitTicks) {
-                if (lane == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                good = 0;
-                break;
-            }
+        while (true) {
             __builtin_amdgcn_s_sleep(1);
+#pragma unroll
+            for (int i = 0; i < N; ++i)
+                if (uint32_t(w[i] >> 32) != want) w[i] = get_word(addr(i));
+            if (__all(ready())) break;
+            if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            if (wall_clock64() - t0 > kWaitTicks) {
+                if ((threadIdx.x & 63) == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                break;
+            }
         }
-        if (lane == 0) ok = good;
     }
-    __syncthreads();
-    return ok != 0;
-}
-
-// Publishes the block's coherent stores, then sets its flag to `value`.
-__device__ __forceinline__ void publish(int *flag, int value) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    if (threadIdx.x == 0) __hip_atomic_store(flag, value, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+    for (int i = 0; i < N; ++i) out[i] = __uint_as_float(uint32_t(w[i]));
 }
 
 // Records one trace timestamp (thread 0) when a timeline is requested.
@@ -1985,31 +1995,42 @@ __device__ __forceinline__ void trace_mark(const PersistArgs &a, int step, int l
         a.trace[((size_t(blockIdx.x) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = wall_clock64();
 }
 
-// Flag words: per sequence 3 team flags (q/k/v of a layer published), H
-// attention flags (a layer's attention state published) and H head flags
-// (a step's logit slice published).
-struct PersistFlags {
-    int *team, *attn, *head;
-    __device__ PersistFlags(const PersistArgs &a, int b)
-        : team(a.sync + size_t(b) * 3), attn(a.sync + size_t(a.batch) * 3 + size_t(b) * a.s.H),
-          head(a.sync + size_t(a.batch) * (3 + a.s.H) + size_t(b) * a.s.H) {}
+// Row-order index of channel c (the layout RowCtx::ridx enumerates).
+template <int NW>
+__device__ __forceinline__ int row_of(int c) {
+    return ((c / (64 * NW)) * NW + c % NW) * 64 + (c / NW) % 64;
+}
+
+// One sequence's exchange words (row order unless noted).  Layer phase
+// g = step * layers + l: q/k/v and the attention output of phase g carry tag
+// g + 1; the residual row entering the last block and the logits of a step
+// carry tag step + 1.
+struct PersistXch {
+    uint64_t *base;
+    int W;
+    __device__ PersistXch(const PersistArgs &a, int b) : base(a.xch + size_t(b) * a.xstride), W(a.s.W) {}
+    // q (t = 0), k (1) or v (2) of phase g, double-buffered by phase parity
+    __device__ uint64_t *qkv(int g, int t) const { return base + size_t((g & 1) * 3 + t) * W; }
+    __device__ uint64_t *y() const { return base + size_t(6) * W; }     // attention output
+    __device__ uint64_t *xrow() const { return base + size_t(7) * W; }  // residual row
+    __device__ uint64_t *logits() const { return base + size_t(8) * W; }  // token order
 };
 
-// Logits of tokens [t0, t1) for the row-order normalised row xn (in LDS):
-// wave w takes tokens t0 + w, t0 + w + NW, ...; each lane a contiguous W/64
-// channels of the row-order token vectors E.  Eight tokens' loads are in
-// flight before their dot products and wave sums.
+// Logits of tokens [t0, t1) for the row-order normalised row xn (in LDS), as
+// words tagged `tag`: wave w takes tokens t0 + w, t0 + w + NW, ...; each lane
+// a contiguous W/64 channels of the row-order token vectors E.  T tokens'
+// loads per wave are in flight before their dot products and wave sums.
 template <int NW, int W>
-__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, float *out, int t0,
-                                                      int t1, int lane, int wave) {
-    constexpr int CW = W / 64, T8 = 8;
+__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, uint64_t *out,
+                                                      int t0, int t1, int tag, int lane, int wave) {
+    constexpr int CW = W / 64, T = 96 / CW < 4 ? 4 : (96 / CW > 16 ? 16 : 96 / CW);
     float xr[CW];
 #pragma unroll
     for (int k = 0; k < CW; ++k) xr[k] = xn[lane * CW + k];
-    for (int base = t0 + wave; base < t1; base += T8 * NW) {
-        float e[T8][CW];
+    for (int base = t0 + wave; base < t1; base += T * NW) {
+        float e[T][CW];
 #pragma unroll
-        for (int u = 0; u < T8; ++u) {
+        for (int u = 0; u < T; ++u) {
             const int t = min(base + u * NW, t1 - 1);
             const float *row = E + size_t(t) * W + lane * CW;
             if constexpr (CW % 4 == 0) {
@@ -2027,21 +2048,30 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
             }
         }
 #pragma unroll
-        for (int u = 0; u < T8; ++u) {
+        for (int u = 0; u < T; ++u) {
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < CW; ++k) acc = fmaf(xr[k], e[u][k], acc);
             acc = wave_sum(acc);
             const int t = base + u * NW;
-            if (lane == 0 && t < t1) store_coherent(out + t, acc);
+            if (lane == 0 && t < t1) put_word(out + t, acc, tag);
         }
     }
+}
+
+// Hides a uniform pointer's value from the optimiser, so the per-load
+// addresses derived from it are formed next to their loads instead of being
+// hoisted out of the step loop, where they would hold dozens of registers.
+template <class T>
+__device__ __forceinline__ T *opaque(T *p) {
+    asm volatile("" : "+s"(p));
+    return p;
 }
 
 template <int NW, int CPL, int GL, int D>
 __device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const float *g, bool fixed, int lane,
                                                    int wave) {
-    if (fixed) row_load_weights<NW, CPL, D>(w, g, lane, wave);
+    if (fixed) row_load_weights<NW, CPL, D>(w, opaque(g), lane, wave);
 }
 
 struct PersistLds {
@@ -2051,6 +2081,41 @@ struct PersistLds {
     uint64_t *rng;
 };
 
+// Post-attention half of the last block on the residual row x, then logit
+// slice `slice` of the 3 + H slices of the vocabulary.
+template <int NW, int CPL, int GL, int DEPTH>
+__device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowCtx<NW, CPL, GL> &c, float (&x)[CPL],
+                                                      const PersistXch &xc, int step, int slice,
+                                                      const PersistLds &m) {
+    constexpr int W = RowCtx<NW, CPL, GL>::W;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : 1;
+    const Shape &s = a.s;
+    const int L = a.layers, g = step * L + L - 1;
+    const size_t gA = 2 * size_t(W) * s.A;
+    const float *wlast = a.w + a.block0 + size_t(L - 1) * (4 * gA + 2 * size_t(W) * s.F);
+    float2 wp[D][CPL], wf[D][CPL];
+    load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
+    load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
+    float yv[2 * CPL];
+    const uint64_t *yw = xc.y(), *vw = xc.qkv(g, 2);
+    take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
+    float y[CPL], v[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        y[j] = yv[j];
+        v[j] = yv[CPL + j];
+    }
+    row_post(c, x, y, v, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
+    const float inv = row_inv_rms(c, x, 3);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
+    __syncthreads();
+    const int nb = 3 + s.H, V = s.V;
+    persistent_head_slice<NW, W>(m.xn, a.E, xc.logits(), slice * V / nb, (slice + 1) * V / nb, step + 1, c.lane,
+                                 c.wave);
+}
+
 // Mesh team `team` of sequence b.
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
 __device__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m) {
@@ -2058,10 +2123,11 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
     constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
     constexpr int D = FIXED ? DEPTH : 1;
+    constexpr int NL = kPersistVocab / (64 * NW);  // logit words per thread
     const Shape &s = a.s;
     Ctx c(m.xch, m.red);
-    const int dim = c.dim(), H = s.H, L = a.layers, V = s.V;
-    const PersistFlags f(a, b);
+    const int dim = c.dim(), L = a.layers, V = s.V;
+    const PersistXch xc(a, b);
     int len = a.len[b];
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
     if (threadIdx.x == 0) *m.rng = a.rng[b];
@@ -2069,14 +2135,14 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
     const size_t blk = 4 * gA + 2 * size_t(W) * s.F;  // floats of one block: q, k, v, proj, ffn
     auto block = [&](int l) { return a.w + a.block0 + size_t(l) * blk; };
     float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
-    bool alive = true;
-    for (int step = 0; step < a.steps && alive; ++step) {
+    for (int step = 0; step < a.steps; ++step) {
         const int pos = len - 1;
         float x[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
         trace_mark(a, step, 0, 0);
         for (int l = 0; l < L; ++l) {
+            const int g = step * L + l;
             const float *wb = block(l);
             load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
             if (l > 0) {
@@ -2084,61 +2150,52 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
                 const float *wq = block(l - 1);
                 load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
                 load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
-                if (!wait_flags(f.attn, H, step * L + l, a.abort)) {
-                    alive = false;
-                    break;
-                }
+                float yv[2 * CPL];
+                const uint64_t *yw = xc.y(), *vw = xc.qkv(g - 1, 2);
+                take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g, yv, a.abort);
                 trace_mark(a, step, l, 0);
                 float y[CPL], v[CPL];
-                const float *dvb = a.dv + (size_t((l - 1) & 1) * a.batch + b) * W;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
-                    const float *pp = a.part + size_t(b * H + c.head_of(j)) * (HDP + 2);
-                    v[j] = load_coherent(dvb + c.ridx(j));
-                    y[j] = load_coherent(pp + dim) / load_coherent(pp + HDP + 1);
+                    y[j] = yv[j];
+                    v[j] = yv[CPL + j];
                 }
                 row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
             }
             if (l + 1 == L && team == 0) {
                 // The attention blocks finish the last block from this row.
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) store_coherent(a.xrow + size_t(b) * W + c.ridx(j), x[j]);
+                for (int j = 0; j < CPL; ++j) put_word(xc.xrow() + c.ridx(j), x[j], step + 1);
             }
             const float inv = row_inv_rms(c, x, 3);
             float n[CPL];
 #pragma unroll
             for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
             row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
-            float *kl = a.kc + size_t(l) * a.layer_elems, *vl = a.vc + size_t(l) * a.layer_elems;
-            if (team == 2) {
-                float *dvb = a.dv + (size_t(l & 1) * a.batch + b) * W;
+            if (team < 2) row_qk_rope(c, n, rope_pair(a.rope, pos, dim, s.half), s);
+            uint64_t *out = xc.qkv(g, team);
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) {
-                    store_coherent(vl + (size_t(b * H + c.head_of(j)) * a.cap + pos) * HDP + dim, n[j]);
-                    store_coherent(dvb + c.ridx(j), n[j]);
-                }
-            } else {
-                row_qk_rope(c, n, rope_pair(a.rope, pos, dim, s.half), s);
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) {
-                    if (team == 0)
-                        store_coherent(a.q + size_t(b) * W + c.chan(j), n[j]);
-                    else
-                        store_coherent(kl + (size_t(b * H + c.head_of(j)) * a.cap + pos) * HDP + dim, n[j]);
-                }
-            }
-            publish(f.team + team, step * L + l + 1);
+            for (int j = 0; j < CPL; ++j) put_word(out + c.ridx(j), n[j], g + 1);
             trace_mark(a, step, l, 1);
         }
-        if (!alive) break;
-        // The logits, then every team draws the same token from the same
-        // logits and state.
-        if (!wait_flags(f.head, H, step + 1, a.abort)) break;
+        persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, team, m);
+        // Every team draws the same token from the same logits and state.
+        float lg[NL];
+        take_words<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
+                       a.abort);
         trace_mark(a, step, L, 0);
-        for (int t = threadIdx.x; t < V; t += blockDim.x) m.row[t] = load_coherent(a.logits + size_t(b) * V + t);
+#pragma unroll
+        for (int i = 0; i < NL; ++i) {
+            const int t = int(threadIdx.x) + i * 64 * NW;
+            if (t < V) m.row[t] = lg[i];
+        }
         __syncthreads();
         tok = uint32_t(choose_token(m.row, V, a.temperature, m.rng, a.flags, SampleLds{m.redf, m.redi, m.redd}));
-        if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
+        if (team == 0) {
+            if (threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
+            if (step + 1 == a.steps)
+                for (int t = threadIdx.x; t < V; t += blockDim.x) a.logits[size_t(b) * V + t] = m.row[t];
+        }
         ++len;
         trace_mark(a, step, L, 1);
     }
@@ -2148,55 +2205,74 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
     }
 }
 
-// Attention block of (sequence b, head h); after the last block's attention
-// it finishes that block from the published residual row and computes the
-// logits of tokens [h*V/H, (h+1)*V/H).
+// Attention block of (sequence b, head h).  Its query, key and value arrive
+// as tagged words; the key/value rows go to the cache for later steps and
+// enter this step's attention from registers, so the cached rows read each
+// layer [0, pos) were all written before the launch or by this block, and the
+// first round of them loads while the layer's meshes still run.
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
 __device__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
     using Ctx = RowCtx<NW, CPL, GL>;
-    constexpr int W = Ctx::W;
-    constexpr bool FIXED = DEPTH > 0;
-    constexpr int D = FIXED ? DEPTH : 1;
+    using S = AttnState<HDP, 64 * NW, kPersistKeys>;
+    using R = typename S::R;
+    constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U;
     const Shape &s = a.s;
-    const int len0 = a.len[b], L = a.layers, H = s.H, V = s.V;
-    const PersistFlags f(a, b);
-    const size_t slab = size_t(b * H + h) * a.cap * HDP;
-    const size_t gA = 2 * size_t(W) * s.A;
-    const float *wlast = a.w + a.block0 + size_t(L - 1) * (4 * gA + 2 * size_t(W) * s.F);
+    const int len0 = a.len[b], L = a.layers;
+    const PersistXch xc(a, b);
+    const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
+    const int grp = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
     Ctx c(m.xch, m.red);
-    const int dim = c.dim();
-    float2 wp[D][CPL], wf[D][CPL];
     for (int step = 0; step < a.steps; ++step) {
+        const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
-            if (!wait_flags(f.team, 3, step * L + l + 1, a.abort)) return;
+            const int g = step * L + l;
+            float *kl = a.kc + size_t(l) * a.layer_elems + slab, *vl = a.vc + size_t(l) * a.layer_elems + slab;
+            R cur;
+            if (pos > 0) cur.load(kl, vl, 0, pos);
+            float qkv[3 * VEC];
+            const uint64_t *qw = xc.qkv(g, 0), *kw = xc.qkv(g, 1), *vw = xc.qkv(g, 2);
+            take_words<3 * VEC>(
+                [&](int i) {
+                    const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
+                    return base + row_of<NW>(h * HDP + d0 + i % VEC);
+                },
+                g + 1, qkv, a.abort);
             trace_mark(a, step, l, 0);
-            attn_share<HDP, true, 64 * NW, true>(a.q + size_t(b) * s.W + h * s.hd, s.hd,
-                                                 a.kc + size_t(l) * a.layer_elems + slab,
-                                                 a.vc + size_t(l) * a.layer_elems + slab, 0, len0 + step,
-                                                 a.scale_log2, a.part + size_t(b * H + h) * (HDP + 2));
-            publish(f.attn + h, step * L + l + 1);
+            float qr[VEC], kn[VEC], vn[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                qr[e] = qkv[e];
+                kn[e] = qkv[VEC + e];
+                vn[e] = qkv[2 * VEC + e];
+            }
+            if (grp == 0) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    kl[size_t(pos) * HDP + d0 + e] = kn[e];
+                    vl[size_t(pos) * HDP + d0 + e] = vn[e];
+                }
+            }
+            S st;
+            for (int j0 = 0; j0 < pos; j0 += G * U) {
+                const bool more = j0 + G * U < pos;
+                R nxt;
+                if (more) nxt.load(kl, vl, j0 + G * U, pos);
+                st.add(qr, cur, j0, pos, a.scale_log2);
+                if (more) cur = nxt;
+            }
+            float sc = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) sc = fmaf(qr[e], kn[e], sc);
+            sc = group_sum<LPK>(sc) * a.scale_log2;
+            if (grp == 0) st.add_one(sc, vn);
+            uint64_t *yw = xc.y();
+            st.combine([&](int d, float acc, float, float den) { put_word(yw + row_of<NW>(h * HDP + d), acc / den, g + 1); });
             trace_mark(a, step, l, 1);
         }
-        // Post-attention half of the last block, then this block's logits.
-        load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
-        load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
-        if (!wait_flags(f.attn, H, step * L + L, a.abort)) return;
-        float x[CPL], y[CPL], v[CPL];
-        const float *dvb = a.dv + (size_t((L - 1) & 1) * a.batch + b) * W;
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            const float *pp = a.part + size_t(b * H + c.head_of(j)) * (HDP + 2);
-            x[j] = load_coherent(a.xrow + size_t(b) * W + c.ridx(j));
-            v[j] = load_coherent(dvb + c.ridx(j));
-            y[j] = load_coherent(pp + dim) / load_coherent(pp + HDP + 1);
-        }
-        row_post(c, x, y, v, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
-        const float inv = row_inv_rms(c, x, 3);
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
-        __syncthreads();
-        persistent_head_slice<NW, W>(m.xn, a.E, a.logits + size_t(b) * V, h * V / H, (h + 1) * V / H, c.lane, c.wave);
-        publish(f.head + h, step + 1);
+        // The last block from the published residual row, then this block's logits.
+        float x[CPL];
+        take_words<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
+        persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
         trace_mark(a, step, L, 1);
     }
 }
@@ -2520,6 +2596,8 @@ const void *persistent_kernel(const Shape &s) {
 }
 
 int persistent_blocks(const Shape &s, int batch) { return 3 * batch + batch * s.H; }
+
+size_t persistent_exchange_words(const Shape &s) { return (size_t(8) * s.W + s.V + 31) / 32 * 32; }
 
 bool persistent_fits(const Shape &s, int batch, int device) {
     const void *f = persistent_kernel(s);

@@ -120,11 +120,7 @@ struct PersistArgs {
     float *kc, *vc;       // KV cache, layer-major
     size_t layer_elems;   // floats of one layer of the cache
     int cap;              // positions per (sequence, head) slab
-    float *q;             // [batch][W] queries
-    float *dv;            // [2][batch][W] value rows in row order, by layer parity
-    float *xrow;          // [batch][W] residual rows (row order) entering the last block
-    float *part;          // [batch][H][hdp + 2] attention states
-    float *logits;        // [batch][V]
+    float *logits;        // [batch][V] logits of the launch's last step
     const float2 *rope;
     uint32_t *tokens;
     int tok_stride;
@@ -132,7 +128,8 @@ struct PersistArgs {
     uint64_t *rng;
     float temperature;
     int *flags;           // bit 0: non-finite logits
-    int *sync;            // [batch][3 + 2*H] hand-off flags, zero at launch
+    uint64_t *xch;        // [batch][xstride] tagged exchange words, zero at launch
+    size_t xstride;       // persistent_exchange_words(shape)
     int *abort;           // zero at launch; set when a wait times out
     float scale_log2;     // set by persistent_decode
     // Optional timeline (nullptr: none): for block k, step t and phase l,
@@ -144,6 +141,9 @@ struct PersistArgs {
     uint64_t *trace;
 };
 bool persistent_fits(const Shape &s, int batch, int device);
+// Exchange words of one sequence: q/k/v of two layer phases, the attention
+// output, the residual row entering the last block and the logits.
+size_t persistent_exchange_words(const Shape &s);
 hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream);
 
 // Split-KV decode attention: one query row per sequence; the len[b] keys are

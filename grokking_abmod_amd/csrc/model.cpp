@@ -84,9 +84,9 @@ struct MeshGpt::Impl {
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
     size_t batch_cap = 0, tcap = 0;
     DevBuf kc, vc, dx, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
-    // Persistent decode kernel state: value rows by layer parity, hand-off
-    // counters and the abort flag.
-    DevBuf pdv, pxrow, psync, pabort;
+    // Persistent decode kernel state: tagged exchange words of every sequence
+    // and the abort flag.
+    DevBuf pxch, pabort;
     size_t batch = 0, length = 0, cached = kNoCache;
     float temperature = 0.0f;
 
@@ -295,9 +295,7 @@ struct MeshGpt::Impl {
             dlogits.ensure(batch_cap * cfg.vocab_size * 4);
             dflags.ensure(4);
             if (persistent_ok) {
-                pdv.ensure(2 * batch_cap * cfg.width * 4);
-                pxrow.ensure(batch_cap * cfg.width * 4);
-                psync.ensure(persist_flag_words(batch_cap) * 4);
+                pxch.ensure(batch_cap * kern::persistent_exchange_words(shape) * 8);
                 pabort.ensure(4);
             }
         }
@@ -543,8 +541,6 @@ struct MeshGpt::Impl {
         return batch > 0 && cached == length - 1 && length - 1 + steps <= cfg.context && length + steps <= tcap;
     }
 
-    size_t persist_flag_words(size_t b) const { return b * (3 + 2 * cfg.heads); }
-
     bool persistent_usable() const {
         return persistent_ok && row_decode && kern::persistent_fits(shape, int(batch), device);
     }
@@ -552,7 +548,8 @@ struct MeshGpt::Impl {
     // `steps` decode steps in one launch of the persistent kernel (the caller
     // checked decodable(steps) and persistent_usable()).
     void persistent(size_t steps, uint64_t *trace = nullptr) {
-        check(hipMemsetAsync(psync.p, 0, persist_flag_words(batch) * 4, stream), "clear flags");
+        const size_t xstride = kern::persistent_exchange_words(shape);
+        check(hipMemsetAsync(pxch.p, 0, batch * xstride * 8, stream), "clear exchange words");
         check(hipMemsetAsync(pabort.p, 0, 4, stream), "clear abort");
         kern::PersistArgs a{};
         a.s = shape;
@@ -566,10 +563,6 @@ struct MeshGpt::Impl {
         a.vc = vc.as<float>();
         a.layer_elems = layer_cache_elems();
         a.cap = int(cfg.context);
-        a.q = dq.as<float>();
-        a.dv = pdv.as<float>();
-        a.xrow = pxrow.as<float>();
-        a.part = part.as<float>();
         a.logits = dlogits.as<float>();
         a.rope = rope.as<float2>();
         a.tokens = dtokens.as<uint32_t>();
@@ -578,7 +571,8 @@ struct MeshGpt::Impl {
         a.rng = drng.as<uint64_t>();
         a.temperature = temperature;
         a.flags = dflags.as<int>();
-        a.sync = psync.as<int>();
+        a.xch = pxch.as<uint64_t>();
+        a.xstride = xstride;
         a.abort = pabort.as<int>();
         a.trace = trace;
         check(kern::persistent_decode(a, stream), "persistent decode launch");
