@@ -1096,8 +1096,8 @@ struct RowCtx {
     int lane, wave, parity;
     float *xch;  // 2*W floats: mesh exchange buffers
     float *red;  // reduction slots of SLOT floats each
-    __device__ RowCtx(float *x, float *r)
-        : lane(int(threadIdx.x) & 63), wave(int(threadIdx.x) >> 6), parity(0), xch(x), red(r) {}
+    __device__ RowCtx(float *x, float *r, int tid = int(threadIdx.x))
+        : lane(tid & 63), wave(tid >> 6), parity(0), xch(x), red(r) {}
     // Head and in-head dim of register j: a head is GL lanes of every wave.
     __device__ int head_of(int j) const { return lane / GL + G * j; }
     __device__ int dim() const { return NW * (lane % GL) + wave; }
@@ -1328,12 +1328,14 @@ struct AttnRound {
     float k[U][VEC], v[U][VEC];
     __device__ __forceinline__ void load(const float *__restrict__ kslab, const float *__restrict__ vslab, int j0,
                                          int end) {
-        const int g = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
+        // 32-bit element offsets from the uniform slab bases (a slab is far
+        // below 2^32 elements), so each load needs one address register.
+        const uint32_t g = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int j = min(j0 + u * G + g, end - 1);
-            load_vec<VEC>(kslab + size_t(j) * HDP + d0, k[u]);
-            load_vec<VEC>(vslab + size_t(j) * HDP + d0, v[u]);
+            const uint32_t at = uint32_t(min(j0 + u * G + int(g), end - 1)) * HDP + d0;
+            load_vec<VEC>(kslab + at, k[u]);
+            load_vec<VEC>(vslab + at, v[u]);
         }
     }
 };
@@ -1945,7 +1947,6 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
 constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
-constexpr int kPersistKeys = 4;            // keys per lane group in one round of attention loads
 
 __device__ __forceinline__ void put_word(uint64_t *p, float v, int tag) {
     __hip_atomic_store(p, (uint64_t(uint32_t(tag)) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
@@ -1989,6 +1990,108 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
     for (int i = 0; i < N; ++i) out[i] = __uint_as_float(uint32_t(w[i]));
 }
 
+// ---- K/V staging through LDS
+//
+// The attention workgroups stream their K/V rows into an LDS ring with
+// direct-to-LDS loads (global_load_lds_dwordx4: each lane's 16 bytes land at
+// a wave-uniform LDS base + 16 * lane), so several rounds are in flight
+// without holding registers.  The loads are issued from inline assembly and
+// waited for with explicit vmcnt counts: issued through the compiler, every
+// LDS read after them would wait for all loads in flight.  Waiting for
+// vmcnt <= n, where n counts only this ring's loads issued after the awaited
+// round, is always sufficient: other memory operations issued meanwhile only
+// make the wait stricter, as loads complete in order.
+
+typedef __attribute__((address_space(3))) float lds_float;
+
+// LDS[l + 16 * lane .. +16) = g[0..4) for every lane; l is wave-uniform.  The
+// LDS reads of earlier rounds are complete first (lgkmcnt), so a slot can be
+// refilled right after it was read; m0 is preserved.
+__device__ __forceinline__ void lds_dma16(const float *g, float *l) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(uint32_t(size_t((lds_float *)l)));
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "global_load_lds_dwordx4 %2, off\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(m), "v"(g)
+        : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Ring of NS rounds of an attention share in LDS: round r (keys from r * G *
+// UL, laid out as AttnRound) fills slot r % NS; each lane's K and V rows of a
+// round are 2 * UL chunks of 16 bytes in its wave's region of the slot.
+template <int HDP, int NW, int UL, int NS>
+struct KvRing {
+    using R = AttnRound<HDP, 64 * NW, UL>;
+    static constexpr int VEC = R::VEC, LPK = R::LPK, G = R::G, CH = 2 * UL;
+    static constexpr int SLOT = CH * NW * 256;  // floats
+    static_assert(VEC == 4, "a lane's part of a row must be one 16-byte load");
+    float *buf;  // NS * SLOT floats
+    __device__ void issue(const float *kl, const float *vl, int r, int end, int tid) const {
+        const int g = tid / LPK, d0 = (tid % LPK) * VEC, wave = tid >> 6;
+        float *slot = buf + (r % NS) * SLOT + wave * 256;
+#pragma unroll
+        for (int u = 0; u < UL; ++u) {
+            const uint32_t at = uint32_t(min(r * G * UL + u * G + g, end - 1)) * HDP + d0;
+            lds_dma16(kl + at, slot + (2 * u) * NW * 256);
+            lds_dma16(vl + at, slot + (2 * u + 1) * NW * 256);
+        }
+    }
+    // Waits until round r has landed, given the rounds issued after it.
+    __device__ void wait(int after) const {
+        static_assert(NS <= 4, "wait counts");
+        switch (after) {
+        case 0: wait_vmem<0>(); break;
+        case 1: wait_vmem<CH>(); break;
+        case 2: wait_vmem<2 * CH>(); break;
+        default: wait_vmem<3 * CH>(); break;
+        }
+    }
+    __device__ void read(int r, R &cur, int tid) const {
+        const float *slot = buf + (r % NS) * SLOT + (tid >> 6) * 256 + (tid & 63) * 4;
+#pragma unroll
+        for (int u = 0; u < UL; ++u) {
+            const float4 k = *reinterpret_cast<const float4 *>(slot + (2 * u) * NW * 256);
+            const float4 v = *reinterpret_cast<const float4 *>(slot + (2 * u + 1) * NW * 256);
+            cur.k[u][0] = k.x;
+            cur.k[u][1] = k.y;
+            cur.k[u][2] = k.z;
+            cur.k[u][3] = k.w;
+            cur.v[u][0] = v.x;
+            cur.v[u][1] = v.y;
+            cur.v[u][2] = v.z;
+            cur.v[u][3] = v.w;
+        }
+    }
+};
+
+// Geometry of the persistent attention ring: keys per lane group in a round
+// (UL) and rounds in flight (NS), chosen to fit beside the kernel's other LDS
+// arrays while the registers' limit of two waves per SIMD stays the only
+// limit on residency (LDS budget 160 KiB * NW / 8 per workgroup).  Rounds of
+// 4 keys per group with two slots are preferred; narrower rounds with more
+// slots when those do not fit.
+template <int NW, int CPL, int GL, int HDP>
+struct PersistRing {
+    static constexpr int W = 64 * NW * CPL, gc = 64 / GL, ga = 64 * NW / (HDP / 4);
+    static constexpr int budget = 160 * 1024 * NW / 8;
+    static constexpr int other = 4 * (2 * W + 8 * CPL * NW * gc + W + kPersistVocab + 2 * NW + 2 * ga + ga * HDP) +
+                                 8 * (NW + 1) + 8 + 64;
+    static constexpr int fit(int ul) { return (budget - other) / (2 * ul * NW * 1024); }
+    static constexpr int UL = fit(4) >= 2 ? 4 : (fit(2) >= 2 ? 2 : 1);
+    static constexpr int NS = UL == 4 ? 2 : (fit(UL) >= 4 ? 4 : (fit(UL) >= 3 ? 3 : 2));
+    static_assert(fit(UL) >= NS, "the attention ring does not fit in LDS");
+};
+
 // Records one trace timestamp (thread 0) when a timeline is requested.
 __device__ __forceinline__ void trace_mark(const PersistArgs &a, int step, int l, int which) {
     if (a.trace && threadIdx.x == 0)
@@ -2031,8 +2134,8 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
         float e[T][CW];
 #pragma unroll
         for (int u = 0; u < T; ++u) {
-            const int t = min(base + u * NW, t1 - 1);
-            const float *row = E + size_t(t) * W + lane * CW;
+            const uint32_t t = uint32_t(min(base + u * NW, t1 - 1));
+            const float *row = E + (t * W + uint32_t(lane * CW));
             if constexpr (CW % 4 == 0) {
 #pragma unroll
                 for (int k = 0; k < CW; k += 4) {
@@ -2075,7 +2178,7 @@ __device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const fl
 }
 
 struct PersistLds {
-    float *xch, *red, *xn, *row, *redf;
+    float *xch, *red, *xn, *row, *redf, *ring;
     int *redi;
     double *redd;
     uint64_t *rng;
@@ -2213,28 +2316,40 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
 __device__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
     using Ctx = RowCtx<NW, CPL, GL>;
-    using S = AttnState<HDP, 64 * NW, kPersistKeys>;
+    using Ring = PersistRing<NW, CPL, GL, HDP>;
+    using S = AttnState<HDP, 64 * NW, Ring::UL>;
     using R = typename S::R;
-    constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U;
+    constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U, NS = Ring::NS;
+    const KvRing<HDP, NW, U, NS> ring{m.ring};
     const Shape &s = a.s;
     const int len0 = a.len[b], L = a.layers;
     const PersistXch xc(a, b);
     const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
-    const int grp = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
-    Ctx c(m.xch, m.red);
+    static_assert(VEC % NW == 0, "lane dims must cover whole row-order columns");
     for (int step = 0; step < a.steps; ++step) {
         const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
             const int g = step * L + l;
+            // Lane values are formed per layer from a thread index hidden from
+            // the optimiser: hoisted out of the loops they would be spilled, and
+            // a spill reload waits for the K/V loads in flight.
+            int tid = int(threadIdx.x);
+            asm volatile("" : "+v"(tid));
+            const int grp = tid / LPK, d0 = (tid % LPK) * VEC;
+            // Row-order word index of this lane's dims d0 + e: at0 + (e % NW) *
+            // 64 + e / NW, as d0 is a multiple of VEC and VEC one of NW.
+            const uint32_t at0 = uint32_t(row_of<NW>(h * HDP + d0));
             float *kl = a.kc + size_t(l) * a.layer_elems + slab, *vl = a.vc + size_t(l) * a.layer_elems + slab;
-            R cur;
-            if (pos > 0) cur.load(kl, vl, 0, pos);
+            // The first NS rounds load while the layer's meshes still run.
+            const int nr = (pos + G * U - 1) / (G * U);
+            for (int r = 0; r < min(NS, nr); ++r) ring.issue(kl, vl, r, pos, tid);
             float qkv[3 * VEC];
-            const uint64_t *qw = xc.qkv(g, 0), *kw = xc.qkv(g, 1), *vw = xc.qkv(g, 2);
+            const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
+                           *vw = opaque(xc.qkv(g, 2)) + at0;
             take_words<3 * VEC>(
                 [&](int i) {
                     const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
-                    return base + row_of<NW>(h * HDP + d0 + i % VEC);
+                    return base + ((i % VEC) % NW * 64 + (i % VEC) / NW);
                 },
                 g + 1, qkv, a.abort);
             trace_mark(a, step, l, 0);
@@ -2253,12 +2368,12 @@ __device__ void persistent_attention(const PersistArgs &a, int b, int h, const P
                 }
             }
             S st;
-            for (int j0 = 0; j0 < pos; j0 += G * U) {
-                const bool more = j0 + G * U < pos;
-                R nxt;
-                if (more) nxt.load(kl, vl, j0 + G * U, pos);
-                st.add(qr, cur, j0, pos, a.scale_log2);
-                if (more) cur = nxt;
+            for (int r = 0; r < nr; ++r) {
+                ring.wait(min(NS - 1, nr - 1 - r));
+                R cur;
+                ring.read(r, cur, tid);
+                if (r + NS < nr) ring.issue(kl, vl, r + NS, pos, tid);
+                st.add(qr, cur, r * G * U, pos, a.scale_log2);
             }
             float sc = 0.0f;
 #pragma unroll
@@ -2269,7 +2384,13 @@ __device__ void persistent_attention(const PersistArgs &a, int b, int h, const P
             st.combine([&](int d, float acc, float, float den) { put_word(yw + row_of<NW>(h * HDP + d), acc / den, g + 1); });
             trace_mark(a, step, l, 1);
         }
-        // The last block from the published residual row, then this block's logits.
+        // The last block from the published residual row, then this block's
+        // logits.  The thread index is hidden from the optimiser so the lane
+        // arithmetic of these meshes is formed here, not hoisted out of the
+        // step loop to occupy registers through the attention.
+        int tid = int(threadIdx.x);
+        asm volatile("" : "+v"(tid));
+        Ctx c(m.xch, m.red, tid);
         float x[CPL];
         take_words<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
@@ -2291,7 +2412,9 @@ persistent_decode_kernel(PersistArgs a) {
     __shared__ int redi[NW];
     __shared__ double redd[NW + 1];
     __shared__ uint64_t rng;
-    const PersistLds m{xch, red, xn, row, redf, redi, redd, &rng};
+    using Ring = PersistRing<NW, CPL, GL, HDP>;
+    __shared__ __align__(16) float ring[KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS];
+    const PersistLds m{xch, red, xn, row, redf, ring, redi, redd, &rng};
     const int blk = blockIdx.x;
     if (blk < 3 * a.batch) {
         persistent_team<NW, CPL, GL, DEPTH, HDP>(a, blk / 3, blk % 3, m);
