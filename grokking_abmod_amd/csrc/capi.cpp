@@ -248,6 +248,13 @@ int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab,
     });
 }
 
+int mg_expf(int device, const float *x, size_t n, float *out) {
+    return guarded([&] {
+        require((x != nullptr && out != nullptr) || n == 0, "inputs and outputs must not be null");
+        device_expf(device, x, n, out);
+    });
+}
+
 int mg_copy_bandwidth(int device, size_t bytes, int iters, double *gbps) {
     return guarded([&] {
         require(gbps != nullptr && bytes >= 16 && iters >= 1, "bytes >= 16, iters >= 1 and output required");

@@ -65,16 +65,50 @@ __device__ __forceinline__ float wave_max(float v) {
     return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
 
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ int dpp_move_int(int old, int v) {
+    return __builtin_amdgcn_update_dpp(old, v, CTRL, ROW_MASK, 0xf, false);
+}
+
 __device__ __forceinline__ int wave_min_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o, 64));
-    return v;
+    v = min(v, dpp_move_int<0xB1>(v, v));
+    v = min(v, dpp_move_int<0x4E>(v, v));
+    v = min(v, dpp_move_int<0x141>(v, v));
+    v = min(v, dpp_move_int<0x140>(v, v));
+    v = min(v, dpp_move_int<0x142, 0xa>(v, v));
+    v = min(v, dpp_move_int<0x143, 0xc>(v, v));
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 __device__ __forceinline__ int wave_or_int(int v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v |= __shfl_xor(v, o, 64);
-    return v;
+    v |= dpp_move_int<0xB1>(v, v);
+    v |= dpp_move_int<0x4E>(v, v);
+    v |= dpp_move_int<0x141>(v, v);
+    v |= dpp_move_int<0x140>(v, v);
+    v |= dpp_move_int<0x142, 0xa>(v, v);
+    v |= dpp_move_int<0x143, 0xc>(v, v);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+// The lane's value moved by a DPP pattern, 0 where the pattern has no source.
+template <int CTRL, int ROW_MASK = 0xf>
+__device__ __forceinline__ double dpp_move_f64(double v) {
+    const uint64_t b = __builtin_bit_cast(uint64_t, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, int(uint32_t(b)), CTRL, ROW_MASK, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, int(uint32_t(b >> 32)), CTRL, ROW_MASK, 0xf, false);
+    return __builtin_bit_cast(double, (uint64_t(uint32_t(hi)) << 32) | uint32_t(lo));
+}
+
+// Inclusive prefix sum over the wave's lanes: row shifts inside each 16-lane
+// row, then the row broadcasts carry row totals forward.
+__device__ __forceinline__ double wave_inclusive_sum(double x) {
+    x += dpp_move_f64<0x111>(x);       // row_shr:1
+    x += dpp_move_f64<0x112>(x);       // row_shr:2
+    x += dpp_move_f64<0x114>(x);       // row_shr:4
+    x += dpp_move_f64<0x118>(x);       // row_shr:8
+    x += dpp_move_f64<0x142, 0xa>(x);  // row_bcast:15
+    x += dpp_move_f64<0x143, 0xc>(x);  // row_bcast:31
+    return x;
 }
 
 // Sum over aligned groups of N lanes (N a power of two <= 64), left in every
@@ -1651,19 +1685,72 @@ __device__ __forceinline__ uint64_t splitmix_next(uint64_t &state) {
 // value except within about 2^-29 ulp of a rounding midpoint, which is what
 // host libm expf returns (the reference's f32::exp).  The device's f32 expf
 // can differ by an ulp, and a near-tie draw then picks another token.
-__device__ __forceinline__ float expf_rounded(float x) { return float(exp(double(x))); }
+// Table of 2^(i/32) in the form the method below uses: the bits of the
+// correctly rounded double 2^(i/32) minus i << 47.
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000, 0x3fefd9b0d3158574, 0x3fefb5586cf9890f, 0x3fef9301d0125b51, 0x3fef72b83c7d517b,
+    0x3fef54873168b9aa, 0x3fef387a6e756238, 0x3fef1e9df51fdee1, 0x3fef06fe0a31b715, 0x3feef1a7373aa9cb,
+    0x3feedea64c123422, 0x3feece086061892d, 0x3feebfdad5362a27, 0x3feeb42b569d4f82, 0x3feeab07dd485429,
+    0x3feea47eb03a5585, 0x3feea09e667f3bcd, 0x3fee9f75e8ec5f74, 0x3feea11473eb0187, 0x3feea589994cce13,
+    0x3feeace5422aa0db, 0x3feeb737b0cdc5e5, 0x3feec49182a3f090, 0x3feed503b23e255d, 0x3feee89f995ad3ad,
+    0x3feeff76f2fb5e47, 0x3fef199bdd85529c, 0x3fef3720dcef9069, 0x3fef5818dcfba487, 0x3fef7c97337b9b5f,
+    0x3fefa4afa2a490da, 0x3fefd0765b6e4540};
+
+// The reference's f32 exp: Rust's f32::exp is the C library's expf, which in
+// glibc >= 2.28 is the exp2f-table method of ARM's optimized-routines
+// (published; e_expf.c): x * 32/ln2 = k + r with |r| <= 1/2, exp(x) =
+// 2^(k/32) * p(r) with a cubic p, all in double, then one rounding to float.
+// This is that method in the operation order of glibc's FMA build (the one
+// x86-64 hosts with FMA run): it equals that expf on every one of the 2^32
+// float inputs (checked on the host against glibc 2.35); glibc's build for
+// hosts without FMA rounds 2 of them differently.
+// `tab` is kExp2Tab staged in LDS (a per-lane lookup in constant memory costs
+// a memory round trip per call).
+__device__ __forceinline__ float expf_rounded(float x, const uint64_t *tab) {
+    constexpr double N = 32.0, InvLn2N = 0x1.71547652b82fep+0 * N, Shift = 0x1.8p+52;
+    constexpr double C0 = 0x1.c6af84b912394p-5 / (N * N * N), C1 = 0x1.ebfce50fac4f3p-3 / (N * N),
+                     C2 = 0x1.62e42ff0c52d6p-1 / N;
+    const uint32_t ux = __float_as_uint(x), abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {  // |x| >= 88, or not finite
+        if (ux == 0xff800000u) return 0.0f;
+        if (abstop >= 0x7f8) return x + x;
+        if (x > 0x1.62e42ep6f) return INFINITY;
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double xd = double(x);
+    double kd = InvLn2N * xd + Shift;  // rounds k to the nearest integer
+    const uint64_t ki = uint64_t(__double_as_longlong(kd));
+    kd -= Shift;
+    const double r = fma(InvLn2N, xd, -kd);
+    const double sc = __longlong_as_double(int64_t(tab[ki & 31] + (ki << 47)));
+    const double z = fma(C0, r, C1), r2 = r * r;
+    double y = fma(C2, r, 1.0);
+    y = fma(z, r2, y);
+    return float(y * sc);
+}
+
+// Copies kExp2Tab to `tab` (32 words of LDS); a barrier must follow before use.
+__device__ __forceinline__ void stage_exp_table(uint64_t *tab) {
+    for (int i = threadIdx.x; i < 32; i += blockDim.x) tab[i] = kExp2Tab[i];
+}
+
+// (l - max) / T in f32 (gpu.rs:2037); division by 1 is exact, so T = 1 skips it.
+__device__ __forceinline__ float scaled_logit(float l, float mx, float temperature) {
+    return temperature == 1.0f ? l - mx : (l - mx) / temperature;
+}
 
 // The reference's sequential f32 sampler (gpu.rs:2034-2048) in one lane, for
-// a given draw u: a token-order f32 sum of p_i = exp((l_i - max)/T), then a
-// token-order scan of u*sum - p_0 - p_1 - ... that stops at the first negative
-// remainder (default: the last token); no multiply-add fusion.  The next
-// sixteen values load while the current sixteen are added.
-__device__ __forceinline__ int sequential_pick(const float *row, int V, float mx, float temperature, float u) {
+// a given draw u and p(i) = p_i = exp((l_i - max)/T): a token-order f32 sum of
+// the p_i, then a token-order scan of u*sum - p_0 - p_1 - ... that stops at
+// the first negative remainder (default: the last token); no multiply-add
+// fusion.  The next sixteen values load while the current sixteen are added.
+template <class P>
+__device__ __forceinline__ int sequential_pick(P p, int V, float u) {
 #pragma clang fp contract(off)
     constexpr int kBatch = 16;
     auto fetch = [&](float (&v)[kBatch], int t) {
 #pragma unroll
-        for (int k = 0; k < kBatch; ++k) v[k] = expf_rounded((row[min(t + k, V - 1)] - mx) / temperature);
+        for (int k = 0; k < kBatch; ++k) v[k] = p(min(t + k, V - 1));
     };
     const int full = V / kBatch * kBatch;
     float sum = 0.0f;
@@ -1676,7 +1763,7 @@ __device__ __forceinline__ int sequential_pick(const float *row, int V, float mx
 #pragma unroll
         for (int k = 0; k < kBatch; ++k) sum = sum + cur[k];
     }
-    for (int t = full; t < V; ++t) sum = sum + expf_rounded((row[t] - mx) / temperature);
+    for (int t = full; t < V; ++t) sum = sum + p(t);
     float sample = u * sum;
     if (full) fetch(nxt, 0);
     for (int t = 0; t < full; t += kBatch) {
@@ -1694,20 +1781,23 @@ __device__ __forceinline__ int sequential_pick(const float *row, int V, float mx
             if (left[k] < 0.0f) return t + k;
     }
     for (int t = full; t < V; ++t) {
-        sample = sample - expf_rounded((row[t] - mx) / temperature);
+        sample = sample - p(t);
         if (sample < 0.0f) return t;
     }
     return V - 1;
 }
 
-// LDS scratch of choose_token: a float, an int and a double per wave, and one
-// more double.
+// LDS scratch of choose_token: a float, an int and a double per wave, one
+// more double, and the exp table (stage_exp_table, before a barrier).
 struct SampleLds {
     float *redf;
     int *redi;
     double *redd;
+    const uint64_t *exp_tab;
 };
 
+// Block minimum.  The slots it writes are free again only after the caller's
+// next barrier.
 __device__ __forceinline__ int block_min_int(int v, const SampleLds &m) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
     v = wave_min_int(v);
@@ -1715,7 +1805,6 @@ __device__ __forceinline__ int block_min_int(int v, const SampleLds &m) {
     __syncthreads();
     v = INT_MAX;
     for (int w = 0; w < nw; ++w) v = min(v, m.redi[w]);
-    __syncthreads();
     return v;
 }
 
@@ -1733,51 +1822,51 @@ __device__ __forceinline__ int block_min_int(int v, const SampleLds &m) {
 // surely non-negative when P_i < u*S_lo - beta and surely negative when
 // P_i > u*S_hi + beta; the first index that is not surely non-negative is the
 // answer when it is surely negative.  Otherwise (a near-tie, or a non-finite
-// row) thread 0 runs the sequential f32 process itself with the same u.
+// row) thread 0 runs the sequential f32 process itself with the same u.  The
+// SampleLds slots are free again only after the caller's next barrier.
 __device__ __forceinline__ int choose_token(const float *row, int V, float temperature, uint64_t *rng, int *flags,
-                                            const SampleLds &m) {
+                                            const SampleLds &m, float *pscratch = nullptr) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, nw = blockDim.x >> 6;
+    // Every wave scans the whole row for the maximum (and for non-finite
+    // values) itself: no exchange between waves, so no barrier.
     float mx = -INFINITY;
     int bad = 0;
-    for (int t = threadIdx.x; t < V; t += blockDim.x) {
+    for (int t = lane; t < V; t += 64) {
         const float v = row[t];
         bad |= !isfinite(v);
         mx = fmaxf(mx, v);
     }
     mx = wave_max(mx);
     bad = wave_or_int(bad);
-    if (lane == 0) {
-        m.redf[wave] = mx;
-        m.redi[wave] = bad;
-    }
-    __syncthreads();
-    mx = -INFINITY;
-    bad = 0;
-    for (int w = 0; w < nw; ++w) {
-        mx = fmaxf(mx, m.redf[w]);
-        bad |= m.redi[w];
-    }
-    __syncthreads();
     if (bad && threadIdx.x == 0) atomicOr(flags, 1);
     if (temperature == 0.0f) {
         int best = INT_MAX;
-        for (int t = threadIdx.x; t < V; t += blockDim.x)
+        for (int t = lane; t < V; t += 64)
             if (row[t] == mx) best = min(best, t);
-        best = block_min_int(best, m);
+        best = wave_min_int(best);
         return best == INT_MAX ? 0 : best;
     }
-    // Each thread takes a contiguous run [i0, i1) of the tokens.
+    // Each thread takes a contiguous run [i0, i1) of the tokens; runs of up to
+    // kRunCache tokens keep their p_i in registers between the two passes.
     const int run = (V + int(blockDim.x) - 1) / int(blockDim.x);
     const int i0 = min(int(threadIdx.x) * run, V), i1 = min(i0 + run, V);
-    auto pexp = [&](int i) { return expf_rounded((row[i] - mx) / temperature); };
+    auto pexp = [&](int i) { return expf_rounded(scaled_logit(row[i], mx, temperature), m.exp_tab); };
+    constexpr int kRunCache = 4;
+    const bool cached = run <= kRunCache;
+    float pc[kRunCache];
     double mine = 0.0;
-    for (int i = i0; i < i1; ++i) mine += double(pexp(i));
-    double incl = mine;
+    if (cached) {
 #pragma unroll
-    for (int o = 1; o < 64; o <<= 1) {
-        const double n = __shfl_up(incl, o, 64);
-        if (lane >= o) incl += n;
+        for (int k = 0; k < kRunCache; ++k) {
+            pc[k] = 0.0f;
+            if (k >= run) break;  // uniform: no exp is evaluated past the run
+            if (i0 + k < i1) pc[k] = pexp(i0 + k);
+            mine += double(pc[k]);
+        }
+    } else {
+        for (int i = i0; i < i1; ++i) mine += double(pexp(i));
     }
+    const double incl = wave_inclusive_sum(mine);
     if (lane == 63) m.redd[wave] = incl;
     if (threadIdx.x == 0) {
         // One SplitMix64 draw per sampled token, as Random::unit (src/mesh.rs:263-265).
@@ -1786,6 +1875,14 @@ __device__ __forceinline__ int choose_token(const float *row, int V, float tempe
         *rng = state;
     }
     __syncthreads();
+    // Every read of the row is done: the p_i overwrite it for the fallback.
+    if (cached && pscratch) {
+#pragma unroll
+        for (int k = 0; k < kRunCache; ++k) {
+            if (k >= run) break;
+            if (i0 + k < i1) pscratch[i0 + k] = pc[k];
+        }
+    }
     double before = 0.0, S = 0.0;
     for (int w = 0; w < nw; ++w) {
         if (w < wave) before += m.redd[w];
@@ -1798,26 +1895,41 @@ __device__ __forceinline__ int choose_token(const float *row, int V, float tempe
     const double beta = double(V + 2) * e * s_hi * 1.01 + slack;
     const double lo = double(u) * s_lo - beta, hi = double(u) * s_hi + beta;
     double prefix = before + incl - mine;
-    int first = INT_MAX, decided = 0;
-    for (int i = i0; i < i1; ++i) {
-        prefix += double(pexp(i));
-        if (!(prefix < lo)) {
-            first = i;
-            decided = prefix > hi;
-            break;
+    // key = 2 * (first index whose prefix reaches lo) + (1 if that index is not
+    // decided by the bounds); the block minimum is the earliest such index.
+    int key = INT_MAX;
+    if (cached) {
+#pragma unroll
+        for (int k = 0; k < kRunCache; ++k) {
+            if (k >= run) break;
+            if (key == INT_MAX && i0 + k < i1) {
+                prefix += double(pc[k]);
+                if (!(prefix < lo)) key = 2 * (i0 + k) + (prefix > hi ? 0 : 1);
+            }
+        }
+    } else {
+        for (int i = i0; i < i1; ++i) {
+            prefix += double(pexp(i));
+            if (!(prefix < lo)) {
+                key = 2 * i + (prefix > hi ? 0 : 1);
+                break;
+            }
         }
     }
-    first = block_min_int(first, m);
-    if (first == INT_MAX) return V - 1;
-    if (first >= i0 && first < i1) m.redi[0] = decided ? first : -1;
-    __syncthreads();
-    int token = m.redi[0];
-    __syncthreads();
-    if (token < 0) {
-        if (threadIdx.x == 0) m.redi[0] = sequential_pick(row, V, mx, temperature, u);
+    key = block_min_int(key, m);
+    if (key == INT_MAX) return V - 1;
+    int token = key >> 1;
+    if (key & 1) {
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            if (cached && pscratch)
+                m.redi[0] = sequential_pick([&](int t) { return pscratch[t]; }, V, u);
+            else
+                m.redi[0] = sequential_pick(
+                    [&](int t) { return expf_rounded(scaled_logit(row[t], mx, temperature), m.exp_tab); }, V, u);
+        }
         __syncthreads();
         token = m.redi[0];
-        __syncthreads();
     }
     return token;
 }
@@ -1841,13 +1953,16 @@ sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64
     __shared__ float redf[kThreads / 64];
     __shared__ int redi[kThreads / 64];
     __shared__ double redd[kThreads / 64 + 1];
+    __shared__ uint64_t tab[32];
     const int b = blockIdx.x;
     const float *src = logits + size_t(b) * V;
     const bool staged = V <= kSampleCap;
     if (staged)
         for (int t = threadIdx.x; t < V; t += blockDim.x) row[t] = src[t];
+    stage_exp_table(tab);
     __syncthreads();
-    const int token = choose_token(staged ? row : src, V, temperature, rng + b, flags, SampleLds{redf, redi, redd});
+    const int token = choose_token(staged ? row : src, V, temperature, rng + b, flags,
+                                   SampleLds{redf, redi, redd, tab}, staged ? row : nullptr);
     append_token(tokens, tok_stride, len, b, token);
 }
 
@@ -1870,7 +1985,9 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
     float *redf = lds.take<float>(kHsThreads / 64);
     int *redi = lds.take<int>(kHsThreads / 64);
     double *redd = lds.take<double>(kHsThreads / 64 + 1);
+    uint64_t *tab = lds.take<uint64_t>(32);
     for (int c = threadIdx.x; c < W; c += blockDim.x) N[c] = xn[size_t(b) * W + c];
+    stage_exp_table(tab);
     __syncthreads();
     const int q = threadIdx.x & 63, g = threadIdx.x >> 6, quads = Vp / 4;
     const float4 *E4 = reinterpret_cast<const float4 *>(Et);
@@ -1910,7 +2027,7 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
         }
         __syncthreads();
     }
-    const int token = choose_token(L, V, temperature, rng + b, flags, SampleLds{redf, redi, redd});
+    const int token = choose_token(L, V, temperature, rng + b, flags, SampleLds{redf, redi, redd, tab}, L);
     append_token(tokens, tok_stride, len, b, token);
 }
 
@@ -2085,7 +2202,7 @@ struct PersistRing {
     static constexpr int W = 64 * NW * CPL, gc = 64 / GL, ga = 64 * NW / (HDP / 4);
     static constexpr int budget = 160 * 1024 * NW / 8;
     static constexpr int other = 4 * (2 * W + 8 * CPL * NW * gc + W + kPersistVocab + 2 * NW + 2 * ga + ga * HDP) +
-                                 8 * (NW + 1) + 8 + 64;
+                                 8 * (NW + 1) + 8 + 256 + 64;
     static constexpr int fit(int ul) { return (budget - other) / (2 * ul * NW * 1024); }
     static constexpr int UL = fit(4) >= 2 ? 4 : (fit(2) >= 2 ? 2 : 1);
     static constexpr int NS = UL == 4 ? 2 : (fit(UL) >= 4 ? 4 : (fit(UL) >= 3 ? 3 : 2));
@@ -2167,8 +2284,12 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
 // hoisted out of the step loop, where they would hold dozens of registers.
 template <class T>
 __device__ __forceinline__ T *opaque(T *p) {
-    asm volatile("" : "+s"(p));
-    return p;
+    // The pointer is wave-uniform; readfirstlane states that, so the operand
+    // can live in scalar registers even where p arrives in vector ones.
+    const uint64_t u = uint64_t(p);
+    uint32_t lo = __builtin_amdgcn_readfirstlane(uint32_t(u)), hi = __builtin_amdgcn_readfirstlane(uint32_t(u >> 32));
+    asm volatile("" : "+s"(lo), "+s"(hi));
+    return reinterpret_cast<T *>((uint64_t(hi) << 32) | lo);
 }
 
 template <int NW, int CPL, int GL, int D>
@@ -2181,7 +2302,7 @@ struct PersistLds {
     float *xch, *red, *xn, *row, *redf, *ring;
     int *redi;
     double *redd;
-    uint64_t *rng;
+    uint64_t *rng, *exp_tab;
 };
 
 // Post-attention half of the last block on the residual row x, then logit
@@ -2214,6 +2335,7 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
 #pragma unroll
     for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
     __syncthreads();
+    if (slice >= 3) trace_mark(a, step, L, 0);
     const int nb = 3 + s.H, V = s.V;
     persistent_head_slice<NW, W>(m.xn, a.E, xc.logits(), slice * V / nb, (slice + 1) * V / nb, step + 1, c.lane,
                                  c.wave);
@@ -2221,7 +2343,7 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
 
 // Mesh team `team` of sequence b.
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
-__device__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m) {
+__device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m) {
     using Ctx = RowCtx<NW, CPL, GL>;
     constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
@@ -2293,12 +2415,11 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
             if (t < V) m.row[t] = lg[i];
         }
         __syncthreads();
-        tok = uint32_t(choose_token(m.row, V, a.temperature, m.rng, a.flags, SampleLds{m.redf, m.redi, m.redd}));
-        if (team == 0) {
-            if (threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
-            if (step + 1 == a.steps)
-                for (int t = threadIdx.x; t < V; t += blockDim.x) a.logits[size_t(b) * V + t] = m.row[t];
-        }
+        if (team == 0 && step + 1 == a.steps)
+            for (int t = threadIdx.x; t < V; t += blockDim.x) a.logits[size_t(b) * V + t] = m.row[t];
+        tok = uint32_t(choose_token(m.row, V, a.temperature, m.rng, a.flags,
+                                    SampleLds{m.redf, m.redi, m.redd, m.exp_tab}, m.row));
+        if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
         ++len;
         trace_mark(a, step, L, 1);
     }
@@ -2314,7 +2435,7 @@ __device__ void persistent_team(const PersistArgs &a, int b, int team, const Per
 // layer [0, pos) were all written before the launch or by this block, and the
 // first round of them loads while the layer's meshes still run.
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
-__device__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
+__device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
     using Ctx = RowCtx<NW, CPL, GL>;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     using S = AttnState<HDP, 64 * NW, Ring::UL>;
@@ -2414,7 +2535,9 @@ persistent_decode_kernel(PersistArgs a) {
     __shared__ uint64_t rng;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     __shared__ __align__(16) float ring[KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS];
-    const PersistLds m{xch, red, xn, row, redf, ring, redi, redd, &rng};
+    __shared__ uint64_t exp_tab[32];
+    stage_exp_table(exp_tab);  // the teams' first barrier comes long before their first draw
+    const PersistLds m{xch, red, xn, row, redf, ring, redi, redd, &rng, exp_tab};
     const int blk = blockIdx.x;
     if (blk < 3 * a.batch) {
         persistent_team<NW, CPL, GL, DEPTH, HDP>(a, blk / 3, blk % 3, m);
@@ -2459,6 +2582,14 @@ mesh_rows_kernel(Shape s, const float *__restrict__ in, float *__restrict__ out,
     const float *res = mesh_team<CPT>(A, B, C, nr, s, reinterpret_cast<const float2 *>(w), depth, threadIdx.x, T,
                                       true);
     for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) out[size_t(r0) * W + idx] = res[idx];
+}
+
+__global__ void __launch_bounds__(kThreads) expf_kernel(const float *__restrict__ x, float *__restrict__ y, size_t n) {
+    __shared__ uint64_t tab[32];
+    stage_exp_table(tab);
+    __syncthreads();
+    const size_t stride = size_t(gridDim.x) * blockDim.x;
+    for (size_t i = size_t(blockIdx.x) * blockDim.x + threadIdx.x; i < n; i += stride) y[i] = expf_rounded(x[i], tab);
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -2545,7 +2676,7 @@ size_t head_lds_bytes(const Shape &s, int rt) {
 size_t head_sample_lds_bytes(const Shape &s) {
     if (s.V > kHeadSampleCap) return size_t(-1);
     return align16(size_t(s.W) * 4) + align16(kHeadSampleCap * 4) + align16(size_t(kHsGroups) * 64 * 16) +
-           2 * align16(kHsThreads / 64 * 4) + align16((kHsThreads / 64 + 1) * 8);
+           2 * align16(kHsThreads / 64 * 4) + align16((kHsThreads / 64 + 1) * 8) + align16(32 * 8);
 }
 
 void configure_lds(size_t max_bytes) {
@@ -2792,6 +2923,12 @@ void head_sample(const Shape &s, const float *xn, int batch, const float *Et, in
                  hipStream_t stream) {
     hipLaunchKernelGGL(head_sample_kernel, dim3(batch), dim3(kHsThreads), head_sample_lds_bytes(s), stream, s, xn,
                        Et, Vp, logits, temperature, rng, tokens, tok_stride, len, flags);
+    HIP_LAUNCH_CHECK();
+}
+
+void device_expf(const float *x, float *y, size_t n, hipStream_t stream) {
+    const int blocks = int(std::min<size_t>((n + kThreads - 1) / kThreads, 4096));
+    if (blocks > 0) hipLaunchKernelGGL(expf_kernel, dim3(blocks), dim3(kThreads), 0, stream, x, y, n);
     HIP_LAUNCH_CHECK();
 }
 

@@ -137,7 +137,8 @@ struct PersistArgs {
     // wall clock (100 MHz) when the phase's inputs were ready and when its
     // outputs were published.  Mesh teams: l = 0..layers (l = layers: logits
     // ready, token drawn); attention blocks: l = 0..layers-1, and l = layers
-    // (slot 1) when their logit slice is published.
+    // when the last block's post-attention half is done (slot 0) and their
+    // logit slice is published (slot 1).
     uint64_t *trace;
 };
 bool persistent_fits(const Shape &s, int batch, int device);
@@ -167,6 +168,8 @@ void head_sample(const Shape &s, const float *xn, int batch, const float *Et, in
 // Greedy / temperature sampling from logits rows; appends the token and bumps len.
 void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng, uint32_t *tokens,
             int tok_stride, int *len, int *flags, hipStream_t stream);
+// y[i] = the sampler's f32 exp of x[i] (for verification).
+void device_expf(const float *x, float *y, size_t n, hipStream_t stream);
 // dst[i] = src[i] for n float4 elements (bandwidth calibration).
 void calibration_copy(const float4 *src, float4 *dst, size_t n, hipStream_t stream);
 

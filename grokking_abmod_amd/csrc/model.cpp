@@ -767,6 +767,22 @@ bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, f
     return flags != 0;
 }
 
+void device_expf(int device, const float *x, size_t n, float *out) {
+    if (n == 0) return;
+    int count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count) throw Error("invalid device ordinal", kDeviceError);
+    check(hipSetDevice(device), "hipSetDevice");
+    DevBuf dx, dy;
+    dx.ensure(n * 4);
+    dy.ensure(n * 4);
+    check(hipMemcpy(dx.p, x, n * 4, hipMemcpyHostToDevice), "upload inputs");
+    kern::device_expf(dx.as<float>(), dy.as<float>(), n, nullptr);
+    check(hipGetLastError(), "expf launch");
+    check(hipDeviceSynchronize(), "hipDeviceSynchronize");
+    check(hipMemcpy(out, dy.p, n * 4, hipMemcpyDeviceToHost), "download results");
+}
+
 double copy_bandwidth(int device, size_t bytes, int iters) {
     int count = 0;
     check(hipGetDeviceCount(&count), "hipGetDeviceCount");

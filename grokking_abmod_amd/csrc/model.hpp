@@ -66,6 +66,8 @@ class MeshGpt {
 // place).  Returns whether any row held a non-finite logit.
 bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
                    uint64_t *rng_states, uint32_t *tokens);
+// out[i] = the sampler's f32 exp of x[i], evaluated on `device`.
+void device_expf(int device, const float *x, size_t n, float *out);
 
 // Mean bandwidth (read + write bytes / s / 1e9) of a plain device copy of
 // `bytes`, repeated `iters` times on `device`.

@@ -133,6 +133,11 @@ void *mg_model_stream(mg_model *model);
 int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
                      uint64_t *rng_states, uint32_t *tokens);
 
+/* out[i] = the f32 exp the sampler of mg_generate uses (the reference's
+ * f32::exp, i.e. the C library's expf), evaluated on `device`.  No separate
+ * reference call: it lets tests compare the device exp with the host's. */
+int mg_expf(int device, const float *x, size_t n, float *out);
+
 /* A plain device-to-device copy of `bytes` (a float4 grid-stride kernel named
  * calibration_copy) run `iters` times on `device`; writes the mean bandwidth
  * counting read plus write bytes.  No reference counterpart: it calibrates the

@@ -121,3 +121,36 @@ def test_nonfinite_rows_are_reported():
     with pytest.raises(G.MeshGptError) as info:
         G.sample_logits(rows, 1.0, np.array([1, 2], np.uint64))
     assert info.value.status == G.MG_NONFINITE
+
+
+def _host_expf():
+    import ctypes
+    import ctypes.util
+    libm = ctypes.CDLL(ctypes.util.find_library("m") or "libm.so.6")
+    libm.expf.restype = ctypes.c_float
+    libm.expf.argtypes = [ctypes.c_float]
+    return libm.expf
+
+
+def test_device_expf_matches_c_library():
+    """The sampler's p_i = exp((l - max) / T) must be the reference's f32::exp,
+    which is the C library's expf.  Special values, the underflow and
+    denormal range, a fine grid and random inputs are compared bit for bit.
+    Two inputs are rounded differently by glibc's build for hosts without
+    FMA; they are skipped when this host's expf is that build."""
+    expf = _host_expf()
+    rng = np.random.default_rng(5)
+    special = np.array([0.0, -0.0, np.inf, -np.inf, 88.0, 88.72283, 88.72284, -87.33655, -88.0, -100.0,
+                        -103.27893, -103.972, -103.97208, -103.9721, -104.0, -120.0, 1e-30, -1e-30,
+                        float.fromhex("0x1.04845ep+5"), -float.fromhex("0x1.f8cbb2p+5")], dtype=np.float32)
+    grid = -np.arange(0, 110 * 1024, dtype=np.float32) / np.float32(1024.0)
+    bits = rng.integers(0x80000000, 0xC2D00000, size=400_000, dtype=np.uint64).astype(np.uint32)
+    x = np.concatenate([special, grid, bits.view(np.float32), rng.uniform(-110, 90, 200_000).astype(np.float32)])
+    got = G.device_expf(x)
+    want = np.array([expf(float(v)) for v in x], dtype=np.float32)
+    differ = got.view(np.uint32) != want.view(np.uint32)
+    differ &= ~(np.isnan(got) & np.isnan(want))
+    non_fma_pair = {np.float32(float.fromhex("0x1.04845ep+5")).view(np.uint32),
+                    np.float32(-float.fromhex("0x1.f8cbb2p+5")).view(np.uint32)}
+    left = [hex(int(v)) for v in x[differ].view(np.uint32) if int(v) not in {int(u) for u in non_fma_pair}]
+    assert not left, f"device expf differs from the C library at {left[:8]}"
