@@ -2305,6 +2305,45 @@ struct PersistLds {
     uint64_t *rng, *exp_tab;
 };
 
+// Inputs of the post-attention half of phase g: the attention output y and
+// the row's value vector v.
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c,
+                                                 const PersistXch &xc, int g, float (&y)[CPL], float (&v)[CPL]) {
+    float yv[2 * CPL];
+    const uint64_t *yw = xc.y(), *vw = xc.qkv(g, 2);
+    take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        y[j] = yv[j];
+        v[j] = yv[CPL + j];
+    }
+}
+
+// The step's token from the published logits, drawn by every workgroup of the
+// sequence alike (same logits, same sampler state in its LDS); the logits are
+// also copied to `out` when given.
+template <int NW, bool MARK>
+__device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const PersistXch &xc, int step,
+                                               const PersistLds &m, float *out) {
+    constexpr int NL = kPersistVocab / (64 * NW);  // logit words per thread
+    const int V = a.s.V;
+    float lg[NL];
+    take_words<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
+                   a.abort);
+    if (MARK) trace_mark(a, step, a.layers, 0);
+#pragma unroll
+    for (int i = 0; i < NL; ++i) {
+        const int t = int(threadIdx.x) + i * 64 * NW;
+        if (t < V) m.row[t] = lg[i];
+    }
+    __syncthreads();
+    if (out)
+        for (int t = threadIdx.x; t < V; t += blockDim.x) out[t] = m.row[t];
+    return uint32_t(
+        choose_token(m.row, V, a.temperature, m.rng, a.flags, SampleLds{m.redf, m.redi, m.redd, m.exp_tab}, m.row));
+}
+
 // Post-attention half of the last block on the residual row x, then logit
 // slice `slice` of the 3 + H slices of the vocabulary.
 template <int NW, int CPL, int GL, int DEPTH>
@@ -2321,15 +2360,8 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
     float2 wp[D][CPL], wf[D][CPL];
     load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
     load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
-    float yv[2 * CPL];
-    const uint64_t *yw = xc.y(), *vw = xc.qkv(g, 2);
-    take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
     float y[CPL], v[CPL];
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        y[j] = yv[j];
-        v[j] = yv[CPL + j];
-    }
+    take_post_inputs(a, c, xc, g, y, v);
     row_post(c, x, y, v, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
     const float inv = row_inv_rms(c, x, 3);
 #pragma unroll
@@ -2348,7 +2380,6 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
     constexpr int D = FIXED ? DEPTH : 1;
-    constexpr int NL = kPersistVocab / (64 * NW);  // logit words per thread
     const Shape &s = a.s;
     Ctx c(m.xch, m.red);
     const int dim = c.dim(), L = a.layers, V = s.V;
@@ -2366,27 +2397,25 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
         trace_mark(a, step, 0, 0);
-        for (int l = 0; l < L; ++l) {
-            const int g = step * L + l;
-            const float *wb = block(l);
-            load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
-            if (l > 0) {
-                // Post-attention half of block l-1, its weights loading during the wait.
-                const float *wq = block(l - 1);
-                load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
-                load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
-                float yv[2 * CPL];
-                const uint64_t *yw = xc.y(), *vw = xc.qkv(g - 1, 2);
-                take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g, yv, a.abort);
-                trace_mark(a, step, l, 0);
-                float y[CPL], v[CPL];
+        // Layer 0's q, k and v are the token's rows of the layer-0 table, which
+        // the attention blocks read themselves: the teams start at block 0's
+        // post-attention half.
+        if (L == 1 && team == 0) {
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) {
-                    y[j] = yv[j];
-                    v[j] = yv[CPL + j];
-                }
-                row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
-            }
+            for (int j = 0; j < CPL; ++j) put_word(xc.xrow() + c.ridx(j), x[j], step + 1);
+        }
+        trace_mark(a, step, 0, 1);
+        for (int l = 1; l < L; ++l) {
+            const int g = step * L + l;
+            const float *wb = block(l), *wq = block(l - 1);
+            // Post-attention half of block l-1, its weights loading during the wait.
+            load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
+            load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
+            load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
+            float y[CPL], v[CPL];
+            take_post_inputs(a, c, xc, g - 1, y, v);
+            trace_mark(a, step, l, 0);
+            row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
             if (l + 1 == L && team == 0) {
                 // The attention blocks finish the last block from this row.
 #pragma unroll
@@ -2404,24 +2433,11 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             trace_mark(a, step, l, 1);
         }
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, team, m);
-        // Every team draws the same token from the same logits and state.
-        float lg[NL];
-        take_words<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
-                       a.abort);
-        trace_mark(a, step, L, 0);
-#pragma unroll
-        for (int i = 0; i < NL; ++i) {
-            const int t = int(threadIdx.x) + i * 64 * NW;
-            if (t < V) m.row[t] = lg[i];
-        }
-        __syncthreads();
-        if (team == 0 && step + 1 == a.steps)
-            for (int t = threadIdx.x; t < V; t += blockDim.x) a.logits[size_t(b) * V + t] = m.row[t];
-        tok = uint32_t(choose_token(m.row, V, a.temperature, m.rng, a.flags,
-                                    SampleLds{m.redf, m.redi, m.redd, m.exp_tab}, m.row));
+        // The launch's last logits are kept for callers that read them.
+        tok = draw_token<NW, true>(a, xc, step, m, team == 0 && step + 1 == a.steps ? a.logits + size_t(b) * V : nullptr);
+        trace_mark(a, step, L, 1);
         if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
         ++len;
-        trace_mark(a, step, L, 1);
     }
     if (team == 0 && threadIdx.x == 0) {
         a.len[b] = len;
@@ -2429,11 +2445,39 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     }
 }
 
+// QK-norm over the head, then RoPE at `pos` (reference.rs:462-482), for an
+// attention lane's dims d0 .. d0 + VEC - 1 (each group of LPK lanes holds the
+// whole head; the RoPE partner dim, hd/2 away, is LPK/2 lanes away).  The
+// arithmetic of row_qk_rope: with VEC == NW its head sums (lanes, then waves
+// in order) are these per-dim lane sums added in dim order.
+template <int LPK, int VEC>
+__device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, int pos, const float2 *rope, const Shape &s) {
+    float sq[VEC], other[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) sq[e] = x[e] * x[e];
+    float ss = 0.0f;
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) ss += group_sum<LPK>(sq[e]);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) other[e] = __shfl_xor(x[e], LPK / 2, 64);
+    const float scale = 1.0f / float(s.hd);
+    const float sc = rsqrtf(ss * scale + kRmsEps);
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) {
+        const int d = d0 + e;
+        const float2 cs = rope_pair(rope, pos, d, s.half);
+        const float self = x[e] * sc, oth = other[e] * sc;
+        x[e] = d < s.half ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
+    }
+}
+
 // Attention block of (sequence b, head h).  Its query, key and value arrive
-// as tagged words; the key/value rows go to the cache for later steps and
-// enter this step's attention from registers, so the cached rows read each
-// layer [0, pos) were all written before the launch or by this block, and the
-// first round of them loads while the layer's meshes still run.
+// as tagged words, except at layer 0, where they are the token's rows of the
+// layer-0 table (QK-norm and RoPE applied here): the block draws each step's
+// token itself, like the teams.  The key/value rows go to the cache for later
+// steps and enter this step's attention from registers, so the cached rows
+// read each layer [0, pos) were all written before the launch or by this
+// block, and the first rounds of them load while the inputs are awaited.
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
 __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
     using Ctx = RowCtx<NW, CPL, GL>;
@@ -2443,10 +2487,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
     constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U, NS = Ring::NS;
     const KvRing<HDP, NW, U, NS> ring{m.ring};
     const Shape &s = a.s;
+    constexpr int W = Ctx::W;
     const int len0 = a.len[b], L = a.layers;
     const PersistXch xc(a, b);
     const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
     static_assert(VEC % NW == 0, "lane dims must cover whole row-order columns");
+    uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len0 - 1];
+    if (threadIdx.x == 0) *m.rng = a.rng[b];
     for (int step = 0; step < a.steps; ++step) {
         const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
@@ -2464,23 +2511,43 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // The first NS rounds load while the layer's meshes still run.
             const int nr = (pos + G * U - 1) / (G * U);
             for (int r = 0; r < min(NS, nr); ++r) ring.issue(kl, vl, r, pos, tid);
-            float qkv[3 * VEC];
-            const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
-                           *vw = opaque(xc.qkv(g, 2)) + at0;
-            take_words<3 * VEC>(
-                [&](int i) {
-                    const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
-                    return base + ((i % VEC) % NW * 64 + (i % VEC) / NW);
-                },
-                g + 1, qkv, a.abort);
-            trace_mark(a, step, l, 0);
             float qr[VEC], kn[VEC], vn[VEC];
+            if (l == 0) {
+                const float *t0 = opaque(a.q0) + size_t(tok) * 3 * W + at0;
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) {
-                qr[e] = qkv[e];
-                kn[e] = qkv[VEC + e];
-                vn[e] = qkv[2 * VEC + e];
+                for (int e = 0; e < VEC; ++e) {
+                    const uint32_t o = (e % NW) * 64 + e / NW;
+                    qr[e] = t0[o];
+                    kn[e] = t0[W + o];
+                    vn[e] = t0[2 * W + o];
+                }
+                lane_qk_rope<LPK, VEC>(qr, d0, pos, a.rope, s);
+                lane_qk_rope<LPK, VEC>(kn, d0, pos, a.rope, s);
+                // The teams' XSA of block 0 needs the value row: each head
+                // publishes its part, as the V team does for later layers.
+                if (grp == 0) {
+                    uint64_t *vo = xc.qkv(g, 2) + at0;
+#pragma unroll
+                    for (int e = 0; e < VEC; ++e) put_word(vo + (e % NW) * 64 + e / NW, vn[e], g + 1);
+                }
+            } else {
+                float qkv[3 * VEC];
+                const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
+                               *vw = opaque(xc.qkv(g, 2)) + at0;
+                take_words<3 * VEC>(
+                    [&](int i) {
+                        const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
+                        return base + ((i % VEC) % NW * 64 + (i % VEC) / NW);
+                    },
+                    g + 1, qkv, a.abort);
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    qr[e] = qkv[e];
+                    kn[e] = qkv[VEC + e];
+                    vn[e] = qkv[2 * VEC + e];
+                }
             }
+            trace_mark(a, step, l, 0);
             if (grp == 0) {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
@@ -2516,6 +2583,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
         take_words<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
         trace_mark(a, step, L, 1);
+        if (step + 1 < a.steps) tok = draw_token<NW, false>(a, xc, step, m, nullptr);
     }
 }
 
@@ -2545,6 +2613,35 @@ persistent_decode_kernel(PersistArgs a) {
         const int i = blk - 3 * a.batch;
         persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, i / a.s.H, i % a.s.H, m);
     }
+}
+
+// Layer-0 table: row (token v, team t) is team t's mesh of block 0 on the
+// RMS-normalised token vector E[v], before QK-norm and RoPE: the arithmetic
+// of a persistent mesh team, so its rows equal what the team would compute.
+template <int NW, int CPL, int GL, int DEPTH>
+__global__ void __launch_bounds__(64 * NW)
+layer0_kernel(Shape s, const float *__restrict__ E, const float *__restrict__ w, size_t block0, float *q0) {
+    using Ctx = RowCtx<NW, CPL, GL>;
+    constexpr int W = Ctx::W;
+    constexpr bool FIXED = DEPTH > 0;
+    constexpr int D = FIXED ? DEPTH : 1;
+    __shared__ float xch[2 * W];
+    __shared__ float red[8 * Ctx::SLOT];
+    Ctx c(xch, red);
+    const int v = int(blockIdx.x) / 3, team = int(blockIdx.x) % 3;
+    const float *wm = w + block0 + size_t(team) * 2 * W * s.A;
+    float2 wr[D][CPL];
+    load_block_weights<NW, CPL, GL, D>(wr, wm, FIXED, c.lane, c.wave);
+    float x[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = E[size_t(v) * W + c.ridx(j)];
+    const float inv = row_inv_rms(c, x, 3);
+    float n[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
+    row_run_mesh(c, n, wr, wm, s.A, s, FIXED);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) q0[(size_t(v) * 3 + team) * W + c.ridx(j)] = n[j];
 }
 
 __global__ void __launch_bounds__(kThreads)
@@ -2821,32 +2918,51 @@ void row_order(const float *src, float *dst, int rows, int W, bool pairs, hipStr
 }
 
 // The persistent kernel instantiation for a shape, or nullptr.
-template <int NW, int CPL, int HDP>
-const void *persistent_pick(const Shape &s) {
+// Calls f(NW, CPL, GL, DEPTH, HDP) (integral constants) with the persistent
+// kernel variant for the shape; false when the shape has none.
+template <int NW, int CPL, int HDP, class F>
+void persistent_depth(const Shape &s, F &&f) {
+    using std::integral_constant;
     constexpr int GL = HDP / NW;
     const bool fixed = s.butterfly && s.A == s.F;
     if constexpr (NW == 4 && CPL == 2 && HDP == 64) {
-        if (fixed && s.A == 9) return reinterpret_cast<const void *>(&persistent_decode_kernel<4, 2, 16, 9, 64>);
+        if (fixed && s.A == 9)
+            return f(integral_constant<int, 4>{}, integral_constant<int, 2>{}, integral_constant<int, 16>{},
+                     integral_constant<int, 9>{}, integral_constant<int, 64>{});
     }
     if constexpr (NW == 2 && CPL == 1 && HDP == 32) {
-        if (fixed && s.A == 7) return reinterpret_cast<const void *>(&persistent_decode_kernel<2, 1, 16, 7, 32>);
+        if (fixed && s.A == 7)
+            return f(integral_constant<int, 2>{}, integral_constant<int, 1>{}, integral_constant<int, 16>{},
+                     integral_constant<int, 7>{}, integral_constant<int, 32>{});
     }
-    return reinterpret_cast<const void *>(&persistent_decode_kernel<NW, CPL, GL, 0, HDP>);
+    f(integral_constant<int, NW>{}, integral_constant<int, CPL>{}, integral_constant<int, GL>{},
+      integral_constant<int, 0>{}, integral_constant<int, HDP>{});
+}
+
+template <class F>
+bool persistent_visit(const Shape &s, F &&f) {
+    if (!row_block_supported(s) || s.hd != s.hdp || s.V > kPersistVocab) return false;
+    const int nw = row_waves(s.W);
+    if (s.hd / nw != 8 && s.hd / nw != 16) return false;
+    switch (s.W * 10000 + s.hd) {
+    case 1280032: persistent_depth<2, 1, 32>(s, f); return true;
+    case 2560032: persistent_depth<4, 1, 32>(s, f); return true;
+    case 2560064: persistent_depth<4, 1, 64>(s, f); return true;
+    case 5120032: persistent_depth<4, 2, 32>(s, f); return true;
+    case 5120064: persistent_depth<4, 2, 64>(s, f); return true;
+    case 10240064: persistent_depth<4, 4, 64>(s, f); return true;
+    default: return false;
+    }
 }
 
 const void *persistent_kernel(const Shape &s) {
-    if (!row_block_supported(s) || s.hd != s.hdp || s.V > kPersistVocab) return nullptr;
-    const int nw = row_waves(s.W);
-    if (s.hd / nw != 8 && s.hd / nw != 16) return nullptr;
-    switch (s.W * 10000 + s.hd) {
-    case 1280032: return persistent_pick<2, 1, 32>(s);
-    case 2560032: return persistent_pick<4, 1, 32>(s);
-    case 2560064: return persistent_pick<4, 1, 64>(s);
-    case 5120032: return persistent_pick<4, 2, 32>(s);
-    case 5120064: return persistent_pick<4, 2, 64>(s);
-    case 10240064: return persistent_pick<4, 4, 64>(s);
-    default: return nullptr;
-    }
+    const void *k = nullptr;
+    persistent_visit(s, [&](auto nw, auto cpl, auto gl, auto depth, auto hdp) {
+        k = reinterpret_cast<const void *>(
+            &persistent_decode_kernel<decltype(nw)::value, decltype(cpl)::value, decltype(gl)::value,
+                                      decltype(depth)::value, decltype(hdp)::value>);
+    });
+    return k;
 }
 
 int persistent_blocks(const Shape &s, int batch) { return 3 * batch + batch * s.H; }
@@ -2870,6 +2986,18 @@ hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream) {
     void *params[] = {&args};
     return hipLaunchCooperativeKernel(f, dim3(persistent_blocks(a.s, a.batch)), dim3(64 * row_waves(a.s.W)), params, 0,
                                       stream);
+}
+
+size_t persistent_layer0_floats(const Shape &s) { return size_t(s.V) * 3 * s.W; }
+
+bool persistent_layer0(const Shape &s, const float *E, const float *w, size_t block0, float *q0, hipStream_t stream) {
+    return persistent_visit(s, [&](auto nw, auto cpl, auto gl, auto depth, auto hdp) {
+        constexpr int NW = decltype(nw)::value;
+        hipLaunchKernelGGL((layer0_kernel<NW, decltype(cpl)::value, decltype(gl)::value, decltype(depth)::value>),
+                           dim3(3 * s.V), dim3(64 * NW), 0, stream, s, E, w, block0, q0);
+        HIP_LAUNCH_CHECK();
+        (void)hdp;
+    });
 }
 
 void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int batch, int nsplit, float *part,

@@ -120,6 +120,7 @@ struct PersistArgs {
     float *kc, *vc;       // KV cache, layer-major
     size_t layer_elems;   // floats of one layer of the cache
     int cap;              // positions per (sequence, head) slab
+    const float *q0;      // layer-0 table (persistent_layer0)
     float *logits;        // [batch][V] logits of the launch's last step
     const float2 *rope;
     uint32_t *tokens;
@@ -145,6 +146,12 @@ bool persistent_fits(const Shape &s, int batch, int device);
 // Exchange words of one sequence: q/k/v of two layer phases, the attention
 // output, the residual row entering the last block and the logits.
 size_t persistent_exchange_words(const Shape &s);
+// Builds the layer-0 table q0 (V x 3 x W floats, row order): for each token,
+// the Q, K and V meshes of block 0 on its normalised vector, before QK-norm
+// and RoPE.  E and w are the row-order token vectors and weights.  False when
+// the shape has no persistent kernel.
+size_t persistent_layer0_floats(const Shape &s);
+bool persistent_layer0(const Shape &s, const float *E, const float *w, size_t block0, float *q0, hipStream_t stream);
 hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream);
 
 // Split-KV decode attention: one query row per sequence; the len[b] keys are

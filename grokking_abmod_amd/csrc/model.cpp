@@ -79,6 +79,7 @@ struct MeshGpt::Impl {
     // Row-order copies of the block weights and token vectors for the row
     // decode kernel (kern::row_order).
     DevBuf wdec, Edec;
+    DevBuf q0;  // persistent decode: layer-0 Q/K/V meshes of every token
 
     // Decode state: KV cache [L][batch_cap][H][context][hdp], per-sequence
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
@@ -262,6 +263,11 @@ struct MeshGpt::Impl {
             kern::row_order(E.as<float>(), Edec.as<float>(), shape.V, shape.W, false, stream);
             kern::row_order(params.as<float>() + emb, wdec.as<float>() + emb, int(block_rows), shape.W, true,
                             stream);
+            if (persistent_ok) {
+                q0.ensure(kern::persistent_layer0_floats(shape) * 4);
+                kern::persistent_layer0(shape, Edec.as<float>(), wdec.as<float>(),
+                                        layout.groups[layout.blocks[0].query].offset, q0.as<float>(), stream);
+            }
         }
         sync();
     }
@@ -563,6 +569,7 @@ struct MeshGpt::Impl {
         a.vc = vc.as<float>();
         a.layer_elems = layer_cache_elems();
         a.cap = int(cfg.context);
+        a.q0 = q0.as<float>();
         a.logits = dlogits.as<float>();
         a.rope = rope.as<float2>();
         a.tokens = dtokens.as<uint32_t>();
