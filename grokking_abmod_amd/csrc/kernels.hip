@@ -2508,9 +2508,16 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // 64 + e / NW, as d0 is a multiple of VEC and VEC one of NW.
             const uint32_t at0 = uint32_t(row_of<NW>(h * HDP + d0));
             float *kl = a.kc + size_t(l) * a.layer_elems + slab, *vl = a.vc + size_t(l) * a.layer_elems + slab;
-            // The first NS rounds load while the layer's meshes still run.
+            // The first NS rounds load into the ring, and the last two rounds
+            // into registers, while the layer's meshes still run (the online
+            // softmax takes rounds in any order).
             const int nr = (pos + G * U - 1) / (G * U);
-            for (int r = 0; r < min(NS, nr); ++r) ring.issue(kl, vl, r, pos, tid);
+            const int ntail = min(max(nr - NS, 0), 2);
+            const int nring = nr - ntail;
+            for (int r = 0; r < min(NS, nring); ++r) ring.issue(kl, vl, r, pos, tid);
+            R last, last2;
+            if (ntail > 0) last.load(kl, vl, nring * G * U, pos);
+            if (ntail > 1) last2.load(kl, vl, (nring + 1) * G * U, pos);
             float qr[VEC], kn[VEC], vn[VEC];
             if (l == 0) {
                 const float *t0 = opaque(a.q0) + size_t(tok) * 3 * W + at0;
@@ -2556,11 +2563,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 }
             }
             S st;
-            for (int r = 0; r < nr; ++r) {
-                ring.wait(min(NS - 1, nr - 1 - r));
+            if (ntail > 0) st.add(qr, last, nring * G * U, pos, a.scale_log2);
+            if (ntail > 1) st.add(qr, last2, (nring + 1) * G * U, pos, a.scale_log2);
+            for (int r = 0; r < nring; ++r) {
+                ring.wait(min(NS - 1, nring - 1 - r));
                 R cur;
                 ring.read(r, cur, tid);
-                if (r + NS < nr) ring.issue(kl, vl, r + NS, pos, tid);
+                if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid);
                 st.add(qr, cur, r * G * U, pos, a.scale_log2);
             }
             float sc = 0.0f;
