@@ -1428,11 +1428,10 @@ struct AttnState {
     }
     // Merges the G groups' states of the block: emit(d, a, M, L) for each
     // d < HDP with a = sum of the rescaled accumulators, M the block maximum
-    // and L the rescaled denominator.
+    // and L the rescaled denominator.  sm and sl hold G floats, sacc G * HDP
+    // (16-byte aligned), all LDS.
     template <class Emit>
-    __device__ __forceinline__ void combine(Emit emit) const {
-        __shared__ float sm[G], sl[G];
-        __shared__ __align__(16) float sacc[G * HDP];
+    __device__ __forceinline__ void combine(Emit emit, float *sm, float *sl, float *sacc) const {
         const int g = threadIdx.x / LPK, li = threadIdx.x % LPK;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) sacc[g * HDP + li * VEC + e] = acc[e];
@@ -1483,13 +1482,17 @@ __device__ __forceinline__ void attn_share(const float *__restrict__ qh, int hd,
         cur.load(kslab, vslab, j0, end);
         st.add(qr, cur, j0, end, scale_log2);
     }
-    st.combine([&](int d, float a, float M, float L) {
-        out[d] = a;
-        if (d == 0) {
-            out[HDP] = M;
-            out[HDP + 1] = L;
-        }
-    });
+    __shared__ float sm[G], sl[G];
+    __shared__ __align__(16) float sacc[G * HDP];
+    st.combine(
+        [&](int d, float a, float M, float L) {
+            out[d] = a;
+            if (d == 0) {
+                out[HDP] = M;
+                out[HDP + 1] = L;
+            }
+        },
+        sm, sl, sacc);
 }
 
 // Split-KV decode attention for one query row per sequence.  Block
@@ -2065,23 +2068,33 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
 constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
 
-__device__ __forceinline__ void put_word(uint64_t *p, float v, int tag) {
-    __hip_atomic_store(p, (uint64_t(uint32_t(tag)) << 32) | __float_as_uint(v), __ATOMIC_RELAXED,
-                       __HIP_MEMORY_SCOPE_AGENT);
+// Hand-off words of a sequence whose workgroups share one XCD ("local") go
+// through that XCD's L2 with non-temporal accesses, which skip the CU's L1
+// cache: about 0.45 us a hand-off instead of 0.75 us with agent-scope
+// atomics, which reach the memory side.  Sequences spread over XCDs use the
+// atomics.  Either way every word is one naturally aligned 64-bit access.
+__device__ __forceinline__ void put_word(uint64_t *p, float v, int tag, bool local) {
+    const uint64_t w = (uint64_t(uint32_t(tag)) << 32) | __float_as_uint(v);
+    if (local)
+        __builtin_nontemporal_store(w, p);
+    else
+        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-__device__ __forceinline__ uint64_t get_word(const uint64_t *p) {
+__device__ __forceinline__ uint64_t get_word(const uint64_t *p, bool local) {
+    if (local) return __builtin_nontemporal_load(p);
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // out[i] = the float of the word at addr(i), i < N, once every such word of
 // the wave carries `tag`.
-template <int N, class Addr>
+template <int N, bool LOCAL, class Addr>
 __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], int *abort) {
+    constexpr bool local = LOCAL;
     const uint32_t want = uint32_t(tag);
     uint64_t w[N];
 #pragma unroll
-    for (int i = 0; i < N; ++i) w[i] = get_word(addr(i));
+    for (int i = 0; i < N; ++i) w[i] = get_word(addr(i), local);
     auto ready = [&] {
         bool r = true;
 #pragma unroll
@@ -2092,9 +2105,10 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
         const uint64_t t0 = wall_clock64();
         while (true) {
             __builtin_amdgcn_s_sleep(1);
+            asm volatile("" ::: "memory");  // the words change under us: load them again
 #pragma unroll
             for (int i = 0; i < N; ++i)
-                if (uint32_t(w[i] >> 32) != want) w[i] = get_word(addr(i));
+                if (uint32_t(w[i] >> 32) != want) w[i] = get_word(addr(i), local);
             if (__all(ready())) break;
             if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
             if (wall_clock64() - t0 > kWaitTicks) {
@@ -2210,9 +2224,9 @@ struct PersistRing {
 };
 
 // Records one trace timestamp (thread 0) when a timeline is requested.
-__device__ __forceinline__ void trace_mark(const PersistArgs &a, int step, int l, int which) {
+__device__ __forceinline__ void trace_mark(const PersistArgs &a, int row, int step, int l, int which) {
     if (a.trace && threadIdx.x == 0)
-        a.trace[((size_t(blockIdx.x) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = wall_clock64();
+        a.trace[((size_t(row) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = wall_clock64();
 }
 
 // Row-order index of channel c (the layout RowCtx::ridx enumerates).
@@ -2225,24 +2239,50 @@ __device__ __forceinline__ int row_of(int c) {
 // g = step * layers + l: q/k/v and the attention output of phase g carry tag
 // g + 1; the residual row entering the last block and the logits of a step
 // carry tag step + 1.
+template <bool LOCAL>  // all workgroups of the sequence on one XCD (see put_word)
 struct PersistXch {
+    static constexpr bool local = LOCAL;
     uint64_t *base;
-    int W;
-    __device__ PersistXch(const PersistArgs &a, int b) : base(a.xch + size_t(b) * a.xstride), W(a.s.W) {}
+    int W, V;
+    int row;  // this workgroup's row of the trace (3 * batch teams, then batch * H heads)
+    __device__ PersistXch(const PersistArgs &a, int b, int row_)
+        : base(a.xch + size_t(b) * a.xstride), W(a.s.W), V(a.s.V), row(row_) {}
     // q (t = 0), k (1) or v (2) of phase g, double-buffered by phase parity
     __device__ uint64_t *qkv(int g, int t) const { return base + size_t((g & 1) * 3 + t) * W; }
     __device__ uint64_t *y() const { return base + size_t(6) * W; }     // attention output
     __device__ uint64_t *xrow() const { return base + size_t(7) * W; }  // residual row
     __device__ uint64_t *logits() const { return base + size_t(8) * W; }  // token order
+    __device__ uint64_t *xcd() const { return base + size_t(8) * W + V; }  // each workgroup's XCD
+    __device__ void put(uint64_t *p, float v, int tag) const { put_word(p, v, tag, LOCAL); }
+    template <int N, class Addr>
+    __device__ void take(Addr addr, int tag, float (&out)[N], int *abort) const {
+        take_words<N, LOCAL>(addr, tag, out, abort);
+    }
 };
+
+// All 3 + H workgroups of a sequence publish their XCD and read everyone's:
+// the sequence's hand-offs use the XCD-local protocol when they agree.  This
+// first exchange always uses the agent-scope atomics.
+__device__ __forceinline__ bool persistent_handshake(const PersistArgs &a, const PersistXch<false> &xc, int role) {
+    const int R = 3 + a.s.H;
+    uint32_t xcd;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcd));
+    xcd &= 0xf;
+    if (threadIdx.x == 0) xc.put(xc.xcd() + role, float(xcd), 1);
+    float seen[1];
+    const int k = int(threadIdx.x) < R ? int(threadIdx.x) : 0;
+    xc.take<1>([&](int) { return xc.xcd() + k; }, 1, seen, a.abort);
+    return __syncthreads_and(seen[0] == float(xcd)) != 0;
+}
 
 // Logits of tokens [t0, t1) for the row-order normalised row xn (in LDS), as
 // words tagged `tag`: wave w takes tokens t0 + w, t0 + w + NW, ...; each lane
 // a contiguous W/64 channels of the row-order token vectors E.  T tokens'
 // loads per wave are in flight before their dot products and wave sums.
-template <int NW, int W>
-__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, uint64_t *out,
+template <int NW, int W, class X>
+__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, const X &xc,
                                                       int t0, int t1, int tag, int lane, int wave) {
+    uint64_t *out = xc.logits();
     constexpr int CW = W / 64, T = 96 / CW < 4 ? 4 : (96 / CW > 16 ? 16 : 96 / CW);
     float xr[CW];
 #pragma unroll
@@ -2274,7 +2314,7 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
             for (int k = 0; k < CW; ++k) acc = fmaf(xr[k], e[u][k], acc);
             acc = wave_sum(acc);
             const int t = base + u * NW;
-            if (lane == 0 && t < t1) put_word(out + t, acc, tag);
+            if (lane == 0 && t < t1) xc.put(out + t, acc, tag);
         }
     }
 }
@@ -2307,12 +2347,12 @@ struct PersistLds {
 
 // Inputs of the post-attention half of phase g: the attention output y and
 // the row's value vector v.
-template <int NW, int CPL, int GL>
-__device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c,
-                                                 const PersistXch &xc, int g, float (&y)[CPL], float (&v)[CPL]) {
+template <int NW, int CPL, int GL, class X>
+__device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c, const X &xc,
+                                                 int g, float (&y)[CPL], float (&v)[CPL]) {
     float yv[2 * CPL];
     const uint64_t *yw = xc.y(), *vw = xc.qkv(g, 2);
-    take_words<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
+    xc.template take<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         y[j] = yv[j];
@@ -2323,15 +2363,15 @@ __device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const Row
 // The step's token from the published logits, drawn by every workgroup of the
 // sequence alike (same logits, same sampler state in its LDS); the logits are
 // also copied to `out` when given.
-template <int NW, bool MARK>
-__device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const PersistXch &xc, int step,
-                                               const PersistLds &m, float *out) {
+template <int NW, bool MARK, class X>
+__device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc, int step, const PersistLds &m,
+                                               float *out) {
     constexpr int NL = kPersistVocab / (64 * NW);  // logit words per thread
     const int V = a.s.V;
     float lg[NL];
-    take_words<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
+    xc.template take<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
                    a.abort);
-    if (MARK) trace_mark(a, step, a.layers, 0);
+    if (MARK) trace_mark(a, xc.row, step, a.layers, 0);
 #pragma unroll
     for (int i = 0; i < NL; ++i) {
         const int t = int(threadIdx.x) + i * 64 * NW;
@@ -2346,10 +2386,9 @@ __device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const Persi
 
 // Post-attention half of the last block on the residual row x, then logit
 // slice `slice` of the 3 + H slices of the vocabulary.
-template <int NW, int CPL, int GL, int DEPTH>
+template <int NW, int CPL, int GL, int DEPTH, class X>
 __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowCtx<NW, CPL, GL> &c, float (&x)[CPL],
-                                                      const PersistXch &xc, int step, int slice,
-                                                      const PersistLds &m) {
+                                                      const X &xc, int step, int slice, const PersistLds &m) {
     constexpr int W = RowCtx<NW, CPL, GL>::W;
     constexpr bool FIXED = DEPTH > 0;
     constexpr int D = FIXED ? DEPTH : 1;
@@ -2367,15 +2406,15 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
 #pragma unroll
     for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
     __syncthreads();
-    if (slice >= 3) trace_mark(a, step, L, 0);
+    if (slice >= 3) trace_mark(a, xc.row, step, L, 0);
     const int nb = 3 + s.H, V = s.V;
-    persistent_head_slice<NW, W>(m.xn, a.E, xc.logits(), slice * V / nb, (slice + 1) * V / nb, step + 1, c.lane,
-                                 c.wave);
+    persistent_head_slice<NW, W>(m.xn, a.E, xc, slice * V / nb, (slice + 1) * V / nb, step + 1, c.lane, c.wave);
 }
 
 // Mesh team `team` of sequence b.
-template <int NW, int CPL, int GL, int DEPTH, int HDP>
-__device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m) {
+template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
+__device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m,
+                                                const X &xc) {
     using Ctx = RowCtx<NW, CPL, GL>;
     constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
@@ -2383,7 +2422,6 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     const Shape &s = a.s;
     Ctx c(m.xch, m.red);
     const int dim = c.dim(), L = a.layers, V = s.V;
-    const PersistXch xc(a, b);
     int len = a.len[b];
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
     if (threadIdx.x == 0) *m.rng = a.rng[b];
@@ -2396,15 +2434,15 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
         float x[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
-        trace_mark(a, step, 0, 0);
+        trace_mark(a, xc.row, step, 0, 0);
         // Layer 0's q, k and v are the token's rows of the layer-0 table, which
         // the attention blocks read themselves: the teams start at block 0's
         // post-attention half.
         if (L == 1 && team == 0) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) put_word(xc.xrow() + c.ridx(j), x[j], step + 1);
+            for (int j = 0; j < CPL; ++j) xc.put(xc.xrow() + c.ridx(j), x[j], step + 1);
         }
-        trace_mark(a, step, 0, 1);
+        trace_mark(a, xc.row, step, 0, 1);
         for (int l = 1; l < L; ++l) {
             const int g = step * L + l;
             const float *wb = block(l), *wq = block(l - 1);
@@ -2414,12 +2452,12 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
             float y[CPL], v[CPL];
             take_post_inputs(a, c, xc, g - 1, y, v);
-            trace_mark(a, step, l, 0);
+            trace_mark(a, xc.row, step, l, 0);
             row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
             if (l + 1 == L && team == 0) {
                 // The attention blocks finish the last block from this row.
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) put_word(xc.xrow() + c.ridx(j), x[j], step + 1);
+                for (int j = 0; j < CPL; ++j) xc.put(xc.xrow() + c.ridx(j), x[j], step + 1);
             }
             const float inv = row_inv_rms(c, x, 3);
             float n[CPL];
@@ -2429,13 +2467,13 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             if (team < 2) row_qk_rope(c, n, rope_pair(a.rope, pos, dim, s.half), s);
             uint64_t *out = xc.qkv(g, team);
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) put_word(out + c.ridx(j), n[j], g + 1);
-            trace_mark(a, step, l, 1);
+            for (int j = 0; j < CPL; ++j) xc.put(out + c.ridx(j), n[j], g + 1);
+            trace_mark(a, xc.row, step, l, 1);
         }
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, team, m);
         // The launch's last logits are kept for callers that read them.
         tok = draw_token<NW, true>(a, xc, step, m, team == 0 && step + 1 == a.steps ? a.logits + size_t(b) * V : nullptr);
-        trace_mark(a, step, L, 1);
+        trace_mark(a, xc.row, step, L, 1);
         if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
         ++len;
     }
@@ -2478,8 +2516,9 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, int pos, c
 // steps and enter this step's attention from registers, so the cached rows
 // read each layer [0, pos) were all written before the launch or by this
 // block, and the first rounds of them load while the inputs are awaited.
-template <int NW, int CPL, int GL, int DEPTH, int HDP>
-__device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m) {
+template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
+__device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m,
+                                                     const X &xc) {
     using Ctx = RowCtx<NW, CPL, GL>;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     using S = AttnState<HDP, 64 * NW, Ring::UL>;
@@ -2489,7 +2528,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
     const Shape &s = a.s;
     constexpr int W = Ctx::W;
     const int len0 = a.len[b], L = a.layers;
-    const PersistXch xc(a, b);
+
     const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
     static_assert(VEC % NW == 0, "lane dims must cover whole row-order columns");
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len0 - 1];
@@ -2535,13 +2574,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 if (grp == 0) {
                     uint64_t *vo = xc.qkv(g, 2) + at0;
 #pragma unroll
-                    for (int e = 0; e < VEC; ++e) put_word(vo + (e % NW) * 64 + e / NW, vn[e], g + 1);
+                    for (int e = 0; e < VEC; ++e) xc.put(vo + (e % NW) * 64 + e / NW, vn[e], g + 1);
                 }
             } else {
                 float qkv[3 * VEC];
                 const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
                                *vw = opaque(xc.qkv(g, 2)) + at0;
-                take_words<3 * VEC>(
+                xc.template take<3 * VEC>(
                     [&](int i) {
                         const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
                         return base + ((i % VEC) % NW * 64 + (i % VEC) / NW);
@@ -2554,7 +2593,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     vn[e] = qkv[2 * VEC + e];
                 }
             }
-            trace_mark(a, step, l, 0);
+            trace_mark(a, xc.row, step, l, 0);
             if (grp == 0) {
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
@@ -2578,8 +2617,12 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             sc = group_sum<LPK>(sc) * a.scale_log2;
             if (grp == 0) st.add_one(sc, vn);
             uint64_t *yw = xc.y();
-            st.combine([&](int d, float acc, float, float den) { put_word(yw + row_of<NW>(h * HDP + d), acc / den, g + 1); });
-            trace_mark(a, step, l, 1);
+            // The merge borrows the LDS of the logits row and of the row
+            // reductions, both idle during the layer loop.
+            static_assert(G * HDP <= kPersistVocab && 2 * G <= 8 * Ctx::SLOT, "merge scratch");
+            st.combine([&](int d, float acc, float, float den) { xc.put(yw + row_of<NW>(h * HDP + d), acc / den, g + 1); },
+                       m.red, m.red + G, m.row);
+            trace_mark(a, xc.row, step, l, 1);
         }
         // The last block from the published residual row, then this block's
         // logits.  The thread index is hidden from the optimiser so the lane
@@ -2589,9 +2632,9 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
         asm volatile("" : "+v"(tid));
         Ctx c(m.xch, m.red, tid);
         float x[CPL];
-        take_words<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
+        xc.template take<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
-        trace_mark(a, step, L, 1);
+        trace_mark(a, xc.row, step, L, 1);
         if (step + 1 < a.steps) tok = draw_token<NW, false>(a, xc, step, m, nullptr);
     }
 }
@@ -2615,13 +2658,25 @@ persistent_decode_kernel(PersistArgs a) {
     __shared__ uint64_t exp_tab[32];
     stage_exp_table(exp_tab);  // the teams' first barrier comes long before their first draw
     const PersistLds m{xch, red, xn, row, redf, ring, redi, redd, &rng, exp_tab};
-    const int blk = blockIdx.x;
-    if (blk < 3 * a.batch) {
-        persistent_team<NW, CPL, GL, DEPTH, HDP>(a, blk / 3, blk % 3, m);
-    } else {
-        const int i = blk - 3 * a.batch;
-        persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, i / a.s.H, i % a.s.H, m);
-    }
+    // Workgroup i runs on XCD i % 8 when the dispatcher deals workgroups out
+    // round-robin, as it does on MI355X: the 3 + H workgroups of a sequence are
+    // i = x + 8 * (R * q + r) for sequence x + 8q and role r, all on XCD x.
+    // (The handshake checks it; any other placement only costs speed.)
+    const int R = 3 + a.s.H, x = int(blockIdx.x) % 8, k = int(blockIdx.x) / 8;
+    const int b = x + 8 * (k / R), r = k % R;
+    if (b >= a.batch) return;
+    const int trow = r < 3 ? 3 * b + r : 3 * a.batch + b * a.s.H + (r - 3);
+    const PersistXch<false> far(a, b, trow);
+    auto run = [&](const auto &xc) {
+        if (r < 3)
+            persistent_team<NW, CPL, GL, DEPTH, HDP>(a, b, r, m, xc);
+        else
+            persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc);
+    };
+    if (persistent_handshake(a, far, r))
+        run(PersistXch<true>(a, b, trow));
+    else
+        run(far);
 }
 
 // Layer-0 table: row (token v, team t) is team t's mesh of block 0 on the
@@ -2974,9 +3029,9 @@ const void *persistent_kernel(const Shape &s) {
     return k;
 }
 
-int persistent_blocks(const Shape &s, int batch) { return 3 * batch + batch * s.H; }
+int persistent_blocks(const Shape &s, int batch) { return 8 * (3 + s.H) * ((batch + 7) / 8); }
 
-size_t persistent_exchange_words(const Shape &s) { return (size_t(8) * s.W + s.V + 31) / 32 * 32; }
+size_t persistent_exchange_words(const Shape &s) { return (size_t(8) * s.W + s.V + 3 + s.H + 31) / 32 * 32; }
 
 bool persistent_fits(const Shape &s, int batch, int device) {
     const void *f = persistent_kernel(s);
