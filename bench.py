@@ -175,7 +175,7 @@ def pmc_traffic(args, config, batch):
         # rocprofv3 may exit with a segmentation fault after the program ends
         # (cooperative launches); the counter file is complete by then.
         out = tempfile.mkdtemp(prefix="mg_pmc_")
-        cmd = ["timeout", "-s", "KILL", "120", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
+        cmd = ["timeout", "-s", "KILL", "90", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
                "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe",
                "--steps", str(args.steps), "--prompt", str(args.prompt), "--batch", str(batch)]
         res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
@@ -259,6 +259,18 @@ def main():
     config = G.named_config("mid")
     if args.prompt + args.steps > config.context or args.prompt + args.warmup > config.context:
         sys.exit(f"prompt + steps must stay within the context ({config.context})")
+    # The counter runs go first, while this process has not touched the GPU:
+    # the profiled child is then the only process on it.
+    traffic = None
+    pmc = None
+    if not args.no_pmc:
+        try:
+            pmc = pmc_traffic(args, config, args.batch)
+        except Exception as exc:  # counters are optional evidence, never the result
+            sys.stderr.write(f"pmc collection failed: {exc}\n")
+            pmc = None
+        if pmc:
+            traffic = round(pmc["FETCH_SIZE"] + pmc["WRITE_SIZE"])
     temperature = 1.0
     prompts = prompts_for(config, args.batch, args.prompt)
     hip = Hip()
@@ -273,17 +285,6 @@ def main():
     positions = args.prompt + np.arange(args.steps)
     total_bytes = float(sum(step_bytes(config, args.batch, p) for p in positions))
     gbps = total_bytes / (ms / 1000.0) / 1e9
-
-    traffic = None
-    pmc = None
-    if not args.no_pmc:
-        try:
-            pmc = pmc_traffic(args, config, args.batch)
-        except Exception as exc:  # counters are optional evidence, never the result
-            sys.stderr.write(f"pmc collection failed: {exc}\n")
-            pmc = None
-        if pmc:
-            traffic = round(pmc["FETCH_SIZE"] + pmc["WRITE_SIZE"])
 
     result = {
         "metric": METRIC,
