@@ -1374,6 +1374,10 @@ struct AttnRound {
     }
 };
 
+// 2^x by the hardware instruction (about 1 ulp).  Results below the normal
+// range flush to zero, which the softmax sums absorb: their largest term is 1.
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // Online-softmax state (reference.rs:510-554) of one key group: scores live in
 // the log2 domain, and q stays unscaled (each score is scaled instead) so its
 // load does not hold back the first K/V loads.
@@ -1399,11 +1403,11 @@ struct AttnState {
         for (int u = 1; u < U; ++u) cm = fmaxf(cm, sc[u]);
         const float mn = fmaxf(m, cm);
         if (mn != -INFINITY) {
-            const float alpha = exp2f(m - mn);
+            const float alpha = exp2_fast(m - mn);
             float pu[U], ps = 0.0f;
 #pragma unroll
             for (int u = 0; u < U; ++u) {
-                pu[u] = exp2f(sc[u] - mn);
+                pu[u] = exp2_fast(sc[u] - mn);
                 ps += pu[u];
             }
             l = l * alpha + ps;
@@ -1420,7 +1424,7 @@ struct AttnState {
     // Folds in one key whose (log2-domain) score is sc and value row v.
     __device__ __forceinline__ void add_one(float sc, const float (&v)[VEC]) {
         const float mn = fmaxf(m, sc);
-        const float alpha = exp2f(m - mn), p = exp2f(sc - mn);
+        const float alpha = exp2_fast(m - mn), p = exp2_fast(sc - mn);
         l = l * alpha + p;
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] = fmaf(p, v[e], acc[e] * alpha);
@@ -1443,10 +1447,10 @@ struct AttnState {
         float M = -INFINITY;
         for (int k = 0; k < G; ++k) M = fmaxf(M, sm[k]);
         float L = 0.0f;
-        for (int k = 0; k < G; ++k) L += exp2f(sm[k] - M) * sl[k];
+        for (int k = 0; k < G; ++k) L += exp2_fast(sm[k] - M) * sl[k];
         for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
             float a = 0.0f;
-            for (int k = 0; k < G; ++k) a += exp2f(sm[k] - M) * sacc[k * HDP + d];
+            for (int k = 0; k < G; ++k) a += exp2_fast(sm[k] - M) * sacc[k * HDP + d];
             emit(d, a, M, L);
         }
         __syncthreads();
@@ -2620,8 +2624,11 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // The merge borrows the LDS of the logits row and of the row
             // reductions, both idle during the layer loop.
             static_assert(G * HDP <= kPersistVocab && 2 * G <= 8 * Ctx::SLOT, "merge scratch");
-            st.combine([&](int d, float acc, float, float den) { xc.put(yw + row_of<NW>(h * HDP + d), acc / den, g + 1); },
-                       m.red, m.red + G, m.row);
+            st.combine(
+                [&](int d, float acc, float, float den) {
+                    xc.put(yw + row_of<NW>(h * HDP + d), acc * __builtin_amdgcn_rcpf(den), g + 1);
+                },
+                m.red, m.red + G, m.row);
             trace_mark(a, xc.row, step, l, 1);
         }
         // The last block from the published residual row, then this block's
