@@ -1444,14 +1444,42 @@ struct AttnState {
             sl[g] = l;
         }
         __syncthreads();
-        float M = -INFINITY;
-        for (int k = 0; k < G; ++k) M = fmaxf(M, sm[k]);
-        float L = 0.0f;
-        for (int k = 0; k < G; ++k) L += exp2_fast(sm[k] - M) * sl[k];
-        for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
-            float a = 0.0f;
-            for (int k = 0; k < G; ++k) a += exp2_fast(sm[k] - M) * sacc[k * HDP + d];
-            emit(d, a, M, L);
+        if constexpr (TH >= HDP) {
+            // One dim per thread, with every LDS read issued before the first
+            // is used (the empty asm keeps the scheduler from interleaving
+            // each read with its use and waiting out each latency in turn).
+            if (int(threadIdx.x) < HDP) {
+                const int d = threadIdx.x;
+                float mk[G], lk[G], ak[G];
+#pragma unroll
+                for (int k = 0; k < G; ++k) {
+                    mk[k] = sm[k];
+                    lk[k] = sl[k];
+                    ak[k] = sacc[k * HDP + d];
+                }
+                asm volatile("" ::: "memory");
+                float M = -INFINITY;
+#pragma unroll
+                for (int k = 0; k < G; ++k) M = fmaxf(M, mk[k]);
+                float L = 0.0f, a = 0.0f;
+#pragma unroll
+                for (int k = 0; k < G; ++k) {
+                    const float f = exp2_fast(mk[k] - M);
+                    L += f * lk[k];
+                    a += f * ak[k];
+                }
+                emit(d, a, M, L);
+            }
+        } else {
+            float M = -INFINITY;
+            for (int k = 0; k < G; ++k) M = fmaxf(M, sm[k]);
+            float L = 0.0f;
+            for (int k = 0; k < G; ++k) L += exp2_fast(sm[k] - M) * sl[k];
+            for (int d = threadIdx.x; d < HDP; d += blockDim.x) {
+                float a = 0.0f;
+                for (int k = 0; k < G; ++k) a += exp2_fast(sm[k] - M) * sacc[k * HDP + d];
+                emit(d, a, M, L);
+            }
         }
         __syncthreads();
     }
