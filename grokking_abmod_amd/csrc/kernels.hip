@@ -1740,19 +1740,15 @@ __constant__ uint64_t kExp2Tab[32] = {
 // float inputs (checked on the host against glibc 2.35); glibc's build for
 // hosts without FMA rounds 2 of them differently.
 // `tab` is kExp2Tab staged in LDS (a per-lane lookup in constant memory costs
-// a memory round trip per call).
+// a memory round trip per call).  Branch-free, so that several calls
+// interleave: the cases outside the method's range (x > 0x1.62e42ep6 gives
+// +inf, x < -0x1.9fe368p6 and -inf give 0, NaN gives NaN) are selected after
+// it runs on x clamped to [-104, 89].
 __device__ __forceinline__ float expf_rounded(float x, const uint64_t *tab) {
     constexpr double N = 32.0, InvLn2N = 0x1.71547652b82fep+0 * N, Shift = 0x1.8p+52;
     constexpr double C0 = 0x1.c6af84b912394p-5 / (N * N * N), C1 = 0x1.ebfce50fac4f3p-3 / (N * N),
                      C2 = 0x1.62e42ff0c52d6p-1 / N;
-    const uint32_t ux = __float_as_uint(x), abstop = (ux >> 20) & 0x7ff;
-    if (abstop >= 0x42b) {  // |x| >= 88, or not finite
-        if (ux == 0xff800000u) return 0.0f;
-        if (abstop >= 0x7f8) return x + x;
-        if (x > 0x1.62e42ep6f) return INFINITY;
-        if (x < -0x1.9fe368p6f) return 0.0f;
-    }
-    const double xd = double(x);
+    const double xd = double(fminf(fmaxf(x, -104.0f), 89.0f));
     double kd = InvLn2N * xd + Shift;  // rounds k to the nearest integer
     const uint64_t ki = uint64_t(__double_as_longlong(kd));
     kd -= Shift;
@@ -1761,7 +1757,10 @@ __device__ __forceinline__ float expf_rounded(float x, const uint64_t *tab) {
     const double z = fma(C0, r, C1), r2 = r * r;
     double y = fma(C2, r, 1.0);
     y = fma(z, r2, y);
-    return float(y * sc);
+    float e = float(y * sc);
+    e = x > 0x1.62e42ep6f ? INFINITY : e;
+    e = x < -0x1.9fe368p6f ? 0.0f : e;
+    return x != x ? x + x : e;
 }
 
 // Copies kExp2Tab to `tab` (32 words of LDS); a barrier must follow before use.
@@ -1969,6 +1968,110 @@ __device__ __forceinline__ int choose_token(const float *row, int V, float tempe
     return token;
 }
 
+// The lowest lane's value of v among the lanes where `has` holds, else `none`
+// (a ballot and a lane read instead of a reduction).
+__device__ __forceinline__ int first_lane_value(bool has, int v, int none) {
+    const uint64_t mask = __ballot(has);
+    return mask ? __builtin_amdgcn_readlane(v, int(__builtin_ctzll(mask))) : none;
+}
+
+// choose_token's decision made by one wave on its own: lane l holds the
+// logits of the contiguous run [l*R, l*R + R) of tokens in lg[0..R),
+// R = ceil(V / 64) <= RMAX, and u is the generator's draw (made by the
+// caller, so that it is ready before the logits are).  Every lane returns the
+// token.  Only a near-tie touches memory: the wave writes its p_i to
+// scratch[0..V) (LDS; several waves may share it, as they write the same
+// values) and runs the sequential f32 process on them.
+template <int RMAX>
+__device__ __forceinline__ int wave_choose_token(const float (&lg)[RMAX], int V, float temperature, float u,
+                                                 const uint64_t *exp_tab, int *flags, float *scratch) {
+    static_assert(RMAX % 4 == 0, "runs are handled four tokens at a time");
+    // Every per-token step below is straight-line code in blocks of four
+    // tokens (a lane's tokens past V are masked by selects), so the f64
+    // evaluations of neighbouring tokens overlap; only `k < R` branches, and
+    // it is wave-uniform.  Since the runs ascend with the lane, the first
+    // token with a property lies in the lowest lane that has one.
+    const int R = (V + 63) / 64, i0 = int(threadIdx.x & 63) * R;
+    float mx = -INFINITY;
+    bool bad = false;
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k) {
+        if (k < R) {
+            const bool v = i0 + k < V;
+            bad = bad || (v && !isfinite(lg[k]));
+            mx = v ? fmaxf(mx, lg[k]) : mx;
+        }
+    }
+    mx = wave_max(mx);
+    if (__ballot(bad) && threadIdx.x == 0) atomicOr(flags, 1);
+    if (temperature == 0.0f) {
+        int best = INT_MAX;
+#pragma unroll
+        for (int k = RMAX - 1; k >= 0; --k)
+            if (k < R && i0 + k < V && lg[k] == mx) best = i0 + k;
+        return first_lane_value(best != INT_MAX, best, 0);
+    }
+    float pc[RMAX];
+    auto exps = [&](auto scaled) {
+#pragma unroll
+        for (int c = 0; c < RMAX / 4; ++c) {
+            if (4 * c < R) {
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const int k = 4 * c + q;
+                    const float p = expf_rounded(scaled(lg[k]), exp_tab);
+                    pc[k] = k < R && i0 + k < V ? p : 0.0f;
+                }
+            }
+        }
+    };
+    // (l - max) / T in f32 (gpu.rs:2037); division by 1 is exact, so T = 1
+    // skips it.
+    if (temperature == 1.0f)
+        exps([&](float l) { return l - mx; });
+    else
+        exps([&](float l) { return (l - mx) / temperature; });
+    double mine = 0.0;  // the masked tokens add exact zeros
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k)
+        if (k < R) mine += double(pc[k]);
+    const double incl = wave_inclusive_sum(mine);
+    const uint64_t sb = __builtin_bit_cast(uint64_t, incl);
+    const double S = __builtin_bit_cast(
+        double, (uint64_t(uint32_t(__builtin_amdgcn_readlane(int(uint32_t(sb >> 32)), 63))) << 32) |
+                    uint32_t(__builtin_amdgcn_readlane(int(uint32_t(sb)), 63)));
+    const double e = 0x1p-24, slack = 1e-12 * S;
+    const double g = double(V + 2) * e * 1.01;
+    const double s_lo = S * (1.0 - g) - slack, s_hi = S * (1.0 + g) + slack;
+    const double beta = double(V + 2) * e * s_hi * 1.01 + slack;
+    const double lo = double(u) * s_lo - beta, hi = double(u) * s_hi + beta;
+    double prefix = incl - mine;
+    int key = INT_MAX;
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k) {
+        if (k < R) {
+            prefix += double(pc[k]);
+            const bool first = key == INT_MAX && i0 + k < V && !(prefix < lo);
+            key = first ? 2 * (i0 + k) + (prefix > hi ? 0 : 1) : key;
+        }
+    }
+    key = first_lane_value(key != INT_MAX, key, INT_MAX);
+    if (key == INT_MAX) return V - 1;
+    if (!(key & 1)) return key >> 1;
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k)
+        if (k < R && i0 + k < V) scratch[i0 + k] = pc[k];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    return sequential_pick([&](int t) { return scratch[t]; }, V, u);
+}
+
+// Random::unit (src/mesh.rs:263-265): one SplitMix64 draw per sampled token.
+__device__ __forceinline__ float rng_unit(uint64_t &state) {
+    return float(uint32_t(splitmix_next(state) >> 40)) / 16777216.0f;
+}
+
 __device__ __forceinline__ void append_token(uint32_t *tokens, int tok_stride, int *len, int b, int token) {
     if (threadIdx.x == 0) {
         const int L = len[b];
@@ -1998,6 +2101,30 @@ sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64
     __syncthreads();
     const int token = choose_token(staged ? row : src, V, temperature, rng + b, flags,
                                    SampleLds{redf, redi, redd, tab}, staged ? row : nullptr);
+    append_token(tokens, tok_stride, len, b, token);
+}
+
+// The same choice made by one wave per sequence (wave_choose_token, the
+// persistent decode's sampler), for vocabularies of at most kWaveSampleVocab.
+constexpr int kWaveSampleVocab = 1024;
+
+__global__ void __launch_bounds__(64)
+wave_sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64_t *rng, uint32_t *tokens,
+                   int tok_stride, int *len, int *flags) {
+    constexpr int RMAX = kWaveSampleVocab / 64;
+    __shared__ uint64_t tab[32];
+    __shared__ float scratch[kWaveSampleVocab];
+    const int b = blockIdx.x, R = (V + 63) / 64, i0 = int(threadIdx.x) * R;
+    const float *src = logits + size_t(b) * V;
+    float lg[RMAX];
+#pragma unroll
+    for (int k = 0; k < RMAX; ++k) lg[k] = k < R && i0 + k < V ? src[i0 + k] : 0.0f;
+    stage_exp_table(tab);
+    __syncthreads();
+    uint64_t state = rng[b];
+    const float u = temperature == 0.0f ? 0.0f : rng_unit(state);  // greedy draws nothing
+    const int token = wave_choose_token(lg, V, temperature, u, tab, flags, scratch);
+    if (threadIdx.x == 0) rng[b] = state;
     append_token(tokens, tok_stride, len, b, token);
 }
 
@@ -2099,6 +2226,7 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
 constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
+static_assert(kPersistVocab <= kWaveSampleVocab, "the persistent path draws with the wave sampler");
 
 // Hand-off words of a sequence whose workgroups share one XCD ("local") go
 // through that XCD's L2 with non-temporal accesses, which skip the CU's L1
@@ -2245,10 +2373,10 @@ struct KvRing {
 // slots when those do not fit.
 template <int NW, int CPL, int GL, int HDP>
 struct PersistRing {
-    static constexpr int W = 64 * NW * CPL, gc = 64 / GL, ga = 64 * NW / (HDP / 4);
+    static constexpr int W = 64 * NW * CPL, gc = 64 / GL;
     static constexpr int budget = 160 * 1024 * NW / 8;
-    static constexpr int other = 4 * (2 * W + 8 * CPL * NW * gc + W + kPersistVocab + 2 * NW + 2 * ga + ga * HDP) +
-                                 8 * (NW + 1) + 8 + 256 + 64;
+    // persistent_decode_kernel's other LDS: xch, red, xn, row and the exp table
+    static constexpr int other = 4 * (2 * W + 8 * CPL * NW * gc + W + kPersistVocab) + 256 + 64;
     static constexpr int fit(int ul) { return (budget - other) / (2 * ul * NW * 1024); }
     static constexpr int UL = fit(4) >= 2 ? 4 : (fit(2) >= 2 ? 2 : 1);
     static constexpr int NS = UL == 4 ? 2 : (fit(UL) >= 4 ? 4 : (fit(UL) >= 3 ? 3 : 2));
@@ -2371,10 +2499,8 @@ __device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const fl
 }
 
 struct PersistLds {
-    float *xch, *red, *xn, *row, *redf, *ring;
-    int *redi;
-    double *redd;
-    uint64_t *rng, *exp_tab;
+    float *xch, *red, *xn, *row, *ring;
+    uint64_t *exp_tab;
 };
 
 // Inputs of the post-attention half of phase g: the attention output y and
@@ -2392,28 +2518,45 @@ __device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const Row
     }
 }
 
-// The step's token from the published logits, drawn by every workgroup of the
-// sequence alike (same logits, same sampler state in its LDS); the logits are
-// also copied to `out` when given.
-template <int NW, bool MARK, class X>
-__device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc, int step, const PersistLds &m,
-                                               float *out) {
-    constexpr int NL = kPersistVocab / (64 * NW);  // logit words per thread
-    const int V = a.s.V;
-    float lg[NL];
-    xc.template take<NL>([&](int i) { return xc.logits() + min(int(threadIdx.x) + i * 64 * NW, V - 1); }, step + 1, lg,
-                   a.abort);
-    if (MARK) trace_mark(a, xc.row, step, a.layers, 0);
+// The step's token from the published logits, drawn by each wave on its own:
+// every wave of every workgroup of the sequence takes the same words and
+// keeps the same generator state (`state`, wave-uniform), so all draw the same
+// token, with no LDS exchange and no barrier (wave_choose_token).  The logits
+// are also copied to `out` when given.
+template <bool MARK, class X>
+__device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc, int step, uint64_t &state,
+                                               const PersistLds &m, float *out) {
+    constexpr int RMAX = kPersistVocab / 64;
+    static_assert(RMAX % 4 == 0, "logit words are taken four at a time");
+    // Lane offsets and word addresses are formed here from a thread index and
+    // base hidden from the optimiser: hoisted out of the step loop, they would
+    // occupy dozens of registers through the layers.
+    int tid = int(threadIdx.x);
+    asm volatile("" : "+v"(tid));
+    const int V = a.s.V, R = (V + 63) / 64, i0 = (tid & 63) * R;
+    const uint64_t *lw = opaque(xc.logits());
+    const float u = a.temperature == 0.0f ? 0.0f : rng_unit(state);  // greedy draws nothing
+    float lg[RMAX];
 #pragma unroll
-    for (int i = 0; i < NL; ++i) {
-        const int t = int(threadIdx.x) + i * 64 * NW;
-        if (t < V) m.row[t] = lg[i];
+    for (int c = 0; c < RMAX / 4; ++c) {
+        if (4 * c < R) {  // uniform: a small vocabulary polls only its words
+            float t[4];
+            xc.template take<4>([&](int k) { return lw + min(i0 + 4 * c + k, V - 1); }, step + 1, t, a.abort);
+#pragma unroll
+            for (int k = 0; k < 4; ++k) lg[4 * c + k] = t[k];
+        }
     }
-    __syncthreads();
-    if (out)
-        for (int t = threadIdx.x; t < V; t += blockDim.x) out[t] = m.row[t];
-    return uint32_t(
-        choose_token(m.row, V, a.temperature, m.rng, a.flags, SampleLds{m.redf, m.redi, m.redd, m.exp_tab}, m.row));
+    if (MARK) trace_mark(a, xc.row, step, a.layers, 0);
+    if (out && tid < 64) {
+        float *o = opaque(out) + i0;
+#pragma unroll
+        for (int k = 0; k < RMAX; ++k)
+            if (k < R && i0 + k < V) o[k] = lg[k];
+    }
+    // A near-tie's scratch is the mesh exchange buffer (2W >= V floats): the
+    // last block's meshes are done before any logit is published, and the
+    // next meshes follow barriers that this wave reaches only after drawing.
+    return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
 }
 
 // Post-attention half of the last block on the residual row x, then logit
@@ -2456,7 +2599,7 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     const int dim = c.dim(), L = a.layers, V = s.V;
     int len = a.len[b];
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
-    if (threadIdx.x == 0) *m.rng = a.rng[b];
+    uint64_t rng = a.rng[b];  // the sampler's state, the same in every wave
     const size_t gA = 2 * size_t(W) * s.A;           // floats of one attention-depth mesh
     const size_t blk = 4 * gA + 2 * size_t(W) * s.F;  // floats of one block: q, k, v, proj, ffn
     auto block = [&](int l) { return a.w + a.block0 + size_t(l) * blk; };
@@ -2504,14 +2647,15 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
         }
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, team, m);
         // The launch's last logits are kept for callers that read them.
-        tok = draw_token<NW, true>(a, xc, step, m, team == 0 && step + 1 == a.steps ? a.logits + size_t(b) * V : nullptr);
+        tok = draw_token<true>(a, xc, step, rng, m,
+                               team == 0 && step + 1 == a.steps ? a.logits + size_t(b) * V : nullptr);
         trace_mark(a, xc.row, step, L, 1);
         if (team == 0 && threadIdx.x == 0) a.tokens[size_t(b) * a.tok_stride + len] = tok;
         ++len;
     }
     if (team == 0 && threadIdx.x == 0) {
         a.len[b] = len;
-        a.rng[b] = *m.rng;
+        a.rng[b] = rng;
     }
 }
 
@@ -2564,7 +2708,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
     const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
     static_assert(VEC % NW == 0, "lane dims must cover whole row-order columns");
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len0 - 1];
-    if (threadIdx.x == 0) *m.rng = a.rng[b];
+    uint64_t rng = a.rng[b];
     for (int step = 0; step < a.steps; ++step) {
         const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
@@ -2670,7 +2814,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
         xc.template take<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
         trace_mark(a, xc.row, step, L, 1);
-        if (step + 1 < a.steps) tok = draw_token<NW, false>(a, xc, step, m, nullptr);
+        if (step + 1 < a.steps) tok = draw_token<false>(a, xc, step, rng, m, nullptr);
     }
 }
 
@@ -2684,15 +2828,11 @@ persistent_decode_kernel(PersistArgs a) {
     __shared__ float red[8 * RowCtx<NW, CPL, GL>::SLOT];
     __shared__ __align__(16) float xn[W];
     __shared__ __align__(16) float row[kPersistVocab];
-    __shared__ float redf[NW];
-    __shared__ int redi[NW];
-    __shared__ double redd[NW + 1];
-    __shared__ uint64_t rng;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     __shared__ __align__(16) float ring[KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS];
     __shared__ uint64_t exp_tab[32];
     stage_exp_table(exp_tab);  // the teams' first barrier comes long before their first draw
-    const PersistLds m{xch, red, xn, row, redf, ring, redi, redd, &rng, exp_tab};
+    const PersistLds m{xch, red, xn, row, ring, exp_tab};
     // Workgroup i runs on XCD i % 8 when the dispatcher deals workgroups out
     // round-robin, as it does on MI355X: the 3 + H workgroups of a sequence are
     // i = x + 8 * (R * q + r) for sequence x + 8q and role r, all on XCD x.
@@ -3040,7 +3180,7 @@ void persistent_depth(const Shape &s, F &&f) {
 
 template <class F>
 bool persistent_visit(const Shape &s, F &&f) {
-    if (!row_block_supported(s) || s.hd != s.hdp || s.V > kPersistVocab) return false;
+    if (!row_block_supported(s) || s.hd != s.hdp || s.V > kPersistVocab || s.V > 2 * s.W) return false;
     const int nw = row_waves(s.W);
     if (s.hd / nw != 8 && s.hd / nw != 16) return false;
     switch (s.W * 10000 + s.hd) {
@@ -3168,8 +3308,12 @@ void calibration_copy(const float4 *src, float4 *dst, size_t n, hipStream_t stre
 
 void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng, uint32_t *tokens,
             int tok_stride, int *len, int *flags, hipStream_t stream) {
-    hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, stream, logits, V, temperature, rng, tokens,
-                       tok_stride, len, flags);
+    if (V <= kWaveSampleVocab)
+        hipLaunchKernelGGL(wave_sample_kernel, dim3(batch), dim3(64), 0, stream, logits, V, temperature, rng, tokens,
+                           tok_stride, len, flags);
+    else
+        hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, stream, logits, V, temperature, rng, tokens,
+                           tok_stride, len, flags);
     HIP_LAUNCH_CHECK();
 }
 
