@@ -6,8 +6,9 @@ on near-ties; it must return exactly the reference's token
 (src/gpt/gpu.rs:2028-2049) for the same f32 logits and SplitMix64 state.  The
 states are chosen here so the draw u lands exactly on, or one f32 step either
 side of, CDF boundaries, which forces both the fallback and the boundary
-handling; random rows cover the common path, V above the sampler's LDS row
-cap covers the global-memory path.
+handling; random rows cover the common path.  Vocabularies up to 1024 run
+the one-wave sampler (the persistent decode's), larger ones the workgroup
+sampler, and V above its LDS row cap its global-memory path.
 """
 import numpy as np
 import pytest
