@@ -561,6 +561,19 @@ __device__ __forceinline__ float lane_read(float v, int byte_addr) {
     return __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute(byte_addr, __builtin_bit_cast(int, v)));
 }
 
+// Lane l gets v of lane (l + 1) mod 64 (DPP wave_rol:1, no LDS round trip).
+__device__ __forceinline__ float wave_rotate1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x134, 0xf, 0xf, false));
+}
+
+// Lanes 0-31 get lanes 32-63 of a, lanes 32-63 get lanes 0-31 of b: one
+// v_permlane32_swap, which leaves (a.lo, b.lo) and (a.hi, b.hi).
+__device__ __forceinline__ float halves_hi_lo(float a, float b, int lane) {
+    const auto sw = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, a), __builtin_bit_cast(int, b), false,
+                                                     false);
+    return __builtin_bit_cast(float, lane < 32 ? int(sw[1]) : int(sw[0]));
+}
+
 // f(integral_constant<int, I>) for I = 0..N-1, expanded by the front end:
 // register-array indices built from I are constants before any optimisation
 // pass runs, so a select between two elements never becomes a select of the
@@ -1002,13 +1015,28 @@ __device__ __forceinline__ void row_partner(const float (&x)[CPL], float (&p)[CP
     } else if (st < 64 * NW) {
         // Reader lane l takes lane (l + k) mod 64; readers that wrap past lane
         // 63 need the next register, and they read exactly the lanes < k.
+        // Rotations by 1 and 2 lanes are DPP wave rotations and by 32 a
+        // half swap; the others go through the LDS crossbar (ds_bpermute).
         const int k = st / NW;
-        const int addr = ((lane + k) & 63) << 2;
         const bool next = lane < k;
-        static_for<CPL>([&](auto J) {
-            constexpr int j = decltype(J)::value;
-            p[j] = lane_read(next ? x[(j + 1) % CPL] : x[j], addr);
-        });
+        if (k == 1 || k == 2) {
+            static_for<CPL>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                const float r = wave_rotate1(next ? x[(j + 1) % CPL] : x[j]);
+                p[j] = k == 1 ? r : wave_rotate1(r);
+            });
+        } else if (k == 32) {
+            static_for<CPL>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                p[j] = halves_hi_lo(x[j], x[(j + 1) % CPL], lane);
+            });
+        } else {
+            const int addr = ((lane + k) & 63) << 2;
+            static_for<CPL>([&](auto J) {
+                constexpr int j = decltype(J)::value;
+                p[j] = lane_read(next ? x[(j + 1) % CPL] : x[j], addr);
+            });
+        }
     } else {
         const int m = st / (64 * NW);
         static_for<CPL>([&](auto M) {
@@ -1176,12 +1204,13 @@ __device__ __forceinline__ float row_inv_rms(RowCtx<NW, CPL, GL> &c, const float
 
 // Post-attention half of a block (reference.rs:194-216) on the residual row x,
 // given the attention output y and the row's own value vector v.
-template <int NW, int CPL, int GL, int D>
+// With XSA false, y arrives with XSA applied (v unused).
+template <int NW, int CPL, int GL, int D, bool XSA = true>
 __device__ __forceinline__ void row_post(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], float (&y)[CPL],
                                          const float (&v)[CPL], const float2 (&wp)[D][CPL],
                                          const float2 (&wf)[D][CPL], const float *gp, const float *gf,
                                          const Shape &s, bool fixed) {
-    row_xsa(c, y, v);
+    if constexpr (XSA) row_xsa(c, y, v);
     row_run_mesh(c, y, wp, gp, s.A, s, fixed);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) x[j] += y[j];
@@ -1429,6 +1458,46 @@ struct AttnState {
 #pragma unroll
         for (int e = 0; e < VEC; ++e) acc[e] = fmaf(p, v[e], acc[e] * alpha);
         m = mn;
+    }
+    // Merges the G groups' states of the block into wave 0: thread d < 64
+    // returns the normalised output of dim d (0 for d >= HDP; other waves
+    // get 0), with the arithmetic of combine.  sm and sl hold G floats, sacc
+    // G * HDP (16-byte aligned), all LDS; the caller's LDS writes before the
+    // call are visible to wave 0 after it.
+    __device__ __forceinline__ float merge_wave0(float *sm, float *sl, float *sacc) const {
+        static_assert(TH >= HDP && HDP <= 64, "one dim per lane of wave 0");
+        const int g = threadIdx.x / LPK, li = threadIdx.x % LPK;
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) sacc[g * HDP + li * VEC + e] = acc[e];
+        if (li == 0) {
+            sm[g] = m;
+            sl[g] = l;
+        }
+        __syncthreads();
+        float y = 0.0f;
+        if (threadIdx.x < 64) {
+            const int d = min(int(threadIdx.x), HDP - 1);
+            float mk[G], lk[G], ak[G];
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                mk[k] = sm[k];
+                lk[k] = sl[k];
+                ak[k] = sacc[k * HDP + d];
+            }
+            asm volatile("" ::: "memory");  // every read issued before the first use
+            float M = -INFINITY;
+#pragma unroll
+            for (int k = 0; k < G; ++k) M = fmaxf(M, mk[k]);
+            float L = 0.0f, a = 0.0f;
+#pragma unroll
+            for (int k = 0; k < G; ++k) {
+                const float f = exp2_fast(mk[k] - M);
+                L += f * lk[k];
+                a += f * ak[k];
+            }
+            y = int(threadIdx.x) < HDP ? a * __builtin_amdgcn_rcpf(L) : 0.0f;
+        }
+        return y;
     }
     // Merges the G groups' states of the block: emit(d, a, M, L) for each
     // d < HDP with a = sum of the rescaled accumulators, M the block maximum
@@ -2439,8 +2508,13 @@ __device__ __forceinline__ bool persistent_handshake(const PersistArgs &a, const
 // words tagged `tag`: wave w takes tokens t0 + w, t0 + w + NW, ...; each lane
 // a contiguous W/64 channels of the row-order token vectors E.  T tokens'
 // loads per wave are in flight before their dot products and wave sums.
-template <int NW, int W, class X>
-__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ E, const X &xc,
+// Logits [t0, t1) of the tied head from the normalised row xn (row order):
+// wave w takes tokens t0 + w + u*NW, T at a time so their row loads and wave
+// sums overlap, and publishes each logit word.  With STAGED the E rows are
+// read from `rows` = LDS row t - t0 (stage_head_rows), else from E in global
+// memory.
+template <int NW, int W, bool STAGED, class X>
+__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ rows, const X &xc,
                                                       int t0, int t1, int tag, int lane, int wave) {
     uint64_t *out = xc.logits();
     constexpr int CW = W / 64, T = 96 / CW < 4 ? 4 : (96 / CW > 16 ? 16 : 96 / CW);
@@ -2451,8 +2525,11 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
         float e[T][CW];
 #pragma unroll
         for (int u = 0; u < T; ++u) {
-            const uint32_t t = uint32_t(min(base + u * NW, t1 - 1));
-            const float *row = E + (t * W + uint32_t(lane * CW));
+            // Past t1 a lane reads a row of its own wave (the staged rows a
+            // wave may read are the ones it copied) and publishes nothing.
+            const int t = base + u * NW;
+            const float *row = STAGED ? rows + ((t < t1 ? t : base) - t0) * W + lane * CW
+                                      : rows + (uint32_t(min(t, t1 - 1)) * W + uint32_t(lane * CW));
             if constexpr (CW % 4 == 0) {
 #pragma unroll
                 for (int k = 0; k < CW; k += 4) {
@@ -2479,6 +2556,20 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
     }
 }
 
+// Rows [t0, t1) of E copied into LDS at stage + (t - t0) * W by direct loads:
+// wave w copies the rows t0 + w + u*NW that it later reads itself, so its own
+// wait (wait_vmem) is the only synchronisation needed.
+template <int NW, int W>
+__device__ __forceinline__ void stage_head_rows(const float *E, float *stage, int t0, int t1, int lane, int wave) {
+    static_assert(W % 256 == 0, "a row is whole 1 KiB wave copies");
+    for (int t = t0 + wave; t < t1; t += NW) {
+        const float *src = E + size_t(t) * W + lane * 4;
+        float *dst = stage + (t - t0) * W;
+#pragma unroll
+        for (int c = 0; c < W / 256; ++c) lds_dma16(src + c * 256, dst + c * 256);
+    }
+}
+
 // Hides a uniform pointer's value from the optimiser, so the per-load
 // addresses derived from it are formed next to their loads instead of being
 // hoisted out of the step loop, where they would hold dozens of registers.
@@ -2501,21 +2592,27 @@ __device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const fl
 struct PersistLds {
     float *xch, *red, *xn, *row, *ring;
     uint64_t *exp_tab;
+    int ring_floats;
 };
 
-// Inputs of the post-attention half of phase g: the attention output y and
-// the row's value vector v.
+// Whether a workgroup's slice of E rows (at most ceil(V / (3 + H)) rows) fits
+// the LDS ring; the teams, which never use the ring otherwise, then keep
+// their slices there for the whole launch (stage_head_rows).  (Staging the
+// attention workgroups' slices after their last layer costs more in the
+// post-attention meshes, which run meanwhile, than the head saves.)
+template <int W>
+__device__ __forceinline__ bool head_rows_staged(const PersistArgs &a, const PersistLds &m) {
+    const int nb = 3 + a.s.H;
+    return W % 256 == 0 && (a.s.V + nb - 1) / nb * W <= m.ring_floats;
+}
+
+// The attention output of phase g (XSA applied by the attention workgroups),
+// the input of the post-attention half.
 template <int NW, int CPL, int GL, class X>
-__device__ __forceinline__ void take_post_inputs(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c, const X &xc,
-                                                 int g, float (&y)[CPL], float (&v)[CPL]) {
-    float yv[2 * CPL];
-    const uint64_t *yw = xc.y(), *vw = xc.qkv(g, 2);
-    xc.template take<2 * CPL>([&](int i) { return (i < CPL ? yw : vw) + c.ridx(i % CPL); }, g + 1, yv, a.abort);
-#pragma unroll
-    for (int j = 0; j < CPL; ++j) {
-        y[j] = yv[j];
-        v[j] = yv[CPL + j];
-    }
+__device__ __forceinline__ void take_attention_output(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c, const X &xc,
+                                                      int g, float (&y)[CPL]) {
+    const uint64_t *yw = xc.y();
+    xc.template take<CPL>([&](int j) { return yw + c.ridx(j); }, g + 1, y, a.abort);
 }
 
 // The step's token from the published logits, drawn by each wave on its own:
@@ -2574,16 +2671,21 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
     float2 wp[D][CPL], wf[D][CPL];
     load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
     load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
-    float y[CPL], v[CPL];
-    take_post_inputs(a, c, xc, g, y, v);
-    row_post(c, x, y, v, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
+    float y[CPL];
+    take_attention_output(a, c, xc, g, y);
+    const int nb = 3 + s.H, V = s.V, t0 = slice * V / nb, t1 = (slice + 1) * V / nb;
+    row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
     const float inv = row_inv_rms(c, x, 3);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
     __syncthreads();
     if (slice >= 3) trace_mark(a, xc.row, step, L, 0);
-    const int nb = 3 + s.H, V = s.V;
-    persistent_head_slice<NW, W>(m.xn, a.E, xc, slice * V / nb, (slice + 1) * V / nb, step + 1, c.lane, c.wave);
+    if (slice < 3 && head_rows_staged<W>(a, m)) {
+        wait_vmem<0>();  // this wave's staged rows (a team's, staged once)
+        persistent_head_slice<NW, W, true>(m.xn, m.ring, xc, t0, t1, step + 1, c.lane, c.wave);
+    } else {
+        persistent_head_slice<NW, W, false>(m.xn, a.E, xc, t0, t1, step + 1, c.lane, c.wave);
+    }
 }
 
 // Mesh team `team` of sequence b.
@@ -2596,16 +2698,20 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     constexpr int D = FIXED ? DEPTH : 1;
     const Shape &s = a.s;
     Ctx c(m.xch, m.red);
-    const int dim = c.dim(), L = a.layers, V = s.V;
+    const int L = a.layers, V = s.V;
     int len = a.len[b];
     uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
     uint64_t rng = a.rng[b];  // the sampler's state, the same in every wave
+    if constexpr (W % 256 == 0) {
+        // The team's slice of E rows stays in the (otherwise unused) ring.
+        const int nb = 3 + s.H;
+        if (head_rows_staged<W>(a, m)) stage_head_rows<NW, W>(a.E, m.ring, team * V / nb, (team + 1) * V / nb, c.lane, c.wave);
+    }
     const size_t gA = 2 * size_t(W) * s.A;           // floats of one attention-depth mesh
     const size_t blk = 4 * gA + 2 * size_t(W) * s.F;  // floats of one block: q, k, v, proj, ffn
     auto block = [&](int l) { return a.w + a.block0 + size_t(l) * blk; };
     float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
     for (int step = 0; step < a.steps; ++step) {
-        const int pos = len - 1;
         float x[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x[j] = a.E[size_t(tok) * W + c.ridx(j)];
@@ -2625,10 +2731,10 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
             load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
             load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
-            float y[CPL], v[CPL];
-            take_post_inputs(a, c, xc, g - 1, y, v);
+            float y[CPL];
+            take_attention_output(a, c, xc, g - 1, y);
             trace_mark(a, xc.row, step, l, 0);
-            row_post(c, x, y, v, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
+            row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
             if (l + 1 == L && team == 0) {
                 // The attention blocks finish the last block from this row.
 #pragma unroll
@@ -2638,8 +2744,9 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             float n[CPL];
 #pragma unroll
             for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
+            // q and k go out before QK-norm and RoPE, which the attention
+            // workgroups apply per head.
             row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
-            if (team < 2) row_qk_rope(c, n, rope_pair(a.rope, pos, dim, s.half), s);
             uint64_t *out = xc.qkv(g, team);
 #pragma unroll
             for (int j = 0; j < CPL; ++j) xc.put(out + c.ridx(j), n[j], g + 1);
@@ -2664,8 +2771,9 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
 // whole head; the RoPE partner dim, hd/2 away, is LPK/2 lanes away).  The
 // arithmetic of row_qk_rope: with VEC == NW its head sums (lanes, then waves
 // in order) are these per-dim lane sums added in dim order.
+// cs[e] is the (cos, sin) pair of dim d0 + e at the position (rope_pair).
 template <int LPK, int VEC>
-__device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, int pos, const float2 *rope, const Shape &s) {
+__device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const float2 (&cs)[VEC], const Shape &s) {
     float sq[VEC], other[VEC];
 #pragma unroll
     for (int e = 0; e < VEC; ++e) sq[e] = x[e] * x[e];
@@ -2673,15 +2781,18 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, int pos, c
 #pragma unroll
     for (int e = 0; e < VEC; ++e) ss += group_sum<LPK>(sq[e]);
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) other[e] = __shfl_xor(x[e], LPK / 2, 64);
+    for (int e = 0; e < VEC; ++e) {
+        // lane ^ 8 inside a 16-lane row is DPP row_ror:8
+        if constexpr (LPK == 16) other[e] = dpp_move<0x128>(0.0f, x[e]);
+        else other[e] = __shfl_xor(x[e], LPK / 2, 64);
+    }
     const float scale = 1.0f / float(s.hd);
     const float sc = rsqrtf(ss * scale + kRmsEps);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
         const int d = d0 + e;
-        const float2 cs = rope_pair(rope, pos, d, s.half);
         const float self = x[e] * sc, oth = other[e] * sc;
-        x[e] = d < s.half ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
+        x[e] = d < s.half ? self * cs[e].x - oth * cs[e].y : self * cs[e].x + oth * cs[e].y;
     }
 }
 
@@ -2723,6 +2834,11 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // 64 + e / NW, as d0 is a multiple of VEC and VEC one of NW.
             const uint32_t at0 = uint32_t(row_of<NW>(h * HDP + d0));
             float *kl = a.kc + size_t(l) * a.layer_elems + slab, *vl = a.vc + size_t(l) * a.layer_elems + slab;
+            // RoPE pairs of this lane's dims at pos, loading before anything
+            // else of the layer so that they are in by the time q and k are.
+            float2 rcs[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) rcs[e] = rope_pair(a.rope, pos, d0 + e, s.half);
             // The first NS rounds load into the ring, and the last two rounds
             // into registers, while the layer's meshes still run (the online
             // softmax takes rounds in any order).
@@ -2743,15 +2859,6 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     kn[e] = t0[W + o];
                     vn[e] = t0[2 * W + o];
                 }
-                lane_qk_rope<LPK, VEC>(qr, d0, pos, a.rope, s);
-                lane_qk_rope<LPK, VEC>(kn, d0, pos, a.rope, s);
-                // The teams' XSA of block 0 needs the value row: each head
-                // publishes its part, as the V team does for later layers.
-                if (grp == 0) {
-                    uint64_t *vo = xc.qkv(g, 2) + at0;
-#pragma unroll
-                    for (int e = 0; e < VEC; ++e) xc.put(vo + (e % NW) * 64 + e / NW, vn[e], g + 1);
-                }
             } else {
                 float qkv[3 * VEC];
                 const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
@@ -2769,6 +2876,10 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     vn[e] = qkv[2 * VEC + e];
                 }
             }
+            // QK-norm and RoPE of this head's query and key (the teams and
+            // the layer-0 table give them before both).
+            lane_qk_rope<LPK, VEC>(qr, d0, rcs, s);
+            lane_qk_rope<LPK, VEC>(kn, d0, rcs, s);
             trace_mark(a, xc.row, step, l, 0);
             if (grp == 0) {
 #pragma unroll
@@ -2792,15 +2903,31 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             for (int e = 0; e < VEC; ++e) sc = fmaf(qr[e], kn[e], sc);
             sc = group_sum<LPK>(sc) * a.scale_log2;
             if (grp == 0) st.add_one(sc, vn);
-            uint64_t *yw = xc.y();
             // The merge borrows the LDS of the logits row and of the row
-            // reductions, both idle during the layer loop.
-            static_assert(G * HDP <= kPersistVocab && 2 * G <= 8 * Ctx::SLOT, "merge scratch");
-            st.combine(
-                [&](int d, float acc, float, float den) {
-                    xc.put(yw + row_of<NW>(h * HDP + d), acc * __builtin_amdgcn_rcpf(den), g + 1);
-                },
-                m.red, m.red + G, m.row);
+            // reductions, both idle during the layer loop; the value row goes
+            // beside the merge scratch for the XSA below.
+            static_assert(G * HDP <= kPersistVocab && 2 * G + HDP <= 8 * Ctx::SLOT, "merge scratch");
+            float *vrow = m.red + 2 * G;
+            if (grp == 0) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) vrow[d0 + e] = vn[e];
+            }
+            // |v|^2 of the head from each lane group's copy of the value row,
+            // ahead of the merge.
+            float vsq = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) vsq = fmaf(vn[e], vn[e], vsq);
+            const float iv = rsqrtf(fmaxf(group_sum<LPK>(vsq), kXsaFloor));
+            const float yd = st.merge_wave0(m.red, m.red + G, m.row);
+            if (tid < 64) {
+                // XSA of the head (reference.rs:577-603): y - (y.u)u with
+                // u = v / max(|v|, eps), in wave 0, one dim per lane.
+                const int d = tid;
+                const float vd = d < HDP ? vrow[d] : 0.0f;
+                const float yv = wave_sum(yd * vd);
+                if (d < HDP) xc.put(xc.y() + row_of<NW>(h * HDP + d), yd - (yv * iv) * (vd * iv), g + 1);
+            }
+            __syncthreads();  // the merge scratch is free again
             trace_mark(a, xc.row, step, l, 1);
         }
         // The last block from the published residual row, then this block's
@@ -2832,7 +2959,7 @@ persistent_decode_kernel(PersistArgs a) {
     __shared__ __align__(16) float ring[KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS];
     __shared__ uint64_t exp_tab[32];
     stage_exp_table(exp_tab);  // the teams' first barrier comes long before their first draw
-    const PersistLds m{xch, red, xn, row, ring, exp_tab};
+    const PersistLds m{xch, red, xn, row, ring, exp_tab, KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS};
     // Workgroup i runs on XCD i % 8 when the dispatcher deals workgroups out
     // round-robin, as it does on MI355X: the 3 + H workgroups of a sequence are
     // i = x + 8 * (R * q + r) for sequence x + 8q and role r, all on XCD x.
