@@ -2458,6 +2458,14 @@ __device__ __forceinline__ void trace_mark(const PersistArgs &a, int row, int st
         a.trace[((size_t(row) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = wall_clock64();
 }
 
+// A trace time taken now and stored later (trace_store): a store in between
+// would count in the vector-memory counter that the LDS ring's waits count.
+__device__ __forceinline__ uint64_t trace_time(const PersistArgs &a) { return a.trace ? wall_clock64() : 0; }
+
+__device__ __forceinline__ void trace_store(const PersistArgs &a, int row, int step, int l, int which, uint64_t t) {
+    if (a.trace && threadIdx.x == 0) a.trace[((size_t(row) * a.steps + step) * (a.layers + 1) + l) * 2 + which] = t;
+}
+
 // Row-order index of channel c (the layout RowCtx::ridx enumerates).
 template <int NW>
 __device__ __forceinline__ int row_of(int c) {
@@ -2880,14 +2888,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // the layer-0 table give them before both).
             lane_qk_rope<LPK, VEC>(qr, d0, rcs, s);
             lane_qk_rope<LPK, VEC>(kn, d0, rcs, s);
-            trace_mark(a, xc.row, step, l, 0);
-            if (grp == 0) {
-#pragma unroll
-                for (int e = 0; e < VEC; ++e) {
-                    kl[size_t(pos) * HDP + d0 + e] = kn[e];
-                    vl[size_t(pos) * HDP + d0 + e] = vn[e];
-                }
-            }
+            const uint64_t t_ready = trace_time(a);
             S st;
             if (ntail > 0) st.add(qr, last, nring * G * U, pos, a.scale_log2);
             if (ntail > 1) st.add(qr, last2, (nring + 1) * G * U, pos, a.scale_log2);
@@ -2927,7 +2928,18 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 const float yv = wave_sum(yd * vd);
                 if (d < HDP) xc.put(xc.y() + row_of<NW>(h * HDP + d), yd - (yv * iv) * (vd * iv), g + 1);
             }
+            // The key and value rows go to the cache for later steps only
+            // now: stored before the ring's last wait, which waits for every
+            // vector-memory operation, they would hold it up.
+            if (grp == 0) {
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) {
+                    kl[size_t(pos) * HDP + d0 + e] = kn[e];
+                    vl[size_t(pos) * HDP + d0 + e] = vn[e];
+                }
+            }
             __syncthreads();  // the merge scratch is free again
+            trace_store(a, xc.row, step, l, 0, t_ready);
             trace_mark(a, xc.row, step, l, 1);
         }
         // The last block from the published residual row, then this block's
