@@ -2487,7 +2487,7 @@ struct PersistXch {
     // q (t = 0), k (1) or v (2) of phase g, double-buffered by phase parity
     __device__ uint64_t *qkv(int g, int t) const { return base + size_t((g & 1) * 3 + t) * W; }
     __device__ uint64_t *y() const { return base + size_t(6) * W; }     // attention output
-    __device__ uint64_t *xrow() const { return base + size_t(7) * W; }  // residual row
+    __device__ uint64_t *xrow() const { return base + size_t(7) * W; }  // normalised final row
     __device__ uint64_t *logits() const { return base + size_t(8) * W; }  // token order
     __device__ uint64_t *xcd() const { return base + size_t(8) * W + V; }  // each workgroup's XCD
     __device__ void put(uint64_t *p, float v, int tag) const { put_word(p, v, tag, LOCAL); }
@@ -2516,21 +2516,16 @@ __device__ __forceinline__ bool persistent_handshake(const PersistArgs &a, const
 // words tagged `tag`: wave w takes tokens t0 + w, t0 + w + NW, ...; each lane
 // a contiguous W/64 channels of the row-order token vectors E.  T tokens'
 // loads per wave are in flight before their dot products and wave sums.
-// Logits [t0, t1) of the tied head from the normalised row xn (row order):
-// wave w takes tokens t0 + w + u*NW, T at a time so their row loads and wave
-// sums overlap, and publishes each logit word.  With STAGED the E rows are
-// read from `rows` = LDS row t - t0 (stage_head_rows), else from E in global
-// memory.
-template <int NW, int W, bool STAGED, class X>
-__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ rows, const X &xc,
-                                                      int t0, int t1, int tag, int lane, int wave) {
-    uint64_t *out = xc.logits();
-    constexpr int CW = W / 64, T = 96 / CW < 4 ? 4 : (96 / CW > 16 ? 16 : 96 / CW);
-    float xr[CW];
-#pragma unroll
-    for (int k = 0; k < CW; ++k) xr[k] = xn[lane * CW + k];
-    for (int base = t0 + wave; base < t1; base += T * NW) {
-        float e[T][CW];
+// T rows of the tied head at a time: row t = base + u*NW of a wave's rows, from
+// E in global memory or from its rows staged in LDS (stage_head_rows: LDS row
+// t - t0), dotted with the normalised row and published as logit words.
+template <int NW, int W>
+struct HeadBatch {
+    static constexpr int CW = W / 64, T = 96 / CW < 4 ? 4 : (96 / CW > 8 ? 8 : 96 / CW);
+    static_assert(T <= 64, "lane u publishes row u");
+    float e[T][CW];
+    template <bool STAGED>
+    __device__ __forceinline__ void load(const float *__restrict__ rows, int t0, int base, int t1, int lane) {
 #pragma unroll
         for (int u = 0; u < T; ++u) {
             // Past t1 a lane reads a row of its own wave (the staged rows a
@@ -2552,15 +2547,41 @@ __device__ __forceinline__ void persistent_head_slice(const float *xn, const flo
                 for (int k = 0; k < CW; ++k) e[u][k] = row[k];
             }
         }
+    }
+    // The T wave sums run without a branch between them (so they overlap);
+    // then lane u publishes row u.
+    template <class X>
+    __device__ __forceinline__ void publish(const float (&xr)[CW], const X &xc, int base, int t1, int tag,
+                                            int lane) const {
+        float mine = 0.0f;
 #pragma unroll
         for (int u = 0; u < T; ++u) {
             float acc = 0.0f;
 #pragma unroll
             for (int k = 0; k < CW; ++k) acc = fmaf(xr[k], e[u][k], acc);
             acc = wave_sum(acc);
-            const int t = base + u * NW;
-            if (lane == 0 && t < t1) xc.put(out + t, acc, tag);
+            mine = lane == u ? acc : mine;
         }
+        const int t = base + lane * NW;
+        if (lane < T && t < t1) xc.put(xc.logits() + t, mine, tag);
+    }
+};
+
+// Logits [t0, t1) of the tied head from the normalised row xn (row order, in
+// LDS), wave w taking rows t0 + w + u*NW from its first batch at `base` on;
+// with STAGED the E rows come from `rows` in LDS (stage_head_rows), else from
+// E in global memory.
+template <int NW, int W, bool STAGED, class X>
+__device__ __forceinline__ void persistent_head_slice(const float *xn, const float *__restrict__ rows, const X &xc,
+                                                      int t0, int base, int t1, int tag, int lane) {
+    using HB = HeadBatch<NW, W>;
+    float xr[HB::CW];
+#pragma unroll
+    for (int k = 0; k < HB::CW; ++k) xr[k] = xn[lane * HB::CW + k];
+    for (; base < t1; base += HB::T * NW) {
+        HB hb;
+        hb.template load<STAGED>(rows, t0, base, t1, lane);
+        hb.publish(xr, xc, base, t1, tag, lane);
     }
 }
 
@@ -2664,8 +2685,11 @@ __device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc
     return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
 }
 
-// Post-attention half of the last block on the residual row x, then logit
-// slice `slice` of the 3 + H slices of the vocabulary.
+// Post-attention half of the last block on team `slice`'s residual row x and
+// the final RMSNorm; team 0 publishes the normalised row for the attention
+// workgroups (which would otherwise wait for the weights, loaded only after
+// their own last attention); then logit slice `slice` of the 3 + H slices of
+// the vocabulary.
 template <int NW, int CPL, int GL, int DEPTH, class X>
 __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowCtx<NW, CPL, GL> &c, float (&x)[CPL],
                                                       const X &xc, int step, int slice, const PersistLds &m) {
@@ -2685,15 +2709,45 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
     row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
     const float inv = row_inv_rms(c, x, 3);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = x[j] * inv;
-    __syncthreads();
-    if (slice >= 3) trace_mark(a, xc.row, step, L, 0);
-    if (slice < 3 && head_rows_staged<W>(a, m)) {
-        wait_vmem<0>();  // this wave's staged rows (a team's, staged once)
-        persistent_head_slice<NW, W, true>(m.xn, m.ring, xc, t0, t1, step + 1, c.lane, c.wave);
-    } else {
-        persistent_head_slice<NW, W, false>(m.xn, a.E, xc, t0, t1, step + 1, c.lane, c.wave);
+    for (int j = 0; j < CPL; ++j) {
+        const float n = x[j] * inv;
+        m.xn[c.ridx(j)] = n;
+        if (slice == 0) xc.put(xc.xrow() + c.ridx(j), n, step + 1);
     }
+    __syncthreads();
+    if (head_rows_staged<W>(a, m)) {
+        wait_vmem<0>();  // this wave's staged rows (staged once)
+        persistent_head_slice<NW, W, true>(m.xn, m.ring, xc, t0, t0 + c.wave, t1, step + 1, c.lane);
+    } else {
+        persistent_head_slice<NW, W, false>(m.xn, a.E, xc, t0, t0 + c.wave, t1, step + 1, c.lane);
+    }
+}
+
+// An attention workgroup's logit slice `slice`, from the normalised final row
+// that team 0 publishes.
+template <int NW, int CPL, int GL, class X>
+__device__ __forceinline__ void persistent_head_logits(const PersistArgs &a, const RowCtx<NW, CPL, GL> &c,
+                                                       const X &xc, int step, int slice, const PersistLds &m) {
+    constexpr int W = RowCtx<NW, CPL, GL>::W;
+    const int nb = 3 + a.s.H, V = a.s.V, t0 = slice * V / nb, t1 = (slice + 1) * V / nb;
+    using HB = HeadBatch<NW, W>;
+    // The first batch of E rows loads while the row is awaited.
+    const int base = t0 + c.wave;
+    HB first;
+    if (base < t1) first.template load<false>(a.E, t0, base, t1, c.lane);
+    float n[CPL];
+    xc.template take<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, n, a.abort);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) m.xn[c.ridx(j)] = n[j];
+    __syncthreads();
+    trace_mark(a, xc.row, step, a.layers, 0);
+    if (base < t1) {
+        float xr[HB::CW];
+#pragma unroll
+        for (int k = 0; k < HB::CW; ++k) xr[k] = m.xn[c.lane * HB::CW + k];
+        first.publish(xr, xc, base, t1, step + 1, c.lane);
+    }
+    persistent_head_slice<NW, W, false>(m.xn, a.E, xc, t0, base + HB::T * NW, t1, step + 1, c.lane);
 }
 
 // Mesh team `team` of sequence b.
@@ -2727,10 +2781,6 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
         // Layer 0's q, k and v are the token's rows of the layer-0 table, which
         // the attention blocks read themselves: the teams start at block 0's
         // post-attention half.
-        if (L == 1 && team == 0) {
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) xc.put(xc.xrow() + c.ridx(j), x[j], step + 1);
-        }
         trace_mark(a, xc.row, step, 0, 1);
         for (int l = 1; l < L; ++l) {
             const int g = step * L + l;
@@ -2743,11 +2793,6 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             take_attention_output(a, c, xc, g - 1, y);
             trace_mark(a, xc.row, step, l, 0);
             row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
-            if (l + 1 == L && team == 0) {
-                // The attention blocks finish the last block from this row.
-#pragma unroll
-                for (int j = 0; j < CPL; ++j) xc.put(xc.xrow() + c.ridx(j), x[j], step + 1);
-            }
             const float inv = row_inv_rms(c, x, 3);
             float n[CPL];
 #pragma unroll
@@ -2942,16 +2987,14 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             trace_store(a, xc.row, step, l, 0, t_ready);
             trace_mark(a, xc.row, step, l, 1);
         }
-        // The last block from the published residual row, then this block's
-        // logits.  The thread index is hidden from the optimiser so the lane
-        // arithmetic of these meshes is formed here, not hoisted out of the
-        // step loop to occupy registers through the attention.
+        // This block's logits from the published final row.  The thread
+        // index is hidden from the optimiser so the lane arithmetic is formed
+        // here, not hoisted out of the step loop to occupy registers through
+        // the attention.
         int tid = int(threadIdx.x);
         asm volatile("" : "+v"(tid));
-        Ctx c(m.xch, m.red, tid);
-        float x[CPL];
-        xc.template take<CPL>([&](int j) { return xc.xrow() + c.ridx(j); }, step + 1, x, a.abort);
-        persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, 3 + h, m);
+        const Ctx c(m.xch, m.red, tid);
+        persistent_head_logits<NW, CPL, GL>(a, c, xc, step, 3 + h, m);
         trace_mark(a, xc.row, step, L, 1);
         if (step + 1 < a.steps) tok = draw_token<false>(a, xc, step, rng, m, nullptr);
     }
