@@ -1202,6 +1202,55 @@ __device__ __forceinline__ float row_inv_rms(RowCtx<NW, CPL, GL> &c, const float
     return rsqrtf(row_total<NW>(acc, c.lane, c.wave, c.slot(k)) * (1.0f / float(c.W)) + kRmsEps);
 }
 
+// n = mesh(x * inv_rms(x)) for a compile-time-depth mesh whose first stride
+// (1) crosses waves: the row reduction of the RMSNorm and that layer's LDS
+// exchange share one barrier (x is exchanged and each lane scales its partner
+// itself).  Same arithmetic as row_inv_rms, then row_run_mesh on x * inv.
+template <int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void row_rms_mesh(RowCtx<NW, CPL, GL> &c, const float (&x)[CPL], float (&n)[CPL],
+                                             const float2 (&w)[D][CPL], int k) {
+    static_assert(NW > 1 && D >= 1, "the first layer's stride 1 crosses waves");
+    constexpr int W = 64 * NW * CPL;
+    constexpr int LOG2W = W == 128 ? 7 : W == 256 ? 8 : W == 512 ? 9 : 10;
+    const int lane = c.lane, wave = c.wave;
+    float acc = 0.0f;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
+    acc = wave_sum(acc);
+    float *red = c.slot(k);
+    if (lane == 0) red[wave] = acc;
+    float *b = c.xch + (c.parity & 1) * (NW * CPL * 64);
+    ++c.parity;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) b[(j * NW + wave) * 64 + lane] = x[j];
+    __syncthreads();
+    float t = 0.0f;
+#pragma unroll
+    for (int v = 0; v < NW; ++v) t += red[v];
+    const float inv = rsqrtf(t * (1.0f / float(W)) + kRmsEps);
+    // Partner of channel c is c + 1: the next wave, or wave 0 one lane on.
+    int w2 = wave + 1, l2 = lane, jc = 0;
+    if (w2 >= NW) {
+        w2 -= NW;
+        ++l2;
+    }
+    if (l2 >= 64) {
+        l2 -= 64;
+        jc = 1;
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int j2 = j + jc < CPL ? j + jc : 0;
+        const float nx = x[j] * inv, np = b[(j2 * NW + w2) * 64 + l2] * inv;
+        const float z = nx * w[0][j].x + np * w[0][j].y;
+        n[j] = D == 1 ? z : elu(z);
+    }
+    static_for<D>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        if constexpr (u > 0) row_layer<NW, CPL>(n, w[u], 1 << (u % LOG2W), u + 1 == D, lane, wave, c.xch, c.parity);
+    });
+}
+
 // Post-attention half of a block (reference.rs:194-216) on the residual row x,
 // given the attention output y and the row's own value vector v.
 // With XSA false, y arrives with XSA applied (v unused).
@@ -1214,6 +1263,14 @@ __device__ __forceinline__ void row_post(RowCtx<NW, CPL, GL> &c, float (&x)[CPL]
     row_run_mesh(c, y, wp, gp, s.A, s, fixed);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) x[j] += y[j];
+    if constexpr (NW > 1 && D > 1) {
+        if (fixed) {
+            row_rms_mesh(c, x, y, wf, 2);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[j] += y[j];
+            return;
+        }
+    }
     const float inv = row_inv_rms(c, x, 2);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
@@ -2793,13 +2850,17 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             take_attention_output(a, c, xc, g - 1, y);
             trace_mark(a, xc.row, step, l, 0);
             row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
-            const float inv = row_inv_rms(c, x, 3);
-            float n[CPL];
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
             // q and k go out before QK-norm and RoPE, which the attention
             // workgroups apply per head.
-            row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
+            float n[CPL];
+            if constexpr (FIXED && NW > 1) {
+                row_rms_mesh(c, x, n, wm, 3);
+            } else {
+                const float inv = row_inv_rms(c, x, 3);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
+                row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
+            }
             uint64_t *out = xc.qkv(g, team);
 #pragma unroll
             for (int j = 0; j < CPL; ++j) xc.put(out + c.ridx(j), n[j], g + 1);
