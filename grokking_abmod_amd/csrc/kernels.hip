@@ -1507,6 +1507,51 @@ struct AttnState {
             m = mn;
         }
     }
+    // Folds in the rounds loaded at j0 and j1 together: their scores and
+    // exponentials are independent, so the two chains overlap.
+    __device__ __forceinline__ void add2(const float (&qr)[VEC], const R &c0, int j0, const R &c1, int j1, int end,
+                                         float scale_log2) {
+        const int g = threadIdx.x / LPK;
+        float sc[2 * U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            float p0 = 0.0f, p1 = 0.0f;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                p0 = fmaf(qr[e], c0.k[u][e], p0);
+                p1 = fmaf(qr[e], c1.k[u][e], p1);
+            }
+            p0 = group_sum<LPK>(p0);
+            p1 = group_sum<LPK>(p1);
+            sc[u] = (j0 + u * G + g < end) ? p0 * scale_log2 : -INFINITY;
+            sc[U + u] = (j1 + u * G + g < end) ? p1 * scale_log2 : -INFINITY;
+        }
+        float cm = sc[0];
+#pragma unroll
+        for (int u = 1; u < 2 * U; ++u) cm = fmaxf(cm, sc[u]);
+        const float mn = fmaxf(m, cm);
+        if (mn != -INFINITY) {
+            const float alpha = exp2_fast(m - mn);
+            float pu[2 * U], ps = 0.0f;
+#pragma unroll
+            for (int u = 0; u < 2 * U; ++u) {
+                pu[u] = exp2_fast(sc[u] - mn);
+                ps += pu[u];
+            }
+            l = l * alpha + ps;
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) {
+                float a = acc[e] * alpha, b = 0.0f;
+#pragma unroll
+                for (int u = 0; u < U; ++u) {
+                    a = fmaf(pu[u], c0.v[u][e], a);
+                    b = fmaf(pu[U + u], c1.v[u][e], b);
+                }
+                acc[e] = a + b;
+            }
+            m = mn;
+        }
+    }
     // Folds in one key whose (log2-domain) score is sc and value row v.
     __device__ __forceinline__ void add_one(float sc, const float (&v)[VEC]) {
         const float mn = fmaxf(m, sc);
@@ -2112,6 +2157,10 @@ template <int RMAX>
 __device__ __forceinline__ int wave_choose_token(const float (&lg)[RMAX], int V, float temperature, float u,
                                                  const uint64_t *exp_tab, int *flags, float *scratch) {
     static_assert(RMAX % 4 == 0, "runs are handled four tokens at a time");
+    // V is hidden from the optimiser so that the f64 constants derived from it
+    // are formed here, not hoisted out of a caller's step loop and spilled.
+    V = __builtin_amdgcn_readfirstlane(V);
+    asm volatile("" : "+s"(V));
     // Every per-token step below is straight-line code in blocks of four
     // tokens (a lane's tokens past V are masked by selects), so the f64
     // evaluations of neighbouring tokens overlap; only `k < R` branches, and
@@ -2996,14 +3045,37 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             lane_qk_rope<LPK, VEC>(kn, d0, rcs, s);
             const uint64_t t_ready = trace_time(a);
             S st;
-            if (ntail > 0) st.add(qr, last, nring * G * U, pos, a.scale_log2);
-            if (ntail > 1) st.add(qr, last2, (nring + 1) * G * U, pos, a.scale_log2);
-            for (int r = 0; r < nring; ++r) {
-                ring.wait(min(NS - 1, nring - 1 - r));
-                R cur;
-                ring.read(r, cur, tid);
-                if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid);
-                st.add(qr, cur, r * G * U, pos, a.scale_log2);
+            if (ntail > 1)
+                st.add2(qr, last, nring * G * U, last2, (nring + 1) * G * U, pos, a.scale_log2);
+            else if (ntail > 0)
+                st.add(qr, last, nring * G * U, pos, a.scale_log2);
+            if constexpr (NS == 2) {
+                // Two rounds at a time: both slots are read, refilled and
+                // folded in together.
+                int r = 0;
+                for (; r + 1 < nring; r += 2) {
+                    ring.wait(0);
+                    R c0, c1;
+                    ring.read(r, c0, tid);
+                    ring.read(r + 1, c1, tid);
+                    if (r + 2 < nring) ring.issue(kl, vl, r + 2, pos, tid);
+                    if (r + 3 < nring) ring.issue(kl, vl, r + 3, pos, tid);
+                    st.add2(qr, c0, r * G * U, c1, (r + 1) * G * U, pos, a.scale_log2);
+                }
+                if (r < nring) {
+                    ring.wait(0);
+                    R cur;
+                    ring.read(r, cur, tid);
+                    st.add(qr, cur, r * G * U, pos, a.scale_log2);
+                }
+            } else {
+                for (int r = 0; r < nring; ++r) {
+                    ring.wait(min(NS - 1, nring - 1 - r));
+                    R cur;
+                    ring.read(r, cur, tid);
+                    if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid);
+                    st.add(qr, cur, r * G * U, pos, a.scale_log2);
+                }
             }
             float sc = 0.0f;
 #pragma unroll
