@@ -3023,20 +3023,28 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     vn[e] = t0[2 * W + o];
                 }
             } else {
-                float qkv[3 * VEC];
-                const uint64_t *qw = opaque(xc.qkv(g, 0)) + at0, *kw = opaque(xc.qkv(g, 1)) + at0,
-                               *vw = opaque(xc.qkv(g, 2)) + at0;
-                xc.template take<3 * VEC>(
-                    [&](int i) {
-                        const uint64_t *base = i < VEC ? qw : (i < 2 * VEC ? kw : vw);
-                        return base + ((i % VEC) % NW * 64 + (i % VEC) / NW);
-                    },
-                    g + 1, qkv, a.abort);
+                // Wave 0 takes the head's q, k and v, one dim of each per lane
+                // (3 words a lane), and hands them to every lane group in LDS.
+                float *qkvs = m.xch;
+                if (tid < 64) {
+                    const int d = min(tid, HDP - 1);
+                    const uint32_t o = uint32_t(row_of<NW>(h * HDP + d));
+                    const uint64_t *qw = opaque(xc.qkv(g, 0)), *kw = opaque(xc.qkv(g, 1)), *vw = opaque(xc.qkv(g, 2));
+                    float t[3];
+                    xc.template take<3>([&](int i) { return (i == 0 ? qw : (i == 1 ? kw : vw)) + o; }, g + 1, t,
+                                        a.abort);
+                    if (tid < HDP) {
+                        qkvs[d] = t[0];
+                        qkvs[HDP + d] = t[1];
+                        qkvs[2 * HDP + d] = t[2];
+                    }
+                }
+                __syncthreads();
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
-                    qr[e] = qkv[e];
-                    kn[e] = qkv[VEC + e];
-                    vn[e] = qkv[2 * VEC + e];
+                    qr[e] = qkvs[d0 + e];
+                    kn[e] = qkvs[HDP + d0 + e];
+                    vn[e] = qkvs[2 * HDP + d0 + e];
                 }
             }
             // QK-norm and RoPE of this head's query and key (the teams and
