@@ -31,6 +31,9 @@ namespace {
 
 constexpr float kRmsEps = 1e-5f;  // src/gpt/mod.rs:38
 // (f64(1e-12f))^2 rounded to f32: the XSA norm floor of reference.rs:591
+// A 64-bit word in global memory: accesses through it are global (not flat)
+// loads and stores, which do not count in the LDS wait counter.
+typedef __attribute__((address_space(1))) uint64_t global_u64;
 constexpr float kXsaFloor = float(double(1e-12f) * double(1e-12f));
 
 #define HIP_LAUNCH_CHECK() (void)hipGetLastError()
@@ -1067,13 +1070,15 @@ __device__ __forceinline__ void row_layer(float (&x)[CPL], const float2 (&w)[CPL
 template <int NW, int CPL, int D>
 __device__ __forceinline__ void row_load_weights(float2 (&w)[D][CPL], const float *wg, int lane, int wave) {
     // A uniform base and 32-bit lane offsets: one address register for all
-    // the loads instead of a 64-bit address per load.
-    const float2 *g = reinterpret_cast<const float2 *>(wg);
+    // the loads instead of a 64-bit address per load.  The weights are in
+    // global memory, said so that the loads are global rather than flat ones
+    // (which would also count in the LDS wait counter).
+    const global_u64 *g = (const global_u64 *)wg;  // a float2 per word
     const uint32_t at = uint32_t(wave * 64 + lane);
 #pragma unroll
     for (int u = 0; u < D; ++u)
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) w[u][j] = g[at + uint32_t((u * CPL + j) * NW * 64)];
+        for (int j = 0; j < CPL; ++j) w[u][j] = __builtin_bit_cast(float2, uint64_t(g[at + uint32_t((u * CPL + j) * NW * 64)]));
 }
 
 // A butterfly mesh stack of compile-time depth D (reference.rs:422-453): all
@@ -2408,17 +2413,20 @@ static_assert(kPersistVocab <= kWaveSampleVocab, "the persistent path draws with
 // cache: about 0.45 us a hand-off instead of 0.75 us with agent-scope
 // atomics, which reach the memory side.  Sequences spread over XCDs use the
 // atomics.  Either way every word is one naturally aligned 64-bit access.
+// The exchange words are in global memory: addressed as such (global_u64),
+// the accesses are global (not flat) loads and stores.
+
 __device__ __forceinline__ void put_word(uint64_t *p, float v, int tag, bool local) {
     const uint64_t w = (uint64_t(uint32_t(tag)) << 32) | __float_as_uint(v);
     if (local)
-        __builtin_nontemporal_store(w, p);
+        __builtin_nontemporal_store(w, (global_u64 *)p);
     else
-        __hip_atomic_store(p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store((global_u64 *)p, w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 __device__ __forceinline__ uint64_t get_word(const uint64_t *p, bool local) {
-    if (local) return __builtin_nontemporal_load(p);
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (local) return __builtin_nontemporal_load((const global_u64 *)p);
+    return __hip_atomic_load((const global_u64 *)p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // out[i] = the float of the word at addr(i), i < N, once every such word of
@@ -2441,11 +2449,14 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
         while (true) {
             __builtin_amdgcn_s_sleep(1);
             asm volatile("" ::: "memory");  // the words change under us: load them again
+            // Every word again (no per-word branch, whose evaluation would
+            // wait inside the loop), and the abort flag with them: one memory
+            // round trip per poll.
 #pragma unroll
-            for (int i = 0; i < N; ++i)
-                if (uint32_t(w[i] >> 32) != want) w[i] = get_word(addr(i), local);
+            for (int i = 0; i < N; ++i) w[i] = get_word(addr(i), local);
+            const int stop = __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (__all(ready())) break;
-            if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+            if (stop != 0) break;
             if (wall_clock64() - t0 > kWaitTicks) {
                 if ((threadIdx.x & 63) == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                 break;
@@ -3014,7 +3025,8 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             if (ntail > 1) last2.load(kl, vl, (nring + 1) * G * U, pos);
             float qr[VEC], kn[VEC], vn[VEC];
             if (l == 0) {
-                const float *t0 = opaque(a.q0) + size_t(tok) * 3 * W + at0;
+                typedef __attribute__((address_space(1))) const float gfloat;
+                gfloat *t0 = (gfloat *)opaque(a.q0) + size_t(tok) * 3 * W + at0;
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) {
                     const uint32_t o = (e % NW) * 64 + e / NW;
