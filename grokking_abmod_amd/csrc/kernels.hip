@@ -128,6 +128,19 @@ __device__ __forceinline__ float group_sum(float v) {
     return v;
 }
 
+// Maximum over aligned groups of N lanes, left in every lane of the group
+// (the lane pattern of group_sum).
+template <int N>
+__device__ __forceinline__ float group_max(float v) {
+    if constexpr (N >= 2) v = fmaxf(v, dpp_move<0xB1>(v, v));
+    if constexpr (N >= 4) v = fmaxf(v, dpp_move<0x4E>(v, v));
+    if constexpr (N >= 8) v = fmaxf(v, dpp_move<0x141>(v, v));
+    if constexpr (N >= 16) v = fmaxf(v, dpp_move<0x140>(v, v));
+    if constexpr (N >= 32) v = fmaxf(v, __shfl_xor(v, 16, 64));
+    if constexpr (N >= 64) v = fmaxf(v, __shfl_xor(v, 32, 64));
+    return v;
+}
+
 // ELU of reference.rs:325-332.  The negative branch is exp(z) - 1 from the
 // hardware exp2: its absolute error (~1e-7 for z near 0) is that of one f32
 // rounding of the row values, far below the logit tolerance; the library
@@ -1557,15 +1570,6 @@ struct AttnState {
             m = mn;
         }
     }
-    // Folds in one key whose (log2-domain) score is sc and value row v.
-    __device__ __forceinline__ void add_one(float sc, const float (&v)[VEC]) {
-        const float mn = fmaxf(m, sc);
-        const float alpha = exp2_fast(m - mn), p = exp2_fast(sc - mn);
-        l = l * alpha + p;
-#pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[e] = fmaf(p, v[e], acc[e] * alpha);
-        m = mn;
-    }
     // Merges the G groups' states of the block into wave 0: thread d < 64
     // returns the normalised output of dim d (0 for d >= HDP; other waves
     // get 0), with the arithmetic of combine.  sm and sl hold G floats, sacc
@@ -1581,28 +1585,25 @@ struct AttnState {
             sl[g] = l;
         }
         __syncthreads();
+        static_assert(G <= 64, "one lane per group state");
         float y = 0.0f;
         if (threadIdx.x < 64) {
-            const int d = min(int(threadIdx.x), HDP - 1);
-            float mk[G], lk[G], ak[G];
+            // Lane k of each G-lane group holds group k's (m, l); the scale
+            // factors are computed once there and read from lane k by all.
+            const int lane = threadIdx.x, d = min(lane, HDP - 1), k = lane % G;
+            const float mk = sm[k], lk = sl[k];
+            float ak[G];
 #pragma unroll
-            for (int k = 0; k < G; ++k) {
-                mk[k] = sm[k];
-                lk[k] = sl[k];
-                ak[k] = sacc[k * HDP + d];
-            }
+            for (int kk = 0; kk < G; ++kk) ak[kk] = sacc[kk * HDP + d];
             asm volatile("" ::: "memory");  // every read issued before the first use
-            float M = -INFINITY;
+            const float M = group_max<G>(mk);
+            const float f = exp2_fast(mk - M);
+            const float L = group_sum<G>(f * lk);
+            float a = 0.0f;
 #pragma unroll
-            for (int k = 0; k < G; ++k) M = fmaxf(M, mk[k]);
-            float L = 0.0f, a = 0.0f;
-#pragma unroll
-            for (int k = 0; k < G; ++k) {
-                const float f = exp2_fast(mk[k] - M);
-                L += f * lk[k];
-                a += f * ak[k];
-            }
-            y = int(threadIdx.x) < HDP ? a * __builtin_amdgcn_rcpf(L) : 0.0f;
+            for (int kk = 0; kk < G; ++kk)
+                a = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), kk)), ak[kk], a);
+            y = lane < HDP ? a * __builtin_amdgcn_rcpf(L) : 0.0f;
         }
         return y;
     }
@@ -3065,6 +3066,21 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             lane_qk_rope<LPK, VEC>(kn, d0, rcs, s);
             const uint64_t t_ready = trace_time(a);
             S st;
+            {
+                // The current token's key first: on the fresh state folding
+                // it in is an initialisation (m its score, l = 1, acc its
+                // value row), done with selects for lane group 0, which holds
+                // it, so no branch splits the rounds that follow.
+                float sc = 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) sc = fmaf(qr[e], kn[e], sc);
+                sc = group_sum<LPK>(sc) * a.scale_log2;
+                const bool mine = grp == 0;
+                st.m = mine ? sc : -INFINITY;
+                st.l = mine ? 1.0f : 0.0f;
+#pragma unroll
+                for (int e = 0; e < VEC; ++e) st.acc[e] = mine ? vn[e] : 0.0f;
+            }
             if (ntail > 1)
                 st.add2(qr, last, nring * G * U, last2, (nring + 1) * G * U, pos, a.scale_log2);
             else if (ntail > 0)
@@ -3097,11 +3113,6 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     st.add(qr, cur, r * G * U, pos, a.scale_log2);
                 }
             }
-            float sc = 0.0f;
-#pragma unroll
-            for (int e = 0; e < VEC; ++e) sc = fmaf(qr[e], kn[e], sc);
-            sc = group_sum<LPK>(sc) * a.scale_log2;
-            if (grp == 0) st.add_one(sc, vn);
             // The merge borrows the LDS of the logits row and of the row
             // reductions, both idle during the layer loop; the value row goes
             // beside the merge scratch for the XSA below.
