@@ -3037,7 +3037,10 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 }
             } else {
                 // Wave 0 takes the head's q, k and v, one dim of each per lane
-                // (3 words a lane), and hands them to every lane group in LDS.
+                // (3 words a lane), and hands them to every lane group in LDS
+                // (the mesh exchange buffer, which attention workgroups use
+                // otherwise only for a near-tie draw, after the layers).
+                static_assert(3 * HDP <= 2 * W && HDP <= 64, "q, k and v of a head in the exchange buffer");
                 float *qkvs = m.xch;
                 if (tid < 64) {
                     const int d = min(tid, HDP - 1);
