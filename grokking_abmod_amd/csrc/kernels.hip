@@ -2592,8 +2592,8 @@ __device__ __forceinline__ int row_of(int c) {
 
 // One sequence's exchange words (row order unless noted).  Layer phase
 // g = step * layers + l: q/k/v and the attention output of phase g carry tag
-// g + 1; the residual row entering the last block and the logits of a step
-// carry tag step + 1.
+// g + 1; the normalised final row and the logits of a step carry tag
+// step + 1.
 template <bool LOCAL>  // all workgroups of the sequence on one XCD (see put_word)
 struct PersistXch {
     static constexpr bool local = LOCAL;
@@ -2973,11 +2973,13 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const floa
 
 // Attention block of (sequence b, head h).  Its query, key and value arrive
 // as tagged words, except at layer 0, where they are the token's rows of the
-// layer-0 table (QK-norm and RoPE applied here): the block draws each step's
-// token itself, like the teams.  The key/value rows go to the cache for later
-// steps and enter this step's attention from registers, so the cached rows
-// read each layer [0, pos) were all written before the launch or by this
-// block, and the first rounds of them load while the inputs are awaited.
+// layer-0 table; QK-norm and RoPE are applied here for every layer.  After
+// the last layer it computes its slice of the logits from the final row team
+// 0 publishes, and it draws each step's token itself, like the teams.  The
+// key/value rows go to the cache for later steps and enter this step's
+// attention from registers, so the cached rows read each layer [0, pos) were
+// all written before the launch or by this block, and the first rounds of
+// them load while the inputs are awaited.
 template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
 __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m,
                                                      const X &xc) {

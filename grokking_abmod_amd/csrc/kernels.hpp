@@ -144,8 +144,7 @@ struct PersistArgs {
 };
 bool persistent_fits(const Shape &s, int batch, int device);
 // Exchange words of one sequence: q/k/v of two layer phases, the attention
-// output, the residual row entering the last block, the logits and each
-// workgroup's XCD.
+// output, the normalised final row, the logits and each workgroup's XCD.
 size_t persistent_exchange_words(const Shape &s);
 // Builds the layer-0 table q0 (V x 3 x W floats, row order): for each token,
 // the Q, K and V meshes of block 0 on its normalised vector, before QK-norm
