@@ -2730,6 +2730,85 @@ __device__ __forceinline__ T *opaque(T *p) {
     return reinterpret_cast<T *>((uint64_t(hi) << 32) | lo);
 }
 
+// Whether row_mesh2 applies: a fixed-depth mesh of depth >= 3 whose first
+// two strides (1 and 2) both cross waves.
+template <int NW, int D>
+constexpr bool kMesh2 = NW >= 4 && D >= 3;
+
+// Layer-0 weights (row order) of channels chan(j) + 2, which row_mesh2 needs
+// besides the lane's own.
+template <int NW, int CPL, int GL>
+__device__ __forceinline__ void load_mesh_far(float2 (&w)[CPL], const float *wg, const RowCtx<NW, CPL, GL> &c) {
+    constexpr int W = RowCtx<NW, CPL, GL>::W;
+    const global_u64 *g = (const global_u64 *)opaque(wg);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) w[j] = __builtin_bit_cast(float2, uint64_t(g[row_of<NW>((c.chan(j) + 2) & (W - 1))]));
+}
+
+// n = mesh(x), or mesh(x * inv_rms(x)) with RMS, for a mesh whose first two
+// strides cross waves: one LDS exchange serves both layers (each lane reads
+// channels c + 1 .. c + 3 and computes layer 0 of channel c + 2 as well, with
+// its weights w0far), and with RMS the row reduction shares its barrier.  The
+// arithmetic of row_inv_rms and row_run_mesh, value for value.
+template <bool RMS, int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void row_mesh2(RowCtx<NW, CPL, GL> &c, const float (&x)[CPL], float (&n)[CPL],
+                                          const float2 (&w)[D][CPL], const float2 (&w0far)[CPL], int k) {
+    static_assert(kMesh2<NW, D>, "strides 1 and 2 must cross waves");
+    constexpr int W = 64 * NW * CPL;
+    constexpr int LOG2W = W == 128 ? 7 : W == 256 ? 8 : W == 512 ? 9 : 10;
+    const int lane = c.lane, wave = c.wave;
+    float *red = c.slot(k);
+    if constexpr (RMS) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc = fmaf(x[j], x[j], acc);
+        acc = wave_sum(acc);
+        if (lane == 0) red[wave] = acc;
+    }
+    float *b = c.xch + (c.parity & 1) * (NW * CPL * 64);
+    ++c.parity;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) b[(j * NW + wave) * 64 + lane] = x[j];
+    __syncthreads();
+    float inv = 1.0f;
+    if constexpr (RMS) {
+        float t = 0.0f;
+#pragma unroll
+        for (int v = 0; v < NW; ++v) t += red[v];
+        inv = rsqrtf(t * (1.0f / float(W)) + kRmsEps);
+    }
+    auto scaled = [&](float v) { return RMS ? v * inv : v; };
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        const int ch = c.chan(j);
+        const float n0 = scaled(x[j]), n1 = scaled(b[row_of<NW>((ch + 1) & (W - 1))]);
+        const float n2 = scaled(b[row_of<NW>((ch + 2) & (W - 1))]), n3 = scaled(b[row_of<NW>((ch + 3) & (W - 1))]);
+        const float z0 = elu(n0 * w[0][j].x + n1 * w[0][j].y);
+        const float z2 = elu(n2 * w0far[j].x + n3 * w0far[j].y);
+        n[j] = elu(z0 * w[1][j].x + z2 * w[1][j].y);
+    }
+    static_for<D>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        if constexpr (u > 1) row_layer<NW, CPL>(n, w[u], 1 << (u % LOG2W), u + 1 == D, lane, wave, c.xch, c.parity);
+    });
+}
+
+// The post-attention half (row_post without XSA) with row_mesh2 heads: the
+// projection mesh on y, the residual, then the FFN mesh on the normalised row
+// and its residual.
+template <int NW, int CPL, int GL, int D>
+__device__ __forceinline__ void team_post_mesh2(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], const float (&y)[CPL],
+                                                const float2 (&wp)[D][CPL], const float2 (&wp2)[CPL],
+                                                const float2 (&wf)[D][CPL], const float2 (&wf2)[CPL]) {
+    float t[CPL];
+    row_mesh2<false>(c, y, t, wp, wp2, 2);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] += t[j];
+    row_mesh2<true>(c, x, t, wf, wf2, 2);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] += t[j];
+}
+
 template <int NW, int CPL, int GL, int D>
 __device__ __forceinline__ void load_block_weights(float2 (&w)[D][CPL], const float *g, bool fixed, int lane,
                                                    int wave) {
@@ -2821,10 +2900,18 @@ __device__ __forceinline__ void persistent_last_block(const PersistArgs &a, RowC
     float2 wp[D][CPL], wf[D][CPL];
     load_block_weights<NW, CPL, GL, D>(wp, wlast + 3 * gA, FIXED, c.lane, c.wave);
     load_block_weights<NW, CPL, GL, D>(wf, wlast + 4 * gA, FIXED, c.lane, c.wave);
+    float2 wp2[CPL], wf2[CPL];
+    if constexpr (FIXED && kMesh2<NW, D>) {
+        load_mesh_far(wp2, wlast + 3 * gA, c);
+        load_mesh_far(wf2, wlast + 4 * gA, c);
+    }
     float y[CPL];
     take_attention_output(a, c, xc, g, y);
     const int nb = 3 + s.H, V = s.V, t0 = slice * V / nb, t1 = (slice + 1) * V / nb;
-    row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
+    if constexpr (FIXED && kMesh2<NW, D>)
+        team_post_mesh2(c, x, y, wp, wp2, wf, wf2);
+    else
+        row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wlast + 3 * gA, wlast + 4 * gA, s, FIXED);
     const float inv = row_inv_rms(c, x, 3);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
@@ -2907,14 +2994,25 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             load_block_weights<NW, CPL, GL, D>(wm, wb + team * gA, FIXED, c.lane, c.wave);
             load_block_weights<NW, CPL, GL, D>(wp, wq + 3 * gA, FIXED, c.lane, c.wave);
             load_block_weights<NW, CPL, GL, D>(wf, wq + 4 * gA, FIXED, c.lane, c.wave);
+            float2 wp2[CPL], wf2[CPL], wm2[CPL];  // layer 0 of channels c + 2 (row_mesh2)
+            if constexpr (FIXED && kMesh2<NW, D>) {
+                load_mesh_far(wp2, wq + 3 * gA, c);
+                load_mesh_far(wf2, wq + 4 * gA, c);
+                load_mesh_far(wm2, wb + team * gA, c);
+            }
             float y[CPL];
             take_attention_output(a, c, xc, g - 1, y);
             trace_mark(a, xc.row, step, l, 0);
-            row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
+            if constexpr (FIXED && kMesh2<NW, D>)
+                team_post_mesh2(c, x, y, wp, wp2, wf, wf2);
+            else
+                row_post<NW, CPL, GL, D, false>(c, x, y, y, wp, wf, wq + 3 * gA, wq + 4 * gA, s, FIXED);
             // q and k go out before QK-norm and RoPE, which the attention
             // workgroups apply per head.
             float n[CPL];
-            if constexpr (FIXED && NW > 1) {
+            if constexpr (FIXED && kMesh2<NW, D>) {
+                row_mesh2<true>(c, x, n, wm, wm2, 3);
+            } else if constexpr (FIXED && NW > 1) {
                 row_rms_mesh(c, x, n, wm, 3);
             } else {
                 const float inv = row_inv_rms(c, x, 3);
