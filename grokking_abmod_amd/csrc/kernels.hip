@@ -2879,6 +2879,13 @@ __device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc
     // A near-tie's scratch is the mesh exchange buffer (2W >= V floats): the
     // last block's meshes are done before any logit is published, and the
     // next meshes follow barriers that this wave reaches only after drawing.
+    // A wave issues one instruction per four cycles and this code runs once
+    // per step on the critical path: a vocabulary of at most 256 tokens (four
+    // per lane) gets the version unrolled for four.
+    if (R <= 4) {
+        const float l4[4] = {lg[0], lg[1], lg[2], lg[3]};
+        return uint32_t(wave_choose_token(l4, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
+    }
     return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
 }
 
