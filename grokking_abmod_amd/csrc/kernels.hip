@@ -3049,17 +3049,17 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
 // QK-norm over the head, then RoPE at `pos` (reference.rs:462-482), for an
 // attention lane's dims d0 .. d0 + VEC - 1 (each group of LPK lanes holds the
 // whole head; the RoPE partner dim, hd/2 away, is LPK/2 lanes away).  The
-// arithmetic of row_qk_rope: with VEC == NW its head sums (lanes, then waves
-// in order) are these per-dim lane sums added in dim order.
+// head's sum of squares adds each lane's dims first, then the lanes (one
+// group reduction instead of one per dim): the same sum as row_qk_rope's in
+// another order, within a few f32 roundings of it.
 // cs[e] is the (cos, sin) pair of dim d0 + e at the position (rope_pair).
 template <int LPK, int VEC>
 __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const float2 (&cs)[VEC], const Shape &s) {
-    float sq[VEC], other[VEC];
+    float other[VEC];
+    float sq = 0.0f;
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) sq[e] = x[e] * x[e];
-    float ss = 0.0f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) ss += group_sum<LPK>(sq[e]);
+    for (int e = 0; e < VEC; ++e) sq = fmaf(x[e], x[e], sq);
+    const float ss = group_sum<LPK>(sq);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
         // lane ^ 8 inside a 16-lane row is DPP row_ror:8
