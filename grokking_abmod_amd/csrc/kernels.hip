@@ -3127,7 +3127,10 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             const int nr = (pos + G * U - 1) / (G * U);
             const int ntail = min(max(nr - NS, 0), 2);
             const int nring = nr - ntail;
-            for (int r = 0; r < min(NS, nring); ++r) ring.issue(kl, vl, r, pos, tid);
+            // Layer 0's first rounds were issued at the end of the previous
+            // step (below), before its logits and draw.
+            if (l > 0 || step == 0)
+                for (int r = 0; r < min(NS, nring); ++r) ring.issue(kl, vl, r, pos, tid);
             R last, last2;
             if (ntail > 0) last.load(kl, vl, nring * G * U, pos);
             if (ntail > 1) last2.load(kl, vl, (nring + 1) * G * U, pos);
@@ -3267,6 +3270,16 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
         // the attention.
         int tid = int(threadIdx.x);
         asm volatile("" : "+v"(tid));
+        if (step + 1 < a.steps) {
+            // The next step's layer-0 ring rounds depend on no token: they
+            // load during the logits and the draw (which wait for them, as
+            // loads complete in order, long after they have landed) instead
+            // of after the draw.  The ring is idle until then.
+            const int p1 = pos + 1, nr1 = (p1 + G * U - 1) / (G * U);
+            const int nring1 = nr1 - min(max(nr1 - NS, 0), 2);
+            const float *kl0 = a.kc + slab, *vl0 = a.vc + slab;
+            for (int r = 0; r < min(NS, nring1); ++r) ring.issue(kl0, vl0, r, p1, tid);
+        }
         const Ctx c(m.xch, m.red, tid);
         persistent_head_logits<NW, CPL, GL>(a, c, xc, step, 3 + h, m);
         trace_mark(a, xc.row, step, L, 1);
