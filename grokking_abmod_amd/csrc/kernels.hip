@@ -3287,6 +3287,53 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
     }
 }
 
+// Role of the k-th of the K = Q * R workgroups of an XCD, as (sequence q of
+// the XCD's Q, role r of R = 3 + H).  The dispatcher gives each of the XCD's C
+// CUs one workgroup in order, then puts workgroup C + p beside workgroup p
+// (two fit per CU): the first P = K - C share a CU with a later one.  Those
+// pairs are attention workgroups, a head of one sequence beside the same
+// head of another, and the mesh teams, whose phase is the longer one on the
+// chain, keep a CU to themselves.  (Measured on config 3 at batch 32: 59.5 us
+// per step, against 62.3 with pairs in plain order and 61.7 with each team
+// beside a head of its own sequence.)  Any other placement only costs speed:
+// every role of a sequence stays on one XCD, and the map is a bijection of
+// [0, K).
+__host__ __device__ inline void persistent_role(int k, int K, int C, int R, int &q, int &r) {
+    const int P = K - C, Q = K / R, H = R - 3;
+    if (P <= 0 || 2 * P > Q * H || Q < 2 || C < P) {
+        q = k / R;
+        r = k % R;
+        return;
+    }
+    // Paired slots take heads in head-major order, (q, h) = (i % Q, i / Q):
+    // slot p the 2p-th, slot C + p the next, of another sequence.
+    auto head_at = [&](int i, int &qq, int &rr) {
+        qq = i % Q;
+        rr = 3 + i / Q;
+    };
+    if (k < P) {
+        head_at(2 * k, q, r);
+        return;
+    }
+    if (k >= C && k < C + P) {
+        head_at(2 * (k - C) + 1, q, r);
+        return;
+    }
+    // The other roles in (q, r) order over the remaining slots.
+    int o = k < C ? k - P : k - 2 * P;
+    for (int qq = 0; qq < Q; ++qq)
+        for (int rr = 0; rr < R; ++rr) {
+            if (rr >= 3 && (rr - 3) * Q + qq < 2 * P) continue;  // a paired head
+            if (o-- == 0) {
+                q = qq;
+                r = rr;
+                return;
+            }
+        }
+    q = Q;  // not reached for k < K
+    r = 0;
+}
+
 // Blocks [0, 3*batch): mesh teams (sequence, team); then (sequence, head)
 // attention blocks.  Needs every block resident at once (cooperative launch).
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
@@ -3303,11 +3350,13 @@ persistent_decode_kernel(PersistArgs a) {
     stage_exp_table(exp_tab);  // the teams' first barrier comes long before their first draw
     const PersistLds m{xch, red, xn, row, ring, exp_tab, KvRing<HDP, NW, Ring::UL, Ring::NS>::SLOT * Ring::NS};
     // Workgroup i runs on XCD i % 8 when the dispatcher deals workgroups out
-    // round-robin, as it does on MI355X: the 3 + H workgroups of a sequence are
-    // i = x + 8 * (R * q + r) for sequence x + 8q and role r, all on XCD x.
-    // (The handshake checks it; any other placement only costs speed.)
+    // round-robin, as it does on MI355X: the 3 + H workgroups of sequence
+    // x + 8q are workgroups x + 8k of XCD x, k given by persistent_role.  (The
+    // handshake checks it; any other placement only costs speed.)
     const int R = 3 + a.s.H, x = int(blockIdx.x) % 8, k = int(blockIdx.x) / 8;
-    const int b = x + 8 * (k / R), r = k % R;
+    int q, r;
+    persistent_role(k, int(gridDim.x) / 8, a.xcd_cus, R, q, r);
+    const int b = x + 8 * q;
     if (b >= a.batch) return;
     const int trow = r < 3 ? 3 * b + r : 3 * a.batch + b * a.s.H + (r - 3);
     const PersistXch<false> far(a, b, trow);
@@ -3691,6 +3740,11 @@ hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream) {
     if (!f) return hipErrorInvalidValue;
     PersistArgs args = a;
     args.scale_log2 = float(1.4426950408889634 / std::sqrt(double(a.s.hd)));
+    int device = 0, cus = 0;
+    if (hipGetDevice(&device) != hipSuccess ||
+        hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
+        return hipErrorInvalidDevice;
+    args.xcd_cus = cus / 8;
     void *params[] = {&args};
     return hipLaunchCooperativeKernel(f, dim3(persistent_blocks(a.s, a.batch)), dim3(64 * row_waves(a.s.W)), params, 0,
                                       stream);

@@ -133,6 +133,7 @@ struct PersistArgs {
     size_t xstride;       // persistent_exchange_words(shape)
     int *abort;           // zero at launch; set when a wait times out
     float scale_log2;     // set by persistent_decode
+    int xcd_cus;          // CUs per XCD, set by persistent_decode
     // Optional timeline (nullptr: none): for block k, step t and phase l,
     // trace[((k * steps + t) * (layers + 1) + l) * 2 + {0, 1}] receive the
     // wall clock (100 MHz) when the phase's inputs were ready and when its

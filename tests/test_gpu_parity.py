@@ -349,6 +349,23 @@ def test_persistent_decode_matches_per_phase_kernels(name, temperature, monkeypa
     assert_close(l0, l1, what="persistent vs per-phase decode logits")
 
 
+def test_persistent_decode_full_batch_matches_per_phase_kernels(monkeypatch):
+    # 32 sequences of config 3 need more workgroups than the GPU has CUs, so
+    # some share a CU and the launch maps roles to workgroups with its pairing
+    # map; it must decode what the per-phase kernels decode.
+    config = G.named_config("mid")
+    prompts = (np.arange(32 * 20).reshape(32, 20) * 5 % config.vocab_size).astype(np.uint32)
+    results = []
+    for disable in ("0", "1"):
+        monkeypatch.setenv("MG_DISABLE_PERSISTENT", disable)
+        with G.MeshGpt(0, config, 7, max_batch=32) as model:
+            tokens = model.generate_tokens(prompts, 24, 1.0, 13)
+            results.append((tokens, model.last_logits(32)))
+    (t0, l0), (t1, l1) = results
+    assert np.array_equal(t0, t1)
+    assert_close(l0, l1, what="persistent vs per-phase decode logits, batch 32")
+
+
 def test_persistent_decode_steps_continue_a_generation():
     # decode(k) after prefill appends exactly the tokens a single generate call
     # produces (the persistent launch picks up the sampler state and lengths).
