@@ -2,19 +2,24 @@
 
 Workload ("mid"): vocabulary 256, width 512, 8 heads x 64,
 6 blocks, butterfly meshes of depth 9, context 1024, batch 32, 64-token
-uniform-random prompts, temperature 1.0 with per-sequence seeds 7+b; seeded
-reference initialisation (seed 7).  A step is one decode step of the whole
-batch (32 tokens).  Prompts are prefilled untimed; the timed region is K decode
-steps starting right after the prompt (K = 512 is the full config-3 run), with
-every input already resident in HBM.
+uniform-random prompts (Random::new(7).index(256)), temperature 1.0 with
+per-sequence seeds 7+b; seeded reference initialisation (seed 7).
 
-The K steps run as one launch of the persistent decode kernel, so the timed
-region is that kernel: HIP events recorded on the model's stream right
-before and after the launch give its duration, and the roofline divides the
-steps' algorithmic HBM bytes (KV-cache reads and appends, mesh weights, tied
-head table, token ids) by it.  Prints one JSON line with that roofline, the
-batch-1 (config 1) figure and the CPU baseline (the f64 oracle on one core, a
-bounded sample of the workload).
+A bench step is one whole config-3 decode: 512 decode steps of all 32
+sequences (positions 64..575, 16384 tokens), in one launch of the persistent
+decode kernel.  The prompts are prefilled once, untimed; before each step the
+decode state is rewound to the prefill's (lengths and sampler states, two tiny
+device copies: mg_decode_rewind), so every step decodes the same 16384 tokens
+from inputs resident in HBM.  `value` is tokens/s over the K timed steps by
+the host clock between device synchronisations; the roofline divides the
+algorithmic HBM bytes of one launch by the launch's average duration from HIP
+events recorded on the model's stream around it.
+
+Beside the headline: the first 20 decode steps alone (the latency-bound
+short-context end), config 1 at batch 1, config 2's single 9409-row prefill,
+config 4's 8192-token prefill and long-context decode, config 5's batch-256
+decode, the measured copy bandwidth of the box, HBM traffic from rocprofv3
+counters, and the CPU baseline (the f64 oracle on one core, a bounded sample).
 """
 import argparse
 import ctypes
@@ -34,8 +39,12 @@ sys.path.insert(0, ROOT)
 
 import grokking_abmod_amd as G  # noqa: E402
 
-HBM_PEAK_GBPS = 8000.0  # MI355X HBM3E, published
+HBM_PEAK_GBPS = 8000.0      # MI355X HBM3E, published
+FP32_PEAK_TFLOPS = 157.3    # MI355X FP32 (vector with packed FP32, and matrix), published
 METRIC = "decode tokens/sec @1 GPU (batch 1 and 32) + % of HBM roofline per decode step"
+KERNEL = "persistent_decode_kernel"
+DECODE_STEPS = 512          # config 3: decode steps per sequence
+PROBE_COPY_BYTES = 256 << 20
 
 
 class Hip:
@@ -47,7 +56,6 @@ class Hip:
         self.lib.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.lib.hipEventSynchronize.argtypes = [ctypes.c_void_p]
         self.lib.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
-        self.lib.hipEventDestroy.argtypes = [ctypes.c_void_p]
         self.lib.hipDeviceSynchronize.argtypes = []
 
     def event(self):
@@ -68,66 +76,51 @@ class Hip:
         assert self.lib.hipDeviceSynchronize() == 0
 
 
-def prompts_for(config, batch, length, seed=7):
-    """Uniform token ids from Random::new(seed).index(V), sequence b after b-1."""
-    state = [seed]
-
-    def next_u64():
-        state[0] = (state[0] + 0x9E3779B97F4A7C15) & 0xFFFFFFFFFFFFFFFF
-        z = state[0]
-        z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & 0xFFFFFFFFFFFFFFFF
-        z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & 0xFFFFFFFFFFFFFFFF
-        return z ^ (z >> 31)
-
-    bound = config.vocab_size
-    threshold = ((1 << 64) - bound) % bound
-    out = np.empty((batch, length), dtype=np.uint32)
-    for b in range(batch):
-        for i in range(length):
-            while True:
-                bits = next_u64()
-                if bits >= threshold:
-                    out[b, i] = bits % bound
-                    break
-    return out
-
-
 def step_bytes(config, batch, position):
-    """Algorithmic HBM bytes of a whole decode step (all layers): KV reads and
-    appends, mesh weights, the tied head table and the token ids."""
+    """Algorithmic HBM bytes of one decode step of every sequence at `position`
+    (all layers): the `position` cached K and V rows read (the current row's
+    key and value stay on chip), the new rows appended, the mesh weights, the
+    tied head table and the token ids."""
     w, layers = config.width, config.layers
     meshes = 4 * config.attention_mesh_depth + config.ffn_mesh_depth
-    return (batch * layers * 2 * w * 4 * (position + 1) + batch * layers * 2 * w * 4
+    return (batch * layers * 2 * w * 4 * position + batch * layers * 2 * w * 4
             + 8 * w * layers * meshes + 4 * config.vocab_size * w + 4 * batch)
 
 
-def run_decode(hip, model, prompts, steps, temperature, seed):
-    """Prefill (untimed) then `steps` timed decode steps (one persistent launch
-    when the model supports it); returns (event ms, wall ms)."""
-    model.prefill(prompts, temperature, seed, reserve=prompts.shape[1] + 1 + steps)
-    hip.synchronize()
+def decode_bytes(config, batch, first, steps):
+    return float(sum(step_bytes(config, batch, p) for p in range(first, first + steps)))
+
+
+def timed_decode(hip, model, steps):
+    """model.decode(steps) bracketed by HIP events on the model's stream (ms)."""
     stream = model.stream()
     start, stop = hip.event(), hip.event()
-    t0 = time.perf_counter()
     hip.record(start, stream)
     model.decode(steps)
     hip.record(stop, stream)
-    hip.synchronize()
-    wall = (time.perf_counter() - t0) * 1000.0
-    return hip.elapsed_ms(start, stop), wall
+    return hip.elapsed_ms(start, stop)
+
+
+def cpu_name():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
 
 
 def cpu_baseline(config, prompts, steps, temperature, budget_s):
     """The f64 oracle's KV-cached decode on one host core over whole sequences
-    of the workload (prompt + all decode steps), until budget_s is spent."""
+    of the workload (prompt, then all decode steps), until budget_s is spent."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
 
     o = O.config(**{k: v for k, v in config.as_dict().items() if k != "long_context"})
     params = O.initialize(o, 7)
-    tokens = 0
-    seconds = 0.0
-    done = 0
+    tokens, seconds, done = 0, 0.0, 0
     for b in range(prompts.shape[0]):
         t0 = time.perf_counter()
         O.generate(o, params, prompts[b], 1, temperature, 7 + b, cached=True)
@@ -139,45 +132,32 @@ def cpu_baseline(config, prompts, steps, temperature, budget_s):
         done += 1
         if t2 - t0 + seconds > budget_s:
             break
-    cpu = platform.processor() or platform.machine()
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {
         "value": round(tokens / seconds, 2),
         "unit": "tokens/s",
         "cores": 1,
         "kind": "port",
         "sample": f"{done} of {prompts.shape[0]} sequences, each its {prompts.shape[1]}-token prompt "
-                  f"then {steps} decode steps; decode time only; f64 KV-cached oracle; {cpu}",
+                  f"then {steps} decode steps; decode time only; f64 KV-cached oracle; {cpu_name()}",
     }
 
 
-KERNEL = "persistent_decode_kernel"
-
-
-def pmc_traffic(args, config, batch):
-    """HBM bytes of the persistent decode launch of the timed steps, from two
-    rocprofv3 --pmc runs of a child process (FETCH_SIZE, then WRITE_SIZE), each
-    scaled by the same counter on a plain copy kernel of known size.  Returns
-    None when unavailable."""
+def pmc_traffic(args):
+    """HBM bytes of one bench-step launch, from two rocprofv3 --pmc runs of a
+    child process (FETCH_SIZE, then WRITE_SIZE), each scaled by the same
+    counter on a plain copy kernel of known size.  Every run's return code is
+    reported; a failed run is not repeated."""
     rocprof = "/opt/rocm/bin/rocprofv3"
+    report = {"runs": []}
     if not os.path.exists(rocprof):
-        return None
+        report["error"] = "rocprofv3 not found"
+        return report
     import csv
 
-    def collect(counter):
-        # rocprofv3 may exit with a segmentation fault after the program ends
-        # (cooperative launches); the counter file is complete by then.
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
         out = tempfile.mkdtemp(prefix="mg_pmc_")
         cmd = ["timeout", "-s", "KILL", "90", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
-               "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe",
-               "--steps", str(args.steps), "--prompt", str(args.prompt), "--batch", str(batch)]
+               "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe"]
         res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
         hits, copy = [], []
         for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
@@ -185,115 +165,182 @@ def pmc_traffic(args, config, batch):
                 for row in csv.DictReader(f):
                     name = row.get("Kernel_Name", "")
                     value = float(row.get("Counter_Value", "nan"))
-                    if KERNEL in name:
+                    if KERNEL in name and "<4, 2, 16, 9, 64>" in name:
                         hits.append(value)
                     elif "calibration_copy" in name:
                         copy.append(value)
+        # rocprofv3 can end with a segmentation fault after its tool
+        # finalisation when the program made cooperative launches; the
+        # counter file is complete by then, so the rows decide.
+        report["runs"].append({"counter": counter, "rc": res.returncode, "kernel_rows": len(hits),
+                               "copy_rows": len(copy)})
         if not hits or not copy:
-            sys.stderr.write(f"pmc {counter}: kernel rows {len(hits)}, copy rows {len(copy)} "
-                             f"(rc={res.returncode})\n{res.stderr[-1500:]}\n")
-        return hits, copy
-
-    per_counter = {}
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        hits, copy = collect(counter)
-        if not hits or not copy:
-            hits, copy = collect(counter)
-        if not hits or not copy:
-            return None
-        copy_kib = PROBE_COPY_BYTES / 1024.0
-        factor = copy_kib / float(np.mean(copy))
-        per_counter[counter] = float(np.mean(hits)) * factor * 1024.0
-        per_counter[counter + "_factor"] = factor
-    return per_counter
+            report["error"] = f"{counter}: no counter rows (rc {res.returncode}): {res.stderr[-300:]}"
+            return report
+        factor = (PROBE_COPY_BYTES / 1024.0) / float(np.mean(copy))
+        report[counter] = float(np.mean(hits)) * factor * 1024.0
+        report[counter + "_factor"] = factor
+    return report
 
 
-PROBE_COPY_BYTES = 256 << 20
-
-
-def probe(args):
-    """Child process under rocprofv3 --pmc: the timed region's decode steps (same
-    positions, one persistent launch) and one plain copy kernel of known size
-    for calibration."""
+def probe():
+    """Child process under rocprofv3 --pmc: one bench step (the prefill, then
+    the 512-step decode launch) and one plain copy of known size."""
     config = G.named_config("mid")
-    prompts = prompts_for(config, args.batch, args.prompt)
-    with G.MeshGpt(0, config, 7, max_batch=args.batch) as model:
-        model.prefill(prompts, 1.0, 7, reserve=args.prompt + 1 + args.steps)
-        model.decode(args.steps)
+    prompts = G.random_prompts(256, 32, 64, 7)
+    with G.MeshGpt(0, config, 7, max_batch=32) as model:
+        model.prefill(prompts, 1.0, 7, reserve=64 + 1 + DECODE_STEPS)
+        model.decode(DECODE_STEPS)
     G.calibration_copy(PROBE_COPY_BYTES)
 
 
 def batch1_figure(hip, steps=128):
     """batch 1, 16-token prompt, greedy decode 128 tokens."""
     config = G.named_config("tiny")
-    prompts = prompts_for(config, 1, 16)
+    prompts = G.random_prompts(64, 1, 16, 7)
     with G.MeshGpt(0, config, 7) as model:
-        run_decode(hip, model, prompts, steps, 0.0, 7)  # warm-up
-        ms, _ = run_decode(hip, model, prompts, steps, 0.0, 7)
+        model.prefill(prompts, 0.0, 7, reserve=16 + 1 + steps)
+        model.decode(steps)  # warm-up
+        model.rewind()
+        ms = timed_decode(hip, model, steps)
     return {"workload": "config 1 (tiny): V64 W128 H4x32 L2 butterfly depth 7, ctx 256, batch 1, "
-                        "16-token prompt, 128 greedy decode steps",
+                        "16-token prompt, 128 greedy decode steps (one persistent launch)",
             "tokens_per_s": round(steps / (ms / 1000.0), 1), "us_per_token": round(1000.0 * ms / steps, 2)}
+
+
+def symbolic_figure():
+    """one prefill of all 9409 'a + b =' rows, last-position
+    logits over the 99 tokens (the grok evaluation's forward)."""
+    config = G.named_config("symbolic")
+    a, b = np.meshgrid(np.arange(97), np.arange(97), indexing="ij")
+    x = np.stack([a.ravel(), np.full(a.size, 97), b.ravel(), np.full(a.size, 98)], axis=1).astype(np.uint32)
+    with G.MeshGpt(0, config, 7) as model:
+        model.logits(x.ravel(), 4, last_only=True)  # warm-up (workspace growth)
+        times = []
+        for _ in range(5):
+            model.logits(x.ravel(), 4, last_only=True)
+            times.append(model.last_call_ms())
+    ms = float(np.median(times))
+    rows, W, L = x.size, config.width, config.layers
+    meshes = 4 * rows * W * L * (4 * config.attention_mesh_depth + config.ffn_mesh_depth)
+    hd = W // config.heads
+    attention = 9409 * L * config.heads * 2 * hd * 4 * 5
+    head = 2 * 9409 * W * config.vocab_size
+    flops = meshes + attention + head
+    return {"workload": "config 2 (symbolic): V99 W128 H4x32 L2 neighbor A4 F6, 9409 rows of 4 tokens, "
+                        "last-position logits; kernel time (HIP events, host copies excluded), median of 5",
+            "us": round(1000.0 * ms, 1), "flop": flops,
+            "tflops": round(flops / (ms / 1000.0) / 1e12, 3),
+            "fp32_frac": round(flops / (ms / 1000.0) / 1e12 / FP32_PEAK_TFLOPS, 4)}
+
+
+def long_figure(hip, decode_steps=256):
+    """batch 8, 8192-token prefill, then 256 greedy decode
+    steps over 8192..8447 keys."""
+    config = G.named_config("long")
+    prompts = G.random_prompts(256, 8, 8192, 7)
+    with G.MeshGpt(0, config, 7, max_batch=8) as model:
+        model.prefill(prompts, 0.0, 7, reserve=8192 + 1 + decode_steps)
+        prefill_ms = model.last_call_ms()
+        model.decode(decode_steps)  # warm-up
+        model.rewind()
+        ms = timed_decode(hip, model, decode_steps)
+    W, L, H = config.width, config.layers, config.heads
+    hd, n = W // H, 8192
+    attention = 8 * L * H * 2 * hd * n * (n + 1)
+    meshes = 4 * 8 * n * W * L * (4 * config.attention_mesh_depth + config.ffn_mesh_depth)
+    nbytes = decode_bytes(config, 8, 8192, decode_steps)
+    return {"workload": "config 4 (long): V256 W512 H8x64 L4 butterfly depth 9, ctx 8448, batch 8, "
+                        "8192-token prompts, 256 greedy decode steps",
+            "prefill_ms": round(prefill_ms, 3),
+            "prefill_tflops": round((attention + meshes) / (prefill_ms / 1000.0) / 1e12, 2),
+            "prefill_attention_flop": attention, "prefill_mesh_flop": meshes,
+            "decode_tokens_per_s": round(8 * decode_steps / (ms / 1000.0), 1),
+            "decode_us_per_step": round(1000.0 * ms / decode_steps, 2),
+            "decode_hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def high_figure(hip, decode_steps=64):
+    """batch 256, W1024 L12, 128-token prompts, greedy decode
+    (the first 64 of its 1024 steps)."""
+    config = G.named_config("high")
+    prompts = G.random_prompts(256, 256, 128, 7)
+    with G.MeshGpt(0, config, 7, max_batch=256) as model:
+        model.prefill(prompts, 0.0, 7, reserve=128 + 1 + decode_steps)
+        prefill_ms = model.last_call_ms()
+        model.decode(decode_steps)  # warm-up and graph capture
+        model.rewind()
+        ms = timed_decode(hip, model, decode_steps)
+    nbytes = decode_bytes(config, 256, 128, decode_steps)
+    return {"workload": "config 5 (high): V256 W1024 H16x64 L12 butterfly depth 10, ctx 2048, batch 256, "
+                        f"128-token prompts, greedy decode steps at positions 128..{127 + decode_steps}",
+            "prefill_ms": round(prefill_ms, 3),
+            "decode_tokens_per_s": round(256 * decode_steps / (ms / 1000.0), 1),
+            "decode_us_per_step": round(1000.0 * ms / decode_steps, 2),
+            "decode_hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def main():
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=512)
-    parser.add_argument("--warmup", type=int, default=16)
-    parser.add_argument("--batch", type=int, default=32)
-    parser.add_argument("--prompt", type=int, default=64)
+    parser.add_argument("--steps", type=int, default=5, help="timed whole 512-step decodes")
+    parser.add_argument("--warmup", type=int, default=2)
     parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-pmc", action="store_true")
+    parser.add_argument("--no-extra", action="store_true", help="config 3 only")
     parser.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
 
     if args.probe:
-        probe(args)
+        probe()
         return
     if args.gpus != 1:
         print(f"bench.py measures one GPU only: this build has no multi-GPU path (asked for --gpus {args.gpus}); "
               "decode would shard by sequence with no per-step exchange between GPUs.", file=sys.stderr)
         sys.exit(2)
+    if args.steps < 1:
+        sys.exit("--steps must be at least 1")
 
-    config = G.named_config("mid")
-    if args.prompt + args.steps > config.context or args.prompt + args.warmup > config.context:
-        sys.exit(f"prompt + steps must stay within the context ({config.context})")
     # The counter runs go first, while this process has not touched the GPU:
     # the profiled child is then the only process on it.
-    traffic = None
-    pmc = None
-    if not args.no_pmc:
-        try:
-            pmc = pmc_traffic(args, config, args.batch)
-        except Exception as exc:  # counters are optional evidence, never the result
-            sys.stderr.write(f"pmc collection failed: {exc}\n")
-            pmc = None
-        if pmc:
-            traffic = round(pmc["FETCH_SIZE"] + pmc["WRITE_SIZE"])
-    temperature = 1.0
-    prompts = prompts_for(config, args.batch, args.prompt)
-    hip = Hip()
-    with G.MeshGpt(0, config, 7, max_batch=args.batch) as model:
-        # Warm-up: a full prefill and W decode steps.
-        if args.warmup:
-            model.prefill(prompts, temperature, 7, reserve=args.prompt + 1 + max(args.steps, args.warmup))
-            model.decode(args.warmup)
-            hip.synchronize()
-        ms, wall_ms = run_decode(hip, model, prompts, args.steps, temperature, 7)
+    pmc = None if args.no_pmc else pmc_traffic(args)
 
-    positions = args.prompt + np.arange(args.steps)
-    total_bytes = float(sum(step_bytes(config, args.batch, p) for p in positions))
-    gbps = total_bytes / (ms / 1000.0) / 1e9
+    config = G.named_config("mid")
+    batch, prompt_len, temperature = 32, 64, 1.0
+    prompts = G.random_prompts(config.vocab_size, batch, prompt_len, 7)
+    hip = Hip()
+    with G.MeshGpt(0, config, 7, max_batch=batch) as model:
+        model.prefill(prompts, temperature, 7, reserve=prompt_len + 1 + DECODE_STEPS)
+        for _ in range(args.warmup):
+            model.rewind()
+            model.decode(DECODE_STEPS)
+        hip.synchronize()
+        launch_ms = []
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            model.rewind()
+            launch_ms.append(timed_decode(hip, model, DECODE_STEPS))
+        hip.synchronize()
+        wall_s = time.perf_counter() - t0
+        # The latency-bound end alone: the first 20 decode steps.
+        model.rewind()
+        early_ms = timed_decode(hip, model, 20)
+
+    avg_ms = float(np.mean(launch_ms))
+    launch_bytes = decode_bytes(config, batch, prompt_len, DECODE_STEPS)
+    gbps = launch_bytes / (avg_ms / 1000.0) / 1e9
+    early_bytes = decode_bytes(config, batch, prompt_len, 20)
+    tokens = batch * DECODE_STEPS * args.steps
 
     result = {
         "metric": METRIC,
-        "value": round(args.batch * args.steps / (ms / 1000.0), 1),
+        "value": round(tokens / wall_s, 1),
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": round(ms / args.steps, 5),
+        "ms_per_step": round(1000.0 * wall_s / args.steps, 4),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -301,34 +348,46 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": "config 3 (mid): V256 W512 H8x64 L6 butterfly depth 9, ctx 1024, batch 32, "
-                        "64-token uniform-random prompts, T=1.0 seeded sampling; timed decode steps "
-                        f"at positions {args.prompt}..{args.prompt + args.steps - 1}",
-            "batch": args.batch, "prompt": args.prompt, "context": config.context, "width": config.width,
-            "heads": config.heads, "layers": config.layers, "mesh_depth": config.attention_mesh_depth,
-            "vocab": config.vocab_size, "temperature": temperature, "init": "reference seed 7",
+                        "64-token uniform-random prompts, T=1.0 seeded sampling; one step = all 512 decode "
+                        "steps of the batch (positions 64..575, 16384 tokens) from the rewound prefill state",
+            "batch": batch, "prompt": prompt_len, "decode_steps_per_step": DECODE_STEPS,
+            "context": config.context, "width": config.width, "heads": config.heads, "layers": config.layers,
+            "mesh_depth": config.attention_mesh_depth, "vocab": config.vocab_size, "temperature": temperature,
+            "init": "reference seed 7",
         },
+        "us_per_decode_step": round(1000.0 * avg_ms / DECODE_STEPS, 2),
         "roofline": {
             "bound": "hbm",
-            "kernel": "persistent_decode_kernel<4, 2, 16, 9, 64> (one launch = all timed steps)",
+            "kernel": "persistent_decode_kernel<4, 2, 16, 9, 64> (one launch = one bench step)",
             "achieved": round(gbps, 1),
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "traffic": traffic,
-            "traffic_calibration": None if not pmc else {
-                "fetch_factor": round(pmc["FETCH_SIZE_factor"], 4), "write_factor": round(pmc["WRITE_SIZE_factor"], 4),
-                "fetch_bytes": round(pmc["FETCH_SIZE"]), "write_bytes": round(pmc["WRITE_SIZE"])},
-            "algorithmic_bytes_per_launch": round(total_bytes),
-            "algorithmic_bytes_per_step": round(total_bytes / args.steps),
-            "avg_launch_us": round(ms * 1000.0, 1),
+            "traffic": None,
+            "algorithmic_bytes_per_launch": round(launch_bytes),
+            "avg_launch_us": round(avg_ms * 1000.0, 1),
+            "launch_us": [round(m * 1000.0, 1) for m in launch_ms],
         },
-        "wall_ms_timed_region": round(wall_ms, 3),
+        "early_slice": {
+            "positions": f"{prompt_len}..{prompt_len + 19}",
+            "us_per_decode_step": round(1000.0 * early_ms / 20, 2),
+            "tokens_per_s": round(batch * 20 / (early_ms / 1000.0), 1),
+            "hbm_frac": round(early_bytes / (early_ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4),
+        },
     }
+    if pmc is not None:
+        result["roofline"]["traffic_calibration"] = pmc
+        if "FETCH_SIZE" in pmc and "WRITE_SIZE" in pmc:
+            result["roofline"]["traffic"] = round(pmc["FETCH_SIZE"] + pmc["WRITE_SIZE"])
     result["batch1"] = batch1_figure(hip)
+    if not args.no_extra:
+        result["config2"] = symbolic_figure()
+        result["config4"] = long_figure(hip)
+        result["config5"] = high_figure(hip)
     # Measured copy roofline of this box (read + write bytes of a plain copy kernel).
     result["copy_gbps"] = round(G.copy_bandwidth(1 << 30, 10), 1)
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline(config, prompts, args.steps, temperature, args.cpu_budget)
+        result["cpu_baseline"] = cpu_baseline(config, prompts, DECODE_STEPS, temperature, args.cpu_budget)
     print(json.dumps(result))
 
 

@@ -23,7 +23,7 @@ EXPORTS = (
     "mg_initial_parameters", "mg_token_codes", "mg_model_create", "mg_model_destroy",
     "mg_model_config", "mg_parameters", "mg_set_parameters", "mg_logits", "mg_token_embeddings",
     "mg_hidden_states", "mg_generate", "mg_generate_text", "mg_prefill", "mg_decode",
-    "mg_decode_profiled", "mg_decode_traced", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
+    "mg_decode_rewind", "mg_last_call_ms", "mg_decode_profiled", "mg_decode_traced", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
     "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_expf",
@@ -98,6 +98,8 @@ def lib():
         "mg_generate_text": (i, [vp, _u32p, sz, ctypes.c_char_p, sz, f, u64, ctypes.c_char_p, sz, _szp]),
         "mg_prefill": (i, [vp, _u32p, sz, sz, f, u64, sz]),
         "mg_decode": (i, [vp, sz]),
+        "mg_decode_rewind": (i, [vp]),
+        "mg_last_call_ms": (i, [vp, ctypes.POINTER(ctypes.c_float)]),
         "mg_decode_profiled": (i, [vp, sz, _f32p, sz]),
         "mg_decode_traced": (i, [vp, sz, ctypes.POINTER(ctypes.c_uint64), sz]),
         "mg_sequence_length": (i, [vp, _szp]),
@@ -285,6 +287,16 @@ class MeshGpt:
     def decode(self, steps):
         _check(lib().mg_decode(self._h, steps))
 
+    def last_call_ms(self):
+        """Kernel time of the last logits / hidden_states / prefill call (ms)."""
+        ms = ctypes.c_float()
+        _check(lib().mg_last_call_ms(self._h, ctypes.byref(ms)))
+        return ms.value
+
+    def rewind(self):
+        """Back to the decode state the last prefill left (mg_decode_rewind)."""
+        _check(lib().mg_decode_rewind(self._h))
+
     def decode_profiled(self, steps):
         out = np.empty(steps * self._config.layers, dtype=np.float32)
         _check(lib().mg_decode_profiled(self._h, steps, _p(out, _f32p), out.size))
@@ -392,6 +404,32 @@ class Checkpoint:
         chars = _u32([ord(c) if isinstance(c, str) else c for c in self.characters])
         _check(lib().mg_checkpoint_save(os.fsencode(path), ctypes.byref(self.config), _p(chars, _u32p),
                                         chars.size, _p(self.parameters, _f32p), self.parameters.size))
+
+
+_MASK64 = (1 << 64) - 1
+
+
+def random_prompts(vocab_size, batch, length, seed=7):
+    """Uniform token ids as the synthetic workloads draw them: Random::new(seed)
+    (SplitMix64, src/mesh.rs:256-274) and index(vocab_size) with its rejection
+    threshold (mesh.rs:277-288), sequence b drawn after sequence b-1; a
+    (batch, length) uint32 array.  The CLI's --random-prompt draws the same."""
+    state = seed & _MASK64
+    bound = int(vocab_size)
+    threshold = ((1 << 64) - bound) % bound
+    out = np.empty((batch, length), dtype=np.uint32)
+    for b in range(batch):
+        for i in range(length):
+            while True:
+                state = (state + 0x9E3779B97F4A7C15) & _MASK64
+                z = state
+                z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & _MASK64
+                z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & _MASK64
+                z ^= z >> 31
+                if z >= threshold:
+                    out[b, i] = z % bound
+                    break
+    return out
 
 
 def named_config(name):

@@ -206,6 +206,17 @@ int mg_decode(mg_model *model, size_t steps) {
     return guarded([&] { model_of(model).decode(steps); });
 }
 
+int mg_last_call_ms(mg_model *model, float *ms) {
+    return guarded([&] {
+        require(ms != nullptr, "output must not be null");
+        *ms = model_of(model).last_call_ms();
+    });
+}
+
+int mg_decode_rewind(mg_model *model) {
+    return guarded([&] { model_of(model).rewind(); });
+}
+
 int mg_decode_profiled(mg_model *model, size_t steps, float *ms, size_t n) {
     return guarded([&] { copy_out(model_of(model).decode_profiled(steps), ms, n); });
 }

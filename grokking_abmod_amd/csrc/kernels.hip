@@ -2152,16 +2152,45 @@ __device__ __forceinline__ int first_lane_value(bool has, int v, int none) {
     return mask ? __builtin_amdgcn_readlane(v, int(__builtin_ctzll(mask))) : none;
 }
 
+// The reference's sequential f32 process (sequential_pick) run by a whole
+// wave on p_i held in its registers: token t = j*R + k is pc[k] of lane j.
+// Each p_i reaches every lane by a lane read (an exact copy), so all lanes
+// compute the same sum and remainder; no memory is touched.
+template <int RMAX>
+__device__ __forceinline__ int wave_sequential_pick(const float (&pc)[RMAX], int R, int V, float u) {
+#pragma clang fp contract(off)
+    auto at = [&](int k, int j) {
+        return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, pc[k]), j));
+    };
+    float sum = 0.0f;
+    for (int j = 0; j < 64; ++j) {
+#pragma unroll
+        for (int k = 0; k < RMAX; ++k)
+            if (k < R && j * R + k < V) sum = sum + at(k, j);
+    }
+    float sample = u * sum;
+    for (int j = 0; j < 64; ++j) {
+#pragma unroll
+        for (int k = 0; k < RMAX; ++k) {
+            if (k < R && j * R + k < V) {
+                sample = sample - at(k, j);
+                if (sample < 0.0f) return j * R + k;
+            }
+        }
+    }
+    return V - 1;
+}
+
 // choose_token's decision made by one wave on its own: lane l holds the
 // logits of the contiguous run [l*R, l*R + R) of tokens in lg[0..R),
 // R = ceil(V / 64) <= RMAX, and u is the generator's draw (made by the
 // caller, so that it is ready before the logits are).  Every lane returns the
-// token.  Only a near-tie touches memory: the wave writes its p_i to
-// scratch[0..V) (LDS; several waves may share it, as they write the same
-// values) and runs the sequential f32 process on them.
+// token.  Nothing touches memory but the non-finite flag: a near-tie runs the
+// sequential f32 process on the wave's registers (wave_sequential_pick), so
+// waves of one workgroup never share scratch and need no barrier.
 template <int RMAX>
 __device__ __forceinline__ int wave_choose_token(const float (&lg)[RMAX], int V, float temperature, float u,
-                                                 const uint64_t *exp_tab, int *flags, float *scratch) {
+                                                 const uint64_t *exp_tab, int *flags) {
     static_assert(RMAX % 4 == 0, "runs are handled four tokens at a time");
     // V is hidden from the optimiser so that the f64 constants derived from it
     // are formed here, not hoisted out of a caller's step loop and spilled.
@@ -2239,13 +2268,7 @@ __device__ __forceinline__ int wave_choose_token(const float (&lg)[RMAX], int V,
     key = first_lane_value(key != INT_MAX, key, INT_MAX);
     if (key == INT_MAX) return V - 1;
     if (!(key & 1)) return key >> 1;
-#pragma unroll
-    for (int k = 0; k < RMAX; ++k)
-        if (k < R && i0 + k < V) scratch[i0 + k] = pc[k];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    return sequential_pick([&](int t) { return scratch[t]; }, V, u);
+    return wave_sequential_pick(pc, R, V, u);
 }
 
 // Random::unit (src/mesh.rs:263-265): one SplitMix64 draw per sampled token.
@@ -2287,14 +2310,16 @@ sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64
 
 // The same choice made by one wave per sequence (wave_choose_token, the
 // persistent decode's sampler), for vocabularies of at most kWaveSampleVocab.
+// RMAX tokens per lane at most: vocabularies of at most 256 run the
+// four-token version the persistent decode uses for them, larger ones the
+// sixteen-token version.
 constexpr int kWaveSampleVocab = 1024;
 
+template <int RMAX>
 __global__ void __launch_bounds__(64)
 wave_sample_kernel(const float *__restrict__ logits, int V, float temperature, uint64_t *rng, uint32_t *tokens,
                    int tok_stride, int *len, int *flags) {
-    constexpr int RMAX = kWaveSampleVocab / 64;
     __shared__ uint64_t tab[32];
-    __shared__ float scratch[kWaveSampleVocab];
     const int b = blockIdx.x, R = (V + 63) / 64, i0 = int(threadIdx.x) * R;
     const float *src = logits + size_t(b) * V;
     float lg[RMAX];
@@ -2304,7 +2329,7 @@ wave_sample_kernel(const float *__restrict__ logits, int V, float temperature, u
     __syncthreads();
     uint64_t state = rng[b];
     const float u = temperature == 0.0f ? 0.0f : rng_unit(state);  // greedy draws nothing
-    const int token = wave_choose_token(lg, V, temperature, u, tab, flags, scratch);
+    const int token = wave_choose_token(lg, V, temperature, u, tab, flags);
     if (threadIdx.x == 0) rng[b] = state;
     append_token(tokens, tok_stride, len, b, token);
 }
@@ -2876,17 +2901,14 @@ __device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc
         for (int k = 0; k < RMAX; ++k)
             if (k < R && i0 + k < V) o[k] = lg[k];
     }
-    // A near-tie's scratch is the mesh exchange buffer (2W >= V floats): the
-    // last block's meshes are done before any logit is published, and the
-    // next meshes follow barriers that this wave reaches only after drawing.
     // A wave issues one instruction per four cycles and this code runs once
     // per step on the critical path: a vocabulary of at most 256 tokens (four
     // per lane) gets the version unrolled for four.
     if (R <= 4) {
         const float l4[4] = {lg[0], lg[1], lg[2], lg[3]};
-        return uint32_t(wave_choose_token(l4, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
+        return uint32_t(wave_choose_token(l4, V, a.temperature, u, m.exp_tab, a.flags));
     }
-    return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags, m.xch));
+    return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags));
 }
 
 // Post-attention half of the last block on team `slice`'s residual row x and
@@ -3831,9 +3853,12 @@ void calibration_copy(const float4 *src, float4 *dst, size_t n, hipStream_t stre
 
 void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng, uint32_t *tokens,
             int tok_stride, int *len, int *flags, hipStream_t stream) {
-    if (V <= kWaveSampleVocab)
-        hipLaunchKernelGGL(wave_sample_kernel, dim3(batch), dim3(64), 0, stream, logits, V, temperature, rng, tokens,
-                           tok_stride, len, flags);
+    if (V <= 256)
+        hipLaunchKernelGGL(wave_sample_kernel<4>, dim3(batch), dim3(64), 0, stream, logits, V, temperature, rng,
+                           tokens, tok_stride, len, flags);
+    else if (V <= kWaveSampleVocab)
+        hipLaunchKernelGGL(wave_sample_kernel<kWaveSampleVocab / 64>, dim3(batch), dim3(64), 0, stream, logits, V,
+                           temperature, rng, tokens, tok_stride, len, flags);
     else
         hipLaunchKernelGGL(sample_kernel, dim3(batch), dim3(kThreads), 0, stream, logits, V, temperature, rng, tokens,
                            tok_stride, len, flags);

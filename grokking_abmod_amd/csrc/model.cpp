@@ -85,6 +85,9 @@ struct MeshGpt::Impl {
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
     size_t batch_cap = 0, tcap = 0;
     DevBuf kc, vc, dx, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
+    // Sampler states and length right after the last prefill (rewind()).
+    DevBuf drng_start;
+    size_t start_length = 0;
     // Persistent decode kernel state: tagged exchange words of every sequence
     // and the abort flag.
     DevBuf pxch, pabort;
@@ -110,10 +113,22 @@ struct MeshGpt::Impl {
     // it (MG_DISABLE_PERSISTENT=1 keeps the per-phase kernels).
     bool persistent_ok = false;
 
+    // Events around the kernels of the last logits / hidden_states / prefill
+    // call (last_call_ms).
+    hipEvent_t call_ev[2] = {nullptr, nullptr};
+    float call_ms = 0.0f;
+
     ~Impl() {
         drop_graph();
+        for (hipEvent_t e : call_ev)
+            if (e) (void)hipEventDestroy(e);
         if (stream) (void)hipStreamDestroy(stream);
     }
+
+    void mark_call(int which) { check(hipEventRecord(call_ev[which], stream), "hipEventRecord"); }
+
+    // After the call's sync: the time between its two marks.
+    void close_call() { check(hipEventElapsedTime(&call_ms, call_ev[0], call_ev[1]), "hipEventElapsedTime"); }
 
     void activate() const { check(hipSetDevice(device), "hipSetDevice"); }
 
@@ -195,6 +210,7 @@ struct MeshGpt::Impl {
         lds_limit = size_t(lds);
         kern::configure_lds(lds_limit);
         check(hipStreamCreateWithFlags(&stream, hipStreamNonBlocking), "hipStreamCreate");
+        for (hipEvent_t &e : call_ev) check(hipEventCreate(&e), "hipEventCreate");
         use_graph = env_int("MG_DISABLE_GRAPH", 0) == 0;
 
         const size_t W = cfg.width, hd = cfg.head_width();
@@ -298,6 +314,7 @@ struct MeshGpt::Impl {
             part.ensure(slots * cfg.heads * (shape.hdp + 2) * 4);
             dlen.ensure(batch_cap * 4);
             drng.ensure(batch_cap * 8);
+            drng_start.ensure(batch_cap * 8);
             dlogits.ensure(batch_cap * cfg.vocab_size * 4);
             dflags.ensure(4);
             if (persistent_ok) {
@@ -399,6 +416,7 @@ struct MeshGpt::Impl {
     void forward_rows(const uint32_t *tokens, size_t n, size_t sequence, size_t out_rows) {
         ensure_workspace(n, out_rows, true);
         check(hipMemcpyAsync(wtok.p, tokens, n * 4, hipMemcpyHostToDevice, stream), "upload tokens");
+        mark_call(0);
         kern::Rows rows{int(n), int(sequence), nullptr, wtok.as<uint32_t>(), int(sequence), 0};
         const kern::KvView kv{wk.as<float>(), wv.as<float>(), int(sequence)};
         run_blocks(rows, int(n / sequence), [&](size_t) { return kv; }, wx.as<float>(), wq.as<float>(),
@@ -413,10 +431,12 @@ struct MeshGpt::Impl {
         kern::head(shape, wxn.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
                    last_only ? int(sequence) - 1 : 0, Et.as<float>(), vpad, wlogits.as<float>(), head_rows(),
                    stream);
+        mark_call(1);
         std::vector<float> out(out_rows * cfg.vocab_size);
         check(hipMemcpyAsync(out.data(), wlogits.p, out.size() * 4, hipMemcpyDeviceToHost, stream),
               "download logits");
         sync();
+        close_call();
         validate_finite(out.data(), out.size(), "logits");
         return out;
     }
@@ -425,9 +445,11 @@ struct MeshGpt::Impl {
         cfg.validate_tokens(tokens, n, sequence);
         activate();
         forward_rows(tokens, n, sequence, 1);
+        mark_call(1);
         std::vector<float> out(n * cfg.width);
         check(hipMemcpyAsync(out.data(), wx.p, out.size() * 4, hipMemcpyDeviceToHost, stream), "download");
         sync();
+        close_call();
         validate_finite(out.data(), out.size(), "features");
         return out;
     }
@@ -455,6 +477,7 @@ struct MeshGpt::Impl {
         length = p;
         cached = 0;
         temperature = t;
+        start_length = 0;
     }
 
     // The head and sampler for `n` sequence rows of xn (row i at i*row_mul+row_add).
@@ -665,8 +688,26 @@ void MeshGpt::prefill(const uint32_t *prompts, size_t batch, size_t prompt_len, 
                       size_t reserve) {
     Impl &m = *impl_;
     m.start(prompts, batch, prompt_len, temperature, seed, std::max(reserve, prompt_len + 1));
+    m.mark_call(0);
     m.step();
+    m.mark_call(1);
     m.finish();
+    m.close_call();
+    check(hipMemcpyAsync(m.drng_start.p, m.drng.p, m.batch * 8, hipMemcpyDeviceToDevice, m.stream), "save rng");
+    m.start_length = m.length;
+    m.sync();
+}
+
+void MeshGpt::rewind() {
+    Impl &m = *impl_;
+    if (m.start_length == 0 || m.length < m.start_length || m.start_length > m.cfg.context)
+        throw Error("rewind needs a prefilled batch");
+    m.activate();
+    check(hipMemcpyAsync(m.drng.p, m.drng_start.p, m.batch * 8, hipMemcpyDeviceToDevice, m.stream),
+          "restore rng");
+    check(hipMemsetD32Async(hipDeviceptr_t(m.dlen.p), int(m.start_length), m.batch, m.stream), "restore lengths");
+    m.length = m.start_length;
+    m.cached = m.length - 1;
 }
 
 void MeshGpt::decode(size_t steps) {
@@ -730,6 +771,8 @@ std::vector<uint64_t> MeshGpt::decode_traced(size_t steps) {
 }
 
 size_t MeshGpt::sequence_length() const { return impl_->length; }
+
+float MeshGpt::last_call_ms() const { return impl_->call_ms; }
 
 void MeshGpt::read_tokens(uint32_t *out, size_t batch, size_t length) { impl_->read_tokens(out, batch, length); }
 

@@ -42,6 +42,10 @@ class MeshGpt {
     void prefill(const uint32_t *prompts, size_t batch, size_t prompt_len, float temperature,
                  uint64_t seed, size_t reserve);
     void decode(size_t steps);
+    // Back to the state the last prefill() left (lengths and sampler states).
+    void rewind();
+    // Kernel time (ms, HIP events) of the last logits / hidden_states / prefill call.
+    float last_call_ms() const;
     // Same steps without graph replay, timing every decode-attention launch
     // with HIP events; returns milliseconds per launch (steps x layers).
     std::vector<float> decode_profiled(size_t steps);

@@ -116,6 +116,18 @@ int mg_decode_profiled(mg_model *model, size_t steps, float *ms, size_t n);
  * inputs were ready and when its outputs were published.  Fails with
  * MG_UNSUPPORTED when the persistent kernel cannot run this model and batch. */
 int mg_decode_traced(mg_model *model, size_t steps, uint64_t *stamps, size_t n);
+/* Restores the decode state that the last mg_prefill left: every sequence's
+ * length and sampler state (no reference counterpart: it lets a benchmark
+ * repeat the same decode steps from resident inputs).  The cache rows of the
+ * prompts stay valid; rows of later positions are rewritten by the next
+ * decode.  Two small device copies on the model's stream; nothing is
+ * allocated. */
+int mg_decode_rewind(mg_model *model);
+/* Device time in milliseconds of the kernels of the last mg_logits,
+ * mg_hidden_states or mg_prefill call on this model (HIP events on the
+ * model's stream around its kernels; host copies excluded).  No reference
+ * counterpart: it lets a benchmark time a prefill without the PCIe copies. */
+int mg_last_call_ms(mg_model *model, float *ms);
 /* Current tokens per sequence (prompt + generated). */
 int mg_sequence_length(const mg_model *model, size_t *out);
 int mg_read_tokens(mg_model *model, uint32_t *out, size_t batch, size_t length);

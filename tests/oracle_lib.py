@@ -281,3 +281,27 @@ def equation_inputs(residue_tokens, eqs, modulus=97):
     x[:, 2] = residue_tokens[eqs[:, 1]]
     x[:, 3] = modulus + 1
     return x.reshape(-1), residue_tokens[eqs[:, 2]]
+
+
+_MASK = (1 << 64) - 1
+_GOLDEN = 0x9E3779B97F4A7C15
+_C1, _C2 = 0xBF58476D1CE4E5B9, 0x94D049BB133111EB
+
+
+def _unxorshift(y, s):
+    x = y
+    for _ in range(64 // s + 1):
+        x = y ^ (x >> s)
+    return x & _MASK
+
+
+def state_for_unit(k):
+    """A SplitMix64 state whose next Random::unit() draw is k / 2^24
+    (src/mesh.rs:263-274), by inverting the output mix."""
+    z = (k << 40) | 0x12345
+    z = _unxorshift(z, 31)
+    z = (z * pow(_C2, -1, 1 << 64)) & _MASK
+    z = _unxorshift(z, 27)
+    z = (z * pow(_C1, -1, 1 << 64)) & _MASK
+    z = _unxorshift(z, 30)
+    return (z - _GOLDEN) & _MASK

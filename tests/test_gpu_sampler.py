@@ -18,28 +18,7 @@ import oracle_lib as O
 
 pytestmark = pytest.mark.gpu
 
-MASK = (1 << 64) - 1
-GOLDEN = 0x9E3779B97F4A7C15
-C1, C2 = 0xBF58476D1CE4E5B9, 0x94D049BB133111EB
-
-
-def _unxorshift(y, s):
-    x = y
-    for _ in range(64 // s + 1):
-        x = y ^ (x >> s)
-    return x & MASK
-
-
-def state_for_unit(k):
-    """A SplitMix64 state whose next Random::unit() draw is k / 2^24
-    (src/mesh.rs:263-274), by inverting the output mix."""
-    z = (k << 40) | 0x12345
-    z = _unxorshift(z, 31)
-    z = (z * pow(C2, -1, 1 << 64)) & MASK
-    z = _unxorshift(z, 27)
-    z = (z * pow(C1, -1, 1 << 64)) & MASK
-    z = _unxorshift(z, 30)
-    return (z - GOLDEN) & MASK
+state_for_unit = O.state_for_unit
 
 
 def oracle_sample(rows, temperature, states):

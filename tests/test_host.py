@@ -107,6 +107,17 @@ def test_parameter_counts_of_the_benchmark_configs():
         assert G.parameter_count(G.named_config(name)) == count
 
 
+def test_random_prompts_are_reference_index_draws():
+    # The synthetic prompts: Random::new(seed).index(V) (src/mesh.rs:277-288)
+    # in sequence order, against the oracle's restatement of the generator.
+    for vocab, batch, length, seed in ((256, 3, 17, 7), (64, 1, 16, 7), (99, 2, 5, 2**64 - 1), (3, 2, 40, 0)):
+        got = G.random_prompts(vocab, batch, length, seed)
+        state = O.ctypes.c_uint64(seed)
+        want = [O.lib().og_rng_index(O.ctypes.byref(state), vocab) for _ in range(batch * length)]
+        assert got.dtype == np.uint32 and got.shape == (batch, length)
+        assert np.array_equal(got.ravel(), np.array(want, dtype=np.uint32))
+
+
 # ---------------------------------------------------------------- tokenizer
 
 def test_tokenizer_round_trip_and_errors():

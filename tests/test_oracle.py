@@ -470,6 +470,90 @@ def test_sampler_temperature_is_f32_cdf_scan():
         assert token == expected, trial
 
 
+# Pins of the temperature sampler (gpu.rs:2028-2049) that the mathematics
+# fixes: the reference holds no sampler vector, so these check the oracle's
+# restatement against closed forms, an exact symmetry and the distribution it
+# must realise.
+
+def _unit_state(k):
+    """A SplitMix64 state whose next Random::unit() is exactly k / 2^24."""
+    return O.state_for_unit(k)
+
+
+def test_sampler_equal_logits_pick_floor_of_u_times_vocab():
+    # V equal logits: every p_i is exp(0) = 1, the f32 sum is exactly V and each
+    # subtraction is exact, so the token is floor(u * V) whenever u * V is not
+    # within rounding of an integer.  A reversed or shifted scan fails this.
+    rng = np.random.default_rng(11)
+    for V in (2, 3, 7, 64, 99, 256, 1000):
+        for T in (0.5, 1.0, 3.0):
+            checked = 0
+            for k in rng.integers(0, 1 << 24, 200):
+                u = int(k) / 16777216.0
+                x = u * V
+                if abs(x - round(x)) < 1e-5:
+                    continue
+                token, _ = O.sample(np.full(V, 1.25, np.float32), T, _unit_state(int(k)))
+                assert token == int(np.floor(x)), (V, T, int(k))
+                checked += 1
+            assert checked > 150
+
+
+def test_sampler_dominant_logit_wins_for_every_draw():
+    # One logit 40/T above the others: its p is 1 and the others' sum is below
+    # V * e^-40 < 2^-24, so for every draw u >= 2^-24 the remainder stays
+    # non-negative until the dominant token, and 1 - u > 0 after it: the
+    # dominant token is drawn, including for the largest u = 1 - 2^-24.  The
+    # draw u = 0 makes the first remainder -p_0 < 0, so token 0 is drawn.
+    for V in (2, 5, 64, 256):
+        for T in (0.25, 1.0, 2.0):
+            for j in sorted({0, V // 2, V - 1}):
+                row = np.zeros(V, np.float32)
+                row[j] = np.float32(40.0 * T)
+                for k in (1, 2, 1 << 23, (1 << 24) - 2, (1 << 24) - 1):
+                    token, _ = O.sample(row, T, _unit_state(k))
+                    assert token == j, (V, T, j, k)
+                assert O.sample(row, T, _unit_state(0))[0] == 0
+
+
+def test_sampler_power_of_two_rescaling_is_exact():
+    # (c*l_i - c*max) / (c*T) rounds exactly as (l_i - max) / T in f32 when c is
+    # a power of two (every product, difference and quotient scales exactly), so
+    # the token and the generator state cannot change.  A sampler that drops T,
+    # or subtracts a different maximum, changes tokens here.
+    rng = np.random.default_rng(5)
+    for trial in range(300):
+        V = int(rng.integers(2, 300))
+        row = (rng.normal(size=V) * 2).astype(np.float32)
+        T = float(rng.choice([0.3, 0.7, 1.0, 2.5]))
+        seed = int(rng.integers(0, 2**63))
+        base = O.sample(row, T, seed)
+        for c in (0.5, 2.0, 8.0):
+            assert O.sample((row * np.float32(c)).astype(np.float32), T * c, seed) == base, (trial, c)
+
+
+def test_sampler_realises_the_softmax_distribution():
+    # Seeded chi-square test over 120000 draws per temperature against the f64
+    # softmax of l / T; the seeds are fixed, so the test is deterministic.  A
+    # sampler that ignores T, scans one token off, or never returns some token
+    # is rejected with a p-value far below the threshold.
+    from scipy.stats import chi2
+    rng = np.random.default_rng(17)
+    V = 12
+    row = (rng.normal(size=V) * 1.5).astype(np.float32)
+    for T in (0.5, 1.0, 2.0):
+        p = np.exp((row.astype(np.float64) - row.max()) / T)
+        p /= p.sum()
+        counts = np.zeros(V)
+        state = 1234567
+        for _ in range(120000):
+            token, state = O.sample(row, T, state)
+            counts[token] += 1
+        expected = p * counts.sum()
+        stat = float(((counts - expected) ** 2 / expected).sum())
+        assert chi2.sf(stat, V - 1) > 1e-6, (T, stat)
+
+
 def test_generate_window_slides_and_cached_decode_matches_recompute():
     # gpu.rs:2006-2053: every step recomputes the last <= context tokens; within
     # the context the KV-cached loop is the same computation.
