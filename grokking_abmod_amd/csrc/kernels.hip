@@ -1380,8 +1380,9 @@ row_block_kernel(BlockArgs a) {
         row_post(c, x, y, v, wp, wf, a.wproj, a.wffn, s, FIXED);
     }
     if (team == 0 && (post || a.embed)) {
+        // Into x_out, never x: the row's other workgroups may not have read x yet.
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) a.x[size_t(row) * W + c.ridx(j)] = x[j];
+        for (int j = 0; j < CPL; ++j) a.x_out[size_t(row) * W + c.ridx(j)] = x[j];
     }
     if (!a.xn && !pre) return;
 

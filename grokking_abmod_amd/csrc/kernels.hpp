@@ -53,7 +53,11 @@ struct KvView {
 struct BlockArgs {
     Shape s;
     Rows ro;
-    float *x;  // residual rows, read and written
+    float *x;  // residual rows, read (and written when x_out is null)
+    // Where the updated residual rows go.  row_block() needs a buffer other
+    // than x: its three workgroups of a row read x, and one of them writes the
+    // update, which the others could otherwise read when they start later.
+    float *x_out;
     // post half: weights, attention output (split partials or rows), block l-1's cache
     const float *wproj, *wffn;
     const float *part;
@@ -102,6 +106,8 @@ void block_decode(const BlockArgs &a, hipStream_t stream);
 // row_waves(W) waves: channel c = wave + NW*(lane + 64*j)).  Needs W in
 // {128, 256, 512, 1024} and hd / NW in {8, 16, 32}.  Its E, x and mesh weights
 // are in row order (row_order()); xn, q and the cache stay in channel order.
+// It reads the residual rows from a.x and writes them to a.x_out, which must
+// be a different buffer.
 int row_waves(int W);
 bool row_block_supported(const Shape &s);
 void row_block(const BlockArgs &a, hipStream_t stream);

@@ -84,7 +84,7 @@ struct MeshGpt::Impl {
     // Decode state: KV cache [L][batch_cap][H][context][hdp], per-sequence
     // tokens [batch_cap][tcap], lengths, SplitMix64 states and logits.
     size_t batch_cap = 0, tcap = 0;
-    DevBuf kc, vc, dx, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
+    DevBuf kc, vc, dx, dx2, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
     // Sampler states and length right after the last prefill (rewind()).
     DevBuf drng_start;
     size_t start_length = 0;
@@ -307,6 +307,7 @@ struct MeshGpt::Impl {
             check(hipMemsetAsync(kc.p, 0, cache, stream), "zero cache");
             check(hipMemsetAsync(vc.p, 0, cache, stream), "zero cache");
             dx.ensure(batch_cap * cfg.width * 4);
+            dx2.ensure(batch_cap * cfg.width * 4);
             dxn.ensure(batch_cap * cfg.width * 4);
             dq.ensure(batch_cap * cfg.width * 4);
             size_t slots = 0;
@@ -354,18 +355,22 @@ struct MeshGpt::Impl {
     // `events`, each decode-attention launch stamps its own begin and end into
     // events[2l] and events[2l+1].
     template <class KvOf>
-    void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *q, float *y, float *xn,
-                    bool decode, hipEvent_t *events = nullptr) {
+    void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *x2, float *q, float *y,
+                    float *xn, bool decode, hipEvent_t *events = nullptr) {
         const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
         const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
         const bool rows_order = decode && row_decode;
         auto weights = [&](size_t id) { return rows_order ? group_rows(id) : group(id); };
+        // The row-order kernel reads the residual rows from one buffer and
+        // writes them to the other (kern::BlockArgs::x_out); the rest update in place.
+        float *xin = x, *xout = rows_order ? x2 : x;
         for (size_t l = 0; l <= L; ++l) {
             kern::BlockArgs a{};
             a.s = shape;
             a.ro = rows;
-            a.x = x;
+            a.x = xin;
+            a.x_out = xout;
             a.rpw = t.rpw;
             a.teams = t.teams;
             if (l > 0) {
@@ -390,8 +395,11 @@ struct MeshGpt::Impl {
             } else {
                 a.xn = xn;
             }
-            if (rows_order)
+            if (rows_order) {
+                if (xout == xin) throw Error("row-order decode needs two residual buffers", kDeviceError);
                 kern::row_block(a, stream);
+                std::swap(xin, xout);
+            }
             else if (decode && wave_decode)
                 kern::block_decode(a, stream);
             else
@@ -419,7 +427,7 @@ struct MeshGpt::Impl {
         mark_call(0);
         kern::Rows rows{int(n), int(sequence), nullptr, wtok.as<uint32_t>(), int(sequence), 0};
         const kern::KvView kv{wk.as<float>(), wv.as<float>(), int(sequence)};
-        run_blocks(rows, int(n / sequence), [&](size_t) { return kv; }, wx.as<float>(), wq.as<float>(),
+        run_blocks(rows, int(n / sequence), [&](size_t) { return kv; }, wx.as<float>(), nullptr, wq.as<float>(),
                    wy.as<float>(), wxn.as<float>(), false);
     }
 
@@ -496,8 +504,8 @@ struct MeshGpt::Impl {
 
     void launch_decode_step(hipEvent_t *events = nullptr) {
         const kern::Rows rows{int(batch), 1, dlen.as<int>(), dtokens.as<uint32_t>(), int(tcap), 0};
-        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, dx.as<float>(), dq.as<float>(),
-                   nullptr, dxn.as<float>(), true, events);
+        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, dx.as<float>(), dx2.as<float>(),
+                   dq.as<float>(), nullptr, dxn.as<float>(), true, events);
         head_and_sample(dxn.as<float>(), 1, 0);
     }
 
@@ -528,8 +536,8 @@ struct MeshGpt::Impl {
     void prefill_step(size_t start, size_t n) {
         ensure_workspace(batch * n, 1, false);
         const kern::Rows rows{int(batch * n), int(n), nullptr, dtokens.as<uint32_t>(), int(tcap), int(start)};
-        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, wx.as<float>(), wq.as<float>(),
-                   wy.as<float>(), wxn.as<float>(), false);
+        run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, wx.as<float>(), nullptr,
+                   wq.as<float>(), wy.as<float>(), wxn.as<float>(), false);
         head_and_sample(wxn.as<float>(), int(n), int(n) - 1);
     }
 
