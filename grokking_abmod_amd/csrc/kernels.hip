@@ -403,7 +403,7 @@ block_kernel(BlockArgs a) {
                 yv = a.ybuf[size_t(row) * W + c];
             }
             Y[idx] = yv;
-            Vs[idx] = a.kv_post.v[(size_t(seq * s.H + h) * a.kv_post.cap + pos) * s.hdp + d];
+            if (a.xsa_post) Vs[idx] = a.kv_post.v[(size_t(seq * s.H + h) * a.kv_post.cap + pos) * s.hdp + d];
         }
         X[idx] = xv;
     }
@@ -420,18 +420,20 @@ block_kernel(BlockArgs a) {
         }
         const float2 *wp = STAGED ? S : reinterpret_cast<const float2 *>(a.wproj);
         const float2 *wf = wp + size_t(s.A) * W;
-        // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
-        segment_dots(Y, Vs, nr * s.H, s.hd, inv1, inv2);
-        __syncthreads();
-        for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
-            int r, c, h, d;
-            split_row(idx, s, r, c);
-            split_head(c, s, h, d);
-            const int sg = r * s.H + h;
-            const float iv = rsqrtf(fmaxf(inv1[sg], kXsaFloor));
-            Y[idx] = Y[idx] - (inv2[sg] * iv) * (Vs[idx] * iv);
+        if (a.xsa_post) {
+            // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
+            segment_dots(Y, Vs, nr * s.H, s.hd, inv1, inv2);
+            __syncthreads();
+            for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
+                int r, c, h, d;
+                split_row(idx, s, r, c);
+                split_head(c, s, h, d);
+                const int sg = r * s.H + h;
+                const float iv = rsqrtf(fmaxf(inv1[sg], kXsaFloor));
+                Y[idx] = Y[idx] - (inv2[sg] * iv) * (Vs[idx] * iv);
+            }
+            __syncthreads();
         }
-        __syncthreads();
         const float *proj = mesh_team<CPTW>(Y, buf(1), N, nr, s, wp, s.A, threadIdx.x, blockDim.x, true);
         for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) X[idx] += proj[idx];
         __syncthreads();

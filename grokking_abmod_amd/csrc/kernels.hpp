@@ -63,6 +63,9 @@ struct BlockArgs {
     const float *part;
     int nsplit;
     const float *ybuf;  // attention rows when part is null
+    // 1: the post half applies XSA to the attention output (split partials,
+    // or rows from attn_prefill); 0: the output already has it (attn_prefill_mfma).
+    int xsa_post;
     KvView kv_post;
     // pre half: weights, token vectors when embed, query rows out, block l's cache
     const float *wq, *wk, *wv;
@@ -171,6 +174,12 @@ void attn_decode(const Shape &s, const float *q, KvView kv, const int *len, int 
 // Causal flash attention over whole sequences already appended to the cache.
 void attn_prefill(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y,
                   hipStream_t stream);
+// The same on the FP32 matrix cores, with XSA applied to each output row when
+// xsa != 0 (then the block's post half must not apply it again).  Supported
+// when attn_prefill_mfma_supported(); the sequences are at least 64 rows long.
+bool attn_prefill_mfma_supported(const Shape &s, int rows_per_seq);
+void attn_prefill_mfma(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y, int xsa,
+                       hipStream_t stream);
 // logits[i][t] = xn[i*row_mul+row_add] . E[t] (xn already RMS-normalised).
 void head(const Shape &s, const float *xn, int nrows, int row_mul, int row_add, const float *Et, int Vp,
           float *logits, int rt, hipStream_t stream);

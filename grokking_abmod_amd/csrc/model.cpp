@@ -112,6 +112,7 @@ struct MeshGpt::Impl {
     // Decode steps run in one persistent launch when the shape and batch allow
     // it (MG_DISABLE_PERSISTENT=1 keeps the per-phase kernels).
     bool persistent_ok = false;
+    bool use_mfma_prefill = true;
 
     // Events around the kernels of the last logits / hidden_states / prefill
     // call (last_call_ms).
@@ -229,6 +230,7 @@ struct MeshGpt::Impl {
         wave_decode = env_int("MG_DISABLE_WAVE_DECODE", 0) == 0 && kern::block_decode_supported(shape);
         row_decode = env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
         persistent_ok = row_decode && env_int("MG_DISABLE_PERSISTENT", 0) == 0;
+        use_mfma_prefill = env_int("MG_DISABLE_MFMA_PREFILL", 0) == 0;
 
         const size_t C = cfg.context;
 
@@ -358,6 +360,10 @@ struct MeshGpt::Impl {
     void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *x2, float *q, float *y,
                     float *xn, bool decode, hipEvent_t *events = nullptr) {
         const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
+        // Prefill attention on the matrix cores (XSA in its epilogue) where the
+        // shape allows it (MG_DISABLE_MFMA_PREFILL=1 keeps the VALU kernel).
+        const bool mfma_prefill = !decode && use_mfma_prefill &&
+                                  kern::attn_prefill_mfma_supported(shape, rows.rows_per_seq);
         const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
         const bool rows_order = decode && row_decode;
@@ -380,6 +386,7 @@ struct MeshGpt::Impl {
                 a.part = decode ? part.as<float>() : nullptr;
                 a.nsplit = nsplit;
                 a.ybuf = decode ? nullptr : y;
+                a.xsa_post = decode || !mfma_prefill ? 1 : 0;
                 a.kv_post = kv_of(l - 1);
             }
             if (l < L) {
@@ -408,6 +415,8 @@ struct MeshGpt::Impl {
             if (decode) {
                 kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream,
                                   events ? events[2 * l] : nullptr, events ? events[2 * l + 1] : nullptr);
+            } else if (mfma_prefill) {
+                kern::attn_prefill_mfma(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, 1, stream);
             } else {
                 kern::attn_prefill(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, stream);
             }

@@ -259,3 +259,32 @@ def test_cli_init_then_generate_matches_oracle(tmp_path):
         with G.MeshGpt(0, g, 7) as model:
             model.set_parameters(saved.parameters)
             check_trajectory(o, params, ids, got, T, 7, last_row_logits(model), cached=False)
+
+
+MFMA_SHAPES = [
+    dict(vocab_size=64, width=128, heads=4, layers=2, attention_mesh_depth=7, ffn_mesh_depth=7, context=512,
+         connectivity=1),
+    dict(vocab_size=256, width=512, heads=8, layers=2, attention_mesh_depth=9, ffn_mesh_depth=9, context=512,
+         connectivity=1),
+]
+
+
+@pytest.mark.parametrize("cfg", MFMA_SHAPES, ids=["hd32", "hd64"])
+def test_matrix_core_prefill_matches_oracle_and_valu(cfg, monkeypatch):
+    # Prefill attention on the FP32 matrix cores (with XSA in its epilogue)
+    # against the oracle's logits for every row, and against the VALU flash
+    # kernel, over sequence lengths around its 16-query blocks, 64-key tiles
+    # and 128-query workgroups.
+    g = G.GptConfig(**cfg)
+    o = oracle_config(g)
+    params = O.initialize(o, 7)
+    for n, batch in ((64, 2), (127, 1), (129, 2), (300, 1), (512, 1)):
+        x = G.random_prompts(cfg["vocab_size"], batch, n, n).reshape(-1)
+        got = {}
+        for disable in ("0", "1"):
+            monkeypatch.setenv("MG_DISABLE_MFMA_PREFILL", disable)
+            with G.MeshGpt(0, g, 7) as model:
+                got[disable] = model.logits(x, n)
+        assert_close(got["0"], got["1"], what=f"matrix-core vs VALU prefill n={n}")
+        ref = O.logits(o, params, x, n)
+        assert_close(got["0"], ref, what=f"matrix-core prefill vs oracle n={n}")
