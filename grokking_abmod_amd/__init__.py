@@ -26,7 +26,7 @@ EXPORTS = (
     "mg_decode_rewind", "mg_last_call_ms", "mg_decode_profiled", "mg_decode_traced", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
-    "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_expf",
+    "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_sample_logits_noalloc", "mg_expf",
 )
 
 
@@ -117,6 +117,7 @@ def lib():
         "mg_tokenizer_encode": (i, [_u32p, sz, ctypes.c_char_p, sz, _u32p, sz, _szp]),
         "mg_tokenizer_decode": (i, [_u32p, sz, _u32p, sz, ctypes.c_char_p, sz, _szp]),
         "mg_sample_logits": (i, [i, _f32p, sz, sz, f, ctypes.POINTER(ctypes.c_uint64), _u32p]),
+        "mg_sample_logits_noalloc": (i, [i, vp, sz, sz, f, vp, vp, vp, vp]),
         "mg_expf": (i, [i, _f32p, sz, _f32p]),
     }
     for name, (res, args) in sigs.items():
@@ -183,6 +184,13 @@ def sample_logits(logits, temperature, rng_states, device=0):
     _check(lib().mg_sample_logits(device, _p(logits, _f32p), rows, vocab, temperature,
                                   states.ctypes.data_as(ctypes.POINTER(ctypes.c_uint64)), _p(out, _u32p)))
     return out, states
+
+
+def sample_logits_noalloc(logits_ptr, rows, vocab, temperature, rng_ptr, tokens_ptr, nonfinite_ptr, stream=None,
+                          device=0):
+    """mg_sample_logits_noalloc on device pointers (ints); enqueued on `stream`."""
+    _check(lib().mg_sample_logits_noalloc(device, logits_ptr, rows, vocab, temperature, rng_ptr, tokens_ptr,
+                                          nonfinite_ptr, stream))
 
 
 def device_expf(x, device=0):

@@ -259,6 +259,16 @@ int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab,
     });
 }
 
+int mg_sample_logits_noalloc(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                             uint64_t *rng_states, uint32_t *tokens, int *nonfinite, void *stream) {
+    return guarded([&] {
+        require((logits != nullptr && rng_states != nullptr && tokens != nullptr) || rows == 0,
+                "logits, states and tokens must not be null");
+        sample_logits_noalloc(device, logits, rows, vocab, temperature, rng_states, tokens, nonfinite,
+                              static_cast<hipStream_t>(stream));
+    });
+}
+
 int mg_expf(int device, const float *x, size_t n, float *out) {
     return guarded([&] {
         require((x != nullptr && out != nullptr) || n == 0, "inputs and outputs must not be null");

@@ -191,6 +191,13 @@ void head_sample(const Shape &s, const float *xn, int batch, const float *Et, in
 // Greedy / temperature sampling from logits rows; appends the token and bumps len.
 void sample(int V, int batch, const float *logits, float temperature, uint64_t *rng, uint32_t *tokens,
             int tok_stride, int *len, int *flags, hipStream_t stream);
+// Rows the allocation-free sampler accepts: its scratch holds one append
+// counter per row (noalloc.hip).
+constexpr int kNoAllocRows = 65536;
+// The device address of that scratch array on `device` (the current device).
+hipError_t noalloc_scratch(int device, int **out);
+// p[0..n) = value, by a kernel (no memset node when a caller captures the stream).
+void fill_int(int *p, int value, int n, hipStream_t stream);
 // y[i] = the sampler's f32 exp of x[i] (for verification).
 void device_expf(const float *x, float *y, size_t n, hipStream_t stream);
 // dst[i] = src[i] for n float4 elements (bandwidth calibration).

@@ -834,6 +834,27 @@ bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, f
     return flags != 0;
 }
 
+void sample_logits_noalloc(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                           uint64_t *rng_states, uint32_t *tokens, int *nonfinite, hipStream_t stream) {
+    if (rows > size_t(kern::kNoAllocRows))
+        throw Error("the allocation-free sampler takes at most " + std::to_string(kern::kNoAllocRows) + " rows");
+    if (vocab == 0 || vocab > size_t(1) << 24) throw Error("vocabulary must hold 1..2^24 tokens");
+    if (!std::isfinite(temperature) || temperature < 0.0f)
+        throw Error("temperature must be finite and nonnegative (0 is greedy)");
+    if (nonfinite == nullptr) throw Error("the non-finite flag must not be null");
+    int count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (device < 0 || device >= count) throw Error("invalid device ordinal", kDeviceError);
+    check(hipSetDevice(device), "hipSetDevice");
+    int *counters = nullptr;
+    check(kern::noalloc_scratch(device, &counters), "hipGetSymbolAddress(scratch)");
+    kern::fill_int(nonfinite, 0, 1, stream);
+    if (rows == 0) return check(hipGetLastError(), "fill launch");
+    kern::fill_int(counters, 0, int(rows), stream);
+    kern::sample(int(vocab), int(rows), logits, temperature, rng_states, tokens, 1, counters, nonfinite, stream);
+    check(hipGetLastError(), "sample launch");
+}
+
 void device_expf(int device, const float *x, size_t n, float *out) {
     if (n == 0) return;
     int count = 0;

@@ -70,6 +70,12 @@ class MeshGpt {
 // place).  Returns whether any row held a non-finite logit.
 bool sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
                    uint64_t *rng_states, uint32_t *tokens);
+// sample_logits on device-resident buffers, enqueued on `stream` without
+// waiting or allocating: its only scratch is the fixed per-device array of
+// kern::kNoAllocRows row counters.  *nonfinite (device) receives 1 when a row
+// holds a non-finite logit, else 0.
+void sample_logits_noalloc(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                           uint64_t *rng_states, uint32_t *tokens, int *nonfinite, hipStream_t stream);
 // out[i] = the sampler's f32 exp of x[i], evaluated on `device`.
 void device_expf(int device, const float *x, size_t n, float *out);
 

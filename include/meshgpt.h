@@ -145,6 +145,22 @@ void *mg_model_stream(mg_model *model);
 int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab, float temperature,
                      uint64_t *rng_states, uint32_t *tokens);
 
+/* No counterpart in the reference: an entry point for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops).  It is
+ * mg_sample_logits on buffers already on `device`: logits (rows x vocab f32),
+ * rng_states (rows, advanced in place when temperature > 0) and tokens (rows,
+ * written) are device pointers the caller owns, and *nonfinite (a device int)
+ * receives 1 when a row holds a non-finite logit, else 0.  The work is
+ * enqueued on `stream` (a hipStream_t; NULL is the default stream) and the
+ * call returns without waiting.  It allocates nothing: its only scratch is one
+ * counter per row in a fixed array of MG_NOALLOC_MAX_ROWS ints on each GPU,
+ * held until the process ends, which every call clears before use.  More rows
+ * are rejected with MG_INVALID_ARGUMENT.  Calls that overlap on one GPU share
+ * that array and race: order them (one stream, or events). */
+#define MG_NOALLOC_MAX_ROWS 65536
+int mg_sample_logits_noalloc(int device, const float *logits, size_t rows, size_t vocab, float temperature,
+                             uint64_t *rng_states, uint32_t *tokens, int *nonfinite, void *stream);
+
 /* out[i] = the f32 exp the sampler of mg_generate uses (the reference's
  * f32::exp, i.e. the C library's expf), evaluated on `device`.  No separate
  * reference call: it lets tests compare the device exp with the host's. */
