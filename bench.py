@@ -289,6 +289,8 @@ def main():
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-pmc", action="store_true")
     parser.add_argument("--no-extra", action="store_true", help="config 3 only")
+    parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5"],
+                        help="print only that figure (for profiling one workload)")
     parser.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
 
@@ -302,6 +304,11 @@ def main():
     if args.steps < 1:
         sys.exit("--steps must be at least 1")
 
+    if args.only:
+        figures = {"batch1": lambda: batch1_figure(Hip()), "config2": symbolic_figure,
+                   "config4": lambda: long_figure(Hip()), "config5": lambda: high_figure(Hip())}
+        print(json.dumps({args.only: figures[args.only]()}))
+        return
     # The counter runs go first, while this process has not touched the GPU:
     # the profiled child is then the only process on it.
     pmc = None if args.no_pmc else pmc_traffic(args)

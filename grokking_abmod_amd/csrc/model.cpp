@@ -591,6 +591,19 @@ struct MeshGpt::Impl {
         return persistent_ok && row_decode && kern::persistent_fits(shape, int(batch), device);
     }
 
+    // Whether `steps` decode steps should run in the persistent kernel (the
+    // caller checked persistent_usable()).  It gives each (sequence, head) one
+    // workgroup, which streams that head's keys alone; with few sequences and
+    // long contexts the per-phase split-KV kernels, which spread the keys over
+    // about 512 workgroups, are faster (config 4, batch 8 at 8192..8447 keys:
+    // 247 us per step against 355).  MG_FORCE_PERSISTENT=1 always prefers it.
+    bool persistent_preferred(size_t steps) const {
+        if (env_int("MG_FORCE_PERSISTENT", 0)) return true;
+        const size_t keys = length - 1 + steps;  // the launch's last step attends over these
+        const size_t slab_bytes = keys * 2 * size_t(shape.hdp) * 4;
+        return batch * cfg.heads >= 96 || slab_bytes <= (size_t(128) << 10);
+    }
+
     // `steps` decode steps in one launch of the persistent kernel (the caller
     // checked decodable(steps) and persistent_usable()).
     void persistent(size_t steps, uint64_t *trace = nullptr) {
@@ -679,7 +692,7 @@ void MeshGpt::generate_tokens(const uint32_t *prompts, size_t batch, size_t prom
         m.step();  // the prompt's prefill and the first token
         ++done;
     }
-    if (done < count && m.decodable(count - done) && m.persistent_usable()) {
+    if (done < count && m.decodable(count - done) && m.persistent_usable() && m.persistent_preferred(count - done)) {
         m.persistent(count - done);
         done = count;
     }
@@ -732,7 +745,7 @@ void MeshGpt::decode(size_t steps) {
     if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
-    if (m.persistent_usable()) {
+    if (m.persistent_usable() && m.persistent_preferred(steps)) {
         m.persistent(steps);
         m.finish();
         return;

@@ -142,7 +142,8 @@ def test_config3_decode_segments_continue_one_launch():
 
 def test_width1024_persistent_decode_past_300_keys(monkeypatch):
     # Config 5's row shape (W1024, H16x64, depth 10, butterfly) at batch 4 runs
-    # the persistent kernel with its three-slot ring; 128-token prompts and 200
+    # the persistent kernel (forced: at this batch and length the per-phase
+    # kernels are the default) with its three-slot ring; 128-token prompts and 200
     # greedy steps reach 327 keys.  Two sequences against the oracle; all four
     # against the per-phase kernels.
     config = G.GptConfig(vocab_size=256, width=1024, heads=16, layers=3, attention_mesh_depth=10,
@@ -154,6 +155,7 @@ def test_width1024_persistent_decode_past_300_keys(monkeypatch):
     runs = {}
     for disable in ("0", "1"):
         monkeypatch.setenv("MG_DISABLE_PERSISTENT", disable)
+        monkeypatch.setenv("MG_FORCE_PERSISTENT", "1" if disable == "0" else "0")
         with G.MeshGpt(0, config, 7, max_batch=4) as model:
             got = model.generate_tokens(prompts, 200, 0.0, 7)
             assert_close(model.last_logits(4), reprefill_last(model, got[:, :-1]),
@@ -171,12 +173,15 @@ def test_config4_long_context_full_size(monkeypatch):
     # Config 4: batch 8, 8192-token prefill (causal flash attention over
     # 8192 keys), then 256 greedy decode steps to 8448 tokens, the whole
     # extended context.  Last-step logits equal a device re-prefill of all
-    # 8448 positions; persistent and per-phase decode give the same tokens.
+    # 8448 positions; persistent (forced: the per-phase kernels are the
+    # default at this batch and length) and per-phase decode give the same
+    # tokens.
     config = G.named_config("long")
     prompts = G.random_prompts(256, 8, 8192, 7)
     runs = {}
     for disable in ("0", "1"):
         monkeypatch.setenv("MG_DISABLE_PERSISTENT", disable)
+        monkeypatch.setenv("MG_FORCE_PERSISTENT", "1" if disable == "0" else "0")
         with G.MeshGpt(0, config, 7, max_batch=8) as model:
             got = model.generate_tokens(prompts, 256, 0.0, 7)
             assert got.shape == (8, 8448)
