@@ -100,6 +100,12 @@ void mesh_rows(const Shape &s, const float *in, float *out, int rows, const floa
 // Et[c][t] = E[t][c], rows of Vp >= V floats with zero padding.
 void transpose(const float *E, float *Et, int V, int Vp, int W, hipStream_t stream);
 void block(const BlockArgs &a, bool staged, hipStream_t stream);
+// Prefill variant of block() for many rows (prefill_rows.hip): tiles of
+// 4096 / W rows, channels of those rows in registers, partners through LDS.
+// Needs W in {128, 256, 512, 1024}, a power-of-two head width dividing 64, and
+// attention rows in a.ybuf (not split partials).
+bool rows_block_supported(const Shape &s);
+void rows_block(const BlockArgs &a, hipStream_t stream);
 // Decode variant of block(): one row per sequence (rows_per_seq == 1), each
 // mesh of a row on one wavefront.  Supported for W a power of two in
 // [64, 1024] and a power-of-two head width >= 8.

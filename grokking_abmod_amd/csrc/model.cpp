@@ -113,6 +113,7 @@ struct MeshGpt::Impl {
     // it (MG_DISABLE_PERSISTENT=1 keeps the per-phase kernels).
     bool persistent_ok = false;
     bool use_mfma_prefill = true;
+    bool use_rows_prefill = true;
 
     // Events around the kernels of the last logits / hidden_states / prefill
     // call (last_call_ms).
@@ -231,6 +232,7 @@ struct MeshGpt::Impl {
         row_decode = env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
         persistent_ok = row_decode && env_int("MG_DISABLE_PERSISTENT", 0) == 0;
         use_mfma_prefill = env_int("MG_DISABLE_MFMA_PREFILL", 0) == 0;
+        use_rows_prefill = env_int("MG_DISABLE_ROWS_PREFILL", 0) == 0;
 
         const size_t C = cfg.context;
 
@@ -364,6 +366,9 @@ struct MeshGpt::Impl {
         // shape allows it (MG_DISABLE_MFMA_PREFILL=1 keeps the VALU kernel).
         const bool mfma_prefill = !decode && use_mfma_prefill &&
                                   kern::attn_prefill_mfma_supported(shape, rows.rows_per_seq);
+        // Prefill blocks on the register-tile kernel where the shape allows it
+        // (MG_DISABLE_ROWS_PREFILL=1 keeps block_kernel).
+        const bool rows_prefill = use_rows_prefill && kern::rows_block_supported(shape);
         const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
         const bool rows_order = decode && row_decode;
@@ -409,6 +414,8 @@ struct MeshGpt::Impl {
             }
             else if (decode && wave_decode)
                 kern::block_decode(a, stream);
+            else if (!decode && rows_prefill)
+                kern::rows_block(a, stream);
             else
                 kern::block(a, staged(t, a.wproj != nullptr, a.wq != nullptr), stream);
             if (l == L) break;

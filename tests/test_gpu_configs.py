@@ -293,3 +293,37 @@ def test_matrix_core_prefill_matches_oracle_and_valu(cfg, monkeypatch):
         assert_close(got["0"], got["1"], what=f"matrix-core vs VALU prefill n={n}")
         ref = O.logits(o, params, x, n)
         assert_close(got["0"], ref, what=f"matrix-core prefill vs oracle n={n}")
+
+
+ROWS_SHAPES = [
+    dict(vocab_size=99, width=128, heads=4, layers=2, attention_mesh_depth=4, ffn_mesh_depth=6, context=80),
+    dict(vocab_size=64, width=256, heads=8, layers=2, attention_mesh_depth=5, ffn_mesh_depth=3, context=80,
+         connectivity=1),
+    dict(vocab_size=256, width=512, heads=16, layers=2, attention_mesh_depth=9, ffn_mesh_depth=9, context=80,
+         connectivity=1),
+    dict(vocab_size=256, width=1024, heads=16, layers=2, attention_mesh_depth=10, ffn_mesh_depth=10, context=80,
+         connectivity=1, embedding=1),
+]
+
+
+@pytest.mark.parametrize("cfg", ROWS_SHAPES, ids=["W128-hd32", "W256-hd32", "W512-hd32", "W1024-hd64-table"])
+def test_register_tile_prefill_matches_oracle_and_block_kernel(cfg, monkeypatch):
+    # The register-tile prefill block kernel (prefill_rows.hip) against the
+    # oracle's logits and hidden states for every row, and against
+    # block_kernel, with row counts that leave partial tiles; short sequences
+    # take the VALU attention (XSA in the block's post half), 70-row ones the
+    # matrix-core attention (XSA in its epilogue).
+    g = G.GptConfig(**cfg)
+    o = oracle_config(g)
+    params = O.initialize(o, 7)
+    for n, batch in ((4, 9), (7, 3), (70, 3)):
+        x = G.random_prompts(cfg["vocab_size"], batch, n, n).reshape(-1)
+        got = {}
+        for disable in ("0", "1"):
+            monkeypatch.setenv("MG_DISABLE_ROWS_PREFILL", disable)
+            with G.MeshGpt(0, g, 7) as model:
+                got[disable] = (model.logits(x, n), model.hidden_states(x, n))
+        ref = O.logits(o, params, x, n)
+        assert_close(got["0"][0], ref, what=f"register-tile prefill logits n={n}")
+        assert_close(got["0"][1], O.hidden_states(o, params, x, n), what=f"register-tile hidden n={n}")
+        assert_close(got["0"][0], got["1"][0], what=f"register-tile vs block_kernel n={n}")
