@@ -110,9 +110,10 @@ __device__ __forceinline__ void issue_tile(const float *slab, int t0, int n, flo
     }
 }
 
-// Block (pair-slot, query tile): the 3 + ... mapping keeps every query tile of
-// one (sequence, head) on one XCD (workgroup i runs on XCD i % 8), longest
-// tiles first, so the tiles that stream the same keys share that XCD's L2.
+// Workgroup i runs on XCD i % 8: the mapping of workgroups to (sequence,
+// head) pairs and query tiles keeps every query tile of a pair on one XCD,
+// consecutive on it and longest first, so the tiles that stream the same keys
+// share that XCD's L2.
 template <int HD>
 __global__ void __launch_bounds__(256)
 attn_prefill_mfma_kernel(Shape s, const float *__restrict__ q, KvView kv, int nseq, int n, float *__restrict__ y,
@@ -298,7 +299,95 @@ attn_prefill_mfma_kernel(Shape s, const float *__restrict__ q, KvView kv, int ns
     }
 }
 
+// Causal attention for short sequences (a few rows each), one thread per
+// (row, head): the row's query against the keys at positions 0..pos of its
+// (sequence, head) slab with the online softmax of reference.rs:510-554, in
+// the log2 domain, then the XSA of reference.rs:577-603 against the value row
+// at pos.  Each thread reads whole 128-byte (hd 32) or 256-byte (hd 64) rows.
+template <int HD>
+__global__ void __launch_bounds__(256)
+attn_short_kernel(Shape s, const float *__restrict__ q, KvView kv, int rows, int n, float *__restrict__ y,
+                  float scale_log2, int xsa) {
+    const int i = int(blockIdx.x) * 256 + int(threadIdx.x);
+    if (i >= rows * s.H) return;
+    const int h = i % s.H, row = i / s.H, seq = row / n, pos = row - seq * n;
+    const size_t slab = size_t(seq * s.H + h) * kv.cap * HD;
+    float qv[HD], acc[HD], vrow[HD];
+    const float4 *q4 = reinterpret_cast<const float4 *>(q + size_t(row) * s.W + h * HD);
+#pragma unroll
+    for (int e = 0; e < HD / 4; ++e) {
+        const float4 t = q4[e];
+        qv[4 * e] = t.x * scale_log2;
+        qv[4 * e + 1] = t.y * scale_log2;
+        qv[4 * e + 2] = t.z * scale_log2;
+        qv[4 * e + 3] = t.w * scale_log2;
+    }
+#pragma unroll
+    for (int e = 0; e < HD; ++e) acc[e] = 0.0f;
+    float m = -INFINITY, l = 0.0f;
+    for (int j = 0; j <= pos; ++j) {
+        const float4 *k4 = reinterpret_cast<const float4 *>(kv.k + slab + size_t(j) * HD);
+        const float4 *v4 = reinterpret_cast<const float4 *>(kv.v + slab + size_t(j) * HD);
+        float sc = 0.0f;
+#pragma unroll
+        for (int e = 0; e < HD / 4; ++e) {
+            const float4 t = k4[e];
+            sc = fmaf(qv[4 * e], t.x, sc);
+            sc = fmaf(qv[4 * e + 1], t.y, sc);
+            sc = fmaf(qv[4 * e + 2], t.z, sc);
+            sc = fmaf(qv[4 * e + 3], t.w, sc);
+        }
+#pragma unroll
+        for (int e = 0; e < HD / 4; ++e) {
+            const float4 t = v4[e];
+            vrow[4 * e] = t.x;
+            vrow[4 * e + 1] = t.y;
+            vrow[4 * e + 2] = t.z;
+            vrow[4 * e + 3] = t.w;
+        }
+        const float mn = fmaxf(m, sc);
+        const float alpha = __builtin_amdgcn_exp2f(m - mn), p = __builtin_amdgcn_exp2f(sc - mn);
+        l = l * alpha + p;
+#pragma unroll
+        for (int e = 0; e < HD; ++e) acc[e] = fmaf(p, vrow[e], acc[e] * alpha);
+        m = mn;
+    }
+    // vrow now holds the value row at pos, the XSA direction.
+    const float inv = 1.0f / l;
+    float dot = 0.0f, vsq = 0.0f;
+#pragma unroll
+    for (int e = 0; e < HD; ++e) {
+        acc[e] *= inv;
+        dot = fmaf(acc[e], vrow[e], dot);
+        vsq = fmaf(vrow[e], vrow[e], vsq);
+    }
+    const float iv = rsqrtf(fmaxf(vsq, kXsaNormFloor));
+    const float c = xsa ? dot * iv : 0.0f;
+    float4 *y4 = reinterpret_cast<float4 *>(y + size_t(row) * s.W + h * HD);
+#pragma unroll
+    for (int e = 0; e < HD / 4; ++e)
+        y4[e] = make_float4(acc[4 * e] - c * (vrow[4 * e] * iv), acc[4 * e + 1] - c * (vrow[4 * e + 1] * iv),
+                            acc[4 * e + 2] - c * (vrow[4 * e + 2] * iv), acc[4 * e + 3] - c * (vrow[4 * e + 3] * iv));
+}
+
 }  // namespace
+
+bool attn_prefill_short_supported(const Shape &s, int rows_per_seq) {
+    return s.hd == s.hdp && (s.hd == 32 || s.hd == 64) && s.W % 4 == 0 && rows_per_seq <= 16;
+}
+
+void attn_prefill_short(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y, int xsa,
+                        hipStream_t stream) {
+    const float scale_log2 = float(1.4426950408889634 / std::sqrt(double(s.hd)));
+    const int rows = nseq * rows_per_seq, blocks = (rows * s.H + 255) / 256;
+    if (s.hd == 32)
+        hipLaunchKernelGGL(attn_short_kernel<32>, dim3(blocks), dim3(256), 0, stream, s, q, kv, rows, rows_per_seq,
+                           y, scale_log2, xsa);
+    else
+        hipLaunchKernelGGL(attn_short_kernel<64>, dim3(blocks), dim3(256), 0, stream, s, q, kv, rows, rows_per_seq,
+                           y, scale_log2, xsa);
+    (void)hipGetLastError();
+}
 
 bool attn_prefill_mfma_supported(const Shape &s, int rows_per_seq) {
     return s.hd == s.hdp && (s.hd == 32 || s.hd == 64) && s.W % 4 == 0 && rows_per_seq >= 64;

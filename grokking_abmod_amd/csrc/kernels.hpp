@@ -184,6 +184,11 @@ void attn_prefill(const Shape &s, const float *q, KvView kv, int nseq, int rows_
 // xsa != 0 (then the block's post half must not apply it again).  Supported
 // when attn_prefill_mfma_supported(); the sequences are at least 64 rows long.
 bool attn_prefill_mfma_supported(const Shape &s, int rows_per_seq);
+// The same for short sequences (at most 16 rows), one thread per (row, head),
+// with XSA applied when xsa != 0.
+bool attn_prefill_short_supported(const Shape &s, int rows_per_seq);
+void attn_prefill_short(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y, int xsa,
+                        hipStream_t stream);
 void attn_prefill_mfma(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y, int xsa,
                        hipStream_t stream);
 // logits[i][t] = xn[i*row_mul+row_add] . E[t] (xn already RMS-normalised).

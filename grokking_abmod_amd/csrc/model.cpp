@@ -114,6 +114,7 @@ struct MeshGpt::Impl {
     bool persistent_ok = false;
     bool use_mfma_prefill = true;
     bool use_rows_prefill = true;
+    bool use_short_prefill = true;
 
     // Events around the kernels of the last logits / hidden_states / prefill
     // call (last_call_ms).
@@ -233,6 +234,7 @@ struct MeshGpt::Impl {
         persistent_ok = row_decode && env_int("MG_DISABLE_PERSISTENT", 0) == 0;
         use_mfma_prefill = env_int("MG_DISABLE_MFMA_PREFILL", 0) == 0;
         use_rows_prefill = env_int("MG_DISABLE_ROWS_PREFILL", 0) == 0;
+        use_short_prefill = env_int("MG_DISABLE_SHORT_PREFILL", 0) == 0;
 
         const size_t C = cfg.context;
 
@@ -366,6 +368,10 @@ struct MeshGpt::Impl {
         // shape allows it (MG_DISABLE_MFMA_PREFILL=1 keeps the VALU kernel).
         const bool mfma_prefill = !decode && use_mfma_prefill &&
                                   kern::attn_prefill_mfma_supported(shape, rows.rows_per_seq);
+        // Short sequences: one thread per (row, head) (MG_DISABLE_SHORT_PREFILL=1
+        // keeps the VALU flash kernel).
+        const bool short_prefill = !decode && use_short_prefill &&
+                                   kern::attn_prefill_short_supported(shape, rows.rows_per_seq);
         // Prefill blocks on the register-tile kernel where the shape allows it
         // (MG_DISABLE_ROWS_PREFILL=1 keeps block_kernel).
         const bool rows_prefill = use_rows_prefill && kern::rows_block_supported(shape);
@@ -391,7 +397,7 @@ struct MeshGpt::Impl {
                 a.part = decode ? part.as<float>() : nullptr;
                 a.nsplit = nsplit;
                 a.ybuf = decode ? nullptr : y;
-                a.xsa_post = decode || !mfma_prefill ? 1 : 0;
+                a.xsa_post = decode || !(mfma_prefill || short_prefill) ? 1 : 0;
                 a.kv_post = kv_of(l - 1);
             }
             if (l < L) {
@@ -424,6 +430,8 @@ struct MeshGpt::Impl {
                                   events ? events[2 * l] : nullptr, events ? events[2 * l + 1] : nullptr);
             } else if (mfma_prefill) {
                 kern::attn_prefill_mfma(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, 1, stream);
+            } else if (short_prefill) {
+                kern::attn_prefill_short(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, 1, stream);
             } else {
                 kern::attn_prefill(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, stream);
             }
