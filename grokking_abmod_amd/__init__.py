@@ -35,7 +35,10 @@ class GptConfig(ctypes.Structure):
 
     _fields_ = [(name, ctypes.c_uint32) for name in (
         "vocab_size", "context", "width", "heads", "layers", "attention_mesh_depth",
-        "ffn_mesh_depth", "embedding", "connectivity", "long_context")]
+        "ffn_mesh_depth", "embedding", "connectivity", "long_context", "rope", "qk_norm", "xsa",
+        "form", "order", "frequency", "harmonics")] + [("overlap", ctypes.c_float)] + [
+        (name, ctypes.c_uint32) for name in ("normalization", "frozen", "preserve_features", "modulus")] + [
+        ("seed", ctypes.c_uint64)]
 
     def __init__(self, **overrides):
         super().__init__()
@@ -43,7 +46,7 @@ class GptConfig(ctypes.Structure):
         for key, value in overrides.items():
             if key not in dict(self._fields_):
                 raise TypeError(f"unknown GptConfig field {key}")
-            setattr(self, key, int(value))
+            setattr(self, key, float(value) if key == "overlap" else int(value))
 
     def as_dict(self):
         return {name: getattr(self, name) for name, _ in self._fields_}

@@ -61,6 +61,24 @@ GptConfig to_config(const mg_config *c) {
     g.embedding = TokenEmbedding(c->embedding);
     g.connectivity = MeshConnectivity(c->connectivity);
     g.long_context = c->long_context != 0;
+    require(c->rope <= 1 && c->qk_norm <= 1 && c->xsa <= 1 && c->frozen <= 1, "invalid checkpoint switch");
+    g.rope = c->rope != 0;
+    g.qk_norm = c->qk_norm != 0;
+    g.xsa = c->xsa != 0;
+    if (c->form > 9) throw Error("unknown checkpoint EmbeddingForm: " + std::to_string(c->form));
+    if (c->order > 2) throw Error("unknown checkpoint EmbeddingOrder: " + std::to_string(c->order));
+    if (c->normalization > 2)
+        throw Error("unknown checkpoint EmbeddingNorm: " + std::to_string(c->normalization));
+    g.geometry.form = EmbeddingForm(c->form);
+    g.geometry.order = EmbeddingOrder(c->order);
+    g.geometry.frequency = c->frequency;
+    g.geometry.harmonics = c->harmonics;
+    g.geometry.overlap = c->overlap;
+    g.geometry.normalization = EmbeddingNorm(c->normalization);
+    g.geometry.frozen = c->frozen != 0;
+    g.geometry.preserve_features = c->preserve_features;
+    g.geometry.modulus = c->modulus;
+    g.geometry.seed = c->seed;
     return g;
 }
 
@@ -75,6 +93,19 @@ void from_config(const GptConfig &g, mg_config *c) {
     c->embedding = uint32_t(g.embedding);
     c->connectivity = uint32_t(g.connectivity);
     c->long_context = g.long_context ? 1 : 0;
+    c->rope = g.rope;
+    c->qk_norm = g.qk_norm;
+    c->xsa = g.xsa;
+    c->form = uint32_t(g.geometry.form);
+    c->order = uint32_t(g.geometry.order);
+    c->frequency = uint32_t(g.geometry.frequency);
+    c->harmonics = uint32_t(g.geometry.harmonics);
+    c->overlap = g.geometry.overlap;
+    c->normalization = uint32_t(g.geometry.normalization);
+    c->frozen = g.geometry.frozen;
+    c->preserve_features = uint32_t(g.geometry.preserve_features);
+    c->modulus = uint32_t(g.geometry.modulus);
+    c->seed = g.geometry.seed;
 }
 
 MeshGpt &model_of(mg_model *m) {

@@ -1,0 +1,244 @@
+// Token-code geometry of the MSHGPT09 ablations (src/gpt/geometry.rs): the
+// constraints on a configuration, the token order of arithmetic vocabularies
+// and the geometric code families.  Compiled without floating-point
+// contraction, like the rest of the host types: every code value is computed
+// in f64 and rounded to f32 exactly as the reference does.
+#include <charconv>
+#include <cmath>
+
+#include "meshgpt_types.hpp"
+
+namespace meshgpt {
+
+namespace {
+
+const char *form_name(EmbeddingForm f) {
+    static const char *names[] = {"parity",      "circle",    "fourier",   "orthogonal",
+                                  "simplex",     "equiangular", "antipodal", "hypercube",
+                                  "signed-permutations", "sphere"};
+    return names[uint32_t(f)];
+}
+
+size_t bit_length(size_t x) {
+    size_t n = 0;
+    for (; x; x >>= 1) ++n;
+    return n;
+}
+
+// Rust's Display of an f32: the shortest decimal that reads back to the same
+// value, never in exponent form.
+std::string display_f32(float v) {
+    if (std::isnan(v)) return "NaN";
+    if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
+    char buf[96];
+    auto res = std::to_chars(buf, buf + sizeof buf, v, std::chars_format::fixed);
+    return std::string(buf, res.ptr);
+}
+
+bool is_prime(size_t n) {
+    if (n < 2) return false;
+    for (size_t d = 2; d < n; ++d)
+        if (n % d == 0) return false;
+    return true;
+}
+
+// The token at each position of the geometric order, and the length of the
+// cyclic part (geometry.rs:186-211).
+std::pair<std::vector<size_t>, size_t> ordered_tokens(const GptConfig &config) {
+    const EmbeddingGeometry &g = config.geometry;
+    std::vector<size_t> order;
+    if (g.order == EmbeddingOrder::Token) {
+        for (size_t t = 0; t < config.vocab_size; ++t) order.push_back(t);
+        return {order, config.vocab_size};
+    }
+    const std::vector<uint32_t> ids = residue_permutation(g.modulus, g.seed);
+    if (g.order == EmbeddingOrder::Residue) {
+        for (uint32_t id : ids) order.push_back(id);
+    } else {
+        const size_t root = primitive_root(g.modulus);
+        size_t residue = 1;
+        for (size_t k = 0; k + 1 < g.modulus; ++k) {
+            order.push_back(ids[residue]);
+            residue = residue * root % g.modulus;
+        }
+    }
+    const size_t cycle = order.size();
+    if (g.order == EmbeddingOrder::DiscreteLog) order.push_back(ids[0]);
+    order.push_back(g.modulus);
+    order.push_back(g.modulus + 1);
+    return {order, cycle};
+}
+
+// Helmert coordinates of a regular unit simplex in R^(n-1) (geometry.rs:226-236).
+double simplex_coordinate(size_t row, size_t column, size_t n) {
+    const double scale = std::sqrt(double(n) / double(n - 1));
+    const double denominator = std::sqrt(double((column + 1) * (column + 2)));
+    if (row <= column) return scale / denominator;
+    if (row == column + 1) return -scale * double(column + 1) / denominator;
+    return 0.0;
+}
+
+constexpr double kTau = 6.283185307179586;
+
+}  // namespace
+
+bool EmbeddingGeometry::operator==(const EmbeddingGeometry &o) const {
+    return form == o.form && order == o.order && frequency == o.frequency && harmonics == o.harmonics &&
+           (overlap == o.overlap || (std::isnan(overlap) && std::isnan(o.overlap))) &&
+           normalization == o.normalization && frozen == o.frozen && preserve_features == o.preserve_features &&
+           modulus == o.modulus && seed == o.seed;
+}
+
+float EmbeddingGeometry::radius(size_t width) const {
+    return normalization == EmbeddingNorm::Rms ? std::sqrt(float(width)) : 1.0f;
+}
+
+void EmbeddingGeometry::validate(const GptConfig &config) const {
+    const size_t v = config.vocab_size, w = config.width;
+    if (frequency == 0 || frequency > 0xFFFFFFFFull || harmonics == 0 || harmonics > w / 2)
+        throw Error("embedding frequency must be positive and harmonics in 1..width/2");
+    if (!std::isfinite(overlap) || preserve_features > w)
+        throw Error("embedding overlap must be finite; preserved features must fit width");
+    if (modulus > 0xFFFFFFFFull) throw Error("embedding modulus exceeds checkpoint field capacity");
+    if (preserve_features > 0 && normalization != EmbeddingNorm::None)
+        throw Error("preserved coordinates require --embedding-norm none; full-vector normalization would "
+                    "rescale the protected feature");
+    bool fits = true;
+    switch (form) {
+    case EmbeddingForm::Orthogonal: fits = w >= v; break;
+    case EmbeddingForm::Simplex: fits = w + 1 >= v; break;
+    case EmbeddingForm::Equiangular: {
+        const float lower = -1.0f / float(v - 1);
+        fits = overlap >= lower && overlap <= 1.0f && (overlap == 1.0f || w + (overlap == lower ? 1 : 0) >= v);
+        break;
+    }
+    case EmbeddingForm::Hypercube: fits = w >= bit_length(v - 1); break;
+    case EmbeddingForm::SignedPermutations: fits = w >= 4 && v <= 256; break;
+    default: break;
+    }
+    if (!fits)
+        throw Error(std::string(form_name(form)) + " embedding does not fit vocabulary " + std::to_string(v) +
+                    ", width " + std::to_string(w) + ", overlap " + display_f32(overlap));
+    if (order != EmbeddingOrder::Token) {
+        if (modulus < 2 || modulus > 254 || !is_prime(modulus) || v != modulus + 2)
+            throw Error("arithmetic embedding order requires a grok prime and vocabulary modulus+2");
+        // Independent directions for zero (discrete-log), the operation and '='.
+        const size_t special = 2 + (order == EmbeddingOrder::DiscreteLog ? 1 : 0);
+        const size_t pairs = form == EmbeddingForm::Fourier ? harmonics : 1;
+        if ((form == EmbeddingForm::Circle || form == EmbeddingForm::Fourier) && w < 2 * pairs + special)
+            throw Error("arithmetic circle/Fourier codes need extra coordinates for special symbols");
+    }
+}
+
+std::vector<uint32_t> residue_permutation(size_t modulus, uint64_t seed) {
+    std::vector<uint32_t> tokens(modulus);
+    for (size_t i = 0; i < modulus; ++i) tokens[i] = uint32_t(i);
+    Random symbols(seed ^ 0x73796d626f6c7301ULL);
+    for (size_t end = modulus; end-- > 1;) std::swap(tokens[end], tokens[symbols.index(end + 1)]);
+    return tokens;
+}
+
+size_t primitive_root(size_t prime) {
+    if (prime == 2) return 1;
+    for (size_t g = 2; g < prime; ++g) {
+        std::vector<bool> seen(prime, false);
+        size_t x = 1;
+        bool ok = true;
+        for (size_t k = 0; k + 1 < prime; ++k) {
+            if (seen[x]) {
+                ok = false;
+                break;
+            }
+            seen[x] = true;
+            x = x * g % prime;
+        }
+        if (ok && x == 1) return g;
+    }
+    throw Error("a prime has a primitive root");
+}
+
+// Parity codes, computed for positions 0..V-1, belong to the tokens of the
+// geometric order (geometry.rs:213-222).
+std::vector<float> reorder_parity(const GptConfig &config, const std::vector<float> &codes) {
+    if (config.geometry.order == EmbeddingOrder::Token) return codes;
+    const size_t W = config.width;
+    const std::vector<size_t> order = ordered_tokens(config).first;
+    std::vector<float> result(codes.size());
+    for (size_t i = 0; i < order.size(); ++i)
+        std::copy(codes.begin() + i * W, codes.begin() + (i + 1) * W, result.begin() + order[i] * W);
+    return result;
+}
+
+// geometry.rs:238-325: the geometric code of each token, V x W.
+std::vector<float> geometric_codes(const GptConfig &config) {
+    const size_t v = config.vocab_size, w = config.width;
+    const EmbeddingGeometry &g = config.geometry;
+    const auto [order, cycle] = ordered_tokens(config);
+    std::vector<float> codes(v * w, 0.0f);
+    Random random(g.seed ^ 0x5350484552453031ULL);
+    for (size_t row = 0; row < order.size(); ++row) {
+        float *code = codes.data() + order[row] * w;
+        switch (g.form) {
+        case EmbeddingForm::Parity: throw Error("parity codes use the original generator");
+        case EmbeddingForm::Circle:
+        case EmbeddingForm::Fourier: {
+            const size_t pairs = g.form == EmbeddingForm::Fourier ? g.harmonics : 1;
+            if (row >= cycle) {
+                code[2 * pairs + row - cycle] = 1.0f;
+            } else {
+                const double scale = 1.0 / std::sqrt(double(pairs));
+                for (size_t pair = 0; pair < pairs; ++pair) {
+                    const size_t frequency = (g.frequency % cycle + pair % cycle) % cycle;
+                    const double angle = kTau * double(frequency) * double(row) / double(cycle);
+                    code[2 * pair] = float(scale * std::cos(angle));
+                    code[2 * pair + 1] = float(scale * std::sin(angle));
+                }
+            }
+            break;
+        }
+        case EmbeddingForm::Orthogonal: code[row] = 1.0f; break;
+        case EmbeddingForm::Simplex:
+        case EmbeddingForm::Equiangular: {
+            const double rho = g.form == EmbeddingForm::Simplex ? -1.0 / double(v - 1) : double(g.overlap);
+            if (rho == 1.0) {
+                code[0] = 1.0f;
+                break;
+            }
+            const double a = std::sqrt((1.0 - rho) * double(v - 1) / double(v));
+            for (size_t c = 0; c + 1 < v; ++c) code[c] = float(a * simplex_coordinate(row, c, v));
+            if (w >= v) code[v - 1] = float(std::sqrt(std::max(1.0 + double(v - 1) * rho, 0.0) / double(v)));
+            break;
+        }
+        case EmbeddingForm::Antipodal: code[0] = row % 2 == 0 ? 1.0f : -1.0f; break;
+        case EmbeddingForm::Hypercube: {
+            const size_t bits = bit_length(v - 1);
+            for (size_t bit = 0; bit < bits; ++bit)
+                code[bit] = ((row & (size_t(1) << bit)) == 0 ? -1.0f : 1.0f) / std::sqrt(float(bits));
+            break;
+        }
+        case EmbeddingForm::SignedPermutations: {
+            const size_t p = row / 16;
+            for (size_t c = 0; c < 4; ++c) {
+                const size_t slot = c < 2 ? (c + p / 2 % 2) % 2 : 2 + (c - 2 + p % 2) % 2;
+                const float magnitude = float(1 + (slot + p / 4) % 4);
+                code[c] = magnitude * ((row & (size_t(1) << c)) == 0 ? 1.0f : -1.0f);
+            }
+            break;
+        }
+        case EmbeddingForm::Sphere: {
+            double squares = 0.0;
+            for (size_t c = 0; c < w; ++c) {
+                const double radius = std::sqrt(-2.0 * std::log(double(std::max(random.unit(), 1.0f / 16777216.0f))));
+                const double angle = kTau * double(random.unit());
+                code[c] = float(radius * std::cos(angle));
+                squares += double(code[c]) * double(code[c]);
+            }
+            for (size_t c = 0; c < w; ++c) code[c] = float(double(code[c]) / std::sqrt(squares));
+            break;
+        }
+        }
+    }
+    return codes;
+}
+
+}  // namespace meshgpt

@@ -500,11 +500,26 @@ block_kernel(BlockArgs a) {
         res0 = X;
         res1 = kres;
     }
-    // QK-Norm per head, split-half RoPE at each row's position, cache append.
-    segment_inv_rms(res0, nr * s.H, s.hd, inv1);
-    segment_inv_rms(res1, nr * s.H, s.hd, inv2);
+    // QK-Norm per head, split-half RoPE at each row's position, cache append
+    // (each skipped when its switch is off, reference.rs:174-193).
+    if (s.qk_norm) {
+        segment_inv_rms(res0, nr * s.H, s.hd, inv1);
+        segment_inv_rms(res1, nr * s.H, s.hd, inv2);
+    } else {
+        for (int i = threadIdx.x; i < nr * s.H; i += blockDim.x) inv1[i] = inv2[i] = 1.0f;
+    }
     __syncthreads();
-    const int pairs = s.H * s.half;
+    if (!s.rope) {
+        for (int idx = threadIdx.x; idx < nr * W; idx += blockDim.x) {
+            int r, c, h, d, seq, pos;
+            split_row(idx, s, r, c);
+            split_head(c, s, h, d);
+            row_position(a.ro, r0 + r, seq, pos);
+            a.q[size_t(r0 + r) * W + c] = res0[idx] * inv1[r * s.H + h];
+            a.kv_pre.k[(size_t(seq * s.H + h) * a.kv_pre.cap + pos) * s.hdp + d] = res1[idx] * inv2[r * s.H + h];
+        }
+    }
+    const int pairs = s.rope ? s.H * s.half : 0;
     for (int idx = threadIdx.x; idx < nr * pairs; idx += blockDim.x) {
         const int r = idx / pairs, rem = idx - r * pairs;
         const int h = rem / s.half, i = rem - h * s.half;
@@ -886,18 +901,20 @@ block_decode_kernel(BlockArgs a) {
                     y[j] = merge_splits<8>(part0 + size_t(head_of(j)) * a.nsplit * stride, a.nsplit, stride,
                                            s.hdp, dim_of(j));
             }
-            // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
-            float vv[CPL], yv[CPL], t[CPL];
+            if (s.xsa) {
+                // XSA (reference.rs:577-603): z = y - (y.u)u with u = v / max(|v|, eps).
+                float vv[CPL], yv[CPL], t[CPL];
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
-            head_sum<CPL, HSEG>(t, vv, rph);
+                for (int j = 0; j < CPL; ++j) t[j] = v[j] * v[j];
+                head_sum<CPL, HSEG>(t, vv, rph);
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
-            head_sum<CPL, HSEG>(t, yv, rph);
+                for (int j = 0; j < CPL; ++j) t[j] = y[j] * v[j];
+                head_sum<CPL, HSEG>(t, yv, rph);
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
-                y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
+                for (int j = 0; j < CPL; ++j) {
+                    const float iv = rsqrtf(fmaxf(vv[j], kXsaFloor));
+                    y[j] = y[j] - (yv[j] * iv) * (v[j] * iv);
+                }
             }
             if constexpr (FIXED) wave_mesh_fixed<CPL, DEPTH>(y, w, lane);
             else
@@ -978,9 +995,9 @@ block_decode_kernel(BlockArgs a) {
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int d = dim_of(j);
-        const float sc = rsqrtf(ss[j] * scale + kRmsEps);
+        const float sc = s.qk_norm ? rsqrtf(ss[j] * scale + kRmsEps) : 1.0f;
         const float self = x[j] * sc, oth = other[j] * sc;
-        const float r = d < half ? self * cs[j].x - oth * cs[j].y : self * cs[j].x + oth * cs[j].y;
+        const float r = !s.rope ? self : (d < half ? self * cs[j].x - oth * cs[j].y : self * cs[j].x + oth * cs[j].y);
         if (wave == 1)
             a.q[size_t(row) * W + j * 64 + lane] = r;
         else
@@ -3426,6 +3443,28 @@ layer0_kernel(Shape s, const float *__restrict__ E, const float *__restrict__ w,
     for (int j = 0; j < CPL; ++j) q0[(size_t(v) * 3 + team) * W + c.ridx(j)] = n[j];
 }
 
+// One workgroup per token row (reference.rs:130-149 with gpu.rs:1261-1333's
+// arithmetic: scale = radius / max(|row|, 1e-12)).
+__global__ void __launch_bounds__(kThreads)
+embedding_geometry_kernel(float *__restrict__ E, const float *__restrict__ codes, int W, float radius,
+                          int normalize, int keep) {
+    __shared__ float red[kThreads / 64];
+    float *row = E + size_t(blockIdx.x) * W;
+    const float *code = codes + size_t(blockIdx.x) * W;
+    float scale = 1.0f;
+    if (normalize) {
+        float a = 0.0f;
+        for (int c = threadIdx.x; c < W; c += blockDim.x) a = fmaf(row[c], row[c], a);
+        a = wave_sum(a);
+        if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = a;
+        __syncthreads();
+        float squares = 0.0f;
+        for (int w = 0; w < int(blockDim.x) / 64; ++w) squares += red[w];
+        scale = radius / fmaxf(sqrtf(squares), 1e-12f);
+    }
+    for (int c = threadIdx.x; c < W; c += blockDim.x) row[c] = c < keep ? code[c] : row[c] * scale;
+}
+
 __global__ void __launch_bounds__(kThreads)
 transpose_kernel(const float *__restrict__ E, float *__restrict__ Et, int V, int Vp, int W) {
     __shared__ float tile[32][33];
@@ -3582,6 +3621,13 @@ void mesh_rows(const Shape &s, const float *in, float *out, int rows, const floa
         hipLaunchKernelGGL(mesh_rows_kernel<decltype(c)::value>, grid, dim3(team_threads(s.W)),
                            mesh_lds_bytes(s, rpw), stream, s, in, out, rows, w, depth, rpw);
     });
+    HIP_LAUNCH_CHECK();
+}
+
+void embedding_geometry(float *E, const float *codes, int V, int W, float radius, int normalize, int keep,
+                        hipStream_t stream) {
+    hipLaunchKernelGGL(embedding_geometry_kernel, dim3(V), dim3(kThreads), 0, stream, E, codes, W, radius, normalize,
+                       keep);
     HIP_LAUNCH_CHECK();
 }
 

@@ -25,6 +25,9 @@ struct Shape {
     int butterfly; // 1 for butterfly connectivity, 0 for neighbor
     int A;         // attention / embedding mesh depth
     int F;         // feed-forward mesh depth
+    int rope;      // operator switches (config.rs:33-35): 1 on, 0 off
+    int qk_norm;
+    int xsa;
 };
 
 // Which rows a launch covers.  Row r belongs to sequence r / rows_per_seq and
@@ -97,6 +100,11 @@ void configure_lds(size_t max_bytes);
 // out = mesh(in) for rows x W (the embedding table from token codes).
 void mesh_rows(const Shape &s, const float *in, float *out, int rows, const float *w, int depth, int rpw,
                hipStream_t stream);
+// The geometry transform of the token vectors (reference.rs:130-149): with
+// `normalize`, each row of E scaled to length `radius`; the first `keep`
+// channels of each row replaced by the token's code (codes, V x W).
+void embedding_geometry(float *E, const float *codes, int V, int W, float radius, int normalize, int keep,
+                        hipStream_t stream);
 // Et[c][t] = E[t][c], rows of Vp >= V floats with zero padding.
 void transpose(const float *E, float *Et, int V, int Vp, int W, hipStream_t stream);
 void block(const BlockArgs &a, bool staged, hipStream_t stream);

@@ -44,8 +44,8 @@ bool GptConfig::operator==(const GptConfig &o) const {
     return vocab_size == o.vocab_size && context == o.context && width == o.width &&
            heads == o.heads && layers == o.layers &&
            attention_mesh_depth == o.attention_mesh_depth && ffn_mesh_depth == o.ffn_mesh_depth &&
-           embedding == o.embedding && connectivity == o.connectivity &&
-           long_context == o.long_context;
+           embedding == o.embedding && connectivity == o.connectivity && geometry == o.geometry &&
+           rope == o.rope && qk_norm == o.qk_norm && xsa == o.xsa && long_context == o.long_context;
 }
 
 void GptConfig::validate() const {
@@ -57,12 +57,13 @@ void GptConfig::validate() const {
     if (heads < 1 || heads > kModelMaxHeads || width % heads != 0)
         throw Error("heads must be in 1..64 and divide width");
     if (width / heads < 2) throw Error("each attention head requires at least two channels");
-    if ((width / heads) % 2 != 0)
+    if (rope && (width / heads) % 2 != 0)
         throw Error("slice RoPE requires an even number of channels per head");
     if (layers < 1 || layers > 64) throw Error("layers must be in 1..64");
     if (attention_mesh_depth < 1 || attention_mesh_depth > 256 || ffn_mesh_depth < 1 ||
         ffn_mesh_depth > 256)
         throw Error("mesh depths must be in 1..256");
+    geometry.validate(*this);
 }
 
 size_t GptConfig::embedding_parameter_count() const {
@@ -112,11 +113,17 @@ size_t Layout::count() const { return groups.empty() ? 0 : groups.back().offset 
 std::vector<float> Layout::initialize(const GptConfig &config, uint64_t seed) const {
     if (config.embedding == TokenEmbedding::Table) {
         // The table starts as the vectors the seeded embedding mesh generates
-        // (config.rs:416-435), so mesh and table models begin as one function.
+        // (config.rs:416-435), so mesh and table models begin as one function;
+        // a geometric form's table starts as its codes.
         GptConfig mesh = config;
         mesh.embedding = TokenEmbedding::Mesh;
         Layout layout = Layout::build(mesh);
-        return tabulate_embedding(mesh, layout.initialize(mesh, seed));
+        std::vector<float> parameters = tabulate_embedding(mesh, layout.initialize(mesh, seed));
+        if (config.geometry.form != EmbeddingForm::Parity) {
+            const std::vector<float> codes = token_codes(config);
+            std::copy(codes.begin(), codes.end(), parameters.begin());
+        }
+        return parameters;
     }
     Random random(seed);
     std::vector<float> parameters(count(), 0.0f);
@@ -137,10 +144,37 @@ std::vector<float> Layout::initialize(const GptConfig &config, uint64_t seed) co
             }
         }
     }
+    for (size_t id = 0; id < groups.size(); ++id) {
+        const auto [begin, end] = constrained_range(config, id);
+        std::fill(parameters.begin() + groups[id].offset + begin, parameters.begin() + groups[id].offset + end,
+                  0.0f);
+    }
     return parameters;
 }
 
+std::pair<size_t, size_t> Layout::constrained_range(const GptConfig &config, size_t id) const {
+    if (config.geometry.preserve_features == 0) return {0, 0};
+    for (const Block &b : blocks)
+        if (b.projection == id || b.ffn == id) {
+            const size_t begin = groups[id].size - 2 * config.width;
+            return {begin, begin + 2 * config.geometry.preserve_features};
+        }
+    return {0, 0};
+}
+
+void Layout::validate_constraints(const GptConfig &config, const float *parameters) const {
+    for (size_t id = 0; id < groups.size(); ++id) {
+        const auto [begin, end] = constrained_range(config, id);
+        for (size_t i = groups[id].offset + begin; i < groups[id].offset + end; ++i)
+            if (parameters[i] != 0.0f) throw Error("protected residual output weights must be zero");
+    }
+}
+
+std::vector<float> geometric_codes(const GptConfig &config);
+std::vector<float> reorder_parity(const GptConfig &config, const std::vector<float> &codes);
+
 std::vector<float> token_codes(const GptConfig &config) {
+    if (config.geometry.form != EmbeddingForm::Parity) return geometric_codes(config);
     const size_t V = config.vocab_size, W = config.width;
     size_t bits = 0;
     for (size_t v = V - 1; v; v >>= 1) ++bits;
@@ -169,7 +203,7 @@ std::vector<float> token_codes(const GptConfig &config) {
             codes[token * W + channel] = value;
         }
     }
-    return codes;
+    return reorder_parity(config, codes);
 }
 
 std::vector<float> tabulate_embedding(const GptConfig &config, const std::vector<float> &parameters) {
@@ -355,11 +389,13 @@ std::vector<uint8_t> Checkpoint::serialize() const {
     if (config.parameter_count() != parameters.size() || config.vocab_size != tokenizer.vocab_size())
         throw Error("checkpoint model, parameters, and tokenizer do not match");
     validate_finite(parameters.data(), parameters.size(), "checkpoint parameters");
+    Layout::build(config).validate_constraints(config, parameters.data());
     bool table = config.embedding == TokenEmbedding::Table;
     bool butterfly = config.connectivity == MeshConnectivity::Butterfly;
-    bool is_default = !table && !butterfly;
+    bool v09 = !config.reference_operators();
+    bool is_default = !table && !butterfly && !v09;
     std::vector<uint8_t> out;
-    const char *magic = is_default ? "MSHGPT07" : "MSHGPT08";
+    const char *magic = v09 ? "MSHGPT09" : (is_default ? "MSHGPT07" : "MSHGPT08");
     out.insert(out.end(), magic, magic + 8);
     for (size_t field : {config.vocab_size, config.context, config.width, config.heads, config.layers,
                          config.attention_mesh_depth, config.ffn_mesh_depth})
@@ -367,6 +403,17 @@ std::vector<uint8_t> Checkpoint::serialize() const {
     if (!is_default) {
         put_u32(out, table ? 1 : 0);
         put_u32(out, butterfly ? 1 : 0);
+    }
+    if (v09) {
+        // Field order of checkpoint.rs:61-78.
+        const EmbeddingGeometry &g = config.geometry;
+        uint32_t overlap;
+        std::memcpy(&overlap, &g.overlap, 4);
+        for (uint32_t field : {uint32_t(g.form), uint32_t(g.order), uint32_t(g.frequency), uint32_t(g.harmonics),
+                               overlap, uint32_t(g.normalization), uint32_t(g.frozen), uint32_t(g.preserve_features),
+                               uint32_t(g.modulus), uint32_t(g.seed), uint32_t(g.seed >> 32), uint32_t(config.rope),
+                               uint32_t(config.qk_norm), uint32_t(config.xsa)})
+            put_u32(out, field);
     }
     for (uint32_t c : tokenizer.characters()) put_u32(out, c);
     for (float p : parameters) {
@@ -452,15 +499,22 @@ Checkpoint Checkpoint::read(const uint8_t *bytes, size_t n) {
         if (norm > 2) throw Error("unknown checkpoint EmbeddingNorm: " + std::to_string(norm));
         bool frozen = read_switch(r.word());
         uint32_t preserve = r.word(), modulus = r.word(), seed_lo = r.word(), seed_hi = r.word();
-        bool rope = read_switch(r.word()), qk_norm = read_switch(r.word()), xsa = read_switch(r.word());
-        bool geometry_default = form == 0 && order == 0 && frequency == 1 && harmonics == 1 &&
-                                overlap == 0 && norm == 0 && !frozen && preserve == 0 && modulus == 0 &&
-                                seed_lo == 0 && seed_hi == 0;
-        if (geometry_default && rope && qk_norm && xsa)
+        EmbeddingGeometry &g = c.geometry;
+        g.form = EmbeddingForm(form);
+        g.order = EmbeddingOrder(order);
+        g.frequency = frequency;
+        g.harmonics = harmonics;
+        std::memcpy(&g.overlap, &overlap, 4);
+        g.normalization = EmbeddingNorm(norm);
+        g.frozen = frozen;
+        g.preserve_features = preserve;
+        g.modulus = modulus;
+        g.seed = uint64_t(seed_lo) | uint64_t(seed_hi) << 32;
+        c.rope = read_switch(r.word());
+        c.qk_norm = read_switch(r.word());
+        c.xsa = read_switch(r.word());
+        if (g.is_default() && c.rope && c.qk_norm && c.xsa)
             throw Error("default geometry must use an older checkpoint layout");
-        throw Error("MSHGPT09 embedding-geometry and operator-switch ablations are not supported "
-                    "by this build",
-                    kUnsupported);
     }
     size_t count = c.parameter_count();
     std::vector<uint32_t> characters(c.vocab_size);
@@ -475,6 +529,7 @@ Checkpoint Checkpoint::read(const uint8_t *bytes, size_t n) {
         std::memcpy(&p, &bits, 4);
     }
     validate_finite(ck.parameters.data(), count, "checkpoint parameters");
+    Layout::build(c).validate_constraints(c, ck.parameters.data());
     if (r.at != n) throw Error("unexpected trailing checkpoint bytes");
     return ck;
 }

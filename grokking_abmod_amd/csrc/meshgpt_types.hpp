@@ -8,6 +8,7 @@
 #include <cstdint>
 #include <stdexcept>
 #include <string>
+#include <utility>
 #include <vector>
 
 namespace meshgpt {
@@ -53,8 +54,40 @@ MeshConnectivity parse_connectivity(const std::string &text);  // config.rs:131-
 // Distance from a neuron's own channel to its second parent (config.rs:116-122).
 size_t stride(MeshConnectivity connectivity, size_t width, size_t layer);
 
-// GptConfig (config.rs:21-56).  Geometry is fixed at its defaults and RoPE,
-// QK-Norm and XSA are always on; checkpoints that change them are rejected.
+// Token-code geometry ablations (geometry.rs:37-47); the numeric values are
+// the checkpoint codes.
+enum class EmbeddingForm : uint32_t {
+    Parity = 0, Circle, Fourier, Orthogonal, Simplex, Equiangular, Antipodal, Hypercube,
+    SignedPermutations, Sphere
+};
+enum class EmbeddingOrder : uint32_t { Token = 0, Residue, DiscreteLog };
+enum class EmbeddingNorm : uint32_t { None = 0, Unit, Rms };
+
+struct GptConfig;
+
+// EmbeddingGeometry (geometry.rs:49-81); defaults keep the signed parity codes.
+struct EmbeddingGeometry {
+    EmbeddingForm form = EmbeddingForm::Parity;
+    EmbeddingOrder order = EmbeddingOrder::Token;
+    size_t frequency = 1;
+    size_t harmonics = 1;
+    float overlap = 0.0f;
+    EmbeddingNorm normalization = EmbeddingNorm::None;
+    bool frozen = false;
+    size_t preserve_features = 0;
+    size_t modulus = 0;
+    uint64_t seed = 0;
+
+    bool operator==(const EmbeddingGeometry &o) const;
+    bool is_default() const { return *this == EmbeddingGeometry{}; }
+    void validate(const GptConfig &config) const;           // geometry.rs:84-151
+    bool transformed() const {                              // geometry.rs:153-155
+        return normalization != EmbeddingNorm::None || preserve_features > 0;
+    }
+    float radius(size_t width) const;                       // geometry.rs:157-162
+};
+
+// GptConfig (config.rs:21-56), with the geometry and operator-switch ablations.
 struct GptConfig {
     size_t vocab_size = 32;
     size_t context = 32;
@@ -65,6 +98,10 @@ struct GptConfig {
     size_t ffn_mesh_depth = 6;
     TokenEmbedding embedding = TokenEmbedding::Mesh;
     MeshConnectivity connectivity = MeshConnectivity::Neighbor;
+    EmbeddingGeometry geometry;
+    bool rope = true;
+    bool qk_norm = true;
+    bool xsa = true;
     bool long_context = false;  // extension flag, never stored in checkpoints
 
     bool operator==(const GptConfig &o) const;
@@ -74,6 +111,8 @@ struct GptConfig {
     std::vector<float> initial_parameters(uint64_t seed) const;           // config.rs:187-190
     void validate_tokens(const uint32_t *tokens, size_t n, size_t sequence) const;  // 210-228
     size_t head_width() const { return width / heads; }
+    // Every operator on and the default geometry: the MSHGPT07/08 architectures.
+    bool reference_operators() const { return rope && qk_norm && xsa && geometry.is_default(); }
 };
 
 struct Group {
@@ -93,10 +132,20 @@ struct Layout {
     static Layout build(const GptConfig &config);
     size_t count() const;
     std::vector<float> initialize(const GptConfig &config, uint64_t seed) const;
+    // The final mesh rows that write protected residual coordinates
+    // (config.rs:461-474): [begin, end) within group `id`.
+    std::pair<size_t, size_t> constrained_range(const GptConfig &config, size_t id) const;
+    // "protected residual output weights must be zero" (config.rs:476-488).
+    void validate_constraints(const GptConfig &config, const float *parameters) const;
 };
 
-// Fixed token codes, vocab x width (config.rs:552-591).
+// Fixed token codes, vocab x width (config.rs:552-591; geometric forms and
+// orders, geometry.rs:186-325).
 std::vector<float> token_codes(const GptConfig &config);
+// The residue token permutation of the grok dataset (grokking.rs:260-271).
+std::vector<uint32_t> residue_permutation(size_t modulus, uint64_t seed);
+// The smallest primitive root of a prime (geometry.rs:166-184).
+size_t primitive_root(size_t prime);
 // Table parameters of a mesh-embedding model (config.rs:505-547).
 std::vector<float> tabulate_embedding(const GptConfig &config, const std::vector<float> &parameters);
 
@@ -134,9 +183,8 @@ std::vector<uint32_t> utf8_decode(const std::string &text);
 std::string utf8_encode(const uint32_t *scalars, size_t n);
 
 // Weights-only checkpoint (src/gpt/checkpoint.rs:14-201): MSHGPT07 for the
-// default architecture, MSHGPT08 with embedding/connectivity codes.  MSHGPT09
-// files are parsed and validated like the reference, then rejected as
-// unsupported when they change geometry or switch an operator off.
+// default architecture, MSHGPT08 with embedding/connectivity codes, MSHGPT09
+// with the geometry and operator switches.
 struct Checkpoint {
     GptConfig config;
     CharacterTokenizer tokenizer;

@@ -229,8 +229,14 @@ struct MeshGpt::Impl {
         shape.butterfly = cfg.connectivity == MeshConnectivity::Butterfly ? 1 : 0;
         shape.A = int(cfg.attention_mesh_depth);
         shape.F = int(cfg.ffn_mesh_depth);
+        shape.rope = cfg.rope;
+        shape.qk_norm = cfg.qk_norm;
+        shape.xsa = cfg.xsa;
+        const bool all_operators = cfg.rope && cfg.qk_norm && cfg.xsa;
         wave_decode = env_int("MG_DISABLE_WAVE_DECODE", 0) == 0 && kern::block_decode_supported(shape);
-        row_decode = env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
+        // The row-order and persistent decode kernels run every operator;
+        // operator ablations decode on the one-wave or general block kernels.
+        row_decode = all_operators && env_int("MG_DISABLE_ROW_DECODE", 0) == 0 && kern::row_block_supported(shape);
         persistent_ok = row_decode && env_int("MG_DISABLE_PERSISTENT", 0) == 0;
         use_mfma_prefill = env_int("MG_DISABLE_MFMA_PREFILL", 0) == 0;
         use_rows_prefill = env_int("MG_DISABLE_ROWS_PREFILL", 0) == 0;
@@ -265,6 +271,7 @@ struct MeshGpt::Impl {
     void set_parameters(const float *values, size_t n) {
         if (n != layout.count()) throw Error("parameter count does not match GPT configuration");
         validate_finite(values, n, "parameters");
+        layout.validate_constraints(cfg, values);
         activate();
         check(hipMemcpyAsync(params.p, values, n * 4, hipMemcpyHostToDevice, stream), "upload parameters");
         // The token vectors depend only on the weights: computed once here, not per token.
@@ -276,6 +283,12 @@ struct MeshGpt::Impl {
                                  stream),
                   "copy table");
         }
+        // The geometry's normalisation or protected coordinates (reference.rs:130-149).
+        if (cfg.geometry.transformed())
+            kern::embedding_geometry(E.as<float>(), codes.as<float>(), shape.V, shape.W,
+                                     cfg.geometry.radius(cfg.width),
+                                     cfg.geometry.normalization != EmbeddingNorm::None ? 1 : 0,
+                                     int(cfg.geometry.preserve_features), stream);
         kern::transpose(E.as<float>(), Et.as<float>(), shape.V, vpad, shape.W, stream);
         if (row_decode) {
             const size_t emb = cfg.embedding_parameter_count();
@@ -397,7 +410,7 @@ struct MeshGpt::Impl {
                 a.part = decode ? part.as<float>() : nullptr;
                 a.nsplit = nsplit;
                 a.ybuf = decode ? nullptr : y;
-                a.xsa_post = decode || !(mfma_prefill || short_prefill) ? 1 : 0;
+                a.xsa_post = cfg.xsa && (decode || !(mfma_prefill || short_prefill)) ? 1 : 0;
                 a.kv_post = kv_of(l - 1);
             }
             if (l < L) {
@@ -429,9 +442,9 @@ struct MeshGpt::Impl {
                 kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream,
                                   events ? events[2 * l] : nullptr, events ? events[2 * l + 1] : nullptr);
             } else if (mfma_prefill) {
-                kern::attn_prefill_mfma(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, 1, stream);
+                kern::attn_prefill_mfma(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, cfg.xsa, stream);
             } else if (short_prefill) {
-                kern::attn_prefill_short(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, 1, stream);
+                kern::attn_prefill_short(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, cfg.xsa, stream);
             } else {
                 kern::attn_prefill(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, stream);
             }

@@ -293,15 +293,19 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
         for (int k = 0; k < CPT; ++k) {
             const int c = t.chan(k), h = c / s.hd, d = c - h * s.hd;
             if (m < 2) {
-                // QK-Norm per head, then RoPE at the row's position; the pair
-                // partner d ^ half is the lane half a head away.
+                // QK-Norm per head, then RoPE at the row's position, each when
+                // its switch is on (reference.rs:174-193); the pair partner
+                // d ^ half is the lane half a head away.
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
-                    const float ss = head_sum(v[k][i] * v[k][i], s.hd);
-                    const float q = v[k][i] * rsqrtf(ss * (1.0f / float(s.hd)) + kEps);
-                    const float p = __shfl_xor(q, s.half, 64);
-                    const float2 cs = a.rope[size_t(pos[i]) * s.half + (d < s.half ? d : d - s.half)];
-                    v[k][i] = q * cs.x + (d < s.half ? -p : p) * cs.y;
+                    float q = v[k][i];
+                    if (s.qk_norm) q *= rsqrtf(head_sum(q * q, s.hd) * (1.0f / float(s.hd)) + kEps);
+                    if (s.rope) {
+                        const float p = __shfl_xor(q, s.half, 64);
+                        const float2 cs = a.rope[size_t(pos[i]) * s.half + (d < s.half ? d : d - s.half)];
+                        q = q * cs.x + (d < s.half ? -p : p) * cs.y;
+                    }
+                    v[k][i] = q;
                 }
             }
 #pragma unroll

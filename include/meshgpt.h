@@ -34,9 +34,9 @@ enum {
 };
 
 /* GptConfig (src/gpt/config.rs:21-56) in checkpoint field order
- * (src/gpt/checkpoint.rs:51-63,129-138).  Geometry stays at its defaults and
- * RoPE, QK-Norm and XSA are on, as in every checkpoint the reference writes
- * as MSHGPT07/08. */
+ * (src/gpt/checkpoint.rs:51-78,129-168).  mg_config_default() gives the
+ * reference's defaults: default geometry and RoPE, QK-Norm and XSA on, as in
+ * every MSHGPT07/08 checkpoint; MSHGPT09 checkpoints change the rest. */
 typedef struct {
     uint32_t vocab_size;
     uint32_t context;
@@ -49,6 +49,24 @@ typedef struct {
     uint32_t connectivity; /* 0 neighbor, 1 butterfly (config.rs:96-106) */
     uint32_t long_context; /* extension: 1 accepts context up to 65536 (reference cap 4096,
                               config.rs:148); such configs cannot be checkpointed */
+    /* Operator switches (config.rs:33-35): 1 on, 0 off. */
+    uint32_t rope;
+    uint32_t qk_norm;
+    uint32_t xsa;
+    /* EmbeddingGeometry (geometry.rs:49-81) with its checkpoint codes: form 0 parity,
+     * 1 circle, 2 fourier, 3 orthogonal, 4 simplex, 5 equiangular, 6 antipodal,
+     * 7 hypercube, 8 signed-permutations, 9 sphere; order 0 token, 1 residue,
+     * 2 discrete-log; normalization 0 none, 1 unit, 2 rms. */
+    uint32_t form;
+    uint32_t order;
+    uint32_t frequency;
+    uint32_t harmonics;
+    float overlap;
+    uint32_t normalization;
+    uint32_t frozen;
+    uint32_t preserve_features;
+    uint32_t modulus;
+    uint64_t seed;
 } mg_config;
 
 typedef struct mg_model mg_model;

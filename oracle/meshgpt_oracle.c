@@ -70,7 +70,251 @@ static void set_err(char *err, size_t len, const char *msg) {
     }
 }
 
-/* src/gpt/config.rs:144-172 (geometry defaults always pass their check) */
+/* ------------------------------------------------------------ geometry */
+
+static uint32_t bit_len(uint64_t x) {
+    uint32_t n = 0;
+    while (x) {
+        x >>= 1;
+        ++n;
+    }
+    return n;
+}
+
+static const char *const form_names[10] = {"parity",  "circle",    "fourier",   "orthogonal",
+                                           "simplex", "equiangular", "antipodal", "hypercube",
+                                           "signed-permutations", "sphere"};
+
+/* src/gpt/geometry.rs:84-151 (the "does not fit" message prints the overlap
+ * with Rust's shortest round-trip Display) */
+static int validate_geometry(const og_config *c, char *err, size_t err_len) {
+    uint32_t v = c->vocab_size, w = c->width;
+    if (c->form > 9 || c->order > 2 || c->normalization > 2 || c->frozen > 1 || c->rope > 1 || c->qk_norm > 1 ||
+        c->xsa > 1) {
+        set_err(err, err_len, "unknown geometry code");
+        return -1;
+    }
+    if (c->frequency == 0 || c->harmonics == 0 || c->harmonics > w / 2) {
+        set_err(err, err_len, "embedding frequency must be positive and harmonics in 1..width/2");
+        return -1;
+    }
+    if (!isfinite(c->overlap) || c->preserve_features > w) {
+        set_err(err, err_len, "embedding overlap must be finite; preserved features must fit width");
+        return -1;
+    }
+    if (c->preserve_features > 0 && c->normalization != 0) {
+        set_err(err, err_len,
+                "preserved coordinates require --embedding-norm none; full-vector normalization would rescale "
+                "the protected feature");
+        return -1;
+    }
+    int fits = 1;
+    if (c->form == 3) fits = w >= v;
+    if (c->form == 4) fits = w + 1 >= v;
+    if (c->form == 5) {
+        float lower = -1.0f / (float)(v - 1);
+        fits = c->overlap >= lower && c->overlap <= 1.0f &&
+               (c->overlap == 1.0f || w + (c->overlap == lower ? 1u : 0u) >= v);
+    }
+    if (c->form == 7) fits = w >= bit_len(v - 1);
+    if (c->form == 8) fits = w >= 4 && v <= 256;
+    if (!fits) {
+        char buf[160];
+        /* shortest decimal of the f32 overlap that reads back exactly, no exponent */
+        char num[64];
+        for (int prec = 0; prec < 60; ++prec) {
+            snprintf(num, sizeof num, "%.*f", prec, (double)c->overlap);
+            if ((float)strtod(num, NULL) == c->overlap) break;
+        }
+        snprintf(buf, sizeof buf, "%s embedding does not fit vocabulary %u, width %u, overlap %s",
+                 form_names[c->form], v, w, num);
+        set_err(err, err_len, buf);
+        return -1;
+    }
+    if (c->order != 0) {
+        int prime = c->modulus >= 2;
+        for (uint32_t d = 2; d < c->modulus; ++d)
+            if (c->modulus % d == 0) prime = 0;
+        if (c->modulus < 2 || c->modulus > 254 || !prime || v != c->modulus + 2) {
+            set_err(err, err_len, "arithmetic embedding order requires a grok prime and vocabulary modulus+2");
+            return -1;
+        }
+        uint32_t special = 2 + (c->order == 2 ? 1 : 0);
+        uint32_t pairs = c->form == 2 ? c->harmonics : 1;
+        if ((c->form == 1 || c->form == 2) && w < 2 * pairs + special) {
+            set_err(err, err_len, "arithmetic circle/Fourier codes need extra coordinates for special symbols");
+            return -1;
+        }
+    }
+    return 0;
+}
+
+/* src/gpt/grokking.rs:260-271: a Fisher-Yates shuffle of 0..modulus from the
+ * tail, with Random::new(seed ^ "symbols\x01") */
+void og_residue_permutation(uint32_t modulus, uint64_t seed, uint32_t *out) {
+    for (uint32_t i = 0; i < modulus; ++i) out[i] = i;
+    uint64_t state = seed ^ 0x73796d626f6c7301ULL;
+    for (uint32_t end = modulus; end-- > 1;) {
+        uint32_t j = (uint32_t)og_rng_index(&state, (uint64_t)end + 1);
+        uint32_t t = out[end];
+        out[end] = out[j];
+        out[j] = t;
+    }
+}
+
+/* src/gpt/geometry.rs:166-184 */
+uint32_t og_primitive_root(uint32_t prime) {
+    if (prime == 2) return 1;
+    unsigned char *seen = (unsigned char *)malloc(prime);
+    for (uint32_t g = 2; g < prime; ++g) {
+        memset(seen, 0, prime);
+        uint64_t x = 1;
+        int ok = 1;
+        for (uint32_t k = 0; k + 1 < prime; ++k) {
+            if (seen[x]) {
+                ok = 0;
+                break;
+            }
+            seen[x] = 1;
+            x = x * g % prime;
+        }
+        if (ok && x == 1) {
+            free(seen);
+            return g;
+        }
+    }
+    free(seen);
+    return 0;
+}
+
+/* src/gpt/geometry.rs:186-211: token at each position and the cycle length */
+static size_t ordered_tokens(const og_config *c, uint32_t *order) {
+    uint32_t V = c->vocab_size;
+    if (c->order == 0) {
+        for (uint32_t t = 0; t < V; ++t) order[t] = t;
+        return V;
+    }
+    uint32_t p = c->modulus;
+    uint32_t *ids = (uint32_t *)malloc(sizeof(uint32_t) * p);
+    og_residue_permutation(p, c->seed, ids);
+    size_t n = 0;
+    if (c->order == 1) {
+        for (uint32_t i = 0; i < p; ++i) order[n++] = ids[i];
+    } else {
+        uint32_t root = og_primitive_root(p);
+        uint64_t residue = 1;
+        for (uint32_t k = 0; k + 1 < p; ++k) {
+            order[n++] = ids[residue];
+            residue = residue * root % p;
+        }
+    }
+    size_t cycle = n;
+    if (c->order == 2) order[n++] = ids[0];
+    order[n++] = p;
+    order[n++] = p + 1;
+    free(ids);
+    return cycle;
+}
+
+static double helmert(size_t row, size_t column, size_t n) {
+    double scale = sqrt((double)n / (double)(n - 1));
+    double den = sqrt((double)((column + 1) * (column + 2)));
+    if (row <= column) return scale / den;
+    if (row == column + 1) return -scale * (double)(column + 1) / den;
+    return 0.0;
+}
+
+/* src/gpt/geometry.rs:238-325 for the non-parity forms */
+static void geometric_codes(const og_config *c, float *out) {
+    size_t V = c->vocab_size, W = c->width;
+    uint32_t *order = (uint32_t *)malloc(sizeof(uint32_t) * V);
+    size_t cycle = ordered_tokens(c, order);
+    memset(out, 0, sizeof(float) * V * W);
+    uint64_t rng = c->seed ^ 0x5350484552453031ULL;
+    const double tau = 6.283185307179586;
+    for (size_t row = 0; row < V; ++row) {
+        float *code = out + (size_t)order[row] * W;
+        switch (c->form) {
+        case 1:
+        case 2: {
+            size_t pairs = c->form == 2 ? c->harmonics : 1;
+            if (row >= cycle) {
+                code[2 * pairs + row - cycle] = 1.0f;
+                break;
+            }
+            double scale = 1.0 / sqrt((double)pairs);
+            for (size_t k = 0; k < pairs; ++k) {
+                size_t f = ((size_t)c->frequency % cycle + k % cycle) % cycle;
+                double angle = tau * (double)f * (double)row / (double)cycle;
+                code[2 * k] = (float)(scale * cos(angle));
+                code[2 * k + 1] = (float)(scale * sin(angle));
+            }
+            break;
+        }
+        case 3: code[row] = 1.0f; break;
+        case 4:
+        case 5: {
+            double rho = c->form == 4 ? -1.0 / (double)(V - 1) : (double)c->overlap;
+            if (rho == 1.0) {
+                code[0] = 1.0f;
+                break;
+            }
+            double a = sqrt((1.0 - rho) * (double)(V - 1) / (double)V);
+            for (size_t col = 0; col + 1 < V; ++col) code[col] = (float)(a * helmert(row, col, V));
+            if (W >= V) {
+                double t = 1.0 + (double)(V - 1) * rho;
+                code[V - 1] = (float)sqrt((t > 0.0 ? t : 0.0) / (double)V);
+            }
+            break;
+        }
+        case 6: code[0] = row % 2 == 0 ? 1.0f : -1.0f; break;
+        case 7: {
+            uint32_t bits = bit_len(V - 1);
+            for (uint32_t b = 0; b < bits; ++b)
+                code[b] = ((row >> b) & 1 ? 1.0f : -1.0f) / sqrtf((float)bits);
+            break;
+        }
+        case 8: {
+            size_t p = row / 16;
+            for (size_t col = 0; col < 4; ++col) {
+                size_t slot = col < 2 ? (col + (p / 2) % 2) % 2 : 2 + (col - 2 + p % 2) % 2;
+                float magnitude = (float)(1 + (slot + p / 4) % 4);
+                code[col] = magnitude * ((row >> col) & 1 ? -1.0f : 1.0f);
+            }
+            break;
+        }
+        case 9: {
+            double squares = 0.0;
+            for (size_t col = 0; col < W; ++col) {
+                float u = og_rng_unit(&rng);
+                if (u < 1.0f / 16777216.0f) u = 1.0f / 16777216.0f;
+                double radius = sqrt(-2.0 * log((double)u));
+                double angle = tau * (double)og_rng_unit(&rng);
+                code[col] = (float)(radius * cos(angle));
+                squares += (double)code[col] * (double)code[col];
+            }
+            for (size_t col = 0; col < W; ++col) code[col] = (float)((double)code[col] / sqrt(squares));
+            break;
+        }
+        default: break;
+        }
+    }
+    free(order);
+}
+
+/* src/gpt/config.rs:461-474: the final-layer rows of every projection and FFN
+ * mesh that write protected residual coordinates, as [begin, end) offsets */
+static void constrained_range(const og_config *c, size_t group, size_t *begin, size_t *end) {
+    *begin = *end = 0;
+    if (c->preserve_features == 0 || group == 0) return;
+    size_t kind = (group - 1) % 5;
+    if (kind != 3 && kind != 4) return;
+    size_t depth = kind == 4 ? c->ffn_mesh_depth : c->attention_mesh_depth;
+    *begin = (depth - 1) * 2 * (size_t)c->width;
+    *end = *begin + 2 * (size_t)c->preserve_features;
+}
+
+/* src/gpt/config.rs:144-172 */
 int og_validate(const og_config *c, int allow_long_context, char *err, size_t err_len) {
     if (c->vocab_size < 2 || c->vocab_size > OG_MAX_VOCAB) {
         set_err(err, err_len, "vocab_size must be in 2..65536");
@@ -92,7 +336,7 @@ int og_validate(const og_config *c, int allow_long_context, char *err, size_t er
         set_err(err, err_len, "each attention head requires at least two channels");
         return -1;
     }
-    if ((c->width / c->heads) % 2 != 0) {
+    if (c->rope && (c->width / c->heads) % 2 != 0) {
         set_err(err, err_len, "slice RoPE requires an even number of channels per head");
         return -1;
     }
@@ -109,7 +353,7 @@ int og_validate(const og_config *c, int allow_long_context, char *err, size_t er
         set_err(err, err_len, "unknown embedding or connectivity code");
         return -1;
     }
-    return 0;
+    return validate_geometry(c, err, err_len);
 }
 
 /* src/gpt/config.rs:179-184 */
@@ -165,6 +409,10 @@ static int is_pow2(uint64_t x) { return x && !(x & (x - 1)); }
 /* src/gpt/config.rs:552-591 with the default Parity form and Token order
  * (reorder_parity is the identity then, geometry.rs:213-216) */
 void og_token_codes(const og_config *c, float *out) {
+    if (c->form != 0) {
+        geometric_codes(c, out);
+        return;
+    }
     uint32_t V = c->vocab_size, W = c->width;
     uint32_t bits = 32 - (uint32_t)__builtin_clz(V - 1);
     uint32_t lanes = W < bits ? W : bits;
@@ -190,6 +438,16 @@ void og_token_codes(const og_config *c, float *out) {
         }
     }
     free(masks);
+    if (c->order != 0) {
+        /* geometry.rs:213-222: the code of position i belongs to token order[i] */
+        uint32_t *order = (uint32_t *)malloc(sizeof(uint32_t) * V);
+        ordered_tokens(c, order);
+        float *copy = (float *)malloc(sizeof(float) * (size_t)V * W);
+        memcpy(copy, out, sizeof(float) * (size_t)V * W);
+        for (uint32_t i = 0; i < V; ++i) memcpy(out + (size_t)order[i] * W, copy + (size_t)i * W, sizeof(float) * W);
+        free(copy);
+        free(order);
+    }
 }
 
 /* src/gpt/config.rs:436-458: SplitMix64 draws in f32, final layer scaled by 0.3 */
@@ -216,6 +474,11 @@ static void initialize_mesh_model(const og_config *c, uint64_t seed, float *out)
             }
         }
     }
+    for (size_t g = 0; g < ngroups; ++g) {
+        size_t begin, end;
+        constrained_range(c, g, &begin, &end);
+        for (size_t i = begin; i < end; ++i) out[offsets[g] + i] = 0.0f;
+    }
     free(offsets);
 }
 
@@ -240,7 +503,7 @@ void og_initialize(const og_config *c, uint64_t seed, float *out) {
     double *tmp = (double *)malloc(sizeof(double) * V * W);
     for (size_t i = 0; i < V * W; ++i) vec[i] = (double)codes[i];
     mesh_rows(vec, tmp, V, W, init, c->attention_mesh_depth, c->connectivity);
-    for (size_t i = 0; i < V * W; ++i) out[i] = (float)vec[i];
+    for (size_t i = 0; i < V * W; ++i) out[i] = c->form != 0 ? codes[i] : (float)vec[i];
     size_t emb = og_embedding_parameter_count(&mesh);
     memcpy(out + V * W, init + emb, sizeof(float) * (count - emb));
     free(init);
@@ -390,20 +653,34 @@ static int check_tokens(const og_config *c, const uint32_t *tokens, size_t n, si
     return 0;
 }
 
-/* reference.rs:104-152 with default geometry */
+/* reference.rs:104-152: the mesh of the codes or the table, then the
+ * geometry's normalisation (rows scaled to the radius) or protected codes */
 int og_token_embeddings(const og_config *c, const float *params, double *out) {
     size_t V = c->vocab_size, W = c->width;
+    float *codes = (float *)malloc(sizeof(float) * V * W);
+    og_token_codes(c, codes);
     if (c->embedding == 1) {
         for (size_t i = 0; i < V * W; ++i) out[i] = (double)params[i];
-        return 0;
+    } else {
+        double *tmp = (double *)malloc(sizeof(double) * V * W);
+        for (size_t i = 0; i < V * W; ++i) out[i] = (double)codes[i];
+        mesh_rows(out, tmp, V, W, params, c->attention_mesh_depth, c->connectivity);
+        free(tmp);
     }
-    float *codes = (float *)malloc(sizeof(float) * V * W);
-    double *tmp = (double *)malloc(sizeof(double) * V * W);
-    og_token_codes(c, codes);
-    for (size_t i = 0; i < V * W; ++i) out[i] = (double)codes[i];
-    mesh_rows(out, tmp, V, W, params, c->attention_mesh_depth, c->connectivity);
+    if (c->normalization != 0) {
+        /* EmbeddingGeometry::radius (geometry.rs:157-162) in f32, then f64 */
+        double scale = c->normalization == 2 ? (double)sqrtf((float)W) : 1.0;
+        double floor = (double)1e-12f * (double)1e-12f;
+        for (size_t t = 0; t < V; ++t) {
+            double *row = out + t * W;
+            double squares = dot(row, row, W);
+            double inverse = 1.0 / sqrt(squares > floor ? squares : floor) * scale;
+            for (size_t i = 0; i < W; ++i) row[i] = row[i] * inverse;
+        }
+    }
+    for (size_t t = 0; t < V; ++t)
+        for (size_t i = 0; i < c->preserve_features; ++i) out[t * W + i] = (double)codes[t * W + i];
     free(codes);
-    free(tmp);
     return 0;
 }
 
@@ -441,11 +718,19 @@ static void forward(const og_config *c, const float *params, const double *E, co
         memcpy(v, nrm, sizeof(double) * rw);
         mesh_rows(v, t1, n, W, params + g[2], A, c->connectivity);
         for (size_t r = 0; r < n; ++r) {
+            /* reference.rs:174-193: QK-Norm, then RoPE, each when switched on */
             size_t position = cache_k ? first_position + r : r % sequence;
-            og_rmsnorm(q + r * W, W, H, row);
-            rotary_row(row, W, H, position, q + r * W);
-            og_rmsnorm(k + r * W, W, H, row);
-            rotary_row(row, W, H, position, k + r * W);
+            double *qk[2] = {q + r * W, k + r * W};
+            for (int m = 0; m < 2; ++m) {
+                if (c->qk_norm) {
+                    og_rmsnorm(qk[m], W, H, row);
+                    memcpy(qk[m], row, sizeof(double) * W);
+                }
+                if (c->rope) {
+                    memcpy(row, qk[m], sizeof(double) * W);
+                    rotary_row(row, W, H, position, qk[m]);
+                }
+            }
         }
         if (cache_k) {
             double *ck = cache_k + b * c->context * W, *cv = cache_v + b * c->context * W;
@@ -456,7 +741,12 @@ static void forward(const og_config *c, const float *params, const double *E, co
         } else {
             og_attention(q, k, v, n, W, H, sequence, t1);
         }
-        for (size_t r = 0; r < n; ++r) og_exclusive(t1 + r * W, v + r * W, W, H, t2 + r * W);
+        for (size_t r = 0; r < n; ++r) {
+            if (c->xsa)
+                og_exclusive(t1 + r * W, v + r * W, W, H, t2 + r * W);
+            else
+                memcpy(t2 + r * W, t1 + r * W, sizeof(double) * W);
+        }
         mesh_rows(t2, t1, n, W, params + g[3], A, c->connectivity);
         for (size_t i = 0; i < rw; ++i) x[i] = x[i] + t2[i];
         for (size_t r = 0; r < n; ++r) og_rmsnorm(x + r * W, W, 1, nrm + r * W);

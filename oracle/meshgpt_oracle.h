@@ -11,8 +11,8 @@
  * Each function below names the reference lines it restates.  How each one is
  * pinned (reference KATs, published whole-model numbers, closed forms,
  * independent numpy restatements) is recorded in tests/test_oracle.py.
- * og_sample with temperature > 0 is parity unpinned: the reference holds no
- * sampler vector, so it is checked only against an independent restatement.
+ * og_sample with temperature > 0 has no reference vector; it is pinned by
+ * closed forms, an exact rescaling symmetry and its realised distribution.
  */
 #ifndef MESHGPT_ORACLE_H
 #define MESHGPT_ORACLE_H
@@ -24,9 +24,9 @@
 extern "C" {
 #endif
 
-/* GptConfig (reference src/gpt/config.rs:21-56); geometry fields are fixed at
- * their defaults (parity codes, token order, no normalisation) and rope, qk_norm,
- * xsa are always on (config.rs:38-55). */
+/* GptConfig (reference src/gpt/config.rs:21-56) with its operator switches
+ * (config.rs:33-35) and EmbeddingGeometry (geometry.rs:49-81); codes as in the
+ * checkpoint (checkpoint.rs:146-168). */
 typedef struct {
     uint32_t vocab_size;
     uint32_t context;
@@ -37,6 +37,17 @@ typedef struct {
     uint32_t ffn_mesh_depth;
     uint32_t embedding;    /* 0 = mesh (default), 1 = table (config.rs:58-67) */
     uint32_t connectivity; /* 0 = neighbor (default), 1 = butterfly (config.rs:96-106) */
+    uint32_t rope, qk_norm, xsa; /* 1 = on (default) */
+    uint32_t form;          /* 0 parity (default) .. 9 sphere, geometry.rs:37-41 */
+    uint32_t order;         /* 0 token (default), 1 residue, 2 discrete-log */
+    uint32_t frequency;     /* default 1 */
+    uint32_t harmonics;     /* default 1 */
+    float overlap;
+    uint32_t normalization; /* 0 none (default), 1 unit, 2 rms */
+    uint32_t frozen;
+    uint32_t preserve_features;
+    uint32_t modulus;
+    uint64_t seed;
 } og_config;
 
 /* ---- SplitMix64 (reference src/mesh.rs:256-288) ---- */
@@ -53,8 +64,11 @@ size_t og_embedding_parameter_count(const og_config *c);
 void og_group_offsets(const og_config *c, size_t *offsets /* 1+5L */);
 uint32_t og_stride(const og_config *c, uint32_t layer);
 void og_initialize(const og_config *c, uint64_t seed, float *out);
-/* fixed token codes, V x W (config.rs:552-591) */
+/* fixed token codes, V x W (config.rs:552-591, geometry.rs:186-325) */
 void og_token_codes(const og_config *c, float *out);
+/* grokking.rs:260-271 (modulus entries) and geometry.rs:166-184 */
+void og_residue_permutation(uint32_t modulus, uint64_t seed, uint32_t *out);
+uint32_t og_primitive_root(uint32_t prime);
 
 /* ---- per-op references used by the reference's own KATs (reference.rs:392-603) ---- */
 void og_rmsnorm(const double *in, size_t width, size_t heads, double *out);
@@ -87,7 +101,7 @@ int og_cross_entropy(const og_config *c, const float *params, const uint32_t *in
 int og_generate(const og_config *c, const float *params, const uint32_t *prompt, size_t P,
                 size_t count, float temperature, uint64_t seed, uint32_t *out);
 /* the f32 sampler of gpu.rs:2028-2049 on one row of f32 logits; returns the token and
- * advances *rng only when temperature > 0 (T > 0: parity unpinned, see above) */
+ * advances *rng only when temperature > 0 */
 uint32_t og_sample(const float *logits, size_t vocab, float temperature, uint64_t *rng);
 
 /* ---- KV-cached incremental decode (same math, used as the CPU baseline) ----

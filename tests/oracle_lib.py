@@ -21,14 +21,22 @@ _szp = ctypes.POINTER(ctypes.c_size_t)
 class OgConfig(ctypes.Structure):
     _fields_ = [(name, ctypes.c_uint32) for name in (
         "vocab_size", "context", "width", "heads", "layers",
-        "attention_mesh_depth", "ffn_mesh_depth", "embedding", "connectivity")]
+        "attention_mesh_depth", "ffn_mesh_depth", "embedding", "connectivity",
+        "rope", "qk_norm", "xsa", "form", "order", "frequency", "harmonics")] + [
+        ("overlap", ctypes.c_float)] + [(name, ctypes.c_uint32) for name in (
+            "normalization", "frozen", "preserve_features", "modulus")] + [("seed", ctypes.c_uint64)]
 
 
 def config(vocab_size=32, context=32, width=32, heads=4, layers=2, attention_mesh_depth=4,
-           ffn_mesh_depth=6, embedding=0, connectivity=0):
-    """GptConfig::default() (reference src/gpt/config.rs:38-55) with overrides."""
+           ffn_mesh_depth=6, embedding=0, connectivity=0, rope=1, qk_norm=1, xsa=1, form=0, order=0,
+           frequency=1, harmonics=1, overlap=0.0, normalization=0, frozen=0, preserve_features=0, modulus=0,
+           seed=0):
+    """GptConfig::default() (reference src/gpt/config.rs:38-55, geometry.rs:66-81)
+    with overrides."""
     return OgConfig(vocab_size, context, width, heads, layers, attention_mesh_depth,
-                    ffn_mesh_depth, embedding, connectivity)
+                    ffn_mesh_depth, embedding, connectivity, rope, qk_norm, xsa, form, order,
+                    frequency, harmonics, overlap, normalization, frozen, preserve_features, modulus,
+                    seed)
 
 
 _lib = None
@@ -52,6 +60,8 @@ def lib():
             "og_stride": (ctypes.c_uint32, [cp, ctypes.c_uint32]),
             "og_initialize": (None, [cp, ctypes.c_uint64, _f32p]),
             "og_token_codes": (None, [cp, _f32p]),
+            "og_residue_permutation": (None, [ctypes.c_uint32, ctypes.c_uint64, _u32p]),
+            "og_primitive_root": (ctypes.c_uint32, [ctypes.c_uint32]),
             "og_rmsnorm": (None, [_f64p, ctypes.c_size_t, ctypes.c_size_t, _f64p]),
             "og_rotary": (None, [_f64p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t, _f64p]),
             "og_exclusive": (None, [_f64p, _f64p, ctypes.c_size_t, ctypes.c_size_t, _f64p]),

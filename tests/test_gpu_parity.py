@@ -349,3 +349,35 @@ def test_persistent_decode_steps_continue_a_generation():
         model.decode(20)
         assert model.sequence_length() == 16 + 33
         assert np.array_equal(model.read_tokens(3), whole)
+
+
+# MSHGPT09 ablations (checkpoint.rs:146-168): operator switches
+# (reference.rs:174-199) and embedding geometry (reference.rs:130-149,
+# geometry.rs:238-325) on the prefill and decode paths.
+ABLATION_BASE = dict(vocab_size=7, context=96, width=128, heads=4, layers=2, attention_mesh_depth=3,
+                     ffn_mesh_depth=3, connectivity=1)
+ABLATIONS = [
+    dict(rope=0), dict(qk_norm=0), dict(xsa=0), dict(rope=0, qk_norm=0, xsa=0), dict(xsa=0, embedding=1),
+    dict(form=9), dict(normalization=2), dict(preserve_features=3), dict(form=1, order=2, modulus=5, seed=17),
+    dict(form=2, harmonics=3, embedding=1, normalization=1), dict(form=5, overlap=0.25, embedding=1, qk_norm=0),
+    dict(width=12, heads=4, rope=0),
+]
+
+
+@pytest.mark.parametrize("kw", ABLATIONS, ids=[str(i) for i in range(len(ABLATIONS))])
+def test_mshgpt09_ablations_match_oracle(kw):
+    cfg = dict(ABLATION_BASE, **kw)
+    g, o = configs_for(**cfg)
+    params = O.initialize(o, 7)
+    with G.MeshGpt(0, g, 7, max_batch=2) as model:
+        assert np.array_equal(model.parameters().view(np.uint32), params.view(np.uint32))
+        assert_close(model.token_embeddings(), O.token_embeddings(o, params), what="embeddings")
+        for batch, n in ((5, 4), (2, 70)):
+            x = G.random_prompts(7, batch, n, n).reshape(-1)
+            assert_close(model.logits(x, n), O.logits(o, params, x, n), what=f"logits n={n}")
+        prompts = G.random_prompts(7, 2, 8, 1)
+        got = model.generate_tokens(prompts, 12, 0.0, 3)
+        last = model.last_logits(2)
+        for b in range(2):
+            assert_close(last[b], O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], what=f"decode seq {b}")
+            check_trajectory(o, params, prompts[b], got[b], 0.0, 3 + b, _device_last(model))

@@ -44,7 +44,9 @@ def test_default_config_is_reference_default():
     # config.rs:38-55
     c = G.GptConfig()
     assert c.as_dict() == dict(vocab_size=32, context=32, width=32, heads=4, layers=2, attention_mesh_depth=4,
-                               ffn_mesh_depth=6, embedding=0, connectivity=0, long_context=0)
+                               ffn_mesh_depth=6, embedding=0, connectivity=0, long_context=0, rope=1, qk_norm=1,
+                               xsa=1, form=0, order=0, frequency=1, harmonics=1, overlap=0.0, normalization=0,
+                               frozen=0, preserve_features=0, modulus=0, seed=0)
     G.validate(c)
     assert G.parameter_count(c) == 3072
 
@@ -71,6 +73,67 @@ def test_validation_messages_match_reference(kw, message):
         G.validate(G.GptConfig(**kw))
     assert info.value.status == G.MG_INVALID_ARGUMENT
     assert O.validate(O.config(**kw)) == message
+
+
+GEOMETRY_BASE = dict(vocab_size=7, width=8, heads=2, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2, embedding=1)
+
+
+@pytest.mark.parametrize("kw,message", [
+    (dict(form=5, overlap=-0.2), "equiangular embedding does not fit vocabulary 7, width 8, overlap -0.2"),
+    (dict(form=5, overlap=1.1), "equiangular embedding does not fit vocabulary 7, width 8, overlap 1.1"),
+    (dict(form=5, overlap=float("nan")), "embedding overlap must be finite; preserved features must fit width"),
+    (dict(form=5, overlap=0.0, width=6, heads=1), "equiangular embedding does not fit vocabulary 7, width 6, overlap 0"),
+    (dict(form=3, width=6, heads=1), "orthogonal embedding does not fit vocabulary 7, width 6, overlap 0"),
+    (dict(form=7, width=2, heads=1, vocab_size=9), "hypercube embedding does not fit vocabulary 9, width 2, overlap 0"),
+    (dict(form=8, vocab_size=257), "signed-permutations embedding does not fit vocabulary 257, width 8, overlap 0"),
+    (dict(harmonics=0), "embedding frequency must be positive and harmonics in 1..width/2"),
+    (dict(harmonics=5), "embedding frequency must be positive and harmonics in 1..width/2"),
+    (dict(frequency=0), "embedding frequency must be positive and harmonics in 1..width/2"),
+    (dict(preserve_features=9), "embedding overlap must be finite; preserved features must fit width"),
+    (dict(preserve_features=1, normalization=1),
+     "preserved coordinates require --embedding-norm none; full-vector normalization would rescale the "
+     "protected feature"),
+    (dict(order=1, modulus=4, vocab_size=6), "arithmetic embedding order requires a grok prime and vocabulary modulus+2"),
+    (dict(order=1, modulus=5, vocab_size=8), "arithmetic embedding order requires a grok prime and vocabulary modulus+2"),
+    (dict(order=2, modulus=5, form=1, width=4),
+     "arithmetic circle/Fourier codes need extra coordinates for special symbols"),
+    (dict(width=6, heads=2), "slice RoPE requires an even number of channels per head"),
+])
+def test_geometry_validation_messages_match_reference(kw, message):
+    # geometry.rs:84-151 and config.rs:160 on the product and the oracle
+    cfg = dict(GEOMETRY_BASE, **kw)
+    with pytest.raises(G.MeshGptError, match=re.escape(message)):
+        G.validate(G.GptConfig(**cfg))
+    assert O.validate(O.config(**cfg)) == message
+
+
+def test_rope_off_allows_odd_head_width_and_valid_geometries_pass():
+    for kw in (dict(width=6, heads=2, rope=0), dict(form=4, width=6, heads=1), dict(form=5, overlap=1.0),
+               dict(order=2, modulus=5, form=1, width=6, heads=3), dict(form=9), dict(preserve_features=8)):
+        cfg = dict(GEOMETRY_BASE, **kw)
+        G.validate(G.GptConfig(**cfg))
+        assert O.validate(O.config(**cfg)) is None
+
+
+GEOMETRY_CONFIGS = [
+    dict(form=1), dict(form=2, harmonics=3, width=12), dict(form=3), dict(form=4), dict(form=5, overlap=0.25),
+    dict(form=5, overlap=1.0), dict(form=6), dict(form=7), dict(form=8, vocab_size=200, width=8), dict(form=9),
+    dict(form=9, seed=123456789012345), dict(form=1, order=1, modulus=5, seed=17),
+    dict(form=2, order=2, modulus=5, seed=17, harmonics=2, width=12), dict(form=0, order=1, modulus=5, seed=3),
+    dict(form=0, order=2, modulus=5, seed=3), dict(preserve_features=3), dict(normalization=2),
+    dict(preserve_features=2, embedding=0), dict(form=3, embedding=0, normalization=1),
+]
+
+
+@pytest.mark.parametrize("kw", GEOMETRY_CONFIGS, ids=[str(i) for i in range(len(GEOMETRY_CONFIGS))])
+def test_geometry_codes_and_initial_parameters_bit_equal_oracle(kw):
+    # geometry.rs:186-325 codes and config.rs:416-459 initialisation (table
+    # rows = codes for geometric forms, protected rows zeroed) on both sides.
+    cfg = dict(GEOMETRY_BASE, **kw)
+    g, o = G.GptConfig(**cfg), O.config(**cfg)
+    assert np.array_equal(G.token_codes(g).view(np.uint32), O.token_codes(o).view(np.uint32))
+    for seed in (0, 7):
+        assert np.array_equal(G.initial_parameters(g, seed).view(np.uint32), O.initialize(o, seed).view(np.uint32))
 
 
 def test_long_context_extension_is_opt_in():
@@ -232,28 +295,55 @@ def test_ablation_checkpoints_use_mshgpt08(tmp_path):
             _read_bytes(tmp_path, default)
 
 
-def test_mshgpt09_default_geometry_rejected_and_ablations_unsupported(tmp_path):
-    # checkpoint.rs:146-168: a 09 file with default geometry and every operator
-    # on must use an older layout; one that changes them is a geometry ablation
-    # this build does not run (status MG_UNSUPPORTED).
+def test_mshgpt09_layout_switches_and_geometry(tmp_path):
+    # checkpoint.rs:61-78,146-168: a 09 file with default geometry and every
+    # operator on must use an older layout; ablations round-trip through 09
+    # with their fields at offsets 44..100; codes out of range are rejected.
     config = G.GptConfig(vocab_size=5)
     params = G.initial_parameters(config, 7)
     _, data = _save(tmp_path, "d.bin", config, "abcde", params)
     dims, rest = data[8:36], data[36:]
     # form, order, frequency, harmonics, overlap bits, normalization, frozen,
-    # preserve, modulus, seed lo, seed hi, rope, qk_norm, xsa -- defaults from
-    # src/gpt/geometry.rs:68-80 (Parity, Token, 1, 1, 0.0, None, false, 0, 0, 0)
+    # preserve, modulus, seed lo, seed hi -- defaults from src/gpt/geometry.rs:68-80
     geometry = [0, 0, 1, 1, 0, 0, 0, 0, 0, 0, 0]
     default09 = b"MSHGPT09" + dims + struct.pack("<2I", 0, 0) + struct.pack("<14I", *geometry, 1, 1, 1) + rest
     with pytest.raises(G.MeshGptError, match="default geometry must use an older checkpoint layout"):
         _read_bytes(tmp_path, default09)
     no_xsa = b"MSHGPT09" + dims + struct.pack("<2I", 0, 0) + struct.pack("<14I", *geometry, 1, 1, 0) + rest
-    with pytest.raises(G.MeshGptError) as info:
-        _read_bytes(tmp_path, no_xsa)
-    assert info.value.status == G.MG_UNSUPPORTED
-    bad_switch = b"MSHGPT09" + dims + struct.pack("<2I", 0, 0) + struct.pack("<14I", *geometry, 1, 1, 2) + rest
-    with pytest.raises(G.MeshGptError, match="invalid checkpoint switch"):
-        _read_bytes(tmp_path, bad_switch)
+    loaded = _read_bytes(tmp_path, no_xsa)
+    assert loaded.config.xsa == 0 and loaded.config.rope == 1 and loaded.config.qk_norm == 1
+    path, again = _save(tmp_path, "x.bin", loaded.config, "abcde", loaded.parameters)
+    assert again == no_xsa
+    for offset, code, message in ((100 - 12 + 8, 2, "invalid checkpoint switch"),
+                                  (44, 10, "unknown checkpoint EmbeddingForm: 10"),
+                                  (48, 3, "unknown checkpoint EmbeddingOrder: 3"),
+                                  (64, 3, "unknown checkpoint EmbeddingNorm: 3"),
+                                  (68, 2, "invalid checkpoint switch")):
+        bad = no_xsa[:offset] + struct.pack("<I", code) + no_xsa[offset + 4:]
+        with pytest.raises(G.MeshGptError, match=message):
+            _read_bytes(tmp_path, bad)
+    # A geometry ablation: circle codes in residue order of the mod-5 grok
+    # vocabulary, a table embedding, protected coordinates; the writer picks 09.
+    config = G.GptConfig(vocab_size=7, width=8, heads=2, embedding=1, form=1, order=1, modulus=5, seed=17,
+                         preserve_features=2, qk_norm=0)
+    params = G.initial_parameters(config, 3)
+    path, data = _save(tmp_path, "g.bin", config, "abcdefg", params)
+    assert data[:8] == b"MSHGPT09"
+    assert struct.unpack("<16I", data[36:100]) == (1, 0, 1, 1, 1, 1, 0, 0, 0, 2, 5, 17, 0, 1, 0, 1)
+    loaded = G.Checkpoint.load(path)
+    assert loaded.config == config and np.array_equal(loaded.parameters, params)
+    # Protected residual outputs must stay zero (config.rs:476-488), on save and load.
+    offsets = O.group_offsets(O.config(**{k: v for k, v in config.as_dict().items() if k != "long_context"}))
+    proj = offsets[1 + 3] + (config.attention_mesh_depth - 1) * 2 * config.width
+    assert params[proj] == 0.0
+    bad = params.copy()
+    bad[proj] = 0.5
+    with pytest.raises(G.MeshGptError, match="protected residual output weights must be zero"):
+        G.Checkpoint(config, "abcdefg", bad).save(str(tmp_path / "bad.bin"))
+    word = 100 + 7 * 4 + 4 * proj
+    corrupt = data[:word] + struct.pack("<f", 0.5) + data[word + 4:]
+    with pytest.raises(G.MeshGptError, match="protected residual output weights must be zero"):
+        _read_bytes(tmp_path, corrupt)
 
 
 # ---------------------------------------------------------------------- CLI

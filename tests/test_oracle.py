@@ -285,17 +285,28 @@ def _numpy_logits(c, params, tokens, sequence):
                     out[r, h * hd + i + half] = b * math.cos(ang) + a * math.sin(ang)
         return out
 
+    if c.normalization:
+        radius = math.sqrt(float(np.float32(math.sqrt(W)))) ** 2 if c.normalization == 2 else 1.0
+        E = E / np.maximum(np.linalg.norm(E, axis=1, keepdims=True), 1e-12) * radius
+    if c.preserve_features:
+        E[:, :c.preserve_features] = O.token_codes(c)[:, :c.preserve_features]
+
+    def qk(x, positions):
+        if c.qk_norm:
+            x = norm(x, H)
+        return rope(x, positions) if c.rope else x
+
     x = E[np.asarray(tokens)]
     positions = [i % sequence for i in range(len(tokens))]
     for b in range(L):
         g = offsets[1 + 5 * b:6 + 5 * b]
         n = norm(x, 1)
-        q = rope(norm(_numpy_mesh(n, params[g[0]:], A, W, bf), H), positions)
-        k = rope(norm(_numpy_mesh(n, params[g[1]:], A, W, bf), H), positions)
+        q = qk(_numpy_mesh(n, params[g[0]:], A, W, bf), positions)
+        k = qk(_numpy_mesh(n, params[g[1]:], A, W, bf), positions)
         v = _numpy_mesh(n, params[g[2]:], A, W, bf)
         y = _numpy_attention(q, k, v, H, sequence)
         z = y.copy()
-        for h in range(H):
+        for h in range(H if c.xsa else 0):
             sl = slice(h * hd, (h + 1) * hd)
             u = v[:, sl] / np.maximum(np.linalg.norm(v[:, sl], axis=1, keepdims=True), 1e-12)
             z[:, sl] = y[:, sl] - (y[:, sl] * u).sum(1, keepdims=True) * u
@@ -312,6 +323,189 @@ def test_whole_model_matches_independent_numpy_forward(emb, conn):
     x = np.arange(15) % 7
     got = O.logits(c, params, x, 5)
     assert np.allclose(got, _numpy_logits(c, params, x, 5), rtol=1e-10, atol=1e-10)
+
+
+@pytest.mark.parametrize("switches", [dict(rope=0), dict(qk_norm=0), dict(xsa=0), dict(rope=0, qk_norm=0, xsa=0),
+                                      dict(normalization=1), dict(normalization=2, embedding=1),
+                                      dict(preserve_features=3), dict(form=2, harmonics=2, rope=0)])
+def test_ablations_match_independent_numpy_forward(switches):
+    # The operator switches (reference.rs:174-199) and the embedding geometry
+    # transforms (reference.rs:130-149) against the numpy restatement.
+    c = O.config(vocab_size=7, context=5, width=8, heads=2, layers=2, attention_mesh_depth=3,
+                 ffn_mesh_depth=4, connectivity=1, **switches)
+    assert O.validate(c) is None
+    params = O.initialize(c, 7)
+    x = np.arange(15) % 7
+    assert np.allclose(O.logits(c, params, x, 5), _numpy_logits(c, params, x, 5), rtol=1e-10, atol=1e-10)
+
+
+def test_without_rope_attention_ignores_key_order():
+    # With RoPE off nothing depends on position, so in a one-block model the
+    # last row's logits are invariant to permuting the tokens before it (its
+    # attention takes the set of keys); with RoPE on they are not.
+    for rope in (0, 1):
+        c = O.config(vocab_size=11, context=8, width=16, heads=2, layers=1, attention_mesh_depth=3,
+                     ffn_mesh_depth=3, connectivity=1, rope=rope)
+        params = O.initialize(c, 5)
+        x = np.array([3, 1, 4, 1, 5, 9, 2, 6])
+        y = np.array([9, 5, 1, 4, 3, 1, 2, 6])
+        same = np.allclose(O.logits(c, params, x, 8)[-1], O.logits(c, params, y, 8)[-1], rtol=1e-12, atol=1e-12)
+        assert same == (rope == 0)
+
+
+def test_xsa_removes_the_whole_attention_output_of_a_single_token():
+    # A one-token sequence attends only to itself (y = v), so XSA's z = y -
+    # (y.u)u is zero and the block adds mesh(0) = 0: the logits equal those of
+    # the same weights with every projection mesh zeroed.  Without XSA they
+    # differ.
+    for xsa in (1, 0):
+        c = O.config(vocab_size=7, context=4, width=8, heads=2, layers=2, attention_mesh_depth=3,
+                     ffn_mesh_depth=3, connectivity=1, xsa=xsa)
+        params = O.initialize(c, 9)
+        zeroed = params.copy()
+        offsets = O.group_offsets(c)
+        for b in range(c.layers):
+            start = offsets[1 + 5 * b + 3]
+            zeroed[start:start + 2 * c.width * c.attention_mesh_depth] = 0.0
+        tokens = np.arange(7)
+        same = np.allclose(O.logits(c, params, tokens, 1), O.logits(c, zeroed, tokens, 1), rtol=1e-12, atol=1e-12)
+        assert same == (xsa == 1)
+
+
+# ---------------------------------------------------------------- geometry
+
+def _table(form, overlap=0.0, **kw):
+    """geometry.rs:330-346: V7 W8 H2 L2 A2 F2 table model with a geometric form."""
+    base = dict(vocab_size=7, width=8, heads=2, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2,
+                embedding=1, form=form, overlap=overlap)
+    base.update(kw)
+    return O.config(**base)
+
+
+FORMS = dict(parity=0, circle=1, fourier=2, orthogonal=3, simplex=4, equiangular=5, antipodal=6, hypercube=7,
+             signed_permutations=8, sphere=9)
+
+
+def test_initialized_tables_realize_the_expected_grams():
+    # geometry.rs:356-406: the initial table's effective embeddings have Gram
+    # matrix 1 on the diagonal and rho off it.
+    for form, rho in (("orthogonal", 0.0), ("simplex", -1.0 / 6.0), ("equiangular", 0.25),
+                      ("equiangular", -1.0 / 6.0), ("equiangular", 1.0)):
+        c = _table(FORMS[form], np.float32(rho))
+        assert O.validate(c) is None
+        E = O.token_embeddings(c, O.initialize(c, 7))
+        gram = E @ E.T
+        expected = np.where(np.eye(7, dtype=bool), 1.0, float(np.float32(rho)))
+        assert np.abs(gram - expected).max() < 3e-7, form
+    simplex = _table(FORMS["simplex"], width=6, heads=1)
+    assert O.validate(simplex) is None
+    assert O.validate(_table(FORMS["equiangular"], 0.0, width=6, heads=1)) is not None
+    assert O.validate(_table(FORMS["orthogonal"], width=6, heads=1)) is not None
+    for rho in (-0.2, 1.1, float("nan")):
+        assert O.validate(_table(FORMS["equiangular"], rho)) is not None
+
+
+def _order(modulus, seed, order, V):
+    """Token at each position of an arithmetic order (geometry.rs:186-211): the
+    residue permutation, or its entries at successive powers of the smallest
+    primitive root, then zero (discrete log), the operation and '='."""
+    ids = np.zeros(modulus, dtype=np.uint32)
+    O.lib().og_residue_permutation(modulus, seed, O.ptr(ids, O._u32p))
+    if order == 1:
+        seq = [int(t) for t in ids]
+    else:
+        root = next(g for g in range(2, modulus) if len({pow(g, k, modulus) for k in range(modulus - 1)}) == modulus - 1)
+        assert O.lib().og_primitive_root(modulus) == root
+        seq = [int(ids[pow(root, k, modulus)]) for k in range(modulus - 1)]
+    cycle = len(seq)
+    if order == 2:
+        seq.append(int(ids[0]))
+    return seq + [modulus, modulus + 1], cycle, ids
+
+
+def test_circle_and_fourier_grams_follow_cosine_identities_in_the_declared_order():
+    # geometry.rs:408-460: the Gram of positions i, j is the mean over the
+    # harmonics k of cos(2 pi (k+1)(i-j)/cycle); the special tokens are unit
+    # vectors orthogonal to the first; the residue order is the grok dataset's.
+    for order in (0, 1, 2):
+        for form in (FORMS["circle"], FORMS["fourier"]):
+            kw = dict(width=12, heads=2, harmonics=3)
+            if order:
+                kw.update(order=order, modulus=5, seed=17)
+            c = _table(form, **kw)
+            assert O.validate(c) is None, O.validate(c)
+            codes = O.token_codes(c).astype(np.float64)
+            if order == 0:
+                ids, cycle = list(range(7)), 7
+            else:
+                ids, cycle, perm = _order(5, 17, order, 7)
+                residues, _, _ = O.equations(modulus=5, seed=17)
+                assert np.array_equal(perm, residues)
+            pairs = 3 if form == FORMS["fourier"] else 1
+            for i in range(cycle):
+                for j in range(cycle):
+                    want = np.mean([math.cos(2 * math.pi * (k + 1) * (i - j) / cycle) for k in range(pairs)])
+                    assert abs(codes[ids[i]] @ codes[ids[j]] - want) < 2e-7
+            for t in ids[cycle:]:
+                assert codes[t] @ codes[t] == 1.0 and codes[t] @ codes[ids[0]] == 0.0
+
+
+def test_integer_signed_codes_are_distinct_and_have_squared_norm_thirty():
+    # geometry.rs:462-476
+    c = _table(FORMS["signed_permutations"], vocab_size=256)
+    codes = O.token_codes(c)
+    assert list(codes[0][:4]) == [1.0, 2.0, 3.0, 4.0]
+    assert list(codes[1][:4]) == [-1.0, 2.0, 3.0, 4.0]
+    assert np.all((codes.astype(np.float64) ** 2).sum(1) == 30.0)
+    assert len({row.tobytes() for row in codes}) == 256
+
+
+def test_hypercube_and_sphere_codes_are_unit_vectors():
+    # geometry.rs:587-592
+    for form in ("hypercube", "sphere"):
+        codes = O.token_codes(_table(FORMS[form])).astype(np.float64)
+        assert np.abs((codes ** 2).sum(1) - 1.0).max() < 2e-7
+
+
+def test_protected_coordinates_survive_arbitrary_embedding_weights():
+    # geometry.rs:478-512: with the embedding weights zeroed, the residual
+    # stream's first 3 coordinates are still each token's code, and the
+    # protected projection/FFN output rows start at zero.
+    for emb in (0, 1):
+        c = _table(FORMS["parity"], embedding=emb, preserve_features=3)
+        params = O.initialize(c, 7)
+        offsets = O.group_offsets(c)
+        for b in range(c.layers):
+            for g, depth in ((3, c.attention_mesh_depth), (4, c.ffn_mesh_depth)):
+                start = offsets[1 + 5 * b + g] + (depth - 1) * 2 * c.width
+                assert np.all(params[start:start + 6] == 0.0)
+        params[:O.lib().og_embedding_parameter_count(c)] = 0.0
+        codes = O.token_codes(c)
+        x = np.array([0, 1, 2, 3, 4, 5, 6, 0])
+        hidden = O.hidden_states(c, params, x, 4)
+        for state, token in zip(hidden, x):
+            assert np.array_equal(state[:3].astype(np.float32), codes[token][:3])
+
+
+def test_normalized_embeddings_have_the_declared_radius():
+    # geometry.rs:514-564 (the forward half): every effective token vector has
+    # squared length radius^2 (1, or W for rms).
+    for emb in (0, 1):
+        for norm in (1, 2):
+            c = _table(FORMS["parity"], embedding=emb, normalization=norm)
+            E = O.token_embeddings(c, O.initialize(c, 7))
+            radius2 = 1.0 if norm == 1 else float(np.float32(math.sqrt(8))) ** 2
+            assert np.abs((E ** 2).sum(1) - radius2).max() < 1e-6
+
+
+def test_all_forms_support_both_parameterizations_and_operator_switches():
+    # geometry.rs:566-606 (the forward half): every form, mesh or table, with
+    # every operator off, gives finite logits.
+    for form in FORMS.values():
+        for emb in (0, 1):
+            c = _table(form, 0.25, embedding=emb, rope=0, qk_norm=0, xsa=0)
+            assert O.validate(c) is None
+            assert np.all(np.isfinite(O.logits(c, O.initialize(c, 7), [0, 1, 2, 3], 4)))
 
 
 def test_zero_embedding_gives_zero_logits():
