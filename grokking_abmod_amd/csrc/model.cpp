@@ -103,6 +103,7 @@ struct MeshGpt::Impl {
     hipGraphExec_t exec[2] = {nullptr, nullptr};
     size_t graph_batch = 0;
     float graph_temperature = -1.0f;
+    int graph_slices = 0;
     bool use_graph = true;
     // Decode blocks run on the row-order kernel when the shape allows it, else
     // on the one-wave-per-mesh kernel, else on the general block kernel
@@ -121,10 +122,22 @@ struct MeshGpt::Impl {
     hipEvent_t call_ev[2] = {nullptr, nullptr};
     float call_ms = 0.0f;
 
+    // Per-phase decode of a large batch runs as independent slices of the
+    // batch on the model's stream and kMaxSlices - 1 more (default priority),
+    // forked from and joined to the model's stream once per graph replay.
+    static constexpr int kMaxSlices = 4;
+    hipStream_t slice_stream[kMaxSlices - 1] = {};
+    hipEvent_t fork_ev = nullptr, join_ev[kMaxSlices - 1] = {};
+
     ~Impl() {
         drop_graph();
         for (hipEvent_t e : call_ev)
             if (e) (void)hipEventDestroy(e);
+        for (int i = 0; i < kMaxSlices - 1; ++i) {
+            if (join_ev[i]) (void)hipEventDestroy(join_ev[i]);
+            if (slice_stream[i]) (void)hipStreamDestroy(slice_stream[i]);
+        }
+        if (fork_ev) (void)hipEventDestroy(fork_ev);
         if (stream) (void)hipStreamDestroy(stream);
     }
 
@@ -329,8 +342,12 @@ struct MeshGpt::Impl {
             dx2.ensure(batch_cap * cfg.width * 4);
             dxn.ensure(batch_cap * cfg.width * 4);
             dq.ensure(batch_cap * cfg.width * 4);
+            // Partial states of the decode attention: for a batch of k, or k in
+            // up to kMaxSlices slices (each at least k / kMaxSlices sequences,
+            // and the split count never grows with the batch).
             size_t slots = 0;
-            for (size_t k = 1; k <= batch_cap; ++k) slots = std::max(slots, k * size_t(splits_for(k)));
+            for (size_t k = 1; k <= batch_cap; ++k)
+                slots = std::max(slots, k * size_t(splits_for(std::max<size_t>(1, k / kMaxSlices))));
             part.ensure(slots * cfg.heads * (shape.hdp + 2) * 4);
             dlen.ensure(batch_cap * 4);
             drng.ensure(batch_cap * 8);
@@ -374,8 +391,11 @@ struct MeshGpt::Impl {
     // `events`, each decode-attention launch stamps its own begin and end into
     // events[2l] and events[2l+1].
     template <class KvOf>
+    // `part_base` is the decode attention's partial-state buffer (default: the
+    // start of `part`).
     void run_blocks(const kern::Rows &rows, int nseq, KvOf kv_of, float *x, float *x2, float *q, float *y,
-                    float *xn, bool decode, hipEvent_t *events = nullptr) {
+                    float *xn, bool decode, hipEvent_t *events = nullptr, float *part_base = nullptr) {
+        if (!part_base) part_base = part.as<float>();
         const int nsplit = decode ? splits_for(size_t(rows.rows)) : 0;
         // Prefill attention on the matrix cores (XSA in its epilogue) where the
         // shape allows it (MG_DISABLE_MFMA_PREFILL=1 keeps the VALU kernel).
@@ -407,7 +427,7 @@ struct MeshGpt::Impl {
                 const Block &prev = layout.blocks[l - 1];
                 a.wproj = weights(prev.projection);
                 a.wffn = weights(prev.ffn);
-                a.part = decode ? part.as<float>() : nullptr;
+                a.part = decode ? part_base : nullptr;
                 a.nsplit = nsplit;
                 a.ybuf = decode ? nullptr : y;
                 a.xsa_post = cfg.xsa && (decode || !(mfma_prefill || short_prefill)) ? 1 : 0;
@@ -439,7 +459,7 @@ struct MeshGpt::Impl {
                 kern::block(a, staged(t, a.wproj != nullptr, a.wq != nullptr), stream);
             if (l == L) break;
             if (decode) {
-                kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part.as<float>(), stream,
+                kern::attn_decode(shape, q, kv_of(l), rows.len, rows.rows, nsplit, part_base, stream,
                                   events ? events[2 * l] : nullptr, events ? events[2 * l + 1] : nullptr);
             } else if (mfma_prefill) {
                 kern::attn_prefill_mfma(shape, q, kv_of(l), nseq, rows.rows_per_seq, y, cfg.xsa, stream);
@@ -539,6 +559,74 @@ struct MeshGpt::Impl {
                      dtokens.as<uint32_t>(), int(tcap), dlen.as<int>(), dflags.as<int>(), stream);
     }
 
+    // Slices of the per-phase decode.  Each sequence's decode is independent
+    // of the others' (rows, cache slabs, generator states and tokens are per
+    // sequence), so the batch splits into slices that run on their own
+    // streams: while one slice's attention streams its keys (memory-bound),
+    // another's row blocks run (latency-bound).  Config 5 (batch 256):
+    // 1231 us per step in one stream, 1072 in two slices, 1062 in four.
+    // Slices need at least 32 sequences each and the fused head-and-sampler
+    // kernel.  MG_DECODE_SLICES overrides the count (1 = one stream).
+    int decode_slices() const {
+        const int want = std::min(env_int("MG_DECODE_SLICES", 2), kMaxSlices);
+        if (kern::head_sample_lds_bytes(shape) > lds_limit) return 1;
+        for (int n = want; n > 1; --n)
+            if (batch >= size_t(32 * n)) return n;
+        return 1;
+    }
+
+    // One decode step of sequences [b0, b0 + nb) on `stream`; the slice's
+    // attention partial states start at slot `slot0` of `part`.
+    void launch_slice_step(size_t b0, size_t nb, size_t slot0) {
+        const size_t W = cfg.width;
+        const kern::Rows rows{int(nb), 1, dlen.as<int>() + b0, dtokens.as<uint32_t>() + b0 * tcap, int(tcap), 0};
+        const size_t kv_off = b0 * size_t(shape.H) * cfg.context * size_t(shape.hdp);
+        run_blocks(rows, int(nb),
+                   [&](size_t l) {
+                       kern::KvView kv = cache_layer(l);
+                       kv.k += kv_off;
+                       kv.v += kv_off;
+                       return kv;
+                   },
+                   dx.as<float>() + b0 * W, dx2.as<float>() + b0 * W, dq.as<float>() + b0 * W, nullptr,
+                   dxn.as<float>() + b0 * W, true, nullptr,
+                   part.as<float>() + slot0 * size_t(shape.H) * (shape.hdp + 2));
+        kern::head_sample(shape, dxn.as<float>() + b0 * W, int(nb), Et.as<float>(), vpad,
+                          dlogits.as<float>() + b0 * shape.V, temperature, drng.as<uint64_t>() + b0,
+                          dtokens.as<uint32_t>() + b0 * tcap, int(tcap), dlen.as<int>() + b0, dflags.as<int>(),
+                          stream);
+    }
+
+    // `n` decode steps of every slice, each slice on its own stream.
+    void enqueue_slices(size_t n, int slices) {
+        if (!fork_ev) {
+            for (int i = 0; i < kMaxSlices - 1; ++i) {
+                check(hipStreamCreateWithFlags(&slice_stream[i], hipStreamNonBlocking), "hipStreamCreate");
+                check(hipEventCreateWithFlags(&join_ev[i], hipEventDisableTiming), "hipEventCreate");
+            }
+            check(hipEventCreateWithFlags(&fork_ev, hipEventDisableTiming), "hipEventCreate");
+        }
+        check(hipEventRecord(fork_ev, stream), "hipEventRecord");
+        for (int i = 0; i + 1 < slices; ++i)
+            check(hipStreamWaitEvent(slice_stream[i], fork_ev, 0), "hipStreamWaitEvent");
+        const hipStream_t own = stream;
+        try {
+            size_t slot0 = 0;
+            for (int p = 0; p < slices; ++p) {
+                const size_t b0 = batch * p / slices, nb = batch * (p + 1) / slices - b0;
+                stream = p == 0 ? own : slice_stream[p - 1];
+                for (size_t i = 0; i < n; ++i) launch_slice_step(b0, nb, slot0);
+                slot0 += nb * size_t(splits_for(nb));
+                if (p > 0) check(hipEventRecord(join_ev[p - 1], stream), "hipEventRecord");
+            }
+        } catch (...) {
+            stream = own;
+            throw;
+        }
+        stream = own;
+        for (int i = 0; i + 1 < slices; ++i) check(hipStreamWaitEvent(stream, join_ev[i], 0), "hipStreamWaitEvent");
+    }
+
     void launch_decode_step(hipEvent_t *events = nullptr) {
         const kern::Rows rows{int(batch), 1, dlen.as<int>(), dtokens.as<uint32_t>(), int(tcap), 0};
         run_blocks(rows, int(batch), [&](size_t l) { return cache_layer(l); }, dx.as<float>(), dx2.as<float>(),
@@ -549,19 +637,27 @@ struct MeshGpt::Impl {
     // `n` decode steps (1 or kGraphSteps) as one graph replay; the graphs are
     // captured on first use for the current batch and temperature.
     void decode_steps(size_t n) {
+        const int slices = decode_slices();
+        auto enqueue = [&] {
+            if (slices > 1)
+                enqueue_slices(n, slices);
+            else
+                for (size_t i = 0; i < n; ++i) launch_decode_step();
+        };
         if (!use_graph) {
-            for (size_t i = 0; i < n; ++i) launch_decode_step();
+            enqueue();
             return;
         }
-        if (graph_batch != batch || graph_temperature != temperature) drop_graph();
+        if (graph_batch != batch || graph_temperature != temperature || graph_slices != slices) drop_graph();
         const int g = n == 1 ? 0 : 1;
         if (!exec[g]) {
             check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "begin capture");
-            for (size_t i = 0; i < n; ++i) launch_decode_step();
+            enqueue();
             check(hipStreamEndCapture(stream, &graph[g]), "end capture");
             check(hipGraphInstantiate(&exec[g], graph[g], nullptr, nullptr, 0), "instantiate graph");
             graph_batch = batch;
             graph_temperature = temperature;
+            graph_slices = slices;
         }
         check(hipGraphLaunch(exec[g], stream), "graph launch");
     }

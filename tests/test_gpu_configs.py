@@ -211,22 +211,70 @@ def test_config4_shape_against_oracle():
 def test_config5_high_batch_full_size():
     # Config 5: batch 256, W1024 L12 H16x64, context 2048 (a 48 GiB KV cache),
     # 128-token prompts, 16 greedy steps on the per-phase kernels (4864
-    # workgroups exceed co-residency, so no persistent launch).  Two
-    # sequences against the oracle; all 256 against a device re-prefill.
+    # workgroups exceed co-residency, so no persistent launch), in two slices
+    # of 128 sequences on two streams.  One sequence of each slice against
+    # the oracle; all 256 against a device re-prefill.
     config = G.named_config("high")
     o = oracle_config(config)
     params = O.initialize(o, 7)
     prompts = G.random_prompts(256, 256, 128, 7)
-    expected = parallel(lambda b: O.generate(o, params, prompts[b], 16, 0.0, 7 + b, cached=True), range(2))
+    checked = (0, 200)
+    expected = parallel(lambda b: O.generate(o, params, prompts[b], 16, 0.0, 7 + b, cached=True), checked)
     with G.MeshGpt(0, config, 7, max_batch=256) as model:
         got = model.generate_tokens(prompts, 16, 0.0, 7)
         last = model.last_logits(256)
         assert_close(last, reprefill_last(model, got[:, :-1]), what="config-5 decode vs re-prefill")
-        refs = parallel(lambda b: O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], range(2))
-        for b in range(2):
-            assert_close(last[b], refs[b], what=f"config-5 logits, sequence {b}")
+        refs = parallel(lambda b: O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], checked)
+        for i, b in enumerate(checked):
+            assert_close(last[b], refs[i], what=f"config-5 logits, sequence {b}")
             check_trajectory(o, params, prompts[b], got[b], 0.0, 7 + b, last_row_logits(model),
-                             expected=expected[b])
+                             expected=expected[i])
+
+
+@pytest.mark.parametrize("temperature,graph", [(0.0, True), (1.0, True), (1.0, False)])
+def test_decode_slices_match_one_stream(temperature, graph, monkeypatch):
+    # The per-phase decode of a large batch runs as slices of the batch on
+    # their own streams (sequences are independent: rows, cache slabs,
+    # generator states and tokens are per sequence).  With the attention
+    # split count fixed, each sequence's arithmetic is that of one stream, so
+    # tokens and final logits must be bit-identical for 1, 2 and 3 slices of
+    # the 96 sequences, over three 8-step graph replays or, without graphs,
+    # 24 single steps.
+    config = G.named_config("mid")
+    monkeypatch.setenv("MG_DISABLE_PERSISTENT", "1")
+    monkeypatch.setenv("MG_DISABLE_GRAPH", "0" if graph else "1")
+    monkeypatch.setenv("MG_DECODE_SPLITS", "2")
+    prompts = G.random_prompts(256, 96, 16, 7)
+    results = {}
+    for slices in ("1", "2", "3"):
+        monkeypatch.setenv("MG_DECODE_SLICES", slices)
+        with G.MeshGpt(0, config, 7, max_batch=96) as model:
+            tokens = model.generate_tokens(prompts, 24, temperature, 7)
+            results[slices] = (tokens, model.last_logits(96))
+    for slices in ("2", "3"):
+        assert np.array_equal(results[slices][0], results["1"][0]), f"{slices} slices: tokens differ"
+        assert np.array_equal(results[slices][1], results["1"][1]), f"{slices} slices: logits differ"
+
+
+def test_decode_slices_with_their_own_split_counts(monkeypatch):
+    # 97 sequences in three slices of 32, 32 and 33: the first two split each
+    # head's keys in two, the third and the whole batch do not, so the
+    # slices' attention partial states sit at uneven offsets.  Greedy tokens
+    # against one stream (up to near-ties) and final logits within TOL.
+    config = G.named_config("mid")
+    monkeypatch.setenv("MG_DISABLE_PERSISTENT", "1")
+    prompts = G.random_prompts(256, 97, 16, 7)
+    monkeypatch.setenv("MG_DECODE_SLICES", "1")
+    with G.MeshGpt(0, config, 7, max_batch=97) as model:
+        one = model.generate_tokens(prompts, 24, 0.0, 7)
+        one_logits = model.last_logits(97)
+    monkeypatch.setenv("MG_DECODE_SLICES", "3")
+    with G.MeshGpt(0, config, 7, max_batch=97) as model:
+        three = model.generate_tokens(prompts, 24, 0.0, 7)
+        compared = assert_same_tokens_or_near_tie(model, three, one, "three slices")
+        assert compared > 0.99 * three.size
+        if np.array_equal(three, one):
+            assert_close(model.last_logits(97), one_logits, what="three slices: final logits")
 
 
 def test_cli_init_then_generate_matches_oracle(tmp_path):
