@@ -20,6 +20,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <cstdlib>
 #include <cmath>
 #include <type_traits>
 #include <utility>
@@ -1430,6 +1431,312 @@ row_block_kernel(BlockArgs a) {
             a.q[size_t(row) * W + c.chan(j)] = x[j];
         else
             a.kv_pre.k[(cache_row + size_t(c.head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[j];
+    }
+}
+
+// ---- Several decode rows per workgroup
+//
+// row_block_kernel's block for RB rows at once, for batches whose three
+// workgroups per row would not fit the GPU in one wave of workgroups: every
+// lane holds the same channels of RB rows, so each mesh weight in its
+// registers serves RB rows, the rows' independent chains overlap in every
+// wave, and a layer whose partner channel is in another wave exchanges all RB
+// rows around one barrier.  Fixed-depth butterfly meshes only.
+
+template <int NW, int CPL, int RB>
+__device__ __forceinline__ void rows_partner(const float (&x)[RB][CPL], float (&p)[RB][CPL], int st, int lane,
+                                             int wave, float *xch, int &parity) {
+    constexpr int W = 64 * NW * CPL;
+    if (st < NW) {
+        float *b = xch + (parity & 1) * (RB * W);
+        ++parity;
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) b[r * W + (j * NW + wave) * 64 + lane] = x[r][j];
+        __syncthreads();
+        int w2 = wave + st, l2 = lane, jc = 0;
+        if (w2 >= NW) {
+            w2 -= NW;
+            ++l2;
+        }
+        if (l2 >= 64) {
+            l2 -= 64;
+            jc = 1;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int j2 = j + jc < CPL ? j + jc : 0;
+                p[r][j] = b[r * W + (j2 * NW + w2) * 64 + l2];
+            }
+    } else {
+        // In-wave partners (row_partner touches no LDS for these strides).
+#pragma unroll
+        for (int r = 0; r < RB; ++r) row_partner<NW, CPL>(x[r], p[r], st, lane, wave, xch, parity);
+    }
+}
+
+template <int NW, int CPL, int D, int RB>
+__device__ __forceinline__ void rows_mesh_fixed(float (&x)[RB][CPL], const float2 (&w)[D][CPL], int lane, int wave,
+                                                float *xch, int &parity) {
+    constexpr int W = 64 * NW * CPL;
+    constexpr int LOG2W = W == 128 ? 7 : W == 256 ? 8 : W == 512 ? 9 : 10;
+    static_for<D>([&](auto U) {
+        constexpr int u = decltype(U)::value;
+        float p[RB][CPL];
+        rows_partner<NW, CPL, RB>(x, p, 1 << (u % LOG2W), lane, wave, xch, parity);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const float z = x[r][j] * w[u][j].x + p[r][j] * w[u][j].y;
+                x[r][j] = u + 1 == D ? z : elu(z);
+            }
+    });
+}
+
+// LDS of the multi-row block: the exchange buffers of rows_partner and
+// reduction slots of RB * SLOT floats.
+template <int NW, int CPL, int GL, int RB>
+struct RowsCtx {
+    static constexpr int W = 64 * NW * CPL, G = 64 / GL, SLOT = CPL * NW * G;
+    int lane, wave, parity;
+    float *xch, *red;
+    __device__ RowsCtx(float *x, float *r) : lane(int(threadIdx.x) & 63), wave(int(threadIdx.x) >> 6), parity(0),
+                                             xch(x), red(r) {}
+    __device__ int head_of(int j) const { return lane / GL + G * j; }
+    __device__ int dim() const { return NW * (lane % GL) + wave; }
+    __device__ int ridx(int j) const { return (j * NW + wave) * 64 + lane; }
+    __device__ int chan(int j) const { return wave + NW * (lane + 64 * j); }
+    __device__ float *slot(int k) const { return red + k * RB * SLOT; }
+};
+
+// inv[r] = 1/sqrt(mean(x_r^2) + eps) for every row (row_inv_rms's order).
+template <int NW, int CPL, int GL, int RB>
+__device__ __forceinline__ void rows_inv_rms(const RowsCtx<NW, CPL, GL, RB> &c, const float (&x)[RB][CPL], int k,
+                                             float (&inv)[RB]) {
+    float *red = c.slot(k);
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc = fmaf(x[r][j], x[r][j], acc);
+        acc = wave_sum(acc);
+        if (c.lane == 0) red[r * NW + c.wave] = acc;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        float t = 0.0f;
+#pragma unroll
+        for (int w = 0; w < NW; ++w) t += red[r * NW + w];
+        inv[r] = rsqrtf(t * (1.0f / float(c.W)) + kRmsEps);
+    }
+}
+
+// Per-head sums of every row (row_head_sums's order).
+template <int NW, int CPL, int GL, int RB>
+__device__ __forceinline__ void rows_head_sums(const RowsCtx<NW, CPL, GL, RB> &c, const float (&v)[RB][CPL],
+                                               float (&out)[RB][CPL], int k) {
+    constexpr int G = 64 / GL, SLOT = RowsCtx<NW, CPL, GL, RB>::SLOT;
+    float *red = c.slot(k);
+    float t[RB][CPL];
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) t[r][j] = group_sum<GL>(v[r][j]);
+    if (c.lane % GL == 0) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) red[r * SLOT + (j * NW + c.wave) * G + c.lane / GL] = t[r][j];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            float a = 0.0f;
+#pragma unroll
+            for (int w = 0; w < NW; ++w) a += red[r * SLOT + (j * NW + w) * G + c.lane / GL];
+            out[r][j] = a;
+        }
+}
+
+template <int NW, int CPL, int GL, int DEPTH, int RB>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(1, 1)))
+row_block_rows_kernel(BlockArgs a) {
+    using Ctx = RowsCtx<NW, CPL, GL, RB>;
+    constexpr int W = Ctx::W, D = DEPTH;
+    static_assert(DEPTH > 0 && NW > 1, "fixed-depth meshes over several waves");
+    __shared__ float xch[2 * RB * W];
+    __shared__ float red[8 * RB * Ctx::SLOT];
+    Ctx c(xch, red);
+    const Shape &s = a.s;
+    const bool pre = a.wq != nullptr, post = a.wproj != nullptr;
+    const int teams = pre ? 3 : 1;
+    const int group = int(blockIdx.x) / teams, team = int(blockIdx.x) - group * teams;
+    const int dim = c.dim();
+    // Rows past the batch repeat its last row and write nothing.
+    int row[RB], seq[RB], pos[RB];
+    bool valid[RB];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        valid[r] = group * RB + r < a.ro.rows;
+        row[r] = min(group * RB + r, a.ro.rows - 1);
+        row_position(a.ro, row[r], seq[r], pos[r]);
+    }
+
+    float x[RB][CPL];
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        if (a.embed) {
+            const uint32_t tok = a.ro.tokens[size_t(seq[r]) * a.ro.tok_stride + a.ro.tok_offset + pos[r]];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[r][j] = a.E[size_t(tok) * W + c.ridx(j)];
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[r][j] = a.x[size_t(row[r]) * W + c.ridx(j)];
+        }
+    }
+    const float *wmine = pre ? (team == 0 ? a.wq : team == 1 ? a.wk : a.wv) : nullptr;
+    float2 wp[D][CPL], wf[D][CPL], wm[D][CPL];
+    if (post) {
+        row_load_weights<NW, CPL, D>(wp, a.wproj, c.lane, c.wave);
+        row_load_weights<NW, CPL, D>(wf, a.wffn, c.lane, c.wave);
+    }
+    if (pre) row_load_weights<NW, CPL, D>(wm, wmine, c.lane, c.wave);
+
+    if (post) {
+        // Post-attention half of the block (row_post): XSA, projection mesh,
+        // residual, RMSNorm, FFN mesh, residual.
+        float y[RB][CPL], v[RB][CPL];
+        const int stride = s.hdp + 2;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const float *part0 = a.part + size_t(seq[r] * s.H) * a.nsplit * stride;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                v[r][j] = a.kv_post.v[(size_t(seq[r] * s.H + c.head_of(j)) * a.kv_post.cap + pos[r]) * s.hdp + dim];
+                const float *pp = part0 + size_t(c.head_of(j)) * a.nsplit * stride;
+                y[r][j] = a.nsplit <= 2 ? merge_splits<2>(pp, a.nsplit, stride, s.hdp, dim)
+                                        : merge_splits<8>(pp, a.nsplit, stride, s.hdp, dim);
+            }
+        }
+        {
+            float t[RB][CPL], vv[RB][CPL], yv[RB][CPL];
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) t[r][j] = v[r][j] * v[r][j];
+            rows_head_sums(c, t, vv, 0);
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) t[r][j] = y[r][j] * v[r][j];
+            rows_head_sums(c, t, yv, 1);
+#pragma unroll
+            for (int r = 0; r < RB; ++r)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const float iv = rsqrtf(fmaxf(vv[r][j], kXsaFloor));
+                    y[r][j] = y[r][j] - (yv[r][j] * iv) * (v[r][j] * iv);
+                }
+        }
+        rows_mesh_fixed<NW, CPL, D, RB>(y, wp, c.lane, c.wave, c.xch, c.parity);
+        float inv[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[r][j] += y[r][j];
+        rows_inv_rms(c, x, 2, inv);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) y[r][j] = x[r][j] * inv[r];
+        rows_mesh_fixed<NW, CPL, D, RB>(y, wf, c.lane, c.wave, c.xch, c.parity);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[r][j] += y[r][j];
+    }
+    if (team == 0 && (post || a.embed)) {
+        // Into x_out, never x: the rows' other workgroups may not have read x yet.
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+            if (valid[r])
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) a.x_out[size_t(row[r]) * W + c.ridx(j)] = x[r][j];
+    }
+    if (!a.xn && !pre) return;
+
+    // The next RMSNorm: the final one for the head, or the block's pre-norm.
+    {
+        float inv[RB];
+        rows_inv_rms(c, x, 3, inv);
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[r][j] *= inv[r];
+    }
+    if (a.xn) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+            if (valid[r])
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) a.xn[size_t(row[r]) * W + c.chan(j)] = x[r][j];
+    }
+    if (!pre) return;
+
+    rows_mesh_fixed<NW, CPL, D, RB>(x, wm, c.lane, c.wave, c.xch, c.parity);
+    if (team == 2) {
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+            if (valid[r]) {
+                const size_t cache_row = size_t(seq[r] * s.H) * a.kv_pre.cap + pos[r];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j)
+                    a.kv_pre.v[(cache_row + size_t(c.head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[r][j];
+            }
+        return;
+    }
+    // QK-Norm per head, then RoPE at each row's position (row_qk_rope).
+    {
+        float sq[RB][CPL], ss[RB][CPL];
+#pragma unroll
+        for (int r = 0; r < RB; ++r)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) sq[r][j] = x[r][j] * x[r][j];
+        rows_head_sums(c, sq, ss, 4);
+        const float scale = 1.0f / float(s.hd);
+        const bool low = dim < s.half;
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const float2 cs = rope_pair(a.rope, pos[r], dim, s.half);
+            float other[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) other[j] = __shfl_xor(x[r][j], GL / 2, 64);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const float sc = rsqrtf(ss[r][j] * scale + kRmsEps);
+                const float self = x[r][j] * sc, oth = other[j] * sc;
+                x[r][j] = low ? self * cs.x - oth * cs.y : self * cs.x + oth * cs.y;
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RB; ++r) {
+        if (!valid[r]) continue;
+        const size_t cache_row = size_t(seq[r] * s.H) * a.kv_pre.cap + pos[r];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            if (team == 0)
+                a.q[size_t(row[r]) * W + c.chan(j)] = x[r][j];
+            else
+                a.kv_pre.k[(cache_row + size_t(c.head_of(j)) * a.kv_pre.cap) * s.hdp + dim] = x[r][j];
+        }
     }
 }
 
@@ -3721,8 +4028,55 @@ void launch_row_block(const BlockArgs &a, dim3 grid, hipStream_t stream) {
     }
 }
 
+// Rows per workgroup of the fixed-depth row blocks: one, or more when the
+// batch's workgroups (three per row with the Q/K/V meshes) would take more
+// than one wave of one workgroup per CU (the kernels hold every mesh weight
+// in registers, so one fits a CU).  MG_ROW_BATCH forces 1, 2 or 4.
+int row_batch(int rows, int teams) {
+    static int cus = 0;
+    if (!cus) {
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess ||
+            hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0)
+            cus = 256;
+    }
+    const char *e = std::getenv("MG_ROW_BATCH");
+    if (e && *e) {
+        const int f = std::atoi(e);
+        if (f == 1 || f == 2 || f == 4) return f;
+    }
+    for (int rb : {1, 2})
+        if (teams * ((rows + rb - 1) / rb) <= cus) return rb;
+    return 4;
+}
+
+template <int NW, int CPL, int GL, int DEPTH>
+void launch_row_block_rows(const BlockArgs &a, int teams, hipStream_t stream) {
+    const int rb = row_batch(a.ro.rows, teams);
+    const dim3 threads(64 * NW);
+    const unsigned groups = unsigned((a.ro.rows + rb - 1) / rb);
+    switch (rb) {
+    case 1: hipLaunchKernelGGL((row_block_kernel<NW, CPL, GL, DEPTH>), dim3(a.ro.rows * teams), threads, 0, stream, a); break;
+    case 2: hipLaunchKernelGGL((row_block_rows_kernel<NW, CPL, GL, DEPTH, 2>), dim3(groups * teams), threads, 0, stream, a); break;
+    default: hipLaunchKernelGGL((row_block_rows_kernel<NW, CPL, GL, DEPTH, 4>), dim3(groups * teams), threads, 0, stream, a); break;
+    }
+}
+
 void row_block(const BlockArgs &a, hipStream_t stream) {
-    const dim3 grid(a.ro.rows * (a.wq != nullptr ? 3 : 1));
+    const int teams = a.wq != nullptr ? 3 : 1;
+    const Shape &s = a.s;
+    const bool fixed = s.butterfly && s.A == s.F && s.hd == 64;
+    if (fixed && s.W == 512 && s.A == 9) {
+        launch_row_block_rows<4, 2, 16, 9>(a, teams, stream);
+        HIP_LAUNCH_CHECK();
+        return;
+    }
+    if (fixed && s.W == 1024 && s.A == 10) {
+        launch_row_block_rows<4, 4, 16, 10>(a, teams, stream);
+        HIP_LAUNCH_CHECK();
+        return;
+    }
+    const dim3 grid(a.ro.rows * teams);
     switch (a.s.W) {
     case 128: launch_row_block<2, 1>(a, grid, stream); break;
     case 256: launch_row_block<4, 1>(a, grid, stream); break;

@@ -244,6 +244,7 @@ def test_decode_slices_match_one_stream(temperature, graph, monkeypatch):
     monkeypatch.setenv("MG_DISABLE_PERSISTENT", "1")
     monkeypatch.setenv("MG_DISABLE_GRAPH", "0" if graph else "1")
     monkeypatch.setenv("MG_DECODE_SPLITS", "2")
+    monkeypatch.setenv("MG_ROW_BATCH", "1")
     prompts = G.random_prompts(256, 96, 16, 7)
     results = {}
     for slices in ("1", "2", "3"):
@@ -263,6 +264,7 @@ def test_decode_slices_with_their_own_split_counts(monkeypatch):
     # against one stream (up to near-ties) and final logits within TOL.
     config = G.named_config("mid")
     monkeypatch.setenv("MG_DISABLE_PERSISTENT", "1")
+    monkeypatch.setenv("MG_ROW_BATCH", "1")
     prompts = G.random_prompts(256, 97, 16, 7)
     monkeypatch.setenv("MG_DECODE_SLICES", "1")
     with G.MeshGpt(0, config, 7, max_batch=97) as model:
@@ -275,6 +277,37 @@ def test_decode_slices_with_their_own_split_counts(monkeypatch):
         assert compared > 0.99 * three.size
         if np.array_equal(three, one):
             assert_close(model.last_logits(97), one_logits, what="three slices: final logits")
+
+
+@pytest.mark.parametrize("name,batch", [("mid", 99), ("high", 23)])
+def test_row_batches_match_single_rows(name, batch, monkeypatch):
+    # The per-phase row blocks with 2 or 4 rows per workgroup (the last
+    # workgroup's spare rows repeat the batch's last row and write nothing:
+    # 99 and 23 rows leave 1 and 3 of them) against one row per workgroup:
+    # greedy tokens up to near-ties, and the final logits within TOL; then
+    # the 4-row run's logits against the oracle on its own tokens.
+    config = G.named_config(name)
+    monkeypatch.setenv("MG_DISABLE_PERSISTENT", "1")
+    monkeypatch.setenv("MG_DECODE_SLICES", "1")
+    prompts = G.random_prompts(256, batch, 16, 7)
+    runs = {}
+    for rb in ("1", "2", "4"):
+        monkeypatch.setenv("MG_ROW_BATCH", rb)
+        with G.MeshGpt(0, config, 7, max_batch=batch) as model:
+            tokens = model.generate_tokens(prompts, 12, 0.0, 7)
+            runs[rb] = (tokens, model.last_logits(batch))
+            if rb == "1":
+                continue
+            compared = assert_same_tokens_or_near_tie(model, tokens, runs["1"][0], f"{rb} rows per workgroup")
+            assert compared > 0.99 * tokens.size
+            same = np.all(tokens == runs["1"][0], axis=1)
+            assert_close(runs[rb][1][same], runs["1"][1][same], what=f"{rb} rows per workgroup: final logits")
+    o = oracle_config(config)
+    params = O.initialize(o, 7)
+    tokens, last = runs["4"]
+    for b in (0, batch - 1):
+        ref = O.logits(o, params, tokens[b, :-1], tokens.shape[1] - 1)[-1]
+        assert_close(last[b], ref, what=f"{name} 4 rows per workgroup, sequence {b}")
 
 
 def test_cli_init_then_generate_matches_oracle(tmp_path):
