@@ -2,8 +2,12 @@
 // the XSA epilogue (reference.rs:510-554 attention, 577-603 exclusive self
 // attention; the reference's GPU kernel is gpt_flash_forward, gpu.rs:381-498).
 //
-// One workgroup of four waves takes 128 queries of one (sequence, head); each
-// wave owns 32 of them (two 16-query blocks).  Keys stream through LDS in
+// One workgroup of eight waves (four at head width 32) takes 256 (128)
+// queries of one (sequence, head); each wave owns 32 of them (two 16-query
+// blocks).  Eight waves share each K/V tile among twice the queries and put
+// four waves on every SIMD (two workgroups per CU, by LDS): config 4's
+// prefill took 23.69 ms against 23.95 with four waves (and 24.8 with 32-key
+// tiles, which let four workgroups share a CU).  Keys stream through LDS in
 // tiles of 64 rows of K and V, double-buffered and loaded with direct-to-LDS
 // loads (global_load_lds_dwordx4), so a tile lands while the previous one is
 // multiplied.  Per tile and 16-query block a wave computes the transposed
@@ -75,7 +79,7 @@ struct MfmaCfg {
     static constexpr int BK = 64;                 // keys per tile
     static constexpr int KB = BK / 16;            // 16-key blocks per tile
     static constexpr int NQB = 2;                 // 16-query blocks per wave
-    static constexpr int WAVES = 4;
+    static constexpr int WAVES = HD == 64 ? 8 : 4;
     static constexpr int QT = 16 * NQB * WAVES;   // queries per workgroup
     static constexpr int KS = HD / 4;             // k-steps of Q.K: dim = KS * (lane / 16) + step
     static constexpr int DB = HD / 16;            // 16-dim blocks of the output
@@ -115,7 +119,7 @@ __device__ __forceinline__ void issue_tile(const float *slab, int t0, int n, flo
 // consecutive on it and longest first, so the tiles that stream the same keys
 // share that XCD's L2.
 template <int HD>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(64 * MfmaCfg<HD>::WAVES)
 attn_prefill_mfma_kernel(Shape s, const float *__restrict__ q, KvView kv, int nseq, int n, float *__restrict__ y,
                          float scale_log2, int xsa) {
     using C = MfmaCfg<HD>;
@@ -396,16 +400,16 @@ bool attn_prefill_mfma_supported(const Shape &s, int rows_per_seq) {
 void attn_prefill_mfma(const Shape &s, const float *q, KvView kv, int nseq, int rows_per_seq, float *y, int xsa,
                        hipStream_t stream) {
     const float scale_log2 = float(1.4426950408889634 / std::sqrt(double(s.hd)));
-    auto launch = [&](auto kernel, int qt) {
+    auto launch = [&](auto kernel, int qt, int waves) {
         const int ntiles = (rows_per_seq + qt - 1) / qt;
         const int px = (nseq * s.H + 7) / 8;
-        hipLaunchKernelGGL(kernel, dim3(8 * px * ntiles), dim3(256), 0, stream, s, q, kv, nseq, rows_per_seq, y,
-                           scale_log2, xsa);
+        hipLaunchKernelGGL(kernel, dim3(8 * px * ntiles), dim3(64 * waves), 0, stream, s, q, kv, nseq,
+                           rows_per_seq, y, scale_log2, xsa);
     };
     if (s.hd == 32)
-        launch(attn_prefill_mfma_kernel<32>, MfmaCfg<32>::QT);
+        launch(attn_prefill_mfma_kernel<32>, MfmaCfg<32>::QT, MfmaCfg<32>::WAVES);
     else
-        launch(attn_prefill_mfma_kernel<64>, MfmaCfg<64>::QT);
+        launch(attn_prefill_mfma_kernel<64>, MfmaCfg<64>::QT, MfmaCfg<64>::WAVES);
     (void)hipGetLastError();
 }
 
