@@ -407,7 +407,7 @@ struct MeshGpt::Impl {
                                    kern::attn_prefill_short_supported(shape, rows.rows_per_seq);
         // Prefill blocks on the register-tile kernel where the shape allows it
         // (MG_DISABLE_ROWS_PREFILL=1 keeps block_kernel).
-        const bool rows_prefill = use_rows_prefill && kern::rows_block_supported(shape);
+        const bool rows_prefill = use_rows_prefill && kern::rows_block_supported(shape) && rows.len == nullptr;
         const BlockTiling t = block_tiling(size_t(rows.rows), decode);
         const size_t L = cfg.layers;
         const bool rows_order = decode && row_decode;

@@ -18,6 +18,7 @@
 // inside a wave (a head is hd <= 64 consecutive channels = consecutive lanes).
 #include <hip/hip_runtime.h>
 
+#include "dpp.hpp"
 #include "kernels.hpp"
 
 namespace meshgpt::kern {
@@ -93,12 +94,13 @@ struct Tile {
 
     // A mesh stack on v in place: layer l maps v[c] to v[c] w0 + v[c + st] w1
     // with ELU on every layer but the last (reference.rs:422-453).
+    // Butterfly strides double from 1 and wrap at W (W is a power of two).
     __device__ void mesh(float (&v)[CPT][RG], const float2 *__restrict__ w, int depth, const Shape &s) {
         float2 wc[CPT];
 #pragma unroll
         for (int k = 0; k < CPT; ++k) wc[k] = w[chan(k)];
+        int st = 1;
         for (int l = 0; l < depth; ++l) {
-            const int st = s.butterfly ? (1 << (l % s.log2w)) : 1;
             put(v);
             __syncthreads();
             float2 wn[CPT];
@@ -108,19 +110,21 @@ struct Tile {
             }
             float p[CPT][RG];
             partner(st, p);
-            const bool last = l + 1 == depth;
-#pragma unroll
-            for (int k = 0; k < CPT; ++k)
-#pragma unroll
-                for (int i = 0; i < RG; ++i) {
-                    const float z = v[k][i] * wc[k].x + p[k][i] * wc[k].y;
-                    v[k][i] = last ? z : elu_f(z);
-                }
             if (l + 1 < depth) {
 #pragma unroll
+                for (int k = 0; k < CPT; ++k)
+#pragma unroll
+                    for (int i = 0; i < RG; ++i) v[k][i] = elu_f(v[k][i] * wc[k].x + p[k][i] * wc[k].y);
+#pragma unroll
                 for (int k = 0; k < CPT; ++k) wc[k] = wn[k];
+            } else {
+#pragma unroll
+                for (int k = 0; k < CPT; ++k)
+#pragma unroll
+                    for (int i = 0; i < RG; ++i) v[k][i] = v[k][i] * wc[k].x + p[k][i] * wc[k].y;
             }
             flip();
+            st = s.butterfly ? (2 * st == W ? 1 : 2 * st) : 1;
         }
     }
 
@@ -136,10 +140,7 @@ struct Tile {
             part[i] = a;
         }
 #pragma unroll
-        for (int i = 0; i < RG; ++i) {
-#pragma unroll
-            for (int m = 32; m >= 1; m >>= 1) part[i] += __shfl_xor(part[i], m, 64);
-        }
+        for (int i = 0; i < RG; ++i) part[i] = wave_sum(part[i]);
         __syncthreads();  // the scratch's previous readers are done
         if (lane == 0) {
 #pragma unroll
@@ -156,13 +157,19 @@ struct Tile {
     }
 };
 
-// Sum over the hd lanes of a head (hd a power of two <= 64, heads aligned to hd lanes).
+// Sum over the hd lanes of a head (hd a power of two <= 64, heads aligned to
+// hd lanes): DPP moves when the head width HD is a compile-time 32 or 64.
+template <int HD>
 __device__ __forceinline__ float head_sum(float v, int hd) {
+    if constexpr (HD > 0) return group_sum<HD>(v);
     for (int m = hd >> 1; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
     return v;
 }
 
-template <int W>
+// HD: the head width when it is 32 or 64 (DPP head sums), else 0.  Rows are
+// whole prefill sequences (Rows.len is null: a row's position is its index
+// within its sequence).
+template <int W, int HD>
 __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
     using C = RowsCfg<W>;
     constexpr int CPT = C::CPT, RG = C::RG;
@@ -180,25 +187,23 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
     const bool post = a.wproj != nullptr, pre = a.wq != nullptr;
     const int r0 = int(blockIdx.x) * C::R;
 
-    // Rows of this thread: sequence, position, and whether the row exists.
-    int seq[RG], pos[RG];
-    size_t grow[RG];
-    bool live[RG];
+    // Rows of this thread: rbase + i; rows past the batch repeat its last row
+    // and write nothing.  Only the sequences are kept; the row indices and
+    // positions are formed where they are used.
+    const int rbase = r0 + t.rg * RG, rps = a.ro.rows_per_seq;
+    auto rowof = [&](int i) { return min(rbase + i, a.ro.rows - 1); };
+    auto live = [&](int i) { return rbase + i < a.ro.rows; };
+    int seq[RG];
 #pragma unroll
-    for (int i = 0; i < RG; ++i) {
-        const int row = r0 + t.row(i);
-        live[i] = row < a.ro.rows;
-        const int rr = live[i] ? row : a.ro.rows - 1;
-        grow[i] = size_t(rr);
-        seq[i] = rr / a.ro.rows_per_seq;
-        pos[i] = (a.ro.len ? a.ro.len[seq[i]] - 1 : 0) + (rr - seq[i] * a.ro.rows_per_seq);
-    }
+    for (int i = 0; i < RG; ++i) seq[i] = rowof(i) / rps;
+    auto grow = [&](int i) { return size_t(rowof(i)); };
+    auto posof = [&](int i) { return rowof(i) - seq[i] * rps; };
 
     float x[CPT][RG];
     if (a.embed) {
 #pragma unroll
         for (int i = 0; i < RG; ++i) {
-            const uint32_t tok = a.ro.tokens[size_t(seq[i]) * a.ro.tok_stride + a.ro.tok_offset + pos[i]];
+            const uint32_t tok = a.ro.tokens[size_t(seq[i]) * a.ro.tok_stride + a.ro.tok_offset + posof(i)];
 #pragma unroll
             for (int k = 0; k < CPT; ++k) x[k][i] = a.E[size_t(tok) * W + t.chan(k)];
         }
@@ -206,7 +211,7 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
 #pragma unroll
         for (int i = 0; i < RG; ++i)
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) x[k][i] = a.x[grow[i] * W + t.chan(k)];
+            for (int k = 0; k < CPT; ++k) x[k][i] = a.x[grow(i) * W + t.chan(k)];
     }
 
     if (post) {
@@ -214,7 +219,7 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
 #pragma unroll
         for (int i = 0; i < RG; ++i)
 #pragma unroll
-            for (int k = 0; k < CPT; ++k) y[k][i] = a.ybuf[grow[i] * W + t.chan(k)];
+            for (int k = 0; k < CPT; ++k) y[k][i] = a.ybuf[grow(i) * W + t.chan(k)];
         if (a.xsa_post) {
             // XSA (reference.rs:577-603): z = y - (y.u)u, u = v / max(|v|, eps).
 #pragma unroll
@@ -223,8 +228,8 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
                     const float v =
-                        a.kv_post.v[(size_t(seq[i] * s.H + h) * a.kv_post.cap + pos[i]) * s.hdp + d];
-                    const float vv = head_sum(v * v, s.hd), yv = head_sum(y[k][i] * v, s.hd);
+                        a.kv_post.v[(size_t(seq[i] * s.H + h) * a.kv_post.cap + posof(i)) * s.hdp + d];
+                    const float vv = head_sum<HD>(v * v, s.hd), yv = head_sum<HD>(y[k][i] * v, s.hd);
                     const float iv = rsqrtf(fmaxf(vv, kXsaNormFloor));
                     y[k][i] = y[k][i] - (yv * iv) * (v * iv);
                 }
@@ -251,9 +256,9 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
     if (post || a.embed) {
 #pragma unroll
         for (int i = 0; i < RG; ++i)
-            if (live[i]) {
+            if (live(i)) {
 #pragma unroll
-                for (int k = 0; k < CPT; ++k) a.x[grow[i] * W + t.chan(k)] = x[k][i];
+                for (int k = 0; k < CPT; ++k) a.x[grow(i) * W + t.chan(k)] = x[k][i];
             }
     }
     if (!a.xn && !pre) return;
@@ -271,9 +276,9 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
     if (a.xn) {
 #pragma unroll
         for (int i = 0; i < RG; ++i)
-            if (live[i]) {
+            if (live(i)) {
 #pragma unroll
-                for (int k = 0; k < CPT; ++k) a.xn[grow[i] * W + t.chan(k)] = n[k][i];
+                for (int k = 0; k < CPT; ++k) a.xn[grow(i) * W + t.chan(k)] = n[k][i];
             }
     }
     if (!pre) return;
@@ -299,10 +304,10 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
 #pragma unroll
                 for (int i = 0; i < RG; ++i) {
                     float q = v[k][i];
-                    if (s.qk_norm) q *= rsqrtf(head_sum(q * q, s.hd) * (1.0f / float(s.hd)) + kEps);
+                    if (s.qk_norm) q *= rsqrtf(head_sum<HD>(q * q, s.hd) * (1.0f / float(s.hd)) + kEps);
                     if (s.rope) {
                         const float p = __shfl_xor(q, s.half, 64);
-                        const float2 cs = a.rope[size_t(pos[i]) * s.half + (d < s.half ? d : d - s.half)];
+                        const float2 cs = a.rope[size_t(posof(i)) * s.half + (d < s.half ? d : d - s.half)];
                         q = q * cs.x + (d < s.half ? -p : p) * cs.y;
                     }
                     v[k][i] = q;
@@ -310,12 +315,12 @@ __global__ void __launch_bounds__(256) rows_block_kernel(BlockArgs a) {
             }
 #pragma unroll
             for (int i = 0; i < RG; ++i) {
-                if (!live[i]) continue;
+                if (!live(i)) continue;
                 if (m == 0) {
-                    a.q[grow[i] * W + c] = v[k][i];
+                    a.q[grow(i) * W + c] = v[k][i];
                 } else {
                     float *dst = m == 1 ? a.kv_pre.k : a.kv_pre.v;
-                    dst[(size_t(seq[i] * s.H + h) * a.kv_pre.cap + pos[i]) * s.hdp + d] = v[k][i];
+                    dst[(size_t(seq[i] * s.H + h) * a.kv_pre.cap + posof(i)) * s.hdp + d] = v[k][i];
                 }
             }
         }
@@ -329,15 +334,23 @@ bool rows_block_supported(const Shape &s) {
            64 % s.hd == 0;
 }
 
+template <int W>
+void launch_rows_block(const BlockArgs &a, hipStream_t stream) {
+    const dim3 grid((a.ro.rows + RowsCfg<W>::R - 1) / RowsCfg<W>::R);
+    if (a.s.hd == 32)
+        hipLaunchKernelGGL((rows_block_kernel<W, 32>), grid, dim3(256), 0, stream, a);
+    else if (a.s.hd == 64)
+        hipLaunchKernelGGL((rows_block_kernel<W, 64>), grid, dim3(256), 0, stream, a);
+    else
+        hipLaunchKernelGGL((rows_block_kernel<W, 0>), grid, dim3(256), 0, stream, a);
+}
+
 void rows_block(const BlockArgs &a, hipStream_t stream) {
-    auto launch = [&](auto kernel, int R) {
-        hipLaunchKernelGGL(kernel, dim3((a.ro.rows + R - 1) / R), dim3(256), 0, stream, a);
-    };
     switch (a.s.W) {
-    case 128: launch(rows_block_kernel<128>, RowsCfg<128>::R); break;
-    case 256: launch(rows_block_kernel<256>, RowsCfg<256>::R); break;
-    case 512: launch(rows_block_kernel<512>, RowsCfg<512>::R); break;
-    default: launch(rows_block_kernel<1024>, RowsCfg<1024>::R); break;
+    case 128: launch_rows_block<128>(a, stream); break;
+    case 256: launch_rows_block<256>(a, stream); break;
+    case 512: launch_rows_block<512>(a, stream); break;
+    default: launch_rows_block<1024>(a, stream); break;
     }
     (void)hipGetLastError();
 }
