@@ -27,7 +27,24 @@ EXPORTS = (
     "mg_model_stream", "mg_checkpoint_load", "mg_checkpoint_info", "mg_checkpoint_characters",
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
     "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_sample_logits_noalloc", "mg_expf",
+    "mg_adamw_default", "mg_cross_entropy", "mg_loss_and_gradient", "mg_train_batch",
 )
+
+IGNORE_TARGET = 0xFFFFFFFF  # MG_IGNORE_TARGET (src/gpt/mod.rs:26)
+
+
+class AdamW(ctypes.Structure):
+    """mg_adamw: AdamWOptions (src/gpt/config.rs:258-276), reference defaults."""
+
+    _fields_ = [(name, ctypes.c_float) for name in ("learning_rate", "weight_decay", "beta1", "beta2", "epsilon")]
+
+    def __init__(self, **overrides):
+        super().__init__()
+        lib().mg_adamw_default(ctypes.byref(self))
+        for key, value in overrides.items():
+            if key not in dict(self._fields_):
+                raise TypeError(f"unknown AdamW field {key}")
+            setattr(self, key, float(value))
 
 
 class GptConfig(ctypes.Structure):
@@ -122,6 +139,10 @@ def lib():
         "mg_sample_logits": (i, [i, _f32p, sz, sz, f, ctypes.POINTER(ctypes.c_uint64), _u32p]),
         "mg_sample_logits_noalloc": (i, [i, vp, sz, sz, f, vp, vp, vp, vp]),
         "mg_expf": (i, [i, _f32p, sz, _f32p]),
+        "mg_adamw_default": (None, [vp]),
+        "mg_cross_entropy": (i, [vp, _u32p, _u32p, sz, sz, ctypes.POINTER(ctypes.c_double)]),
+        "mg_loss_and_gradient": (i, [vp, _u32p, _u32p, sz, sz, ctypes.POINTER(ctypes.c_double), _f32p, sz]),
+        "mg_train_batch": (i, [vp, _u32p, _u32p, sz, sz, vp, ctypes.POINTER(ctypes.c_double)]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -257,6 +278,38 @@ class MeshGpt:
         _check(lib().mg_logits(self._h, _p(tokens, _u32p), tokens.size, sequence, int(last_only),
                                _p(out, _f32p), out.size))
         return out[:rows]
+
+    def cross_entropy(self, inputs, targets, sequence):
+        """gpu.rs:1915-1929: mean next-token loss over supervised rows."""
+        inputs, targets = _u32(inputs).reshape(-1), _u32(targets).reshape(-1)
+        if inputs.size != targets.size:
+            raise MeshGptError(MG_INVALID_ARGUMENT, "inputs and targets must have equal lengths")
+        loss = ctypes.c_double()
+        _check(lib().mg_cross_entropy(self._h, _p(inputs, _u32p), _p(targets, _u32p), inputs.size, sequence,
+                                      ctypes.byref(loss)))
+        return loss.value
+
+    def loss_and_gradient(self, inputs, targets, sequence):
+        """gpu.rs:1931-1946: (loss, gradient of every parameter)."""
+        inputs, targets = _u32(inputs).reshape(-1), _u32(targets).reshape(-1)
+        if inputs.size != targets.size:
+            raise MeshGptError(MG_INVALID_ARGUMENT, "inputs and targets must have equal lengths")
+        grad = np.empty(parameter_count(self._config), dtype=np.float32)
+        loss = ctypes.c_double()
+        _check(lib().mg_loss_and_gradient(self._h, _p(inputs, _u32p), _p(targets, _u32p), inputs.size, sequence,
+                                          ctypes.byref(loss), _p(grad, _f32p), grad.size))
+        return loss.value, grad
+
+    def train_batch(self, inputs, targets, sequence, options=None):
+        """gpu.rs:1950-2003: the loss before one AdamW update."""
+        inputs, targets = _u32(inputs).reshape(-1), _u32(targets).reshape(-1)
+        if inputs.size != targets.size:
+            raise MeshGptError(MG_INVALID_ARGUMENT, "inputs and targets must have equal lengths")
+        options = AdamW() if options is None else options
+        loss = ctypes.c_double()
+        _check(lib().mg_train_batch(self._h, _p(inputs, _u32p), _p(targets, _u32p), inputs.size, sequence,
+                                    ctypes.byref(options), ctypes.byref(loss)))
+        return loss.value
 
     def token_embeddings(self):
         out = np.empty((self._config.vocab_size, self._config.width), dtype=np.float32)

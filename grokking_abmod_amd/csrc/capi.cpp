@@ -188,6 +188,46 @@ int mg_logits(mg_model *model, const uint32_t *tokens, size_t n, size_t sequence
     });
 }
 
+void mg_adamw_default(mg_adamw *out) {
+    if (!out) return;
+    const AdamWOptions d;
+    *out = mg_adamw{d.learning_rate, d.weight_decay, d.beta1, d.beta2, d.epsilon};
+}
+
+int mg_cross_entropy(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                     double *loss) {
+    return guarded([&] {
+        require(inputs != nullptr && targets != nullptr && loss != nullptr, "inputs, targets and loss must not be null");
+        *loss = model_of(model).cross_entropy(inputs, targets, n, sequence);
+    });
+}
+
+int mg_loss_and_gradient(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n,
+                         size_t sequence, double *loss, float *gradient, size_t n_gradient) {
+    return guarded([&] {
+        require(inputs != nullptr && targets != nullptr && loss != nullptr, "inputs, targets and loss must not be null");
+        std::vector<float> g;
+        const double l = model_of(model).loss_and_gradient(inputs, targets, n, sequence, g);
+        copy_out(g, gradient, n_gradient);
+        *loss = l;
+    });
+}
+
+int mg_train_batch(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                   const mg_adamw *options, double *loss) {
+    return guarded([&] {
+        require(inputs != nullptr && targets != nullptr && options != nullptr && loss != nullptr,
+                "inputs, targets, options and loss must not be null");
+        AdamWOptions o;
+        o.learning_rate = options->learning_rate;
+        o.weight_decay = options->weight_decay;
+        o.beta1 = options->beta1;
+        o.beta2 = options->beta2;
+        o.epsilon = options->epsilon;
+        *loss = model_of(model).train_batch(inputs, targets, n, sequence, o);
+    });
+}
+
 int mg_token_embeddings(mg_model *model, float *out, size_t n) {
     return guarded([&] { copy_out(model_of(model).token_embeddings(), out, n); });
 }

@@ -77,6 +77,14 @@ std::vector<float> GptConfig::initial_parameters(uint64_t seed) const {
     return Layout::build(*this).initialize(*this, seed);
 }
 
+void AdamWOptions::validate() const {
+    auto fin = [](float x) { return std::isfinite(x); };
+    if (!fin(learning_rate) || learning_rate <= 0.0f || !fin(weight_decay) || weight_decay < 0.0f || !fin(beta1) ||
+        !(beta1 >= 0.0f && beta1 < 1.0f) || !fin(beta2) || !(beta2 >= 0.0f && beta2 < 1.0f) || !fin(epsilon) ||
+        epsilon <= 0.0f)
+        throw Error("AdamW requires finite positive learning rate/epsilon, nonnegative decay, and betas in [0, 1)");
+}
+
 void GptConfig::validate_tokens(const uint32_t *tokens, size_t n, size_t sequence) const {
     if (sequence == 0 || sequence > context || n == 0 || n % sequence != 0 || n > kMaxRows)
         throw Error(

@@ -31,6 +31,7 @@ struct Error : std::runtime_error {
         : std::runtime_error(message), status(code) {}
 };
 
+constexpr uint32_t kIgnoreTarget = 0xFFFFFFFFu;  // IGNORE_TARGET, src/gpt/mod.rs:26
 constexpr size_t kMaxRows = 131072;        // src/gpt/mod.rs:31
 constexpr size_t kModelMaxWidth = 4096;    // src/gpt/mod.rs:33
 constexpr size_t kModelMaxContext = 4096;  // src/gpt/mod.rs:34
@@ -66,6 +67,16 @@ enum class EmbeddingNorm : uint32_t { None = 0, Unit, Rms };
 struct GptConfig;
 
 // EmbeddingGeometry (geometry.rs:49-81); defaults keep the signed parity codes.
+// AdamWOptions (config.rs:258-276) with its defaults.
+struct AdamWOptions {
+    float learning_rate = 0.003f;
+    float weight_decay = 0.01f;
+    float beta1 = 0.9f;
+    float beta2 = 0.999f;
+    float epsilon = 1e-8f;
+    void validate() const;  // config.rs:278-295
+};
+
 struct EmbeddingGeometry {
     EmbeddingForm form = EmbeddingForm::Parity;
     EmbeddingOrder order = EmbeddingOrder::Token;

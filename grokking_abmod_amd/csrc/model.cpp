@@ -2,6 +2,7 @@
 // decode sequences of kernel launches, and the HIP graph that replays one
 // decode step.
 #include "model.hpp"
+#include "train.hpp"
 
 #include <algorithm>
 #include <cmath>
@@ -116,6 +117,13 @@ struct MeshGpt::Impl {
     bool use_mfma_prefill = true;
     bool use_rows_prefill = true;
     bool use_short_prefill = true;
+
+    // Training (gpu.rs:1915-2003): the activations of the last forward, the
+    // gradient, AdamW's moments and the running powers of its betas (reset
+    // with the weights, gpu.rs:1856-1872).
+    DevBuf tact, tgrad, tm, tv, tpart, ttok, ttgt;
+    float beta1_power = 1.0f, beta2_power = 1.0f;
+    bool derived_stale = false;  // E and the decode tables lag the weights
 
     // Events around the kernels of the last logits / hidden_states / prefill
     // call (last_call_ms).
@@ -287,6 +295,21 @@ struct MeshGpt::Impl {
         layout.validate_constraints(cfg, values);
         activate();
         check(hipMemcpyAsync(params.p, values, n * 4, hipMemcpyHostToDevice, stream), "upload parameters");
+        reset_optimizer();
+        refresh_derived();
+    }
+
+    // Tables derived from the weights (E, its transpose, the row-order copies
+    // and the layer-0 table): rebuilt when the weights change, not per token.
+    // After training steps they are rebuilt before the next inference call.
+    void ensure_derived() {
+        if (!derived_stale) return;
+        activate();
+        refresh_derived();
+    }
+
+    void refresh_derived() {
+        const size_t n = layout.count();
         // The token vectors depend only on the weights: computed once here, not per token.
         if (cfg.embedding == TokenEmbedding::Mesh) {
             kern::mesh_rows(shape, codes.as<float>(), E.as<float>(), shape.V, params.as<float>(), shape.A,
@@ -318,6 +341,7 @@ struct MeshGpt::Impl {
             }
         }
         sync();
+        derived_stale = false;
     }
 
     void sync() {
@@ -491,6 +515,7 @@ struct MeshGpt::Impl {
     std::vector<float> logits(const uint32_t *tokens, size_t n, size_t sequence, bool last_only) {
         cfg.validate_tokens(tokens, n, sequence);
         activate();
+        ensure_derived();
         const size_t out_rows = last_only ? n / sequence : n;
         forward_rows(tokens, n, sequence, out_rows);
         kern::head(shape, wxn.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
@@ -509,6 +534,7 @@ struct MeshGpt::Impl {
     std::vector<float> hidden_states(const uint32_t *tokens, size_t n, size_t sequence) {
         cfg.validate_tokens(tokens, n, sequence);
         activate();
+        ensure_derived();
         forward_rows(tokens, n, sequence, 1);
         mark_call(1);
         std::vector<float> out(n * cfg.width);
@@ -517,6 +543,261 @@ struct MeshGpt::Impl {
         close_call();
         validate_finite(out.data(), out.size(), "features");
         return out;
+    }
+
+    // ---- training -------------------------------------------------------------
+
+    void reset_optimizer() {
+        beta1_power = beta2_power = 1.0f;
+        if (tm.p) {
+            check(hipMemsetAsync(tm.p, 0, tm.bytes, stream), "clear moments");
+            check(hipMemsetAsync(tv.p, 0, tv.bytes, stream), "clear moments");
+        }
+    }
+
+    // Offsets (floats) of the training forward's activations and the
+    // backward's scratch in tact, for R rows.
+    struct TrainBlock {
+        size_t n1, inv1, qs, ks, vs, qr, kr, qinv, kinv, y, lse, z, ps, xm, inv2, n2, fs;
+    };
+    struct TrainPlan {
+        size_t es, x, invf, nf, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
+        std::vector<TrainBlock> blocks;
+    };
+
+    TrainPlan train_plan(size_t R) const {
+        const size_t W = cfg.width, H = cfg.heads, V = cfg.vocab_size, A = cfg.attention_mesh_depth;
+        const size_t F = cfg.ffn_mesh_depth, RW = R * W, RH = R * H;
+        size_t at = 0;
+        auto take = [&](size_t n) {
+            const size_t o = at;
+            at += (n + 63) / 64 * 64;
+            return o;
+        };
+        TrainPlan p;
+        p.es = take(cfg.embedding == TokenEmbedding::Mesh ? A * V * W : 0);
+        p.x = take((cfg.layers + 1) * RW);
+        for (size_t b = 0; b < cfg.layers; ++b) {
+            TrainBlock k;
+            k.n1 = take(RW);
+            k.inv1 = take(R);
+            k.qs = take(A * RW);
+            k.ks = take(A * RW);
+            k.vs = take(A * RW);
+            k.qr = take(RW);
+            k.kr = take(RW);
+            k.qinv = take(RH);
+            k.kinv = take(RH);
+            k.y = take(RW);
+            k.lse = take(RH);
+            k.z = take(RW);
+            k.ps = take(A * RW);
+            k.xm = take(RW);
+            k.inv2 = take(R);
+            k.n2 = take(RW);
+            k.fs = take(F * RW);
+            p.blocks.push_back(k);
+        }
+        p.invf = take(R);
+        p.nf = take(RW);
+        p.logits = take(R * V);
+        p.dlogits = take(R * V);
+        p.loss = take(R);
+        p.dx = take(RW);
+        p.dn = take(RW);
+        p.dq = take(RW);
+        p.dk = take(RW);
+        p.dv = take(RW);
+        p.dy = take(RW);
+        p.dt = take(RW);
+        p.dsum = take(RH);
+        p.dE = take(V * W);
+        p.total = at;
+        return p;
+    }
+
+    void check_trainable() const {
+        if (cfg.geometry.transformed())
+            throw Error("training supports embeddings without normalisation or protected coordinates", kUnsupported);
+        if (cfg.width > size_t(kern::train::kMaxWidth) || cfg.head_width() > size_t(kern::train::kMaxHeadWidth) ||
+            cfg.attention_mesh_depth > size_t(kern::train::kMaxDepth) ||
+            cfg.ffn_mesh_depth > size_t(kern::train::kMaxDepth))
+            throw Error("training supports width <= 1024, head width <= 128 and mesh depth <= 16", kUnsupported);
+    }
+
+    // config.rs:230-252: inputs as validate_tokens, equal lengths, targets in
+    // the vocabulary or IGNORE_TARGET, at least one supervised.
+    size_t validate_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence) const {
+        cfg.validate_tokens(inputs, n, sequence);
+        size_t supervised = 0;
+        for (size_t i = 0; i < n; ++i) {
+            if (targets[i] == kIgnoreTarget) continue;
+            if (targets[i] >= cfg.vocab_size) throw Error("target ID is outside the vocabulary");
+            ++supervised;
+        }
+        if (supervised == 0) throw Error("batch must contain at least one supervised target");
+        return supervised;
+    }
+
+    // The training forward over n rows (reference.rs:104-228) keeping every
+    // activation, the loss kernel, and with `backward` the gradient of the
+    // mean loss in tgrad (reference.rs:61-89, masked as config.rs:490-500).
+    // Returns the mean loss over the supervised rows.
+    double train_pass(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence, bool backward) {
+        namespace T = kern::train;
+        check_trainable();
+        const size_t supervised = validate_batch(inputs, targets, n, sequence);
+        activate();
+        const int R = int(n), W = int(cfg.width), H = int(cfg.heads), V = int(cfg.vocab_size), seq = int(sequence);
+        const int A = int(cfg.attention_mesh_depth), F = int(cfg.ffn_mesh_depth), L = int(cfg.layers);
+        const size_t RW = n * cfg.width, P = layout.count();
+        const TrainPlan p = train_plan(n);
+        tact.ensure(p.total * 4);
+        const T::Mesh ma{W, A, shape.butterfly, shape.log2w}, mf{W, F, shape.butterfly, shape.log2w};
+        tpart.ensure(std::max({T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
+                               T::mesh_partial_floats(ma, V)}) * 4);
+        tgrad.ensure(P * 4);
+        ttok.ensure(n * 4);
+        ttgt.ensure(n * 4);
+        check(hipMemcpyAsync(ttok.p, inputs, n * 4, hipMemcpyHostToDevice, stream), "upload inputs");
+        check(hipMemcpyAsync(ttgt.p, targets, n * 4, hipMemcpyHostToDevice, stream), "upload targets");
+        float *act = tact.as<float>(), *part = tpart.as<float>(), *grad = tgrad.as<float>();
+        const float *w = params.as<float>();
+        const uint32_t *tok = ttok.as<uint32_t>();
+        const float2 *table = rope.as<float2>();
+        auto at = [&](size_t o) { return act + o; };
+        auto group = [&](size_t id) { return layout.groups[id].offset; };
+        const size_t emb = group(layout.embedding);
+
+        // Token vectors: the embedding mesh of the codes (its layers kept), or the table.
+        const float *Ev = w + emb;
+        if (cfg.embedding == TokenEmbedding::Mesh) {
+            T::mesh_forward(ma, codes.as<float>(), at(p.es), w + emb, V, stream);
+            Ev = at(p.es) + size_t(A - 1) * V * W;
+        }
+        T::gather(Ev, tok, at(p.x), R, W, stream);
+        auto X = [&](int b) { return at(p.x) + size_t(b) * RW; };
+        auto last = [&](size_t o, int depth) { return at(o) + size_t(depth - 1) * RW; };
+        for (int b = 0; b < L; ++b) {
+            const TrainBlock &k = p.blocks[b];
+            const Block &g = layout.blocks[b];
+            T::rmsnorm_forward(X(b), at(k.n1), at(k.inv1), R, W, 1, stream);
+            T::mesh_forward(ma, at(k.n1), at(k.qs), w + group(g.query), R, stream);
+            T::mesh_forward(ma, at(k.n1), at(k.ks), w + group(g.key), R, stream);
+            T::mesh_forward(ma, at(k.n1), at(k.vs), w + group(g.value), R, stream);
+            // reference.rs:174-193: QK-Norm, then RoPE, each when switched on
+            const std::pair<size_t, size_t> qk[2] = {{k.qs, k.qr}, {k.ks, k.kr}};
+            const size_t qkinv[2] = {k.qinv, k.kinv};
+            for (int m = 0; m < 2; ++m) {
+                if (cfg.qk_norm)
+                    T::rmsnorm_forward(last(qk[m].first, A), at(qk[m].second), at(qkinv[m]), R, W, H, stream);
+                else
+                    check(hipMemcpyAsync(at(qk[m].second), last(qk[m].first, A), RW * 4, hipMemcpyDeviceToDevice,
+                                         stream),
+                          "copy");
+                if (cfg.rope) T::rope(at(qk[m].second), table, R, seq, W, H, false, stream);
+            }
+            T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), R, seq, W, H, stream);
+            if (cfg.xsa)
+                T::xsa_forward(at(k.y), last(k.vs, A), at(k.z), R, W, H, stream);
+            else
+                check(hipMemcpyAsync(at(k.z), at(k.y), RW * 4, hipMemcpyDeviceToDevice, stream), "copy");
+            T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);
+            T::add(X(b), last(k.ps, A), at(k.xm), RW, stream);
+            T::rmsnorm_forward(at(k.xm), at(k.n2), at(k.inv2), R, W, 1, stream);
+            T::mesh_forward(mf, at(k.n2), at(k.fs), w + group(g.ffn), R, stream);
+            T::add(at(k.xm), last(k.fs, F), X(b + 1), RW, stream);
+        }
+        T::rmsnorm_forward(X(L), at(p.nf), at(p.invf), R, W, 1, stream);
+        T::head_logits(at(p.nf), Ev, at(p.logits), R, W, V, stream);
+        T::cross_entropy(at(p.logits), ttgt.as<uint32_t>(), at(p.dlogits), at(p.loss), R, V, int(supervised),
+                         stream);
+
+        if (backward) {
+            float *dx = at(p.dx), *dn = at(p.dn), *dq = at(p.dq), *dk = at(p.dk), *dv = at(p.dv);
+            float *dy = at(p.dy), *dt = at(p.dt);
+            T::head_backward(at(p.dlogits), Ev, dn, R, W, V, stream);
+            T::rmsnorm_backward(X(L), at(p.invf), dn, dx, false, R, W, 1, stream);
+            for (int b = L - 1; b >= 0; --b) {
+                const TrainBlock &k = p.blocks[b];
+                const Block &g = layout.blocks[b];
+                // x_{b+1} = xm + ffn(rmsnorm(xm)); xm = x_b + proj(attention)
+                T::mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, false, w + group(g.ffn), part, grad + group(g.ffn),
+                                 R, stream);
+                T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
+                T::mesh_backward(ma, at(k.z), at(k.ps), dx, dt, false, w + group(g.projection), part,
+                                 grad + group(g.projection), R, stream);
+                if (cfg.xsa) {
+                    T::xsa_backward(at(k.y), last(k.vs, A), dt, dy, dv, R, W, H, stream);
+                } else {
+                    check(hipMemcpyAsync(dy, dt, RW * 4, hipMemcpyDeviceToDevice, stream), "copy");
+                    check(hipMemsetAsync(dv, 0, RW * 4, stream), "clear");
+                }
+                T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dy, dq, dk, dv,
+                                      at(p.dsum), R, seq, W, H, stream);
+                float *dqk[2] = {dq, dk};
+                const size_t pre[2] = {k.qs, k.ks}, qkinv[2] = {k.qinv, k.kinv};
+                for (int m = 0; m < 2; ++m) {
+                    if (cfg.rope) T::rope(dqk[m], table, R, seq, W, H, true, stream);
+                    if (cfg.qk_norm)
+                        T::rmsnorm_backward(last(pre[m], A), at(qkinv[m]), dqk[m], dqk[m], false, R, W, H, stream);
+                }
+                T::mesh_backward(ma, at(k.n1), at(k.qs), dq, dn, false, w + group(g.query), part,
+                                 grad + group(g.query), R, stream);
+                T::mesh_backward(ma, at(k.n1), at(k.ks), dk, dn, true, w + group(g.key), part, grad + group(g.key),
+                                 R, stream);
+                T::mesh_backward(ma, at(k.n1), at(k.vs), dv, dn, true, w + group(g.value), part,
+                                 grad + group(g.value), R, stream);
+                T::rmsnorm_backward(X(b), at(k.inv1), dn, dx, true, R, W, 1, stream);
+            }
+            // The tied vectors collect the head's gradient and the gathered rows'.
+            T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), R, W, V, stream);
+            if (cfg.embedding == TokenEmbedding::Mesh)
+                T::mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, false, w + emb, part,
+                                 grad + emb, V, stream);
+            else
+                check(hipMemcpyAsync(grad + emb, at(p.dE), size_t(V) * W * 4, hipMemcpyDeviceToDevice, stream),
+                      "copy");
+            if (cfg.geometry.frozen)
+                check(hipMemsetAsync(grad + emb, 0, cfg.embedding_parameter_count() * 4, stream), "mask");
+        }
+        // gpu.rs:2296-2313: per-row f32 losses summed in f64 on the host.
+        std::vector<float> rows(n);
+        check(hipMemcpyAsync(rows.data(), at(p.loss), n * 4, hipMemcpyDeviceToHost, stream), "download loss");
+        sync();
+        validate_finite(rows.data(), rows.size(), "cross-entropy");
+        double total = 0.0;
+        for (float v : rows) total += double(v);
+        return total / double(supervised);
+    }
+
+    std::vector<float> gradient() {
+        std::vector<float> out(layout.count());
+        check(hipMemcpy(out.data(), tgrad.p, out.size() * 4, hipMemcpyDeviceToHost), "download gradients");
+        validate_finite(out.data(), out.size(), "gradients");
+        return out;
+    }
+
+    // gpu.rs:1971-2003: the gradient, then one AdamW update of every group
+    // (the embedding group stays when the geometry is frozen).
+    double train_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                       const AdamWOptions &o) {
+        o.validate();
+        const double loss = train_pass(inputs, targets, n, sequence, true);
+        const size_t P = layout.count();
+        if (tm.ensure(P * 4) | tv.ensure(P * 4)) {
+            check(hipMemsetAsync(tm.p, 0, tm.bytes, stream), "clear moments");
+            check(hipMemsetAsync(tv.p, 0, tv.bytes, stream), "clear moments");
+        }
+        beta1_power *= o.beta1;
+        beta2_power *= o.beta2;
+        const kern::train::AdamW a{o.learning_rate, o.weight_decay, o.beta1,  o.beta2,
+                                   o.epsilon,       1.0f - beta1_power, 1.0f - beta2_power};
+        const size_t begin = cfg.geometry.frozen ? cfg.embedding_parameter_count() : 0;
+        kern::train::adam(params.as<float>(), tm.as<float>(), tv.as<float>(), tgrad.as<float>(), begin, P, a, stream);
+        sync();
+        derived_stale = true;
+        return loss;
     }
 
     // ---- generation -------------------------------------------------------
@@ -528,6 +809,7 @@ struct MeshGpt::Impl {
         for (size_t i = 0; i < b * p; ++i)
             if (prompts[i] >= cfg.vocab_size) throw Error("token ID is outside the vocabulary");
         activate();
+        ensure_derived();
         ensure_decode(b, std::max(reserve, p));
         check(hipMemcpy2DAsync(dtokens.p, tcap * 4, prompts, p * 4, p * 4, b, hipMemcpyHostToDevice, stream),
               "upload prompts");
@@ -797,10 +1079,27 @@ std::vector<float> MeshGpt::logits(const uint32_t *tokens, size_t n, size_t sequ
 
 std::vector<float> MeshGpt::token_embeddings() {
     impl_->activate();
+    impl_->ensure_derived();
     std::vector<float> out(impl_->cfg.vocab_size * impl_->cfg.width);
     check(hipMemcpy(out.data(), impl_->E.p, out.size() * 4, hipMemcpyDeviceToHost), "download embeddings");
     validate_finite(out.data(), out.size(), "features");
     return out;
+}
+
+double MeshGpt::cross_entropy(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence) {
+    return impl_->train_pass(inputs, targets, n, sequence, false);
+}
+
+double MeshGpt::loss_and_gradient(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                                  std::vector<float> &gradient) {
+    const double loss = impl_->train_pass(inputs, targets, n, sequence, true);
+    gradient = impl_->gradient();
+    return loss;
+}
+
+double MeshGpt::train_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                            const AdamWOptions &options) {
+    return impl_->train_batch(inputs, targets, n, sequence, options);
 }
 
 std::vector<float> MeshGpt::hidden_states(const uint32_t *tokens, size_t n, size_t sequence) {

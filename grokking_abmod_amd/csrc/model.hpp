@@ -30,6 +30,16 @@ class MeshGpt {
     std::vector<float> logits(const uint32_t *tokens, size_t n, size_t sequence, bool last_only = false);
     std::vector<float> token_embeddings();                  // gpu.rs:2056-2068, V x W
     std::vector<float> hidden_states(const uint32_t *tokens, size_t n, size_t sequence);  // gpu.rs:2070
+    // Training (gpu.rs:1915-2003).  Targets equal to kIgnoreTarget are not
+    // supervised.  cross_entropy: the mean next-token loss; loss_and_gradient:
+    // the loss and the gradient of every parameter (masked as config.rs:490-500);
+    // train_batch: the loss before one AdamW update of the weights (the moments
+    // persist across calls until set_parameters).
+    double cross_entropy(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence);
+    double loss_and_gradient(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                             std::vector<float> &gradient);
+    double train_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                       const AdamWOptions &options);
     // gpu.rs:2006-2053 on text; batch rows b use seed + b.
     std::string generate(const CharacterTokenizer &tokenizer, const std::string &prompt, size_t count,
                          float temperature, uint64_t seed);

@@ -1,0 +1,86 @@
+// Launch wrappers for the training kernels (train.hip): the forward pass that
+// keeps every activation the backward needs, the backward of each operator,
+// the next-token loss and AdamW.  Rows are [rows][W] f32 in channel order;
+// row r of a batch is position r % sequence of sequence r / sequence.
+#pragma once
+
+#include <hip/hip_runtime_api.h>
+
+#include <cstddef>
+#include <cstdint>
+
+namespace meshgpt::kern::train {
+
+constexpr int kMaxDepth = 16;       // mesh layers per stack (weight gradients stay in registers)
+constexpr int kMaxWidth = 1024;     // one thread per channel
+constexpr int kMaxHeadWidth = 128;  // attention keeps a head row per thread
+
+struct Mesh {
+    int W, depth, butterfly, log2w;
+};
+
+// stack[l] (rows x W, l < depth) = output of mesh layer l on `in`
+// (reference.rs:422-453): z = x[c] w_self + x[(c + s) % W] w_partner, ELU on
+// all layers but the last.
+void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream);
+// Scratch floats mesh_backward needs for `rows` rows.
+size_t mesh_partial_floats(const Mesh &m, int rows);
+// Backward of mesh_forward: dout is d loss / d stack[depth - 1]; din (when not
+// null) receives d loss / d in (added to what it holds when accumulate); the
+// weights' gradient goes to grad[0 .. 2 * W * depth) in the parameter layout.
+// Deterministic: per-workgroup partial sums in `partials`, then one reduction.
+void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
+                   bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream);
+
+// RMSNorm over `groups` equal groups of each row (reference.rs:392-409):
+// y = x / sqrt(mean(x^2) + 1e-5); inv[row * groups + g] keeps the factor.
+void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream);
+// dx = inv dy - x inv^3 (dy . x) / n per group (dx may alias dy; added to
+// dx's contents when accumulate, then it must not alias).
+void rmsnorm_backward(const float *x, const float *inv, const float *dy, float *dx, bool accumulate, int rows,
+                      int W, int groups, hipStream_t stream);
+
+// Slice RoPE in place (reference.rs:462-482) at position r % sequence, from
+// the (cos, sin) table [position][hd / 2]; inverse = the transposed rotation
+// (its backward).
+void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, bool inverse, hipStream_t stream);
+
+// Causal softmax attention per (sequence, head) (reference.rs:510-554);
+// lse[r * H + h] = max + ln(sum) of the row's scaled scores.
+void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
+                       int sequence, int W, int H, hipStream_t stream);
+// Its backward: dq and dk written, dv added to; dsum (rows x H) is scratch.
+void attention_backward(const float *q, const float *k, const float *v, const float *y, const float *lse,
+                        const float *dy, float *dq, float *dk, float *dv, float *dsum, int rows, int sequence,
+                        int W, int H, hipStream_t stream);
+
+// XSA (reference.rs:577-603): z = y - (y.u) u, u = v / max(|v|, 1e-12) per head.
+void xsa_forward(const float *y, const float *v, float *z, int rows, int W, int H, hipStream_t stream);
+// Its backward: dy and dv written.
+void xsa_backward(const float *y, const float *v, const float *dz, float *dy, float *dv, int rows, int W, int H,
+                  hipStream_t stream);
+
+// x[r] = E[tokens[r]]
+void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream);
+// out = a + b (elementwise, n floats; out may alias a)
+void add(const float *a, const float *b, float *out, size_t n, hipStream_t stream);
+// logits[r][t] = n[r] . E[t]
+void head_logits(const float *n, const float *E, float *logits, int rows, int W, int V, hipStream_t stream);
+// The loss kernel of gpu.rs:949-994: per row the f32 cross-entropy and
+// d loss / d logits = (softmax - onehot) / supervised; ignored rows give 0.
+void cross_entropy(const float *logits, const uint32_t *targets, float *dlogits, float *loss, int rows, int V,
+                   int supervised, hipStream_t stream);
+// dn[r][c] = sum_t dlogits[r][t] E[t][c]
+void head_backward(const float *dlogits, const float *E, float *dn, int rows, int W, int V, hipStream_t stream);
+// dE[t][c] = sum_r dlogits[r][t] n[r][c] + sum over rows r of token t of dx[r][c]
+void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
+                        int rows, int W, int V, hipStream_t stream);
+
+struct AdamW {
+    float learning_rate, weight_decay, beta1, beta2, epsilon, correction1, correction2;
+};
+// gpu.rs:1366-1391 over params[begin, end): f32 moments m, v.
+void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,
+          hipStream_t stream);
+
+}  // namespace meshgpt::kern::train

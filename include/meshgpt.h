@@ -100,6 +100,35 @@ int mg_set_parameters(mg_model *model, const float *values, size_t n);
  * each sequence's last row when last_only != 0. */
 int mg_logits(mg_model *model, const uint32_t *tokens, size_t n, size_t sequence, int last_only,
               float *out, size_t out_len);
+/* AdamWOptions (config.rs:258-276); mg_adamw_default fills the reference's
+ * defaults (learning rate 0.003, weight decay 0.01, betas 0.9 and 0.999,
+ * epsilon 1e-8). */
+typedef struct {
+    float learning_rate;
+    float weight_decay;
+    float beta1;
+    float beta2;
+    float epsilon;
+} mg_adamw;
+void mg_adamw_default(mg_adamw *out);
+/* Target id of a row without supervision (IGNORE_TARGET, src/gpt/mod.rs:26). */
+#define MG_IGNORE_TARGET 0xFFFFFFFFu
+/* SpecializedMeshGpt::cross_entropy (gpu.rs:1915-1929): the mean next-token
+ * cross-entropy over rows whose target is not MG_IGNORE_TARGET; n inputs and
+ * n targets in sequences of `sequence`. */
+int mg_cross_entropy(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                     double *loss);
+/* SpecializedMeshGpt::loss_and_gradient (gpu.rs:1931-1946): the loss and the
+ * gradient of every parameter (n_gradient = the parameter count), masked as
+ * config.rs:490-500.  The reference returns the f32 gradient widened to f64;
+ * this returns the f32 values. */
+int mg_loss_and_gradient(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n,
+                         size_t sequence, double *loss, float *gradient, size_t n_gradient);
+/* SpecializedMeshGpt::train_batch_with_optimizer (gpu.rs:1950-2003): the loss
+ * before one AdamW update; the moments and step count persist across calls
+ * until mg_set_parameters resets them. */
+int mg_train_batch(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
+                   const mg_adamw *options, double *loss);
 /* SpecializedMeshGpt::token_embeddings (gpu.rs:2056-2068): vocab_size x width. */
 int mg_token_embeddings(mg_model *model, float *out, size_t n);
 /* SpecializedMeshGpt::hidden_states (gpu.rs:2070-2092): n x width. */

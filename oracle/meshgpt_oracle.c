@@ -304,7 +304,7 @@ static void geometric_codes(const og_config *c, float *out) {
 
 /* src/gpt/config.rs:461-474: the final-layer rows of every projection and FFN
  * mesh that write protected residual coordinates, as [begin, end) offsets */
-static void constrained_range(const og_config *c, size_t group, size_t *begin, size_t *end) {
+void og_constrained_range(const og_config *c, size_t group, size_t *begin, size_t *end) {
     *begin = *end = 0;
     if (c->preserve_features == 0 || group == 0) return;
     size_t kind = (group - 1) % 5;
@@ -476,7 +476,7 @@ static void initialize_mesh_model(const og_config *c, uint64_t seed, float *out)
     }
     for (size_t g = 0; g < ngroups; ++g) {
         size_t begin, end;
-        constrained_range(c, g, &begin, &end);
+        og_constrained_range(c, g, &begin, &end);
         for (size_t i = begin; i < end; ++i) out[offsets[g] + i] = 0.0f;
     }
     free(offsets);

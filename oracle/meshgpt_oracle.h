@@ -95,6 +95,20 @@ int og_hidden_states(const og_config *c, const float *params, const uint32_t *to
 int og_cross_entropy(const og_config *c, const float *params, const uint32_t *inputs,
                      const uint32_t *targets, size_t n, size_t sequence, double *loss);
 
+/* ---- training (meshgpt_oracle_grad.c) ---- */
+/* the gradient mask's range of group `group` (config.rs:461-474), as offsets in the group */
+void og_constrained_range(const og_config *c, size_t group, size_t *begin, size_t *end);
+/* reference.rs:61-89: mean next-token cross-entropy over rows whose target != UINT32_MAX and
+ * its gradient (og_parameter_count entries, masked as config.rs:490-500), by reverse
+ * accumulation over the reference's scalar tape.  0 on success; -1 invalid inputs, -3 a
+ * target outside the vocabulary, -4 no supervised target, -5 non-finite, -6 out of memory. */
+int og_loss_and_gradient(const og_config *c, const float *params, const uint32_t *inputs,
+                         const uint32_t *targets, size_t n, size_t sequence, double *loss, double *gradient);
+/* one f32 AdamW update (gpu.rs:1366-1391) of `count` parameters with moments m, v and the
+ * step's bias corrections 1 - beta^t */
+void og_adam(float *value, float *m, float *v, const float *gradient, size_t count, float learning_rate,
+             float weight_decay, float beta1, float beta2, float epsilon, float correction1, float correction2);
+
 /* ---- generate (reference src/gpt/gpu.rs:2006-2053) ----
  * prompt of P tokens; writes P+count tokens into out.  Every step recomputes the
  * window of at most `context` tokens, exactly as the reference does. */

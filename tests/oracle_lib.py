@@ -86,6 +86,11 @@ def lib():
             "og_equations": (ctypes.c_int, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double,
                                             ctypes.c_uint64, _u32p, _u32p, _u32p, _szp, _szp]),
             "og_row_metrics": (ctypes.c_double, [_f32p, ctypes.c_size_t, ctypes.c_size_t, _szp]),
+            "og_loss_and_gradient": (ctypes.c_int, [cp, _f32p, _u32p, _u32p, ctypes.c_size_t,
+                                                    ctypes.c_size_t, _f64p, _f64p]),
+            "og_adam": (None, [_f32p, _f32p, _f32p, _f32p, ctypes.c_size_t, ctypes.c_float, ctypes.c_float,
+                               ctypes.c_float, ctypes.c_float, ctypes.c_float, ctypes.c_float,
+                               ctypes.c_float]),
         }
         for name, (res, args) in sigs.items():
             fn = getattr(L, name)
@@ -218,6 +223,49 @@ def cross_entropy(c, params, inputs, targets, sequence):
     if rc:
         raise ValueError("oracle rejected the batch")
     return out.value
+
+
+IGNORE = 0xFFFFFFFF  # IGNORE_TARGET (src/gpt/mod.rs:26)
+
+
+def loss_and_gradient(c, params, inputs, targets, sequence):
+    """(loss, gradient) of reference.rs:61-89 by the restated tape; raises
+    ValueError with the oracle's status on a rejected batch."""
+    params, inputs, targets = f32(params), u32(inputs), u32(targets)
+    grad = np.zeros(parameter_count(c), dtype=np.float64)
+    loss = ctypes.c_double()
+    rc = lib().og_loss_and_gradient(ctypes.byref(c), ptr(params, _f32p), ptr(inputs, _u32p),
+                                    ptr(targets, _u32p), inputs.size, sequence, ctypes.byref(loss),
+                                    ptr(grad, _f64p))
+    if rc:
+        raise ValueError(f"oracle rejected the batch ({rc})")
+    return loss.value, grad
+
+
+class Adam:
+    """AdamW state of the GPU path (gpu.rs:1366-1391,1971-2003): f32 moments and
+    f32 running powers of the betas."""
+
+    def __init__(self, params, learning_rate=0.003, weight_decay=0.01, beta1=0.9, beta2=0.999, epsilon=1e-8):
+        self.value = f32(params).copy()
+        self.m = np.zeros_like(self.value)
+        self.v = np.zeros_like(self.value)
+        self.opts = [np.float32(x) for x in (learning_rate, weight_decay, beta1, beta2, epsilon)]
+        self.p1 = np.float32(1.0)
+        self.p2 = np.float32(1.0)
+
+    def step(self, gradient, skip=0):
+        """One update with `gradient` (cast to f32); the first `skip` parameters
+        (a frozen embedding group) are left alone."""
+        lr, wd, b1, b2, eps = self.opts
+        self.p1 = np.float32(self.p1 * b1)
+        self.p2 = np.float32(self.p2 * b2)
+        g = f32(gradient)
+        n = self.value.size - skip
+        lib().og_adam(ptr(self.value[skip:], _f32p), ptr(self.m[skip:], _f32p), ptr(self.v[skip:], _f32p),
+                      ptr(g[skip:], _f32p), n, lr, wd, b1, b2, eps, np.float32(1.0) - self.p1,
+                      np.float32(1.0) - self.p2)
+        return self.value
 
 
 def generate(c, params, prompt, count, temperature, seed, cached=False):

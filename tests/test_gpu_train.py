@@ -1,0 +1,197 @@
+"""GPU parity of the training step (f4): loss, gradients and AdamW through the C ABI.
+
+Mirrors the training half of the reference's GPU verification
+(src/bin/mesh-gpt.rs:324-553): seeded weights (seed 7), x[i] = i % V,
+y[i] = (i + 2) % V and the answer-only targets (the last row of each sequence),
+loss and every gradient within TOL * (1 + |ref|) of the f64 tape oracle (the
+reference allows 5e-4; TOL is 1e-4); then three AdamW steps under the two
+optimizer settings it checks, each step's gradient against the oracle's on the
+GPU's own weights and the update against the f32 AdamW applied to the GPU's
+own gradient.  Rejections carry the reference's messages.
+"""
+import numpy as np
+import pytest
+
+import grokking_abmod_amd as G
+import oracle_lib as O
+from conftest import TOL, assert_close
+
+pytestmark = pytest.mark.gpu
+
+IGN = G.IGNORE_TARGET
+
+
+def configs_for(**kw):
+    return G.GptConfig(**kw), O.config(**kw)
+
+
+# (config, cases) from src/bin/mesh-gpt.rs:651-857 whose head width is at most
+# 128 (the training kernels' limit), plus the demo and grok training shapes.
+TRAIN = [
+    (dict(vocab_size=129, context=3, width=2, heads=1, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(1, 1), (2, 3), (43, 3)]),
+    (dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(1, 1), (1, 3), (2, 3), (43, 3)]),
+    (dict(vocab_size=7, context=5, width=8, heads=2, layers=2, attention_mesh_depth=3, ffn_mesh_depth=4),
+     [(1, 3), (43, 3)]),
+    (dict(vocab_size=9, context=3, width=64, heads=8, layers=1, attention_mesh_depth=1, ffn_mesh_depth=1),
+     [(2, 3), (43, 3)]),
+    (dict(vocab_size=9, context=3, width=128, heads=4, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(2, 3), (43, 3)]),
+    (dict(vocab_size=11, context=5, width=6, heads=3, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(2, 3), (43, 3)]),
+    (dict(vocab_size=257, context=129, width=256, heads=16, layers=3, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(1, 3), (2, 3)]),
+    (dict(vocab_size=5, context=129, width=4, heads=2, layers=1, attention_mesh_depth=1, ffn_mesh_depth=1),
+     [(1, 129)]),
+    (dict(vocab_size=99, context=4, width=32, heads=4, layers=1, attention_mesh_depth=5, ffn_mesh_depth=6,
+          embedding=1, connectivity=1), [(2, 4), (33, 4)]),
+    (dict(vocab_size=9, context=3, width=128, heads=4, layers=1, attention_mesh_depth=8, ffn_mesh_depth=8,
+          connectivity=1), [(2, 3), (43, 3)]),
+    # the demo training shape (docs/mesh-gpt.md:240-243) and the grok shape
+    (dict(vocab_size=26, context=32, width=32, heads=4, layers=2), [(2, 32)]),
+    (dict(vocab_size=99, context=4, width=128, heads=4, layers=2), [(32, 4)]),
+    (dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          rope=0), [(2, 3)]),
+    (dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          qk_norm=0), [(2, 3)]),
+    (dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          xsa=0), [(2, 3)]),
+    (dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          frozen=1), [(2, 3)]),
+]
+
+
+def _ids(cfg):
+    extra = "".join(f"-{k}{v}" for k, v in cfg.items() if k in ("embedding", "connectivity", "rope", "qk_norm",
+                                                                  "xsa", "frozen"))
+    full = dict(attention_mesh_depth=4, ffn_mesh_depth=6)  # GptConfig::default() depths
+    full.update(cfg)
+    return "V{vocab_size}-W{width}-H{heads}-L{layers}-A{attention_mesh_depth}-F{ffn_mesh_depth}".format(**full) + extra
+
+
+def batch(V, b, s):
+    x = np.arange(b * s) % V
+    y = (np.arange(b * s) + 2) % V
+    answer = np.where(np.arange(b * s) % s == s - 1, y, IGN)
+    return x.astype(np.uint32), y.astype(np.uint32), answer.astype(np.uint32)
+
+
+@pytest.mark.parametrize("cfg,cases", TRAIN, ids=[_ids(c) for c, _ in TRAIN])
+def test_loss_and_gradients_match_the_oracle(cfg, cases):
+    g, o = configs_for(**cfg)
+    params = O.initialize(o, 7)
+    with G.MeshGpt(0, g, 7) as model:
+        for b, s in cases:
+            x, y, answer = batch(cfg["vocab_size"], b, s)
+            for targets in (y, answer):
+                ref_loss, ref_grad = O.loss_and_gradient(o, params, x, targets, s)
+                loss, grad = model.loss_and_gradient(x, targets, s)
+                assert abs(loss - ref_loss) <= TOL * (1 + abs(ref_loss)), (b, s, loss, ref_loss)
+                assert_close(grad, ref_grad, what=f"gradient b={b} s={s}")
+                assert abs(model.cross_entropy(x, targets, s) - loss) <= 1e-6 * (1 + abs(loss))
+
+
+@pytest.mark.parametrize("setting", [dict(learning_rate=0.002, weight_decay=0.01),
+                                     dict(learning_rate=0.001, weight_decay=1.0, beta2=0.98)])
+@pytest.mark.parametrize("frozen", [0, 1])
+def test_adamw_steps(setting, frozen):
+    """mesh-gpt.rs:400-470: three steps; each gradient against the oracle on the
+    GPU's weights, each update against f32 AdamW on the GPU's own gradient."""
+    cfg = dict(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+               frozen=frozen)
+    g, o = configs_for(**cfg)
+    x = np.array([0, 1, 3, 2, 4, 1], dtype=np.uint32)
+    y = (np.array([IGN, IGN, 2, IGN, IGN, 0]) if setting.get("beta2") else np.array([1, 3, 2, 4, 1, 0])).astype(
+        np.uint32)
+    opts = G.AdamW(**setting)
+    skip = O.lib().og_embedding_parameter_count(__import__("ctypes").byref(o)) if frozen else 0
+    with G.MeshGpt(0, g, 7) as model:
+        cpu = O.Adam(model.parameters(), **setting)
+        for step in range(3):
+            before = model.parameters()
+            _, expected = O.loss_and_gradient(o, before, x, y, 3)
+            _, grad = model.loss_and_gradient(x, y, 3)
+            assert_close(grad, expected, what=f"step {step} gradient")
+            cpu.value = before.copy()
+            want = cpu.step(grad, skip=skip)
+            model.train_batch(x, y, 3, opts)
+            got = model.parameters()
+            # The same f32 update on the same inputs; only sqrt and division
+            # rounding may differ.
+            np.testing.assert_allclose(got, want, rtol=2e-6, atol=1e-9)
+            if frozen:
+                assert np.array_equal(got[:skip], before[:skip])
+
+
+def test_training_then_inference_uses_the_new_weights():
+    """After train_batch the tables derived from the weights are rebuilt before
+    the next inference call: logits equal the oracle's on the trained weights."""
+    cfg = dict(vocab_size=26, context=32, width=32, heads=4, layers=2)
+    g, o = configs_for(**cfg)
+    x, y, _ = batch(26, 2, 32)
+    with G.MeshGpt(0, g, 7) as model:
+        before = model.logits(x, 32)
+        for _ in range(5):
+            model.train_batch(x, y, 32)
+        params = model.parameters()
+        after = model.logits(x, 32)
+        assert not np.allclose(before, after)
+        assert_close(after, O.logits(o, params, x, 32), what="logits after training")
+        assert_close(model.token_embeddings(), O.token_embeddings(o, params), what="embeddings after training")
+        toks = model.generate_tokens(x[None, :16], 4, 0.0, 7)[0]
+        assert np.array_equal(toks, O.generate(o, params, x[:16], 4, 0.0, 7, cached=True))
+
+
+def test_training_trajectory_follows_the_oracle():
+    """Twenty AdamW steps of the grok shape (answer-only targets): the GPU's
+    losses track the oracle's (f64 gradients, f32 AdamW) step by step."""
+    cfg = dict(vocab_size=99, context=4, width=128, heads=4, layers=2)
+    g, o = configs_for(**cfg)
+    rng = np.random.default_rng(11)
+    a, b = rng.integers(0, 97, 64), rng.integers(0, 97, 64)
+    x = np.stack([a, np.full(64, 97), b, np.full(64, 98)], 1).reshape(-1).astype(np.uint32)
+    y = np.stack([np.full(64, IGN), np.full(64, IGN), np.full(64, IGN), (a + b) % 97], 1).reshape(-1).astype(np.uint32)
+    setting = dict(learning_rate=0.001, weight_decay=1.0, beta2=0.98)
+    with G.MeshGpt(0, g, 7) as model:
+        cpu = O.Adam(model.parameters(), **setting)
+        opts = G.AdamW(**setting)
+        for step in range(20):
+            ref_loss, ref_grad = O.loss_and_gradient(o, cpu.value, x, y, 4)
+            loss = model.train_batch(x, y, 4, opts)
+            assert abs(loss - ref_loss) <= 1e-4 * (1 + abs(ref_loss)), (step, loss, ref_loss)
+            cpu.step(ref_grad)
+        np.testing.assert_allclose(model.parameters(), cpu.value, rtol=0, atol=2e-4)
+
+
+def test_training_rejections_carry_the_reference_messages():
+    g, _ = configs_for(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2,
+                       ffn_mesh_depth=2)
+    x = np.array([0, 1, 3], dtype=np.uint32)
+    with G.MeshGpt(0, g, 7) as model:
+        cases = [
+            (lambda: model.loss_and_gradient(x, np.full(3, IGN, np.uint32), 3),
+             "batch must contain at least one supervised target"),
+            (lambda: model.loss_and_gradient(x, np.array([0, 1, 9], np.uint32), 3),
+             "target ID is outside the vocabulary"),
+            (lambda: model.cross_entropy(np.array([0, 7, 1], np.uint32), x, 3), "token ID is outside the vocabulary"),
+            (lambda: model.train_batch(x, x, 3, G.AdamW(learning_rate=0.0)),
+             "AdamW requires finite positive learning rate/epsilon, nonnegative decay, and betas in [0, 1)"),
+            (lambda: model.train_batch(x, x, 3, G.AdamW(beta2=1.0)),
+             "AdamW requires finite positive learning rate/epsilon, nonnegative decay, and betas in [0, 1)"),
+        ]
+        for call, message in cases:
+            with pytest.raises(G.MeshGptError) as err:
+                call()
+            assert message in str(err.value)
+        # A rejected step changes nothing.
+        before = model.parameters()
+        with pytest.raises(G.MeshGptError):
+            model.train_batch(x, x, 3, G.AdamW(epsilon=0.0))
+        assert np.array_equal(model.parameters(), before)
+    wide, _ = configs_for(vocab_size=7, context=3, width=1024, heads=4, layers=1, attention_mesh_depth=2,
+                          ffn_mesh_depth=2)
+    with G.MeshGpt(0, wide, 7) as model:
+        with pytest.raises(G.MeshGptError) as err:
+            model.loss_and_gradient(np.zeros(3, np.uint32), np.zeros(3, np.uint32), 3)
+        assert err.value.status == G.MG_UNSUPPORTED
