@@ -280,6 +280,46 @@ def high_figure(hip, decode_steps=64):
             "decode_hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
+def training_figure(steps=30, warmup=10, trials=3):
+    """The reference's training benchmark (src/bin/mesh-gpt-bench.rs:29-237,
+    timing protocol docs/cuda-performance.md:25-35): add mod 97 with the seeded
+    half split, the first 512 training equations (i % split), W128 H4 L2 A4 F6
+    V99, context 4, AdamW lr 0.001, weight decay 1, betas 0.9/0.98; each trial
+    restores the initial weights, runs `warmup` untimed updates, then times
+    `steps` updates by the host clock, including the final parameter download."""
+    config = G.GptConfig(vocab_size=99, context=4, width=128, heads=4, layers=2)
+    n_train, _ = G.equation_split()
+    inputs, targets = G.equation_batch(np.arange(512) % n_train)
+    opts = G.AdamW(learning_rate=0.001, weight_decay=1.0, beta2=0.98)
+    results = []
+    with G.MeshGpt(0, config, 7) as model:
+        initial = model.parameters()
+        for _ in range(trials):
+            model.set_parameters(initial)
+            for _ in range(warmup):
+                model.train_batch(inputs, targets, 4, opts)
+            model.parameters()
+            t0 = time.perf_counter()
+            first = last = 0.0
+            for step in range(steps):
+                last = model.train_batch(inputs, targets, 4, opts)
+                if step == 0:
+                    first = last
+            model.parameters()
+            ms = 1000.0 * (time.perf_counter() - t0) / steps
+            results.append((ms, first, last))
+    ms = float(np.median([r[0] for r in results]))
+    return {"workload": "reference training benchmark (mesh-gpt-bench defaults): add mod 97, 512 training equations, "
+                        "W128 H4 L2 A4 F6 V99 ctx 4, AdamW lr 1e-3 wd 1 betas 0.9/0.98; "
+                        f"{trials} trials of {warmup} warm-up + {steps} timed updates, parameter download included",
+            "ms_per_update": round(ms, 4), "trials_ms": [round(r[0], 4) for r in results],
+            "tokens_per_s": round(len(inputs) * 1000.0 / ms, 1),
+            "ce_first_last": [round(results[0][1], 6), round(results[0][2], 6)],
+            "published_ms_per_update": 5.759,
+            "published_hardware": "RTX 3050 Laptop GPU (docs/cuda-performance.md:36-61)",
+            "speedup_vs_published": round(5.759 / ms, 2)}
+
+
 def main():
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
@@ -289,7 +329,7 @@ def main():
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-pmc", action="store_true")
     parser.add_argument("--no-extra", action="store_true", help="config 3 only")
-    parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5"],
+    parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5", "training"],
                         help="print only that figure (for profiling one workload)")
     parser.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
@@ -306,7 +346,8 @@ def main():
 
     if args.only:
         figures = {"batch1": lambda: batch1_figure(Hip()), "config2": symbolic_figure,
-                   "config4": lambda: long_figure(Hip()), "config5": lambda: high_figure(Hip())}
+                   "config4": lambda: long_figure(Hip()), "config5": lambda: high_figure(Hip()),
+                   "training": training_figure}
         print(json.dumps({args.only: figures[args.only]()}))
         return
     # The counter runs go first, while this process has not touched the GPU:
@@ -391,6 +432,7 @@ def main():
         result["config2"] = symbolic_figure()
         result["config4"] = long_figure(hip)
         result["config5"] = high_figure(hip)
+        result["training"] = training_figure()
     # Measured copy roofline of this box (read + write bytes of a plain copy kernel).
     result["copy_gbps"] = round(G.copy_bandwidth(1 << 30, 10), 1)
     if not args.no_cpu:

@@ -28,6 +28,7 @@ EXPORTS = (
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
     "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_sample_logits_noalloc", "mg_expf",
     "mg_adamw_default", "mg_cross_entropy", "mg_loss_and_gradient", "mg_train_batch",
+    "mg_equation_split", "mg_equation_batch",
 )
 
 IGNORE_TARGET = 0xFFFFFFFF  # MG_IGNORE_TARGET (src/gpt/mod.rs:26)
@@ -143,6 +144,9 @@ def lib():
         "mg_cross_entropy": (i, [vp, _u32p, _u32p, sz, sz, ctypes.POINTER(ctypes.c_double)]),
         "mg_loss_and_gradient": (i, [vp, _u32p, _u32p, sz, sz, ctypes.POINTER(ctypes.c_double), _f32p, sz]),
         "mg_train_batch": (i, [vp, _u32p, _u32p, sz, sz, vp, ctypes.POINTER(ctypes.c_double)]),
+        "mg_equation_split": (i, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, u64, _szp, _szp]),
+        "mg_equation_batch": (i, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, u64, i, _szp, sz, _u32p,
+                                  _u32p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -228,6 +232,23 @@ def device_expf(x, device=0):
 def calibration_copy(nbytes, device=0):
     """One warm-up and one timed launch of calibration_copy over nbytes."""
     return copy_bandwidth(nbytes, 1, device)
+
+
+def equation_split(modulus=97, operation=0, train_fraction=0.5, seed=7):
+    """EquationDataset::new (grokking.rs:128-186): (training, validation) sizes."""
+    a, b = ctypes.c_size_t(), ctypes.c_size_t()
+    _check(lib().mg_equation_split(modulus, operation, train_fraction, seed, ctypes.byref(a), ctypes.byref(b)))
+    return a.value, b.value
+
+
+def equation_batch(indices, validation=False, modulus=97, operation=0, train_fraction=0.5, seed=7):
+    """EquationDataset::batch (grokking.rs:225-258): (inputs, targets), 4 rows an equation."""
+    idx = np.ascontiguousarray(indices, dtype=np.uintp).reshape(-1)
+    inputs = np.empty(4 * max(idx.size, 1), dtype=np.uint32)
+    targets = np.empty_like(inputs)
+    _check(lib().mg_equation_batch(modulus, operation, train_fraction, seed, int(validation),
+                                   idx.ctypes.data_as(_szp), idx.size, _p(inputs, _u32p), _p(targets, _u32p)))
+    return inputs[:4 * idx.size], targets[:4 * idx.size]
 
 
 class MeshGpt:

@@ -188,6 +188,26 @@ int mg_logits(mg_model *model, const uint32_t *tokens, size_t n, size_t sequence
     });
 }
 
+int mg_equation_split(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed, size_t *n_train,
+                      size_t *n_valid) {
+    return guarded([&] {
+        require(n_train != nullptr && n_valid != nullptr, "outputs must not be null");
+        const EquationDataset d = EquationDataset::build(modulus, operation, train_fraction, seed);
+        *n_train = d.training.size();
+        *n_valid = d.validation.size();
+    });
+}
+
+int mg_equation_batch(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed, int validation,
+                      const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets) {
+    return guarded([&] {
+        require((indices != nullptr || n == 0) && inputs != nullptr && targets != nullptr,
+                "indices and outputs must not be null");
+        EquationDataset::build(modulus, operation, train_fraction, seed)
+            .batch(validation != 0, indices, n, inputs, targets);
+    });
+}
+
 void mg_adamw_default(mg_adamw *out) {
     if (!out) return;
     const AdamWOptions d;

@@ -138,6 +138,73 @@ std::vector<uint32_t> residue_permutation(size_t modulus, uint64_t seed) {
     return tokens;
 }
 
+namespace {
+
+uint64_t modular_inverse(uint64_t value, uint64_t modulus) {  // grokking.rs:94-106 (Fermat)
+    uint64_t result = 1, base = value % modulus;
+    for (uint64_t e = modulus - 2; e; e >>= 1) {
+        if (e & 1) result = result * base % modulus;
+        base = base * base % modulus;
+    }
+    return result;
+}
+
+// ModularOperation::apply (grokking.rs:52-67), codes in declaration order.
+size_t apply_operation(uint32_t op, uint64_t a, uint64_t b, uint64_t p) {
+    switch (op) {
+    case 0: return (a + b) % p;
+    case 1: return a * b % p;
+    case 2: return (a + p - b) % p;
+    case 3: return a * modular_inverse(b, p) % p;
+    case 4: return b % 2 == 1 ? a * modular_inverse(b, p) % p : (a + p - b) % p;
+    case 5: return (a * a + b * b) % p;
+    case 6: return (a * a + a * b + b * b) % p;
+    case 7: return (a * a + a * b + b * b + a) % p;
+    case 8: return (a * a * a + a * b) % p;
+    default: return (a * a * a + a * b * b + b) % p;
+    }
+}
+
+}  // namespace
+
+EquationDataset EquationDataset::build(size_t modulus, uint32_t operation, double train_fraction, uint64_t seed) {
+    bool prime = modulus >= 2 && modulus <= 254;  // MAX_VOCAB (256, src/gpt/mod.rs:29) - 2
+    for (size_t d = 2; prime && d < modulus; ++d) prime = modulus % d != 0;
+    if (!prime) throw Error("modulus must be a prime in 2..254 (two vocabulary slots are reserved)");
+    if (operation > 9) throw Error("unknown modular operation");
+    if (!std::isfinite(train_fraction) || !(train_fraction > 0.0 && train_fraction < 1.0))
+        throw Error("train fraction must be finite and strictly between 0 and 1");
+    EquationDataset d;
+    d.modulus = modulus;
+    d.residue_tokens = residue_permutation(modulus, seed);
+    std::vector<Equation> all;
+    for (size_t a = 0; a < modulus; ++a)
+        for (size_t b = operation == 3 ? 1 : 0; b < modulus; ++b)
+            all.push_back({a, b, apply_operation(operation, a, b, modulus)});
+    const size_t split = size_t(std::floor(double(all.size()) * train_fraction));
+    if (split < 2 || split >= all.size())
+        throw Error("split needs at least two training equations and one validation equation");
+    Random splits(seed ^ 0x73706c6974730002ULL);
+    for (size_t end = all.size(); end-- > 1;) std::swap(all[end], all[splits.index(end + 1)]);
+    d.training.assign(all.begin(), all.begin() + split);
+    d.validation.assign(all.begin() + split, all.end());
+    return d;
+}
+
+void EquationDataset::batch(bool validation, const size_t *indices, size_t n, uint32_t *inputs,
+                            uint32_t *targets) const {
+    if (n == 0 || n > kMaxRows / 4) throw Error("equation batches need 1..32768 examples");
+    const std::vector<Equation> &split = validation ? this->validation : training;
+    for (size_t i = 0; i < n; ++i) {
+        if (indices[i] >= split.size()) throw Error("equation index is outside the split");
+        const Equation &e = split[indices[i]];
+        const uint32_t row[4] = {residue_tokens[e.a], uint32_t(modulus), residue_tokens[e.b], uint32_t(modulus + 1)};
+        const uint32_t want[4] = {kIgnoreTarget, kIgnoreTarget, kIgnoreTarget, residue_tokens[e.answer]};
+        std::copy(row, row + 4, inputs + 4 * i);
+        std::copy(want, want + 4, targets + 4 * i);
+    }
+}
+
 size_t primitive_root(size_t prime) {
     if (prime == 2) return 1;
     for (size_t g = 2; g < prime; ++g) {

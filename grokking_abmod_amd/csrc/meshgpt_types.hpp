@@ -155,6 +155,21 @@ struct Layout {
 std::vector<float> token_codes(const GptConfig &config);
 // The residue token permutation of the grok dataset (grokking.rs:260-271).
 std::vector<uint32_t> residue_permutation(size_t modulus, uint64_t seed);
+// EquationDataset (grokking.rs:116-258): the whole table of a modular
+// operation (codes in ModularOperation order: 0 add, 1 multiply, 2 subtract,
+// 3 divide, ...), split by a seeded shuffle; batches are a, op, b, '=' with
+// only the answer supervised.
+struct EquationDataset {
+    struct Equation {
+        size_t a, b, answer;
+    };
+    size_t modulus = 0;
+    std::vector<Equation> training, validation;
+    std::vector<uint32_t> residue_tokens;
+    static EquationDataset build(size_t modulus, uint32_t operation, double train_fraction, uint64_t seed);
+    // inputs and targets of 4 * n rows for the split's equations `indices`
+    void batch(bool validation, const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets) const;
+};
 // The smallest primitive root of a prime (geometry.rs:166-184).
 size_t primitive_root(size_t prime);
 // Table parameters of a mesh-embedding model (config.rs:505-547).

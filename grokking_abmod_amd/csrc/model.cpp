@@ -121,9 +121,21 @@ struct MeshGpt::Impl {
     // Training (gpu.rs:1915-2003): the activations of the last forward, the
     // gradient, AdamW's moments and the running powers of its betas (reset
     // with the weights, gpu.rs:1856-1872).
-    DevBuf tact, tgrad, tm, tv, tpart, ttok, ttgt;
+    DevBuf tact, tgrad, tm, tv, tpart, ttok, ttgt, thyper;
+    kern::train::StepScalars hyper{};  // host copy uploaded before each step (kept alive for the async copy)
     float beta1_power = 1.0f, beta2_power = 1.0f;
     bool derived_stale = false;  // E and the decode tables lag the weights
+    // The captured training step and what it was captured for.
+    struct TrainKey {
+        size_t n = 0, sequence = 0;
+        float lr = 0, wd = 0, b1 = 0, b2 = 0, eps = 0;
+        bool operator==(const TrainKey &o) const {
+            return n == o.n && sequence == o.sequence && lr == o.lr && wd == o.wd && b1 == o.b1 && b2 == o.b2 &&
+                   eps == o.eps;
+        }
+    } tkey;
+    hipGraph_t tgraph = nullptr;
+    hipGraphExec_t texec = nullptr;
 
     // Events around the kernels of the last logits / hidden_states / prefill
     // call (last_call_ms).
@@ -139,6 +151,7 @@ struct MeshGpt::Impl {
 
     ~Impl() {
         drop_graph();
+        drop_train_graph();
         for (hipEvent_t e : call_ev)
             if (e) (void)hipEventDestroy(e);
         for (int i = 0; i < kMaxSlices - 1; ++i) {
@@ -561,7 +574,7 @@ struct MeshGpt::Impl {
         size_t n1, inv1, qs, ks, vs, qr, kr, qinv, kinv, y, lse, z, ps, xm, inv2, n2, fs;
     };
     struct TrainPlan {
-        size_t es, x, invf, nf, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
+        size_t es, x, invf, nf, et, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
         std::vector<TrainBlock> blocks;
     };
 
@@ -600,6 +613,7 @@ struct MeshGpt::Impl {
         }
         p.invf = take(R);
         p.nf = take(RW);
+        p.et = take(V * W);
         p.logits = take(R * V);
         p.dlogits = take(R * V);
         p.loss = take(R);
@@ -639,32 +653,62 @@ struct MeshGpt::Impl {
         return supervised;
     }
 
-    // The training forward over n rows (reference.rs:104-228) keeping every
-    // activation, the loss kernel, and with `backward` the gradient of the
-    // mean loss in tgrad (reference.rs:61-89, masked as config.rs:490-500).
-    // Returns the mean loss over the supervised rows.
-    double train_pass(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence, bool backward) {
+    // Buffers of a training step over n rows (grown, never shrunk); a
+    // reallocation invalidates the captured step.
+    void train_prepare(size_t n) {
         namespace T = kern::train;
-        check_trainable();
-        const size_t supervised = validate_batch(inputs, targets, n, sequence);
-        activate();
-        const int R = int(n), W = int(cfg.width), H = int(cfg.heads), V = int(cfg.vocab_size), seq = int(sequence);
-        const int A = int(cfg.attention_mesh_depth), F = int(cfg.ffn_mesh_depth), L = int(cfg.layers);
-        const size_t RW = n * cfg.width, P = layout.count();
-        const TrainPlan p = train_plan(n);
-        tact.ensure(p.total * 4);
-        const T::Mesh ma{W, A, shape.butterfly, shape.log2w}, mf{W, F, shape.butterfly, shape.log2w};
-        tpart.ensure(std::max({T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
-                               T::mesh_partial_floats(ma, V)}) * 4);
-        tgrad.ensure(P * 4);
-        ttok.ensure(n * 4);
-        ttgt.ensure(n * 4);
+        const int R = int(n), W = int(cfg.width), V = int(cfg.vocab_size);
+        const T::Mesh ma{W, int(cfg.attention_mesh_depth), shape.butterfly, shape.log2w};
+        const T::Mesh mf{W, int(cfg.ffn_mesh_depth), shape.butterfly, shape.log2w};
+        const size_t P = layout.count();
+        bool grown = tact.ensure(train_plan(n).total * 4);
+        grown |= tpart.ensure(std::max({T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
+                                        T::mesh_partial_floats(ma, V), T::embedding_partial_floats(R, W, V)}) *
+                              4);
+        grown |= tgrad.ensure(P * 4);
+        grown |= ttok.ensure(n * 4);
+        grown |= ttgt.ensure(n * 4);
+        grown |= thyper.ensure(sizeof(T::StepScalars));
+        if (tm.ensure(P * 4) | tv.ensure(P * 4)) {
+            grown = true;
+            check(hipMemsetAsync(tm.p, 0, tm.bytes, stream), "clear moments");
+            check(hipMemsetAsync(tv.p, 0, tv.bytes, stream), "clear moments");
+        }
+        if (grown) drop_train_graph();
+    }
+
+    void drop_train_graph() {
+        if (texec) (void)hipGraphExecDestroy(texec);
+        if (tgraph) (void)hipGraphDestroy(tgraph);
+        texec = nullptr;
+        tgraph = nullptr;
+    }
+
+    // Uploads a step's inputs, targets and scalars (outside any graph).
+    void train_upload(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t supervised, float c1,
+                      float c2) {
         check(hipMemcpyAsync(ttok.p, inputs, n * 4, hipMemcpyHostToDevice, stream), "upload inputs");
         check(hipMemcpyAsync(ttgt.p, targets, n * 4, hipMemcpyHostToDevice, stream), "upload targets");
+        hyper = kern::train::StepScalars{c1, c2, 1.0f / float(supervised), 0};
+        check(hipMemcpyAsync(thyper.p, &hyper, sizeof(hyper), hipMemcpyHostToDevice, stream), "upload scalars");
+    }
+
+    // The training forward over n rows (reference.rs:104-228) keeping every
+    // activation, the loss kernel, and with `backward` the gradient of the
+    // mean loss in tgrad (reference.rs:61-89, masked as config.rs:490-500):
+    // kernels only, enqueued on the stream (so a step can be captured).
+    void train_enqueue(size_t n, size_t sequence, bool backward) {
+        namespace T = kern::train;
+        const int R = int(n), W = int(cfg.width), H = int(cfg.heads), V = int(cfg.vocab_size), seq = int(sequence);
+        const int A = int(cfg.attention_mesh_depth), F = int(cfg.ffn_mesh_depth), L = int(cfg.layers);
+        const size_t RW = n * cfg.width;
+        const TrainPlan p = train_plan(n);
+        const T::Mesh ma{W, A, shape.butterfly, shape.log2w}, mf{W, F, shape.butterfly, shape.log2w};
         float *act = tact.as<float>(), *part = tpart.as<float>(), *grad = tgrad.as<float>();
         const float *w = params.as<float>();
         const uint32_t *tok = ttok.as<uint32_t>();
         const float2 *table = rope.as<float2>();
+        auto *sc = thyper.as<T::StepScalars>();
         auto at = [&](size_t o) { return act + o; };
         auto group = [&](size_t id) { return layout.groups[id].offset; };
         const size_t emb = group(layout.embedding);
@@ -686,22 +730,13 @@ struct MeshGpt::Impl {
             T::mesh_forward(ma, at(k.n1), at(k.ks), w + group(g.key), R, stream);
             T::mesh_forward(ma, at(k.n1), at(k.vs), w + group(g.value), R, stream);
             // reference.rs:174-193: QK-Norm, then RoPE, each when switched on
-            const std::pair<size_t, size_t> qk[2] = {{k.qs, k.qr}, {k.ks, k.kr}};
-            const size_t qkinv[2] = {k.qinv, k.kinv};
-            for (int m = 0; m < 2; ++m) {
-                if (cfg.qk_norm)
-                    T::rmsnorm_forward(last(qk[m].first, A), at(qk[m].second), at(qkinv[m]), R, W, H, stream);
-                else
-                    check(hipMemcpyAsync(at(qk[m].second), last(qk[m].first, A), RW * 4, hipMemcpyDeviceToDevice,
-                                         stream),
-                          "copy");
-                if (cfg.rope) T::rope(at(qk[m].second), table, R, seq, W, H, false, stream);
-            }
+            T::qk_forward(last(k.qs, A), at(k.qr), at(k.qinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+            T::qk_forward(last(k.ks, A), at(k.kr), at(k.kinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
             T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), R, seq, W, H, stream);
             if (cfg.xsa)
                 T::xsa_forward(at(k.y), last(k.vs, A), at(k.z), R, W, H, stream);
             else
-                check(hipMemcpyAsync(at(k.z), at(k.y), RW * 4, hipMemcpyDeviceToDevice, stream), "copy");
+                T::copy(at(k.y), at(k.z), RW, stream);
             T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);
             T::add(X(b), last(k.ps, A), at(k.xm), RW, stream);
             T::rmsnorm_forward(at(k.xm), at(k.n2), at(k.inv2), R, W, 1, stream);
@@ -709,66 +744,74 @@ struct MeshGpt::Impl {
             T::add(at(k.xm), last(k.fs, F), X(b + 1), RW, stream);
         }
         T::rmsnorm_forward(X(L), at(p.nf), at(p.invf), R, W, 1, stream);
-        T::head_logits(at(p.nf), Ev, at(p.logits), R, W, V, stream);
-        T::cross_entropy(at(p.logits), ttgt.as<uint32_t>(), at(p.dlogits), at(p.loss), R, V, int(supervised),
-                         stream);
+        T::head_logits(at(p.nf), Ev, at(p.et), at(p.logits), R, W, V, stream);
+        T::cross_entropy(at(p.logits), ttgt.as<uint32_t>(), at(p.dlogits), at(p.loss), R, V, sc, stream);
+        if (!backward) return;
 
-        if (backward) {
-            float *dx = at(p.dx), *dn = at(p.dn), *dq = at(p.dq), *dk = at(p.dk), *dv = at(p.dv);
-            float *dy = at(p.dy), *dt = at(p.dt);
-            T::head_backward(at(p.dlogits), Ev, dn, R, W, V, stream);
-            T::rmsnorm_backward(X(L), at(p.invf), dn, dx, false, R, W, 1, stream);
-            for (int b = L - 1; b >= 0; --b) {
-                const TrainBlock &k = p.blocks[b];
-                const Block &g = layout.blocks[b];
-                // x_{b+1} = xm + ffn(rmsnorm(xm)); xm = x_b + proj(attention)
-                T::mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, false, w + group(g.ffn), part, grad + group(g.ffn),
-                                 R, stream);
-                T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
-                T::mesh_backward(ma, at(k.z), at(k.ps), dx, dt, false, w + group(g.projection), part,
-                                 grad + group(g.projection), R, stream);
-                if (cfg.xsa) {
-                    T::xsa_backward(at(k.y), last(k.vs, A), dt, dy, dv, R, W, H, stream);
-                } else {
-                    check(hipMemcpyAsync(dy, dt, RW * 4, hipMemcpyDeviceToDevice, stream), "copy");
-                    check(hipMemsetAsync(dv, 0, RW * 4, stream), "clear");
-                }
-                T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dy, dq, dk, dv,
-                                      at(p.dsum), R, seq, W, H, stream);
-                float *dqk[2] = {dq, dk};
-                const size_t pre[2] = {k.qs, k.ks}, qkinv[2] = {k.qinv, k.kinv};
-                for (int m = 0; m < 2; ++m) {
-                    if (cfg.rope) T::rope(dqk[m], table, R, seq, W, H, true, stream);
-                    if (cfg.qk_norm)
-                        T::rmsnorm_backward(last(pre[m], A), at(qkinv[m]), dqk[m], dqk[m], false, R, W, H, stream);
-                }
-                T::mesh_backward(ma, at(k.n1), at(k.qs), dq, dn, false, w + group(g.query), part,
-                                 grad + group(g.query), R, stream);
-                T::mesh_backward(ma, at(k.n1), at(k.ks), dk, dn, true, w + group(g.key), part, grad + group(g.key),
-                                 R, stream);
-                T::mesh_backward(ma, at(k.n1), at(k.vs), dv, dn, true, w + group(g.value), part,
-                                 grad + group(g.value), R, stream);
-                T::rmsnorm_backward(X(b), at(k.inv1), dn, dx, true, R, W, 1, stream);
+        float *dx = at(p.dx), *dn = at(p.dn), *dq = at(p.dq), *dk = at(p.dk), *dv = at(p.dv);
+        float *dy = at(p.dy), *dt = at(p.dt);
+        T::head_backward(at(p.dlogits), Ev, dn, R, W, V, stream);
+        T::rmsnorm_backward(X(L), at(p.invf), dn, dx, false, R, W, 1, stream);
+        for (int b = L - 1; b >= 0; --b) {
+            const TrainBlock &k = p.blocks[b];
+            const Block &g = layout.blocks[b];
+            // x_{b+1} = xm + ffn(rmsnorm(xm)); xm = x_b + proj(attention)
+            T::mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, false, w + group(g.ffn), part, grad + group(g.ffn), R,
+                             stream);
+            T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
+            T::mesh_backward(ma, at(k.z), at(k.ps), dx, dt, false, w + group(g.projection), part,
+                             grad + group(g.projection), R, stream);
+            if (cfg.xsa) {
+                T::xsa_backward(at(k.y), last(k.vs, A), dt, dy, dv, R, W, H, stream);
+            } else {
+                T::copy(dt, dy, RW, stream);
+                T::fill(dv, 0.0f, RW, stream);
             }
-            // The tied vectors collect the head's gradient and the gathered rows'.
-            T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), R, W, V, stream);
-            if (cfg.embedding == TokenEmbedding::Mesh)
-                T::mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, false, w + emb, part,
-                                 grad + emb, V, stream);
-            else
-                check(hipMemcpyAsync(grad + emb, at(p.dE), size_t(V) * W * 4, hipMemcpyDeviceToDevice, stream),
-                      "copy");
-            if (cfg.geometry.frozen)
-                check(hipMemsetAsync(grad + emb, 0, cfg.embedding_parameter_count() * 4, stream), "mask");
+            T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dy, dq, dk, dv, at(p.dsum),
+                                  R, seq, W, H, stream);
+            if (cfg.rope || cfg.qk_norm) {
+                T::qk_backward(dq, last(k.qs, A), at(k.qinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+                T::qk_backward(dk, last(k.ks, A), at(k.kinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+            }
+            T::mesh_backward(ma, at(k.n1), at(k.qs), dq, dn, false, w + group(g.query), part, grad + group(g.query),
+                             R, stream);
+            T::mesh_backward(ma, at(k.n1), at(k.ks), dk, dn, true, w + group(g.key), part, grad + group(g.key), R,
+                             stream);
+            T::mesh_backward(ma, at(k.n1), at(k.vs), dv, dn, true, w + group(g.value), part, grad + group(g.value),
+                             R, stream);
+            T::rmsnorm_backward(X(b), at(k.inv1), dn, dx, true, R, W, 1, stream);
         }
-        // gpu.rs:2296-2313: per-row f32 losses summed in f64 on the host.
+        // The tied vectors collect the head's gradient and the gathered rows'.
+        T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), part, R, W, V, stream);
+        if (cfg.embedding == TokenEmbedding::Mesh)
+            T::mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, false, w + emb, part, grad + emb, V,
+                             stream);
+        else
+            T::copy(at(p.dE), grad + emb, size_t(V) * W, stream);
+        if (cfg.geometry.frozen) T::fill(grad + emb, 0.0f, cfg.embedding_parameter_count(), stream);
+    }
+
+    // gpu.rs:2296-2313: the per-row f32 losses summed in f64 on the host.
+    double train_loss(size_t n, size_t supervised) {
         std::vector<float> rows(n);
-        check(hipMemcpyAsync(rows.data(), at(p.loss), n * 4, hipMemcpyDeviceToHost, stream), "download loss");
+        check(hipMemcpyAsync(rows.data(), tact.as<float>() + train_plan(n).loss, n * 4, hipMemcpyDeviceToHost,
+                             stream),
+              "download loss");
         sync();
         validate_finite(rows.data(), rows.size(), "cross-entropy");
         double total = 0.0;
         for (float v : rows) total += double(v);
         return total / double(supervised);
+    }
+
+    double train_pass(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence, bool backward) {
+        check_trainable();
+        const size_t supervised = validate_batch(inputs, targets, n, sequence);
+        activate();
+        train_prepare(n);
+        train_upload(inputs, targets, n, supervised, 1.0f, 1.0f);
+        train_enqueue(n, sequence, backward);
+        return train_loss(n, supervised);
     }
 
     std::vector<float> gradient() {
@@ -779,24 +822,44 @@ struct MeshGpt::Impl {
     }
 
     // gpu.rs:1971-2003: the gradient, then one AdamW update of every group
-    // (the embedding group stays when the geometry is frozen).
+    // (the embedding group stays when the geometry is frozen).  The whole
+    // step is captured once per (rows, sequence, options) as a HIP graph and
+    // replayed; a non-finite loss leaves the weights, moments and step count
+    // as they were.
     double train_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
                        const AdamWOptions &o) {
         o.validate();
-        const double loss = train_pass(inputs, targets, n, sequence, true);
-        const size_t P = layout.count();
-        if (tm.ensure(P * 4) | tv.ensure(P * 4)) {
-            check(hipMemsetAsync(tm.p, 0, tm.bytes, stream), "clear moments");
-            check(hipMemsetAsync(tv.p, 0, tv.bytes, stream), "clear moments");
+        check_trainable();
+        const size_t supervised = validate_batch(inputs, targets, n, sequence);
+        activate();
+        train_prepare(n);
+        const float p1 = beta1_power * o.beta1, p2 = beta2_power * o.beta2;
+        train_upload(inputs, targets, n, supervised, 1.0f - p1, 1.0f - p2);
+        const TrainKey key{n, sequence, o.learning_rate, o.weight_decay, o.beta1, o.beta2, o.epsilon};
+        auto enqueue = [&] {
+            train_enqueue(n, sequence, true);
+            const size_t begin = cfg.geometry.frozen ? cfg.embedding_parameter_count() : 0;
+            kern::train::adam(params.as<float>(), tm.as<float>(), tv.as<float>(), tgrad.as<float>(), begin,
+                              layout.count(), {o.learning_rate, o.weight_decay, o.beta1, o.beta2, o.epsilon},
+                              thyper.as<kern::train::StepScalars>(), stream);
+        };
+        if (use_graph) {
+            if (!texec || !(key == tkey)) {
+                drop_train_graph();
+                check(hipStreamBeginCapture(stream, hipStreamCaptureModeThreadLocal), "begin capture");
+                enqueue();
+                check(hipStreamEndCapture(stream, &tgraph), "end capture");
+                check(hipGraphInstantiate(&texec, tgraph, nullptr, nullptr, 0), "instantiate training graph");
+                tkey = key;
+            }
+            check(hipGraphLaunch(texec, stream), "replay training step");
+        } else {
+            enqueue();
         }
-        beta1_power *= o.beta1;
-        beta2_power *= o.beta2;
-        const kern::train::AdamW a{o.learning_rate, o.weight_decay, o.beta1,  o.beta2,
-                                   o.epsilon,       1.0f - beta1_power, 1.0f - beta2_power};
-        const size_t begin = cfg.geometry.frozen ? cfg.embedding_parameter_count() : 0;
-        kern::train::adam(params.as<float>(), tm.as<float>(), tv.as<float>(), tgrad.as<float>(), begin, P, a, stream);
-        sync();
         derived_stale = true;
+        const double loss = train_loss(n, supervised);  // throws (weights unchanged) on a non-finite loss
+        beta1_power = p1;
+        beta2_power = p2;
         return loss;
     }
 

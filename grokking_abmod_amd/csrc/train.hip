@@ -21,6 +21,7 @@ namespace {
 constexpr float kRmsEps = 1e-5f;                                         // src/gpt/mod.rs:38
 constexpr float kXsaFloor = float(double(1e-12f) * double(1e-12f));      // XSA_EPSILON^2
 constexpr int kThreads = 256;
+constexpr int kRowThreads = 64;  // per-(row, head) kernels: one wave per workgroup spreads few rows widely
 
 __device__ __forceinline__ float elu(float z) { return z >= 0.0f ? z : expm1f(z); }
 
@@ -45,8 +46,8 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_forward_kernel(Mesh m, const f
             if (c < W) {
                 int p = c + stride_of(m, l);
                 if (p >= W) p -= W;
-                const float *wl = w + size_t(l) * 2 * W;
-                float z = cur[c] * wl[2 * c] + cur[p] * wl[2 * c + 1];
+                const float2 wl = reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W)[c];
+                float z = cur[c] * wl.x + cur[p] * wl.y;
                 if (l + 1 < m.depth) z = elu(z);
                 nxt[c] = z;
                 stack[(size_t(l) * rows + r) * W + c] = z;
@@ -59,41 +60,58 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_forward_kernel(Mesh m, const f
     }
 }
 
-// Each workgroup takes rows blockIdx.x, blockIdx.x + gridDim.x, ...; thread c
-// carries d loss / d (channel c) down the layers and adds its two weights'
-// gradients over those rows in registers.
+// Rows per workgroup of the mesh backward: sub-blocks of SUB = W rounded up to
+// 64 threads, one row each, kMaxWidth threads in all.
+__host__ __device__ inline int mesh_sub(int W) { return (W + 63) / 64 * 64; }
+__host__ __device__ inline int mesh_rpb(int W) { return kMaxWidth / mesh_sub(W); }
+
+// Sub-block k of workgroup g takes rows (g + j * gridDim.x) * RPB + k; thread
+// c of it carries d loss / d (channel c) down the layers and adds its two
+// weights' gradients over its rows in registers.  At the end the sub-blocks'
+// sums are added in LDS (in sub-block order) into the workgroup's partial.
 __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const float *__restrict__ in,
                                                                   const float *__restrict__ stack,
                                                                   const float *__restrict__ dout, float *din,
                                                                   int accumulate, const float *__restrict__ w,
                                                                   float *__restrict__ partials, int rows) {
-    extern __shared__ float dz_row[];
-    const int c = threadIdx.x, W = m.W, depth = m.depth;
+    extern __shared__ float lds[];  // RPB rows of dz, then RPB x W x 2 sums
+    const int W = m.W, depth = m.depth, SUB = mesh_sub(W), RPB = mesh_rpb(W);
+    const int sub = threadIdx.x / SUB, c = threadIdx.x % SUB;
+    float *dz_row = lds + sub * W;
     float gs[kMaxDepth], gp[kMaxDepth];
 #pragma unroll
     for (int l = 0; l < kMaxDepth; ++l) gs[l] = gp[l] = 0.0f;
-    for (int r = blockIdx.x; r < rows; r += gridDim.x) {
-        float g = c < W ? dout[size_t(r) * W + c] : 0.0f;
+    for (int base = blockIdx.x * RPB; base < rows; base += gridDim.x * RPB) {
+        const int r = base + sub;
+        const bool live = sub < RPB && r < rows && c < W;
+        float g = live ? dout[size_t(r) * W + c] : 0.0f;
+        // Every layer's input (own channel and partner) and output for this
+        // row, loaded at once: the layer chain below waits on none of them.
+        float xs[kMaxDepth], xp[kMaxDepth], act[kMaxDepth];
+#pragma unroll
+        for (int l = 0; l < kMaxDepth; ++l) {
+            xs[l] = xp[l] = act[l] = 0.0f;
+            if (l >= depth || !live) continue;
+            const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
+            int p = c + stride_of(m, l);
+            if (p >= W) p -= W;
+            xs[l] = x[c];
+            xp[l] = x[p];
+            if (l + 1 < depth) act[l] = stack[(size_t(l) * rows + r) * W + c];
+        }
 #pragma unroll
         for (int l = kMaxDepth - 1; l >= 0; --l) {
             if (l >= depth) continue;
             const int s = stride_of(m, l);
-            if (c < W) {
-                float dz = g;
-                if (l + 1 < depth) {
-                    // ELU'(z) from its output a: 1 for a >= 0, else exp(z) = a + 1.
-                    const float a = stack[(size_t(l) * rows + r) * W + c];
-                    dz = a >= 0.0f ? g : g * (a + 1.0f);
-                }
-                const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
-                int p = c + s;
-                if (p >= W) p -= W;
-                gs[l] = fmaf(dz, x[c], gs[l]);
-                gp[l] = fmaf(dz, x[p], gp[l]);
+            if (live) {
+                // ELU'(z) from its output a: 1 for a >= 0, else exp(z) = a + 1.
+                const float dz = l + 1 < depth && act[l] < 0.0f ? g * (act[l] + 1.0f) : g;
+                gs[l] = fmaf(dz, xs[l], gs[l]);
+                gp[l] = fmaf(dz, xp[l], gp[l]);
                 dz_row[c] = dz;
             }
             __syncthreads();
-            if (c < W) {
+            if (live) {
                 // Channel c feeds itself (weight 2c) and channel c - s (weight 2(c - s) + 1).
                 int q = c - s;
                 if (q < 0) q += W;
@@ -102,32 +120,215 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const 
             }
             __syncthreads();
         }
-        if (c < W && din) {
+        if (live && din) {
             const size_t i = size_t(r) * W + c;
             din[i] = accumulate ? din[i] + g : g;
         }
     }
-    if (c < W) {
+    float *sums = lds + RPB * W;
 #pragma unroll
-        for (int l = 0; l < kMaxDepth; ++l)
-            if (l < depth) {
-                float *o = partials + ((size_t(blockIdx.x) * depth + l) * W + c) * 2;
-                o[0] = gs[l];
-                o[1] = gp[l];
-            }
+    for (int l = 0; l < kMaxDepth; ++l) {
+        if (l >= depth) continue;
+        if (sub < RPB && c < W) {
+            sums[(sub * W + c) * 2] = gs[l];
+            sums[(sub * W + c) * 2 + 1] = gp[l];
+        }
+        __syncthreads();
+        if (threadIdx.x < 2 * W) {
+            float acc = 0.0f;
+            for (int k = 0; k < RPB; ++k) acc += sums[k * 2 * W + threadIdx.x];
+            partials[(size_t(blockIdx.x) * depth + l) * 2 * W + threadIdx.x] = acc;
+        }
+        __syncthreads();
     }
 }
 
-__global__ void __launch_bounds__(kThreads) mesh_reduce_kernel(const float *__restrict__ partials, int groups,
-                                                               int n, float *__restrict__ grad) {
-    const int i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= n) return;
+// out[i] = sum over g < groups of part[g * n + i], in g order per wave and
+// the waves' sums in wave order: 64 outputs per workgroup, wave k of its 16
+// adding groups k, k + 16, ...
+__global__ void __launch_bounds__(1024) reduce_groups_kernel(const float *__restrict__ part, int groups, int n,
+                                                            float *__restrict__ out) {
+    __shared__ float sums[16][64];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = blockIdx.x * 64 + lane;
     float acc = 0.0f;
-    for (int g = 0; g < groups; ++g) acc += partials[size_t(g) * n + i];
-    grad[i] = acc;
+    if (i < n)
+        for (int g = wave; g < groups; g += 16) acc += part[size_t(g) * n + i];
+    sums[wave][lane] = acc;
+    __syncthreads();
+    if (wave == 0 && i < n) {
+        float t = 0.0f;
+        for (int k = 0; k < 16; ++k) t += sums[k][lane];
+        out[i] = t;
+    }
 }
 
-int mesh_groups(const Mesh &m, int rows) { return std::max(1, std::min(rows, 256)); }
+int mesh_groups(const Mesh &m, int rows) {
+    const int rpb = mesh_rpb(m.W);
+    return std::max(1, std::min((rows + rpb - 1) / rpb, 256));
+}
+
+// ---- mesh stacks of width <= 64 or 128: one wave per row, channel
+// lane + 64 j in register j, partners by lane shuffles (no barriers).
+
+// out[j] = the value of channel (lane + 64 j + d) mod W, for 0 <= d < W.
+template <int CPL>
+__device__ __forceinline__ void channel_shift(const float (&x)[CPL], int d, int W, int lane, float (&out)[CPL]) {
+    if constexpr (CPL == 1) {
+        int src = lane + d;
+        if (src >= W) src -= W;
+        out[0] = __shfl(x[0], src & 63, 64);
+    } else {
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            int t = lane + 64 * j + d;
+            if (t >= W) t -= W;
+            float v = 0.0f;
+#pragma unroll
+            for (int k = 0; k < CPL; ++k) {
+                const float u = __shfl(x[k], t & 63, 64);
+                if ((t >> 6) == k) v = u;
+            }
+            out[j] = v;
+        }
+    }
+}
+
+constexpr int kMeshWaveRows = 2;  // rows per wave of the wave-per-row mesh backward
+
+template <int CPL>
+__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, const float *__restrict__ in,
+                                                              float *__restrict__ stack, const float *__restrict__ w,
+                                                              int rows) {
+    const int lane = threadIdx.x & 63, W = m.W;
+    const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), waves = gridDim.x * (kThreads / 64);
+    // The stack's weights of this lane's channels, loaded once.
+    float2 wt[kMaxDepth][CPL];
+#pragma unroll
+    for (int l = 0; l < kMaxDepth; ++l)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            wt[l][j] = l < m.depth && lane + 64 * j < W
+                           ? reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W)[lane + 64 * j]
+                           : make_float2(0.0f, 0.0f);
+    for (int r = wave; r < rows; r += waves) {
+        float x[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[j] = lane + 64 * j < W ? in[size_t(r) * W + lane + 64 * j] : 0.0f;
+#pragma unroll
+        for (int l = 0; l < kMaxDepth; ++l) {
+            if (l >= m.depth) continue;
+            float p[CPL];
+            channel_shift(x, stride_of(m, l), W, lane, p);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                float z = x[j] * wt[l][j].x + p[j] * wt[l][j].y;
+                if (l + 1 < m.depth) z = elu(z);
+                x[j] = z;
+                if (c < W) stack[(size_t(l) * rows + r) * W + c] = z;
+            }
+        }
+    }
+}
+
+// Each wave carries d loss / d (its row) down the layers, row after row, and
+// adds the weights' gradients in registers; the workgroup's waves add theirs
+// in LDS (in wave order) into the workgroup's partial.
+template <int CPL>
+__global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, const float *__restrict__ in,
+                                                               const float *__restrict__ stack,
+                                                               const float *__restrict__ dout, float *din,
+                                                               int accumulate, const float *__restrict__ w,
+                                                               float *__restrict__ partials, int rows) {
+    extern __shared__ float sums[];  // (kThreads / 64) x depth x W x 2
+    const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, W = m.W, depth = m.depth;
+    const int wave = blockIdx.x * (kThreads / 64) + wv, waves = gridDim.x * (kThreads / 64);
+    float gs[kMaxDepth][CPL], gp[kMaxDepth][CPL];
+#pragma unroll
+    for (int l = 0; l < kMaxDepth; ++l)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) gs[l][j] = gp[l][j] = 0.0f;
+    for (int r = wave; r < rows; r += waves) {
+        float g[CPL];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) g[j] = lane + 64 * j < W ? dout[size_t(r) * W + lane + 64 * j] : 0.0f;
+        // Every layer's input and output of this row, loaded at once: the
+        // layer chain below waits only on lane shuffles.
+        float xin[kMaxDepth][CPL], act[kMaxDepth][CPL];
+#pragma unroll
+        for (int l = 0; l < kMaxDepth; ++l)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                const bool ok = l < depth && c < W;
+                const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
+                xin[l][j] = ok ? x[c] : 0.0f;
+                act[l][j] = ok && l + 1 < depth ? stack[(size_t(l) * rows + r) * W + c] : 0.0f;
+            }
+#pragma unroll
+        for (int l = kMaxDepth - 1; l >= 0; --l) {
+            if (l >= depth) continue;
+            const int s = stride_of(m, l);
+            const float2 *wl = reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W);
+            float x[CPL], xp[CPL], dz[CPL], t[CPL], back[CPL];
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                x[j] = xin[l][j];
+                // ELU'(z) from its output a: 1 for a >= 0, else exp(z) = a + 1.
+                const float d = act[l][j] < 0.0f ? g[j] * (act[l][j] + 1.0f) : g[j];
+                dz[j] = c < W ? d : 0.0f;
+                t[j] = c < W ? dz[j] * wl[c].y : 0.0f;
+            }
+            channel_shift(x, s, W, lane, xp);
+            // Channel c feeds itself and channel c - s: its input gradient is
+            // dz[c] w_self[c] + dz[c - s] w_partner[c - s].
+            channel_shift(t, W - s, W, lane, back);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                gs[l][j] = fmaf(dz[j], x[j], gs[l][j]);
+                gp[l][j] = fmaf(dz[j], xp[j], gp[l][j]);
+                g[j] = c < W ? dz[j] * wl[c].x + back[j] : 0.0f;
+            }
+        }
+        if (din) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                if (c >= W) continue;
+                const size_t i = size_t(r) * W + c;
+                din[i] = accumulate ? din[i] + g[j] : g[j];
+            }
+        }
+    }
+#pragma unroll
+    for (int l = 0; l < kMaxDepth; ++l) {
+        if (l >= depth) continue;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+            const int c = lane + 64 * j;
+            if (c >= W) continue;
+            float *o = sums + ((size_t(wv) * depth + l) * W + c) * 2;
+            o[0] = gs[l][j];
+            o[1] = gp[l][j];
+        }
+    }
+    __syncthreads();
+    const int n = depth * W * 2;
+    for (int i = threadIdx.x; i < n; i += kThreads) {
+        float acc = 0.0f;
+        for (int k = 0; k < kThreads / 64; ++k) acc += sums[size_t(k) * n + i];
+        partials[size_t(blockIdx.x) * n + i] = acc;
+    }
+}
+
+int mesh_wave_cpl(int W) { return W <= 64 ? 1 : (W == 128 ? 2 : 0); }
+
+int mesh_wave_groups(int rows) {
+    const int per = kMeshWaveRows * (kThreads / 64);
+    return std::max(1, std::min((rows + per - 1) / per, 256));
+}
 
 // ---- norms (one wave per (row, group))
 
@@ -182,13 +383,13 @@ __global__ void __launch_bounds__(kThreads) rope_kernel(float *x, const float2 *
 // ---- attention (one thread per (row, head); the head row in registers)
 
 template <int HD>
-__global__ void __launch_bounds__(kThreads) attention_forward_kernel(const float *__restrict__ q,
+__global__ void __launch_bounds__(kRowThreads) attention_forward_kernel(const float *__restrict__ q,
                                                                      const float *__restrict__ k,
                                                                      const float *__restrict__ v,
                                                                      float *__restrict__ y,
                                                                      float *__restrict__ lse, int rows,
                                                                      int sequence, int W, int H, float scale) {
-    const int t = blockIdx.x * kThreads + threadIdx.x;
+    const int t = blockIdx.x * kRowThreads + threadIdx.x;
     if (t >= rows * H) return;
     const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
     float qr[HD], acc[HD];
@@ -221,7 +422,7 @@ __global__ void __launch_bounds__(kThreads) attention_forward_kernel(const float
 
 // dq_i = scale sum_j P_ij (dy_i . v_j - D_i) k_j with D_i = dy_i . y_i.
 template <int HD>
-__global__ void __launch_bounds__(kThreads) attention_dq_kernel(const float *__restrict__ q,
+__global__ void __launch_bounds__(kRowThreads) attention_dq_kernel(const float *__restrict__ q,
                                                                 const float *__restrict__ k,
                                                                 const float *__restrict__ v,
                                                                 const float *__restrict__ y,
@@ -229,7 +430,7 @@ __global__ void __launch_bounds__(kThreads) attention_dq_kernel(const float *__r
                                                                 const float *__restrict__ dy, float *__restrict__ dq,
                                                                 float *__restrict__ dsum, int rows, int sequence,
                                                                 int W, int H, float scale) {
-    const int t = blockIdx.x * kThreads + threadIdx.x;
+    const int t = blockIdx.x * kRowThreads + threadIdx.x;
     if (t >= rows * H) return;
     const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
     const size_t o = size_t(r) * W + h * hd;
@@ -266,7 +467,7 @@ __global__ void __launch_bounds__(kThreads) attention_dq_kernel(const float *__r
 // For key row j: dv_j += sum_i P_ij dy_i, dk_j = scale sum_i P_ij (dy_i . v_j - D_i) q_i over the
 // queries i >= j of its sequence.
 template <int HD>
-__global__ void __launch_bounds__(kThreads) attention_dkv_kernel(const float *__restrict__ q,
+__global__ void __launch_bounds__(kRowThreads) attention_dkv_kernel(const float *__restrict__ q,
                                                                  const float *__restrict__ k,
                                                                  const float *__restrict__ v,
                                                                  const float *__restrict__ lse,
@@ -274,7 +475,7 @@ __global__ void __launch_bounds__(kThreads) attention_dkv_kernel(const float *__
                                                                  const float *__restrict__ dsum,
                                                                  float *__restrict__ dk, float *dv, int rows,
                                                                  int sequence, int W, int H, float scale) {
-    const int t = blockIdx.x * kThreads + threadIdx.x;
+    const int t = blockIdx.x * kRowThreads + threadIdx.x;
     if (t >= rows * H) return;
     const int j = t / H, h = t % H, hd = W / H, pos = j % sequence, last = j - pos + sequence;
     const size_t o = size_t(j) * W + h * hd;
@@ -311,74 +512,273 @@ __global__ void __launch_bounds__(kThreads) attention_dkv_kernel(const float *__
         }
 }
 
-// ---- XSA (one thread per (row, head))
+// ---- one wave per (row, head), lanes over the head's dims (dim lane + 64 e)
 
-template <int HD>
-__global__ void __launch_bounds__(kThreads) xsa_forward_kernel(const float *__restrict__ y,
-                                                               const float *__restrict__ v, float *__restrict__ z,
-                                                               int rows, int W, int H) {
-    const int t = blockIdx.x * kThreads + threadIdx.x;
+template <int EPL>
+__device__ __forceinline__ void lanes_load(const float *row, int hd, int lane, float (&v)[EPL]) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) v[e] = lane + 64 * e < hd ? row[lane + 64 * e] : 0.0f;
+}
+
+template <int EPL>
+__device__ __forceinline__ void lanes_store(float *row, int hd, int lane, const float (&v)[EPL]) {
+#pragma unroll
+    for (int e = 0; e < EPL; ++e)
+        if (lane + 64 * e < hd) row[lane + 64 * e] = v[e];
+}
+
+template <int EPL>
+__device__ __forceinline__ float lanes_dot(const float (&a)[EPL], const float (&b)[EPL]) {
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc = fmaf(a[e], b[e], acc);
+    return wave_sum(acc);
+}
+
+// The RoPE partner of each lane's dims (d + half or d - half).
+template <int EPL>
+__device__ __forceinline__ void lanes_partner(const float (&x)[EPL], int hd, int lane, float (&out)[EPL]) {
+    const int half = hd / 2;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        const int d = lane + 64 * e, pd = d < half ? d + half : d - half;
+        float v = 0.0f;
+#pragma unroll
+        for (int f = 0; f < EPL; ++f) {
+            const float t = __shfl(x[f], pd & 63, 64);
+            if ((pd >> 6) == f) v = t;
+        }
+        out[e] = d < hd ? v : 0.0f;
+    }
+}
+
+__device__ __forceinline__ int row_wave() { return int((blockIdx.x * kThreads + threadIdx.x) >> 6); }
+
+// QK-Norm (per-head RMSNorm) then RoPE of row r, head h, in place; inv keeps
+// the norm's factor (reference.rs:174-193, 392-409, 462-482).
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) qk_forward_kernel(float *x, const float *__restrict__ pre,
+                                                              float *__restrict__ inv, const float2 *__restrict__ table,
+                                                              int rows, int sequence, int W, int H, int norm,
+                                                              int rotate) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int r = t / H, h = t % H, hd = W / H, half = hd / 2;
+    float v[EPL];
+    lanes_load(pre + size_t(r) * W + h * hd, hd, lane, v);
+    if (norm) {
+        const float iv = rsqrtf(lanes_dot(v, v) * (1.0f / float(hd)) + kRmsEps);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[e] *= iv;
+        if (lane == 0) inv[t] = iv;
+    }
+    if (rotate) {
+        float o[EPL];
+        lanes_partner(v, hd, lane, o);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int d = lane + 64 * e;
+            const float2 cs = table[size_t(r % sequence) * half + (d < half ? d : d - half) % max(half, 1)];
+            v[e] = d < half ? v[e] * cs.x - o[e] * cs.y : v[e] * cs.x + o[e] * cs.y;
+        }
+    }
+    lanes_store(x + size_t(r) * W + h * hd, hd, lane, v);
+}
+
+// Its backward in place on g: the transposed rotation, then the norm's
+// backward against the pre-norm rows `pre`.
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) qk_backward_kernel(float *g, const float *__restrict__ pre,
+                                                               const float *__restrict__ inv,
+                                                               const float2 *__restrict__ table, int rows,
+                                                               int sequence, int W, int H, int norm, int rotate) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int r = t / H, h = t % H, hd = W / H, half = hd / 2;
+    float *row = g + size_t(r) * W + h * hd;
+    float v[EPL];
+    lanes_load(row, hd, lane, v);
+    if (rotate) {
+        float o[EPL];
+        lanes_partner(v, hd, lane, o);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int d = lane + 64 * e;
+            const float2 cs = table[size_t(r % sequence) * half + (d < half ? d : d - half) % max(half, 1)];
+            v[e] = d < half ? v[e] * cs.x + o[e] * cs.y : v[e] * cs.x - o[e] * cs.y;
+        }
+    }
+    if (norm) {
+        float x[EPL];
+        lanes_load(pre + size_t(r) * W + h * hd, hd, lane, x);
+        const float iv = inv[t], k = lanes_dot(v, x) * iv * iv * iv * (1.0f / float(hd));
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) v[e] = iv * v[e] - x[e] * k;
+    }
+    lanes_store(row, hd, lane, v);
+}
+
+// Causal attention for short sequences: one wave per query row and head.
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) attention_forward_wave(const float *__restrict__ q,
+                                                                   const float *__restrict__ k,
+                                                                   const float *__restrict__ v, float *__restrict__ y,
+                                                                   float *__restrict__ lse, int rows, int sequence,
+                                                                   int W, int H, float scale) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
+    float qr[EPL], acc[EPL] = {};
+    lanes_load(q + size_t(r) * W + h * hd, hd, lane, qr);
+    float m = -INFINITY, l = 0.0f;
+    for (int j = 0; j <= pos; ++j) {
+        float kr[EPL], vr[EPL];
+        lanes_load(k + size_t(first + j) * W + h * hd, hd, lane, kr);
+        lanes_load(v + size_t(first + j) * W + h * hd, hd, lane, vr);
+        const float s = lanes_dot(qr, kr) * scale;
+        const float mn = fmaxf(m, s), alpha = expf(m - mn), p = expf(s - mn);
+        l = l * alpha + p;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(p, vr[e], acc[e] * alpha);
+        m = mn;
+    }
+    const float il = 1.0f / l;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] *= il;
+    lanes_store(y + size_t(r) * W + h * hd, hd, lane, acc);
+    if (lane == 0) lse[t] = m + logf(l);
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) attention_dq_wave(const float *__restrict__ q, const float *__restrict__ k,
+                                                              const float *__restrict__ v, const float *__restrict__ y,
+                                                              const float *__restrict__ lse,
+                                                              const float *__restrict__ dy, float *__restrict__ dq,
+                                                              float *__restrict__ dsum, int rows, int sequence, int W,
+                                                              int H, float scale) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
+    const size_t o = size_t(r) * W + h * hd;
+    float qr[EPL], g[EPL], yv[EPL], acc[EPL] = {};
+    lanes_load(q + o, hd, lane, qr);
+    lanes_load(dy + o, hd, lane, g);
+    lanes_load(y + o, hd, lane, yv);
+    const float D = lanes_dot(g, yv), L = lse[t];
+    for (int j = 0; j <= pos; ++j) {
+        float kr[EPL], vr[EPL];
+        lanes_load(k + size_t(first + j) * W + h * hd, hd, lane, kr);
+        lanes_load(v + size_t(first + j) * W + h * hd, hd, lane, vr);
+        const float ds = expf(lanes_dot(qr, kr) * scale - L) * (lanes_dot(g, vr) - D);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] = fmaf(ds, kr[e], acc[e]);
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) acc[e] *= scale;
+    lanes_store(dq + o, hd, lane, acc);
+    if (lane == 0) dsum[t] = D;
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) attention_dkv_wave(const float *__restrict__ q,
+                                                               const float *__restrict__ k,
+                                                               const float *__restrict__ v,
+                                                               const float *__restrict__ lse,
+                                                               const float *__restrict__ dy,
+                                                               const float *__restrict__ dsum, float *__restrict__ dk,
+                                                               float *dv, int rows, int sequence, int W, int H,
+                                                               float scale) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int j = t / H, h = t % H, hd = W / H, pos = j % sequence, last = j - pos + sequence;
+    const size_t o = size_t(j) * W + h * hd;
+    float kr[EPL], vr[EPL], ak[EPL] = {}, av[EPL] = {};
+    lanes_load(k + o, hd, lane, kr);
+    lanes_load(v + o, hd, lane, vr);
+    for (int i = j; i < last; ++i) {
+        float qi[EPL], gi[EPL];
+        lanes_load(q + size_t(i) * W + h * hd, hd, lane, qi);
+        lanes_load(dy + size_t(i) * W + h * hd, hd, lane, gi);
+        const float p = expf(lanes_dot(qi, kr) * scale - lse[size_t(i) * H + h]);
+        const float ds = p * (lanes_dot(gi, vr) - dsum[size_t(i) * H + h]);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            av[e] = fmaf(p, gi[e], av[e]);
+            ak[e] = fmaf(ds, qi[e], ak[e]);
+        }
+    }
+    float old[EPL];
+    lanes_load(dv + o, hd, lane, old);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        ak[e] *= scale;
+        old[e] += av[e];
+    }
+    lanes_store(dk + o, hd, lane, ak);
+    lanes_store(dv + o, hd, lane, old);
+}
+
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) xsa_forward_wave(const float *__restrict__ y, const float *__restrict__ v,
+                                                             float *__restrict__ z, int rows, int W, int H) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
     if (t >= rows * H) return;
     const int hd = W / H;
     const size_t o = size_t(t / H) * W + (t % H) * hd;
-    float yv[HD], u[HD], sq = 0.0f;
+    float yv[EPL], u[EPL];
+    lanes_load(y + o, hd, lane, yv);
+    lanes_load(v + o, hd, lane, u);
+    const float inv = rsqrtf(fmaxf(lanes_dot(u, u), kXsaFloor));
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
-        yv[d] = d < hd ? y[o + d] : 0.0f;
-        u[d] = d < hd ? v[o + d] : 0.0f;
-        sq = fmaf(u[d], u[d], sq);
-    }
-    const float inv = rsqrtf(fmaxf(sq, kXsaFloor));
-    float s = 0.0f;
+    for (int e = 0; e < EPL; ++e) u[e] *= inv;
+    const float s = lanes_dot(yv, u);
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
-        u[d] *= inv;
-        s = fmaf(yv[d], u[d], s);
-    }
-#pragma unroll
-    for (int d = 0; d < HD; ++d)
-        if (d < hd) z[o + d] = yv[d] - s * u[d];
+    for (int e = 0; e < EPL; ++e) yv[e] -= s * u[e];
+    lanes_store(z + o, hd, lane, yv);
 }
 
 // dy = dz - (dz.u) u;  du = -((y.u) dz + (dz.u) y);  dv = inv (du - u (u.du))
 // above the norm floor, inv du below it.
-template <int HD>
-__global__ void __launch_bounds__(kThreads) xsa_backward_kernel(const float *__restrict__ y,
-                                                                const float *__restrict__ v,
-                                                                const float *__restrict__ dz, float *__restrict__ dy,
-                                                                float *__restrict__ dv, int rows, int W, int H) {
-    const int t = blockIdx.x * kThreads + threadIdx.x;
+template <int EPL>
+__global__ void __launch_bounds__(kThreads) xsa_backward_wave(const float *__restrict__ y, const float *__restrict__ v,
+                                                              const float *__restrict__ dz, float *__restrict__ dy,
+                                                              float *__restrict__ dv, int rows, int W, int H) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
     if (t >= rows * H) return;
     const int hd = W / H;
     const size_t o = size_t(t / H) * W + (t % H) * hd;
-    float yv[HD], u[HD], g[HD], sq = 0.0f;
+    float yv[EPL], u[EPL], g[EPL];
+    lanes_load(y + o, hd, lane, yv);
+    lanes_load(v + o, hd, lane, u);
+    lanes_load(dz + o, hd, lane, g);
+    const float sq = lanes_dot(u, u), inv = rsqrtf(fmaxf(sq, kXsaFloor));
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
-        yv[d] = d < hd ? y[o + d] : 0.0f;
-        u[d] = d < hd ? v[o + d] : 0.0f;
-        g[d] = d < hd ? dz[o + d] : 0.0f;
-        sq = fmaf(u[d], u[d], sq);
+    for (int e = 0; e < EPL; ++e) u[e] *= inv;
+    const float s = lanes_dot(yv, u), tg = lanes_dot(g, u);
+    float du[EPL], gy[EPL];
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        du[e] = -(s * g[e] + tg * yv[e]);
+        gy[e] = g[e] - tg * u[e];
     }
-    const float inv = rsqrtf(fmaxf(sq, kXsaFloor));
-    float s = 0.0f, tg = 0.0f;
+    const float udu = sq >= kXsaFloor ? lanes_dot(u, du) : 0.0f;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) {
-        u[d] *= inv;
-        s = fmaf(yv[d], u[d], s);
-        tg = fmaf(g[d], u[d], tg);
-    }
-    float udu = 0.0f;
-#pragma unroll
-    for (int d = 0; d < HD; ++d) udu = fmaf(u[d], -(s * g[d] + tg * yv[d]), udu);
-    const float keep = sq >= kXsaFloor ? 1.0f : 0.0f;
-#pragma unroll
-    for (int d = 0; d < HD; ++d)
-        if (d < hd) {
-            const float du = -(s * g[d] + tg * yv[d]);
-            dy[o + d] = g[d] - tg * u[d];
-            dv[o + d] = inv * (du - keep * u[d] * udu);
-        }
+    for (int e = 0; e < EPL; ++e) du[e] = inv * (du[e] - u[e] * udu);
+    lanes_store(dy + o, hd, lane, gy);
+    lanes_store(dv + o, hd, lane, du);
 }
+
+template <class F>
+void by_lanes(int hd, F &&f) {
+    if (hd <= 64)
+        f(std::integral_constant<int, 1>{});
+    else
+        f(std::integral_constant<int, 2>{});
+}
+
+// Sequences up to this length take the wave-per-row attention kernels; longer
+// ones the thread-per-row kernels, whose key loops do 64 rows' work per wave.
+constexpr int kWaveAttentionMax = 64;
 
 // ---- head, loss and embedding gradient
 
@@ -396,85 +796,149 @@ __global__ void __launch_bounds__(kThreads) add_kernel(const float *a, const flo
     if (i < n) out[i] = a[i] + b[i];
 }
 
-__global__ void __launch_bounds__(kThreads) head_logits_kernel(const float *__restrict__ n,
-                                                               const float *__restrict__ E,
-                                                               float *__restrict__ logits, int rows, int W, int V) {
+__global__ void __launch_bounds__(kThreads) fill_kernel(float *p, float v, size_t n) {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= size_t(rows) * V) return;
-    const size_t r = i / V, t = i % V;
-    const float *a = n + r * W, *b = E + t * W;
-    float acc = 0.0f;
-    for (int c = 0; c < W; ++c) acc = fmaf(a[c], b[c], acc);
-    logits[i] = acc;
+    if (i < n) p[i] = v;
 }
 
+__global__ void __launch_bounds__(kThreads) copy_kernel(const float *__restrict__ a, float *__restrict__ b, size_t n) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) b[i] = a[i];
+}
+
+// logits[r][t] = n[r] . E[t] with E given transposed (Et[c][t]): a workgroup
+// stages kHeadRows rows of n in LDS; thread t of it takes token t0 + t for
+// all of them, reading each Et value once, coalesced across threads.
+constexpr int kHeadRows = 16;
+
+__global__ void __launch_bounds__(kThreads) head_logits_kernel(const float *__restrict__ n,
+                                                               const float *__restrict__ Et,
+                                                               float *__restrict__ logits, int rows, int W, int V) {
+    extern __shared__ float nr[];  // kHeadRows x W
+    const int r0 = blockIdx.x * kHeadRows, t = blockIdx.y * kThreads + threadIdx.x;
+    for (int i = threadIdx.x; i < kHeadRows * W; i += kThreads) {
+        const int r = r0 + i / W;
+        nr[i] = r < rows ? n[size_t(r) * W + i % W] : 0.0f;
+    }
+    __syncthreads();
+    if (t >= V) return;
+    float acc[kHeadRows] = {};
+    for (int c = 0; c < W; ++c) {
+        const float e = Et[size_t(c) * V + t];
+#pragma unroll
+        for (int k = 0; k < kHeadRows; ++k) acc[k] = fmaf(nr[k * W + c], e, acc[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        if (r0 + k < rows) logits[size_t(r0 + k) * V + t] = acc[k];
+}
+
+__global__ void __launch_bounds__(kThreads) transpose_kernel(const float *__restrict__ E, float *__restrict__ Et,
+                                                             int V, int W) {
+    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= size_t(V) * W) return;
+    const size_t c = i / V, t = i % V;
+    Et[i] = E[t * W + c];
+}
+
+// One wave per row: the maximum and the sum over the vocabulary by wave
+// reductions (the loss kernel of gpu.rs:949-994 sums sequentially; the
+// difference is f32 rounding).
 __global__ void __launch_bounds__(kThreads) cross_entropy_kernel(const float *__restrict__ logits,
                                                                  const uint32_t *__restrict__ targets,
                                                                  float *__restrict__ dlogits, float *__restrict__ loss,
-                                                                 int rows, int V, int supervised) {
-    const int r = blockIdx.x * kThreads + threadIdx.x;
+                                                                 int rows, int V, StepScalars *sc) {
+    const int r = (blockIdx.x * kThreads + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (r >= rows) return;
     const float *row = logits + size_t(r) * V;
     float *out = dlogits + size_t(r) * V;
     const uint32_t target = targets[r];
     if (target == 0xFFFFFFFFu) {
-        for (int t = 0; t < V; ++t) out[t] = 0.0f;
-        loss[r] = 0.0f;
+        for (int t = lane; t < V; t += 64) out[t] = 0.0f;
+        if (lane == 0) loss[r] = 0.0f;
         return;
     }
     float maximum = -INFINITY;
-    for (int t = 0; t < V; ++t) maximum = fmaxf(maximum, row[t]);
+    for (int t = lane; t < V; t += 64) maximum = fmaxf(maximum, row[t]);
+    for (int k = 32; k >= 1; k >>= 1) maximum = fmaxf(maximum, __shfl_xor(maximum, k, 64));
     float sum = 0.0f;
-    for (int t = 0; t < V; ++t) {
-        out[t] = expf(row[t] - maximum);
-        sum += out[t];
+    for (int t = lane; t < V; t += 64) sum += expf(row[t] - maximum);
+    sum = wave_sum(sum);
+    const float value = logf(sum) + maximum - row[target];
+    if (lane == 0) {
+        loss[r] = value;
+        if (!isfinite(value)) atomicOr(&sc->nonfinite, 1);
     }
-    loss[r] = logf(sum) + maximum - row[target];
-    const float scale = 1.0f / float(supervised);
-    for (int t = 0; t < V; ++t) out[t] = (out[t] / sum - (uint32_t(t) == target ? 1.0f : 0.0f)) * scale;
+    const float scale = sc->inv_supervised;
+    for (int t = lane; t < V; t += 64)
+        out[t] = (expf(row[t] - maximum) / sum - (uint32_t(t) == target ? 1.0f : 0.0f)) * scale;
 }
 
+// dn[r][c] = sum_t dlogits[r][t] E[t][c]: a workgroup takes kHeadRows rows and
+// channels c0 + threadIdx.x; the rows' gradients pass through LDS in chunks of
+// kThreads tokens, and each E value loaded serves all the rows.
 __global__ void __launch_bounds__(kThreads) head_backward_kernel(const float *__restrict__ dlogits,
                                                                  const float *__restrict__ E, float *__restrict__ dn,
                                                                  int rows, int W, int V) {
-    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= size_t(rows) * W) return;
-    const size_t r = i / W, c = i % W;
-    const float *g = dlogits + r * V;
-    float acc = 0.0f;
-    for (int t = 0; t < V; ++t) acc = fmaf(g[t], E[size_t(t) * W + c], acc);
-    dn[i] = acc;
+    __shared__ float g[kHeadRows][kThreads];
+    const int r0 = blockIdx.x * kHeadRows, c = blockIdx.y * kThreads + threadIdx.x;
+    float acc[kHeadRows] = {};
+    for (int t0 = 0; t0 < V; t0 += kThreads) {
+        const int nt = min(kThreads, V - t0);
+        __syncthreads();
+        for (int k = 0; k < kHeadRows; ++k)
+            g[k][threadIdx.x] = r0 + k < rows && int(threadIdx.x) < nt ? dlogits[size_t(r0 + k) * V + t0 + threadIdx.x]
+                                                                        : 0.0f;
+        __syncthreads();
+        if (c < W)
+            for (int t = 0; t < nt; ++t) {
+                const float e = E[size_t(t0 + t) * W + c];
+#pragma unroll
+                for (int k = 0; k < kHeadRows; ++k) acc[k] = fmaf(g[k][t], e, acc[k]);
+            }
+    }
+    if (c >= W) return;
+#pragma unroll
+    for (int k = 0; k < kHeadRows; ++k)
+        if (r0 + k < rows) dn[size_t(r0 + k) * W + c] = acc[k];
 }
+
+// Partial sums of dE over chunk blockIdx.y of kEmbeddingChunk rows:
+// part[chunk][t][c] = sum_r dlogits[r][t] n[r][c] + (rows of token t) dx[r][c].
+constexpr int kEmbeddingChunk = 32;
 
 __global__ void __launch_bounds__(kThreads) embedding_gradient_kernel(const float *__restrict__ dlogits,
                                                                       const float *__restrict__ n,
                                                                       const uint32_t *__restrict__ tokens,
                                                                       const float *__restrict__ dx,
-                                                                      float *__restrict__ dE, int rows, int W,
+                                                                      float *__restrict__ part, int rows, int W,
                                                                       int V) {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
     if (i >= size_t(V) * W) return;
     const size_t t = i / W, c = i % W;
+    const int r0 = blockIdx.y * kEmbeddingChunk, r1 = min(rows, r0 + kEmbeddingChunk);
     float acc = 0.0f;
-    for (int r = 0; r < rows; ++r) {
+    for (int r = r0; r < r1; ++r) {
         acc = fmaf(dlogits[size_t(r) * V + t], n[size_t(r) * W + c], acc);
         if (tokens[r] == t) acc += dx[size_t(r) * W + c];
     }
-    dE[i] = acc;
+    part[size_t(blockIdx.y) * V * W + i] = acc;
 }
 
 __global__ void __launch_bounds__(kThreads) adam_kernel(float *__restrict__ params, float *__restrict__ m,
                                                         float *__restrict__ v, const float *__restrict__ grad,
-                                                        size_t begin, size_t end, AdamW o) {
+                                                        size_t begin, size_t end, AdamW o,
+                                                        const StepScalars *__restrict__ sc) {
     const size_t i = begin + size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= end) return;
+    // A non-finite loss stops the step before the update (gpu.rs:2296-2313).
+    if (i >= end || sc->nonfinite) return;
     // The arithmetic of gpu.rs:1383-1389, unfused.
     const float g = grad[i];
     const float mi = __fadd_rn(__fmul_rn(o.beta1, m[i]), __fmul_rn(1.0f - o.beta1, g));
     const float vi = __fadd_rn(__fmul_rn(o.beta2, v[i]), __fmul_rn(__fmul_rn(1.0f - o.beta2, g), g));
     m[i] = mi;
     v[i] = vi;
-    const float mh = mi / o.correction1, vh = vi / o.correction2;
+    const float mh = mi / sc->correction1, vh = vi / sc->correction2;
     const float step = __fadd_rn(mh / __fadd_rn(sqrtf(vh), o.epsilon), __fmul_rn(o.weight_decay, params[i]));
     params[i] = __fsub_rn(params[i], __fmul_rn(o.learning_rate, step));
 }
@@ -496,6 +960,14 @@ void by_head_width(int hd, F &&f) {
 }  // namespace
 
 void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
+    if (const int cpl = mesh_wave_cpl(m.W)) {
+        const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)));
+        if (cpl == 1)
+            hipLaunchKernelGGL(mesh_forward_wave<1>, grid, dim3(kThreads), 0, stream, m, in, stack, w, rows);
+        else
+            hipLaunchKernelGGL(mesh_forward_wave<2>, grid, dim3(kThreads), 0, stream, m, in, stack, w, rows);
+        return;
+    }
     const int threads = block_for(m.W);
     const unsigned grid = unsigned(std::min(rows, 2048));
     hipLaunchKernelGGL(mesh_forward_kernel, dim3(grid), dim3(threads), 2 * m.W * sizeof(float), stream, m, in,
@@ -503,16 +975,30 @@ void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, 
 }
 
 size_t mesh_partial_floats(const Mesh &m, int rows) {
-    return size_t(mesh_groups(m, rows)) * m.depth * m.W * 2;
+    const int groups = mesh_wave_cpl(m.W) ? mesh_wave_groups(rows) : mesh_groups(m, rows);
+    return size_t(groups) * m.depth * m.W * 2;
 }
 
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
                    bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream) {
-    const int groups = mesh_groups(m, rows), threads = block_for(m.W);
-    hipLaunchKernelGGL(mesh_backward_kernel, dim3(groups), dim3(threads), m.W * sizeof(float), stream, m, in, stack,
-                       dout, din, int(accumulate), w, partials, rows);
     const int n = m.depth * m.W * 2;
-    hipLaunchKernelGGL(mesh_reduce_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, partials, groups, n, grad);
+    int groups;
+    if (const int cpl = mesh_wave_cpl(m.W)) {
+        groups = mesh_wave_groups(rows);
+        const size_t lds = size_t(kThreads / 64) * n * sizeof(float);
+        if (cpl == 1)
+            hipLaunchKernelGGL(mesh_backward_wave<1>, dim3(groups), dim3(kThreads), lds, stream, m, in, stack, dout,
+                               din, int(accumulate), w, partials, rows);
+        else
+            hipLaunchKernelGGL(mesh_backward_wave<2>, dim3(groups), dim3(kThreads), lds, stream, m, in, stack, dout,
+                               din, int(accumulate), w, partials, rows);
+    } else {
+        groups = mesh_groups(m, rows);
+        const int rpb = mesh_rpb(m.W);
+        hipLaunchKernelGGL(mesh_backward_kernel, dim3(groups), dim3(kMaxWidth), size_t(3) * rpb * m.W * sizeof(float),
+                           stream, m, in, stack, dout, din, int(accumulate), w, partials, rows);
+    }
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3((n + 63) / 64), dim3(1024), 0, stream, partials, groups, n, grad);
 }
 
 void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream) {
@@ -537,9 +1023,16 @@ void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, b
 void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
                        int sequence, int W, int H, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
+    if (sequence <= kWaveAttentionMax) {
+        by_lanes(W / H, [&](auto e) {
+            hipLaunchKernelGGL(attention_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
+                               dim3(kThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
+        });
+        return;
+    }
     by_head_width(W / H, [&](auto hd) {
-        hipLaunchKernelGGL(attention_forward_kernel<decltype(hd)::value>, dim3(blocks_for(size_t(rows) * H)),
-                           dim3(kThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
+        hipLaunchKernelGGL(attention_forward_kernel<decltype(hd)::value>, dim3(blocks_for(size_t(rows) * H, kRowThreads)),
+                           dim3(kRowThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
     });
 }
 
@@ -547,27 +1040,56 @@ void attention_backward(const float *q, const float *k, const float *v, const fl
                         const float *dy, float *dq, float *dk, float *dv, float *dsum, int rows, int sequence, int W,
                         int H, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
+    if (sequence <= kWaveAttentionMax) {
+        by_lanes(W / H, [&](auto e) {
+            constexpr int EPL = decltype(e)::value;
+            const dim3 grid(blocks_for(size_t(rows) * H * 64));
+            hipLaunchKernelGGL(attention_dq_wave<EPL>, grid, dim3(kThreads), 0, stream, q, k, v, y, lse, dy, dq, dsum,
+                               rows, sequence, W, H, scale);
+            hipLaunchKernelGGL(attention_dkv_wave<EPL>, grid, dim3(kThreads), 0, stream, q, k, v, lse, dy, dsum, dk, dv,
+                               rows, sequence, W, H, scale);
+        });
+        return;
+    }
     by_head_width(W / H, [&](auto hd) {
         constexpr int HD = decltype(hd)::value;
-        hipLaunchKernelGGL(attention_dq_kernel<HD>, dim3(blocks_for(size_t(rows) * H)), dim3(kThreads), 0, stream, q,
+        hipLaunchKernelGGL(attention_dq_kernel<HD>, dim3(blocks_for(size_t(rows) * H, kRowThreads)), dim3(kRowThreads), 0, stream, q,
                            k, v, y, lse, dy, dq, dsum, rows, sequence, W, H, scale);
-        hipLaunchKernelGGL(attention_dkv_kernel<HD>, dim3(blocks_for(size_t(rows) * H)), dim3(kThreads), 0, stream,
+        hipLaunchKernelGGL(attention_dkv_kernel<HD>, dim3(blocks_for(size_t(rows) * H, kRowThreads)), dim3(kRowThreads), 0, stream,
                            q, k, v, lse, dy, dsum, dk, dv, rows, sequence, W, H, scale);
     });
 }
 
 void xsa_forward(const float *y, const float *v, float *z, int rows, int W, int H, hipStream_t stream) {
-    by_head_width(W / H, [&](auto hd) {
-        hipLaunchKernelGGL(xsa_forward_kernel<decltype(hd)::value>, dim3(blocks_for(size_t(rows) * H)),
+    by_lanes(W / H, [&](auto e) {
+        hipLaunchKernelGGL(xsa_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
                            dim3(kThreads), 0, stream, y, v, z, rows, W, H);
     });
 }
 
 void xsa_backward(const float *y, const float *v, const float *dz, float *dy, float *dv, int rows, int W, int H,
                   hipStream_t stream) {
-    by_head_width(W / H, [&](auto hd) {
-        hipLaunchKernelGGL(xsa_backward_kernel<decltype(hd)::value>, dim3(blocks_for(size_t(rows) * H)),
+    by_lanes(W / H, [&](auto e) {
+        hipLaunchKernelGGL(xsa_backward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
                            dim3(kThreads), 0, stream, y, v, dz, dy, dv, rows, W, H);
+    });
+}
+
+void qk_forward(const float *pre, float *out, float *inv, const float2 *table, int rows, int sequence, int W, int H,
+                bool norm, bool rotate, hipStream_t stream) {
+    by_lanes(W / H, [&](auto e) {
+        hipLaunchKernelGGL(qk_forward_kernel<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
+                           dim3(kThreads), 0, stream, out, pre, inv, table, rows, sequence, W, H, int(norm),
+                           int(rotate));
+    });
+}
+
+void qk_backward(float *g, const float *pre, const float *inv, const float2 *table, int rows, int sequence, int W,
+                 int H, bool norm, bool rotate, hipStream_t stream) {
+    by_lanes(W / H, [&](auto e) {
+        hipLaunchKernelGGL(qk_backward_kernel<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
+                           dim3(kThreads), 0, stream, g, pre, inv, table, rows, sequence, W, H, int(norm),
+                           int(rotate));
     });
 }
 
@@ -580,33 +1102,50 @@ void add(const float *a, const float *b, float *out, size_t n, hipStream_t strea
     hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, a, b, out, n);
 }
 
-void head_logits(const float *n, const float *E, float *logits, int rows, int W, int V, hipStream_t stream) {
-    hipLaunchKernelGGL(head_logits_kernel, dim3(blocks_for(size_t(rows) * V)), dim3(kThreads), 0, stream, n, E,
+void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
+                 hipStream_t stream) {
+    hipLaunchKernelGGL(transpose_kernel, dim3(blocks_for(size_t(V) * W)), dim3(kThreads), 0, stream, E, Et, V, W);
+    const dim3 grid(unsigned((rows + kHeadRows - 1) / kHeadRows), blocks_for(V));
+    hipLaunchKernelGGL(head_logits_kernel, grid, dim3(kThreads), size_t(kHeadRows) * W * sizeof(float), stream, n, Et,
                        logits, rows, W, V);
 }
 
 void cross_entropy(const float *logits, const uint32_t *targets, float *dlogits, float *loss, int rows, int V,
-                   int supervised, hipStream_t stream) {
-    hipLaunchKernelGGL(cross_entropy_kernel, dim3(blocks_for(rows)), dim3(kThreads), 0, stream, logits, targets,
-                       dlogits, loss, rows, V, supervised);
+                   StepScalars *scalars, hipStream_t stream) {
+    hipLaunchKernelGGL(cross_entropy_kernel, dim3(blocks_for(size_t(rows) * 64)), dim3(kThreads), 0, stream, logits,
+                       targets, dlogits, loss, rows, V, scalars);
+}
+
+void fill(float *p, float v, size_t n, hipStream_t stream) {
+    if (n) hipLaunchKernelGGL(fill_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, p, v, n);
+}
+
+void copy(const float *a, float *b, size_t n, hipStream_t stream) {
+    if (n) hipLaunchKernelGGL(copy_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, a, b, n);
 }
 
 void head_backward(const float *dlogits, const float *E, float *dn, int rows, int W, int V, hipStream_t stream) {
-    hipLaunchKernelGGL(head_backward_kernel, dim3(blocks_for(size_t(rows) * W)), dim3(kThreads), 0, stream, dlogits,
-                       E, dn, rows, W, V);
+    const dim3 grid(unsigned((rows + kHeadRows - 1) / kHeadRows), blocks_for(W));
+    hipLaunchKernelGGL(head_backward_kernel, grid, dim3(kThreads), 0, stream, dlogits, E, dn, rows, W, V);
+}
+
+size_t embedding_partial_floats(int rows, int W, int V) {
+    return size_t((rows + kEmbeddingChunk - 1) / kEmbeddingChunk) * V * W;
 }
 
 void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
-                        int rows, int W, int V, hipStream_t stream) {
-    hipLaunchKernelGGL(embedding_gradient_kernel, dim3(blocks_for(size_t(V) * W)), dim3(kThreads), 0, stream,
-                       dlogits, n, tokens, dx, dE, rows, W, V);
+                        float *partials, int rows, int W, int V, hipStream_t stream) {
+    const int chunks = (rows + kEmbeddingChunk - 1) / kEmbeddingChunk, nvw = V * W;
+    hipLaunchKernelGGL(embedding_gradient_kernel, dim3(blocks_for(size_t(nvw)), chunks), dim3(kThreads), 0, stream,
+                       dlogits, n, tokens, dx, partials, rows, W, V);
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, partials, chunks, nvw, dE);
 }
 
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,
-          hipStream_t stream) {
+          const StepScalars *scalars, hipStream_t stream) {
     if (end <= begin) return;
     hipLaunchKernelGGL(adam_kernel, dim3(blocks_for(end - begin)), dim3(kThreads), 0, stream, params, m, v, grad,
-                       begin, end, o);
+                       begin, end, o, scalars);
 }
 
 }  // namespace meshgpt::kern::train

@@ -45,6 +45,14 @@ void rmsnorm_backward(const float *x, const float *inv, const float *dy, float *
 // (its backward).
 void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, bool inverse, hipStream_t stream);
 
+// QK-Norm (when norm) then RoPE (when rotate) of the rows `pre` into `out`
+// (reference.rs:174-193); inv (rows x H) keeps the norm's factors.
+void qk_forward(const float *pre, float *out, float *inv, const float2 *table, int rows, int sequence, int W, int H,
+                bool norm, bool rotate, hipStream_t stream);
+// Its backward in place on g (d loss / d out -> d loss / d pre).
+void qk_backward(float *g, const float *pre, const float *inv, const float2 *table, int rows, int sequence, int W,
+                 int H, bool norm, bool rotate, hipStream_t stream);
+
 // Causal softmax attention per (sequence, head) (reference.rs:510-554);
 // lse[r * H + h] = max + ln(sum) of the row's scaled scores.
 void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
@@ -64,23 +72,40 @@ void xsa_backward(const float *y, const float *v, const float *dz, float *dy, fl
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream);
 // out = a + b (elementwise, n floats; out may alias a)
 void add(const float *a, const float *b, float *out, size_t n, hipStream_t stream);
-// logits[r][t] = n[r] . E[t]
-void head_logits(const float *n, const float *E, float *logits, int rows, int W, int V, hipStream_t stream);
+// logits[r][t] = n[r] . E[t]; Et (W x V floats) receives E transposed.
+void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
+                 hipStream_t stream);
+// A training step's scalars in device memory, written before each step, so
+// that a captured step replays with new values: the AdamW bias corrections
+// 1 - beta^t, 1 / (supervised rows), and a flag the loss kernel raises on a
+// non-finite loss (the update is then skipped).
+struct StepScalars {
+    float correction1, correction2, inv_supervised;
+    int nonfinite;
+};
+
 // The loss kernel of gpu.rs:949-994: per row the f32 cross-entropy and
 // d loss / d logits = (softmax - onehot) / supervised; ignored rows give 0.
 void cross_entropy(const float *logits, const uint32_t *targets, float *dlogits, float *loss, int rows, int V,
-                   int supervised, hipStream_t stream);
+                   StepScalars *scalars, hipStream_t stream);
+// p[0 .. n) = v;  b[0 .. n) = a[0 .. n)  (kernels: nothing a graph replays badly)
+void fill(float *p, float v, size_t n, hipStream_t stream);
+void copy(const float *a, float *b, size_t n, hipStream_t stream);
 // dn[r][c] = sum_t dlogits[r][t] E[t][c]
 void head_backward(const float *dlogits, const float *E, float *dn, int rows, int W, int V, hipStream_t stream);
-// dE[t][c] = sum_r dlogits[r][t] n[r][c] + sum over rows r of token t of dx[r][c]
+// dE[t][c] = sum_r dlogits[r][t] n[r][c] + sum over rows r of token t of dx[r][c],
+// by chunks of rows into `partials` (embedding_partial_floats), then one
+// deterministic reduction.
+size_t embedding_partial_floats(int rows, int W, int V);
 void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
-                        int rows, int W, int V, hipStream_t stream);
+                        float *partials, int rows, int W, int V, hipStream_t stream);
 
 struct AdamW {
-    float learning_rate, weight_decay, beta1, beta2, epsilon, correction1, correction2;
+    float learning_rate, weight_decay, beta1, beta2, epsilon;
 };
-// gpu.rs:1366-1391 over params[begin, end): f32 moments m, v.
+// gpu.rs:1366-1391 over params[begin, end): f32 moments m, v; the bias
+// corrections come from scalars, and nothing changes when its flag is set.
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,
-          hipStream_t stream);
+          const StepScalars *scalars, hipStream_t stream);
 
 }  // namespace meshgpt::kern::train

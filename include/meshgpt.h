@@ -129,6 +129,16 @@ int mg_loss_and_gradient(mg_model *model, const uint32_t *inputs, const uint32_t
  * until mg_set_parameters resets them. */
 int mg_train_batch(mg_model *model, const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
                    const mg_adamw *options, double *loss);
+/* EquationDataset::new (grokking.rs:128-186): the split sizes of the seeded
+ * table of `operation` (ModularOperation order: 0 add, 1 multiply, 2 subtract,
+ * 3 divide, 4 mixed, 5 square-sum, 6 quadratic, 7 quadratic-linear, 8
+ * cubic-product, 9 cubic-mixed) modulo the prime `modulus`. */
+int mg_equation_split(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed, size_t *n_train,
+                      size_t *n_valid);
+/* EquationDataset::batch (grokking.rs:225-258): 4 * n inputs (a, op, b, '=')
+ * and targets (MG_IGNORE_TARGET but the answer) for the split's equations. */
+int mg_equation_batch(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed, int validation,
+                      const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets);
 /* SpecializedMeshGpt::token_embeddings (gpu.rs:2056-2068): vocab_size x width. */
 int mg_token_embeddings(mg_model *model, float *out, size_t n);
 /* SpecializedMeshGpt::hidden_states (gpu.rs:2070-2092): n x width. */
