@@ -18,8 +18,10 @@ events recorded on the model's stream around it.
 Beside the headline: the first 20 decode steps alone (the latency-bound
 short-context end), config 1 at batch 1, config 2's single 9409-row prefill,
 config 4's 8192-token prefill and long-context decode, config 5's batch-256
-decode, the measured copy bandwidth of the box, HBM traffic from rocprofv3
-counters, and the CPU baseline (the f64 oracle on one core, a bounded sample).
+decode, the training step on the reference's training benchmark
+(mesh-gpt-bench defaults, ms per AdamW update against its published 5.759 ms),
+the measured copy bandwidth of the box, HBM traffic from rocprofv3 counters,
+and the CPU baseline (the f64 oracle on one core, a bounded sample).
 """
 import argparse
 import ctypes
@@ -331,6 +333,8 @@ def main():
     parser.add_argument("--no-extra", action="store_true", help="config 3 only")
     parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5", "training"],
                         help="print only that figure (for profiling one workload)")
+    parser.add_argument("--calibrate", action="store_true",
+                        help="with --only: a plain copy of 256 MiB after the figure (the scale of counter runs)")
     parser.add_argument("--probe", action="store_true", help=argparse.SUPPRESS)
     args = parser.parse_args()
 
@@ -349,6 +353,8 @@ def main():
                    "config4": lambda: long_figure(Hip()), "config5": lambda: high_figure(Hip()),
                    "training": training_figure}
         print(json.dumps({args.only: figures[args.only]()}))
+        if args.calibrate:
+            G.calibration_copy(PROBE_COPY_BYTES)
         return
     # The counter runs go first, while this process has not touched the GPU:
     # the profiled child is then the only process on it.

@@ -195,3 +195,44 @@ def test_training_rejections_carry_the_reference_messages():
         with pytest.raises(G.MeshGptError) as err:
             model.loss_and_gradient(np.zeros(3, np.uint32), np.zeros(3, np.uint32), 3)
         assert err.value.status == G.MG_UNSUPPORTED
+
+
+def test_reference_default_training_run():
+    """The reference's default `mesh-gpt train` (src/bin/mesh-gpt.rs:173-299):
+    demo corpus, 1000 AdamW steps, a report every 100.  Step 0 is the published
+    3.38668 / 3.37963 (docs/mesh-gpt.md:264); every report follows the oracle's
+    f64-gradient run (tests/golden/demo_training.json, written by
+    make_demo_training.py) to 1e-4 through step 300, after which the two f32
+    update trajectories drift apart by rounding (at most 2.7e-3 observed, bound
+    5e-3); step 1000 is within 1e-2 of the published 1.70316 / 1.91340, itself
+    a third such trajectory (the CUDA f32 run), 1.3e-3 / 6.8e-3 from the f64 one."""
+    import json
+    import os
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    with open(os.path.join(here, "golden", "mesh-gpt-demo.txt"), encoding="utf-8") as f:
+        text = f.read()
+    chars = sorted(set(text))
+    index = {ch: i for i, ch in enumerate(chars)}
+    tokens = np.array([index[ch] for ch in text], dtype=np.uint32)
+    with open(os.path.join(here, "golden", "demo_training.json")) as f:
+        expected = {r["step"]: r for r in json.load(f)["reports"]}
+    ex, ey = O.text_batch(tokens, True, 32, 8, 101)
+    x0, y0 = O.text_batch(tokens, False, 32, 8, 7)
+    with G.MeshGpt(0, G.GptConfig(vocab_size=26), 7) as model:
+        reports = {0: (model.cross_entropy(x0, y0, 32), model.cross_entropy(ex, ey, 32))}
+        assert abs(reports[0][0] - 3.38668) <= 1e-5 and abs(reports[0][1] - 3.37963) <= 1e-5
+        opts = G.AdamW(learning_rate=0.003, weight_decay=0.01)
+        total, count = 0.0, 0
+        for step in range(1, 1001):
+            x, y = O.text_batch(tokens, False, 32, 8, 7 + step)
+            total += model.train_batch(x, y, 32, opts)
+            count += 1
+            if step % 100 == 0:
+                reports[step] = (total / count, model.cross_entropy(ex, ey, 32))
+                total, count = 0.0, 0
+    for step, (train, valid) in reports.items():
+        bound = 1e-4 if step <= 300 else 5e-3
+        assert abs(train - expected[step]["train"]) <= bound, (step, train, expected[step])
+        assert abs(valid - expected[step]["validation"]) <= bound, (step, valid, expected[step])
+    assert abs(reports[1000][0] - 1.70316) <= 1e-2 and abs(reports[1000][1] - 1.91340) <= 1e-2
