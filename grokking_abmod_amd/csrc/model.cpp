@@ -574,7 +574,7 @@ struct MeshGpt::Impl {
         size_t n1, inv1, qs, ks, vs, qr, kr, qinv, kinv, y, lse, z, ps, xm, inv2, n2, fs;
     };
     struct TrainPlan {
-        size_t es, x, invf, nf, et, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
+        size_t es, eg, er, x, invf, nf, et, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
         std::vector<TrainBlock> blocks;
     };
 
@@ -589,6 +589,8 @@ struct MeshGpt::Impl {
         };
         TrainPlan p;
         p.es = take(cfg.embedding == TokenEmbedding::Mesh ? A * V * W : 0);
+        p.eg = take(cfg.geometry.transformed() ? V * W : 0);
+        p.er = take(V);
         p.x = take((cfg.layers + 1) * RW);
         for (size_t b = 0; b < cfg.layers; ++b) {
             TrainBlock k;
@@ -631,12 +633,10 @@ struct MeshGpt::Impl {
     }
 
     void check_trainable() const {
-        if (cfg.geometry.transformed())
-            throw Error("training supports embeddings without normalisation or protected coordinates", kUnsupported);
         if (cfg.width > size_t(kern::train::kMaxWidth) || cfg.head_width() > size_t(kern::train::kMaxHeadWidth) ||
             cfg.attention_mesh_depth > size_t(kern::train::kMaxDepth) ||
             cfg.ffn_mesh_depth > size_t(kern::train::kMaxDepth))
-            throw Error("training supports width <= 1024, head width <= 128 and mesh depth <= 16", kUnsupported);
+            throw Error("training supports width <= 1024 and mesh depth <= 16", kUnsupported);
     }
 
     // config.rs:230-252: inputs as validate_tokens, equal lengths, targets in
@@ -714,10 +714,19 @@ struct MeshGpt::Impl {
         const size_t emb = group(layout.embedding);
 
         // Token vectors: the embedding mesh of the codes (its layers kept), or the table.
-        const float *Ev = w + emb;
+        const float *Eraw = w + emb;
         if (cfg.embedding == TokenEmbedding::Mesh) {
             T::mesh_forward(ma, codes.as<float>(), at(p.es), w + emb, V, stream);
-            Ev = at(p.es) + size_t(A - 1) * V * W;
+            Eraw = at(p.es) + size_t(A - 1) * V * W;
+        }
+        // The geometry's normalisation and protected coordinates (reference.rs:130-149).
+        const bool geometry = cfg.geometry.transformed(), normalize = cfg.geometry.normalization != EmbeddingNorm::None;
+        const float radius = cfg.geometry.radius(cfg.width);
+        const int preserve = int(cfg.geometry.preserve_features);
+        const float *Ev = Eraw;
+        if (geometry) {
+            T::geometry_forward(Eraw, codes.as<float>(), at(p.eg), at(p.er), V, W, radius, normalize, preserve, stream);
+            Ev = at(p.eg);
         }
         T::gather(Ev, tok, at(p.x), R, W, stream);
         auto X = [&](int b) { return at(p.x) + size_t(b) * RW; };
@@ -783,12 +792,20 @@ struct MeshGpt::Impl {
         }
         // The tied vectors collect the head's gradient and the gathered rows'.
         T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), part, R, W, V, stream);
+        if (geometry) T::geometry_backward(Eraw, at(p.er), at(p.dE), V, W, radius, normalize, preserve, stream);
         if (cfg.embedding == TokenEmbedding::Mesh)
             T::mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, false, w + emb, part, grad + emb, V,
                              stream);
         else
             T::copy(at(p.dE), grad + emb, size_t(V) * W, stream);
+        // config.rs:490-500: the frozen embedding group, and the final mesh rows
+        // that write protected residual coordinates.
         if (cfg.geometry.frozen) T::fill(grad + emb, 0.0f, cfg.embedding_parameter_count(), stream);
+        for (size_t id = 0; id < layout.groups.size(); ++id) {
+            const auto range = layout.constrained_range(cfg, id);
+            if (range.second > range.first)
+                T::fill(grad + layout.groups[id].offset + range.first, 0.0f, range.second - range.first, stream);
+        }
     }
 
     // gpu.rs:2296-2313: the per-row f32 losses summed in f64 on the host.

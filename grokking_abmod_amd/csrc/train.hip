@@ -134,10 +134,10 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const 
             sums[(sub * W + c) * 2 + 1] = gp[l];
         }
         __syncthreads();
-        if (threadIdx.x < 2 * W) {
+        for (int i = threadIdx.x; i < 2 * W; i += kMaxWidth) {
             float acc = 0.0f;
-            for (int k = 0; k < RPB; ++k) acc += sums[k * 2 * W + threadIdx.x];
-            partials[(size_t(blockIdx.x) * depth + l) * 2 * W + threadIdx.x] = acc;
+            for (int k = 0; k < RPB; ++k) acc += sums[k * 2 * W + i];
+            partials[(size_t(blockIdx.x) * depth + l) * 2 * W + i] = acc;
         }
         __syncthreads();
     }
@@ -539,6 +539,20 @@ __device__ __forceinline__ float lanes_dot(const float (&a)[EPL], const float (&
 template <int EPL>
 __device__ __forceinline__ void lanes_partner(const float (&x)[EPL], int hd, int lane, float (&out)[EPL]) {
     const int half = hd / 2;
+    if (EPL > 1 && half % 64 == 0) {
+        // The partner sits in the same lane, half / 64 registers away.
+        const int k = half / 64;
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            const int pe = 64 * e < half ? e + k : e - k;
+            float v = 0.0f;
+#pragma unroll
+            for (int f = 0; f < EPL; ++f)
+                if (f == pe) v = x[f];
+            out[e] = lane + 64 * e < hd ? v : 0.0f;
+        }
+        return;
+    }
 #pragma unroll
     for (int e = 0; e < EPL; ++e) {
         const int d = lane + 64 * e, pd = d < half ? d + half : d - half;
@@ -772,13 +786,67 @@ template <class F>
 void by_lanes(int hd, F &&f) {
     if (hd <= 64)
         f(std::integral_constant<int, 1>{});
-    else
+    else if (hd <= 128)
         f(std::integral_constant<int, 2>{});
+    else if (hd <= 256)
+        f(std::integral_constant<int, 4>{});
+    else if (hd <= 512)
+        f(std::integral_constant<int, 8>{});
+    else
+        f(std::integral_constant<int, 16>{});
 }
 
 // Sequences up to this length take the wave-per-row attention kernels; longer
-// ones the thread-per-row kernels, whose key loops do 64 rows' work per wave.
+// ones the thread-per-row kernels, whose key loops do 64 rows' work per wave
+// (head widths up to 128; wider heads always take the wave kernels).
 constexpr int kWaveAttentionMax = 64;
+
+// ---- embedding geometry (reference.rs:130-149): rows scaled to the radius,
+// then protected coordinates replaced by their codes.  One wave per token.
+
+__global__ void __launch_bounds__(kThreads) geometry_forward_kernel(const float *__restrict__ raw,
+                                                                    const float *__restrict__ codes,
+                                                                    float *__restrict__ out, float *__restrict__ rinv,
+                                                                    int V, int W, float radius, int normalize,
+                                                                    int preserve) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= V) return;
+    const float *x = raw + size_t(t) * W;
+    float scale = 1.0f;
+    if (normalize) {
+        float sq = 0.0f;
+        for (int c = lane; c < W; c += 64) sq = fmaf(x[c], x[c], sq);
+        const float r = rsqrtf(fmaxf(wave_sum(sq), kXsaFloor));
+        if (lane == 0) rinv[t] = r;
+        scale = r * radius;
+    }
+    for (int c = lane; c < W; c += 64)
+        out[size_t(t) * W + c] = c < preserve ? codes[size_t(t) * W + c] : x[c] * scale;
+}
+
+// In place on g (d loss / d geometry output -> d loss / d raw rows): protected
+// coordinates are constants (gradient 0); the scaling's Jacobian is
+// radius r (g - r^2 raw (g . raw)) above the norm floor, radius r g below it.
+__global__ void __launch_bounds__(kThreads) geometry_backward_kernel(const float *__restrict__ raw,
+                                                                     const float *__restrict__ rinv, float *g, int V,
+                                                                     int W, float radius, int normalize,
+                                                                     int preserve) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= V) return;
+    const float *x = raw + size_t(t) * W;
+    float *row = g + size_t(t) * W;
+    for (int c = lane; c < min(preserve, W); c += 64) row[c] = 0.0f;
+    if (!normalize) return;
+    float dot = 0.0f, sq = 0.0f;
+    for (int c = lane; c < W; c += 64) {
+        dot = fmaf(row[c], x[c], dot);
+        sq = fmaf(x[c], x[c], sq);
+    }
+    dot = wave_sum(dot);
+    sq = wave_sum(sq);
+    const float r = rinv[t], k = sq >= kXsaFloor ? r * r * dot : 0.0f;
+    for (int c = lane; c < W; c += 64) row[c] = radius * r * (row[c] - k * x[c]);
+}
 
 // ---- head, loss and embedding gradient
 
@@ -1023,7 +1091,7 @@ void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, b
 void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
                        int sequence, int W, int H, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
-    if (sequence <= kWaveAttentionMax) {
+    if (sequence <= kWaveAttentionMax || W / H > 128) {
         by_lanes(W / H, [&](auto e) {
             hipLaunchKernelGGL(attention_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
                                dim3(kThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
@@ -1040,7 +1108,7 @@ void attention_backward(const float *q, const float *k, const float *v, const fl
                         const float *dy, float *dq, float *dk, float *dv, float *dsum, int rows, int sequence, int W,
                         int H, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
-    if (sequence <= kWaveAttentionMax) {
+    if (sequence <= kWaveAttentionMax || W / H > 128) {
         by_lanes(W / H, [&](auto e) {
             constexpr int EPL = decltype(e)::value;
             const dim3 grid(blocks_for(size_t(rows) * H * 64));
@@ -1091,6 +1159,18 @@ void qk_backward(float *g, const float *pre, const float *inv, const float2 *tab
                            dim3(kThreads), 0, stream, g, pre, inv, table, rows, sequence, W, H, int(norm),
                            int(rotate));
     });
+}
+
+void geometry_forward(const float *raw, const float *codes, float *out, float *rinv, int V, int W, float radius,
+                      bool normalize, int preserve, hipStream_t stream) {
+    hipLaunchKernelGGL(geometry_forward_kernel, dim3(blocks_for(size_t(V) * 64)), dim3(kThreads), 0, stream, raw,
+                       codes, out, rinv, V, W, radius, int(normalize), preserve);
+}
+
+void geometry_backward(const float *raw, const float *rinv, float *g, int V, int W, float radius, bool normalize,
+                       int preserve, hipStream_t stream) {
+    hipLaunchKernelGGL(geometry_backward_kernel, dim3(blocks_for(size_t(V) * 64)), dim3(kThreads), 0, stream, raw,
+                       rinv, g, V, W, radius, int(normalize), preserve);
 }
 
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream) {

@@ -13,7 +13,7 @@ namespace meshgpt::kern::train {
 
 constexpr int kMaxDepth = 16;       // mesh layers per stack (weight gradients stay in registers)
 constexpr int kMaxWidth = 1024;     // one thread per channel
-constexpr int kMaxHeadWidth = 128;  // attention keeps a head row per thread
+constexpr int kMaxHeadWidth = 1024; // wave-per-row kernels keep up to 16 dims a lane
 
 struct Mesh {
     int W, depth, butterfly, log2w;
@@ -67,6 +67,15 @@ void xsa_forward(const float *y, const float *v, float *z, int rows, int W, int 
 // Its backward: dy and dv written.
 void xsa_backward(const float *y, const float *v, const float *dz, float *dy, float *dv, int rows, int W, int H,
                   hipStream_t stream);
+
+// The embedding geometry (reference.rs:130-149) on V raw token rows: scaled to
+// `radius` when normalize (rinv[t] keeps 1 / max(|row|, 1e-12)), then the first
+// `preserve` coordinates replaced by the codes.
+void geometry_forward(const float *raw, const float *codes, float *out, float *rinv, int V, int W, float radius,
+                      bool normalize, int preserve, hipStream_t stream);
+// Its backward in place on g (d loss / d out -> d loss / d raw).
+void geometry_backward(const float *raw, const float *rinv, float *g, int V, int W, float radius, bool normalize,
+                       int preserve, hipStream_t stream);
 
 // x[r] = E[tokens[r]]
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream);

@@ -25,8 +25,8 @@ def configs_for(**kw):
     return G.GptConfig(**kw), O.config(**kw)
 
 
-# (config, cases) from src/bin/mesh-gpt.rs:651-857 whose head width is at most
-# 128 (the training kernels' limit), plus the demo and grok training shapes.
+# (config, cases) from src/bin/mesh-gpt.rs:651-857, the demo and grok training
+# shapes, each operator switched off, and the frozen geometry.
 TRAIN = [
     (dict(vocab_size=129, context=3, width=2, heads=1, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2),
      [(1, 1), (2, 3), (43, 3)]),
@@ -48,6 +48,10 @@ TRAIN = [
           embedding=1, connectivity=1), [(2, 4), (33, 4)]),
     (dict(vocab_size=9, context=3, width=128, heads=4, layers=1, attention_mesh_depth=8, ffn_mesh_depth=8,
           connectivity=1), [(2, 3), (43, 3)]),
+    (dict(vocab_size=7, context=3, width=1024, heads=4, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(1, 1), (1, 3), (2, 3)]),
+    (dict(vocab_size=7, context=5, width=512, heads=1, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2),
+     [(2, 5)]),
     # the demo training shape (docs/mesh-gpt.md:240-243) and the grok shape
     (dict(vocab_size=26, context=32, width=32, heads=4, layers=2), [(2, 32)]),
     (dict(vocab_size=99, context=4, width=128, heads=4, layers=2), [(32, 4)]),
@@ -62,9 +66,24 @@ TRAIN = [
 ]
 
 
+# MSHGPT09 ablations (the inference tests' list, tests/test_gpu_parity.py):
+# operator switches and embedding geometry forms, normalisation and protected
+# coordinates (reference.rs:130-149, geometry.rs:238-325).
+ABLATION_BASE = dict(vocab_size=7, context=12, width=128, heads=4, layers=2, attention_mesh_depth=3,
+                     ffn_mesh_depth=3, connectivity=1)
+ABLATIONS = [
+    dict(rope=0, qk_norm=0, xsa=0), dict(xsa=0, embedding=1), dict(form=9), dict(normalization=2),
+    dict(preserve_features=3), dict(form=1, order=2, modulus=5, seed=17),
+    dict(form=2, harmonics=3, embedding=1, normalization=1), dict(form=5, overlap=0.25, embedding=1, qk_norm=0),
+    dict(width=12, heads=4, rope=0), dict(preserve_features=2, frozen=1),
+]
+TRAIN += [(dict(ABLATION_BASE, **kw), [(3, 12)]) for kw in ABLATIONS]
+
+
 def _ids(cfg):
     extra = "".join(f"-{k}{v}" for k, v in cfg.items() if k in ("embedding", "connectivity", "rope", "qk_norm",
-                                                                  "xsa", "frozen"))
+                                                                  "xsa", "frozen", "form", "normalization",
+                                                                  "preserve_features", "order", "overlap"))
     full = dict(attention_mesh_depth=4, ffn_mesh_depth=6)  # GptConfig::default() depths
     full.update(cfg)
     return "V{vocab_size}-W{width}-H{heads}-L{layers}-A{attention_mesh_depth}-F{ffn_mesh_depth}".format(**full) + extra
@@ -124,10 +143,14 @@ def test_adamw_steps(setting, frozen):
                 assert np.array_equal(got[:skip], before[:skip])
 
 
-def test_training_then_inference_uses_the_new_weights():
+@pytest.mark.parametrize("geometry", [{}, dict(normalization=2), dict(preserve_features=2)],
+                         ids=["default", "normalised", "protected"])
+def test_training_then_inference_uses_the_new_weights(geometry):
     """After train_batch the tables derived from the weights are rebuilt before
-    the next inference call: logits equal the oracle's on the trained weights."""
-    cfg = dict(vocab_size=26, context=32, width=32, heads=4, layers=2)
+    the next inference call: logits equal the oracle's on the trained weights.
+    With protected coordinates, the weights that would write them stay zero
+    (set_parameters accepts the trained vector: config.rs:476-488)."""
+    cfg = dict(vocab_size=26, context=32, width=32, heads=4, layers=2, **geometry)
     g, o = configs_for(**cfg)
     x, y, _ = batch(26, 2, 32)
     with G.MeshGpt(0, g, 7) as model:
@@ -141,6 +164,7 @@ def test_training_then_inference_uses_the_new_weights():
         assert_close(model.token_embeddings(), O.token_embeddings(o, params), what="embeddings after training")
         toks = model.generate_tokens(x[None, :16], 4, 0.0, 7)[0]
         assert np.array_equal(toks, O.generate(o, params, x[:16], 4, 0.0, 7, cached=True))
+        model.set_parameters(params)
 
 
 def test_training_trajectory_follows_the_oracle():
@@ -189,9 +213,9 @@ def test_training_rejections_carry_the_reference_messages():
         with pytest.raises(G.MeshGptError):
             model.train_batch(x, x, 3, G.AdamW(epsilon=0.0))
         assert np.array_equal(model.parameters(), before)
-    wide, _ = configs_for(vocab_size=7, context=3, width=1024, heads=4, layers=1, attention_mesh_depth=2,
+    deep, _ = configs_for(vocab_size=7, context=3, width=8, heads=2, layers=1, attention_mesh_depth=17,
                           ffn_mesh_depth=2)
-    with G.MeshGpt(0, wide, 7) as model:
+    with G.MeshGpt(0, deep, 7) as model:
         with pytest.raises(G.MeshGptError) as err:
             model.loss_and_gradient(np.zeros(3, np.uint32), np.zeros(3, np.uint32), 3)
         assert err.value.status == G.MG_UNSUPPORTED
