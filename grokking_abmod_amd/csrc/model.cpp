@@ -633,10 +633,8 @@ struct MeshGpt::Impl {
     }
 
     void check_trainable() const {
-        if (cfg.width > size_t(kern::train::kMaxWidth) || cfg.head_width() > size_t(kern::train::kMaxHeadWidth) ||
-            cfg.attention_mesh_depth > size_t(kern::train::kMaxDepth) ||
-            cfg.ffn_mesh_depth > size_t(kern::train::kMaxDepth))
-            throw Error("training supports width <= 1024 and mesh depth <= 16", kUnsupported);
+        if (cfg.width > size_t(kern::train::kMaxWidth) || cfg.head_width() > size_t(kern::train::kMaxHeadWidth))
+            throw Error("training supports width <= 1024", kUnsupported);
     }
 
     // config.rs:230-252: inputs as validate_tokens, equal lengths, targets in

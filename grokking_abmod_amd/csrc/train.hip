@@ -25,7 +25,12 @@ constexpr int kRowThreads = 64;  // per-(row, head) kernels: one wave per workgr
 
 __device__ __forceinline__ float elu(float z) { return z >= 0.0f ? z : expm1f(z); }
 
-__device__ __forceinline__ int stride_of(const Mesh &m, int l) { return m.butterfly ? 1 << (l % m.log2w) : 1; }
+__device__ __forceinline__ int stride_of(const Mesh &m, int l) {
+    return m.butterfly ? 1 << ((m.layer0 + l) % m.log2w) : 1;
+}
+
+// Whether layer l of a launch applies the ELU (every layer but the stack's last).
+__device__ __forceinline__ bool elu_layer(const Mesh &m, int l) { return l + 1 < m.depth || !m.linear_top; }
 
 int block_for(int W) { return std::max(64, (W + 63) / 64 * 64); }
 
@@ -48,7 +53,7 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_forward_kernel(Mesh m, const f
                 if (p >= W) p -= W;
                 const float2 wl = reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W)[c];
                 float z = cur[c] * wl.x + cur[p] * wl.y;
-                if (l + 1 < m.depth) z = elu(z);
+                if (elu_layer(m, l)) z = elu(z);
                 nxt[c] = z;
                 stack[(size_t(l) * rows + r) * W + c] = z;
             }
@@ -97,7 +102,7 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const 
             if (p >= W) p -= W;
             xs[l] = x[c];
             xp[l] = x[p];
-            if (l + 1 < depth) act[l] = stack[(size_t(l) * rows + r) * W + c];
+            if (elu_layer(m, l)) act[l] = stack[(size_t(l) * rows + r) * W + c];
         }
 #pragma unroll
         for (int l = kMaxDepth - 1; l >= 0; --l) {
@@ -105,7 +110,7 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const 
             const int s = stride_of(m, l);
             if (live) {
                 // ELU'(z) from its output a: 1 for a >= 0, else exp(z) = a + 1.
-                const float dz = l + 1 < depth && act[l] < 0.0f ? g * (act[l] + 1.0f) : g;
+                const float dz = elu_layer(m, l) && act[l] < 0.0f ? g * (act[l] + 1.0f) : g;
                 gs[l] = fmaf(dz, xs[l], gs[l]);
                 gp[l] = fmaf(dz, xp[l], gp[l]);
                 dz_row[c] = dz;
@@ -223,7 +228,7 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, const floa
             for (int j = 0; j < CPL; ++j) {
                 const int c = lane + 64 * j;
                 float z = x[j] * wt[l][j].x + p[j] * wt[l][j].y;
-                if (l + 1 < m.depth) z = elu(z);
+                if (elu_layer(m, l)) z = elu(z);
                 x[j] = z;
                 if (c < W) stack[(size_t(l) * rows + r) * W + c] = z;
             }
@@ -263,7 +268,7 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, const flo
                 const bool ok = l < depth && c < W;
                 const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
                 xin[l][j] = ok ? x[c] : 0.0f;
-                act[l][j] = ok && l + 1 < depth ? stack[(size_t(l) * rows + r) * W + c] : 0.0f;
+                act[l][j] = ok && elu_layer(m, l) ? stack[(size_t(l) * rows + r) * W + c] : 0.0f;
             }
 #pragma unroll
         for (int l = kMaxDepth - 1; l >= 0; --l) {
@@ -1027,7 +1032,9 @@ void by_head_width(int hd, F &&f) {
 
 }  // namespace
 
-void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
+// One launch over at most kMaxDepth layers.
+void mesh_forward_launch(const Mesh &m, const float *in, float *stack, const float *w, int rows,
+                         hipStream_t stream) {
     if (const int cpl = mesh_wave_cpl(m.W)) {
         const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)));
         if (cpl == 1)
@@ -1042,13 +1049,32 @@ void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, 
                        stack, w, rows);
 }
 
-size_t mesh_partial_floats(const Mesh &m, int rows) {
-    const int groups = mesh_wave_cpl(m.W) ? mesh_wave_groups(rows) : mesh_groups(m, rows);
-    return size_t(groups) * m.depth * m.W * 2;
+// Layers [l0, l0 + kMaxDepth) of m as one launch's stack.
+Mesh mesh_chunk(const Mesh &m, int l0) {
+    Mesh c = m;
+    c.layer0 = m.layer0 + l0;
+    c.depth = std::min(kMaxDepth, m.depth - l0);
+    c.linear_top = l0 + c.depth == m.depth ? m.linear_top : 0;
+    return c;
 }
 
-void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
-                   bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream) {
+void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
+    const size_t plane = size_t(rows) * m.W;
+    for (int l0 = 0; l0 < m.depth; l0 += kMaxDepth)
+        mesh_forward_launch(mesh_chunk(m, l0), l0 == 0 ? in : stack + (l0 - 1) * plane, stack + l0 * plane,
+                            w + size_t(l0) * 2 * m.W, rows, stream);
+}
+
+size_t mesh_partial_floats(const Mesh &m, int rows) {
+    const int groups = mesh_wave_cpl(m.W) ? mesh_wave_groups(rows) : mesh_groups(m, rows);
+    const size_t partial = size_t(groups) * std::min(m.depth, kMaxDepth) * m.W * 2;
+    return m.depth > kMaxDepth ? partial + 2 * size_t(rows) * m.W : partial;
+}
+
+// One launch over at most kMaxDepth layers, then the reduction of its partials.
+void mesh_backward_launch(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
+                          bool accumulate, const float *w, float *partials, float *grad, int rows,
+                          hipStream_t stream) {
     const int n = m.depth * m.W * 2;
     int groups;
     if (const int cpl = mesh_wave_cpl(m.W)) {
@@ -1067,6 +1093,23 @@ void mesh_backward(const Mesh &m, const float *in, const float *stack, const flo
                            stream, m, in, stack, dout, din, int(accumulate), w, partials, rows);
     }
     hipLaunchKernelGGL(reduce_groups_kernel, dim3((n + 63) / 64), dim3(1024), 0, stream, partials, groups, n, grad);
+}
+
+// Deep stacks go down kMaxDepth layers a launch, from the top; the gradient
+// rows between launches alternate between two planes after the partial sums.
+void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
+                   bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream) {
+    const size_t plane = size_t(rows) * m.W;
+    const int top = (m.depth - 1) / kMaxDepth * kMaxDepth;
+    float *between = partials + (mesh_partial_floats(m, rows) - (top > 0 ? 2 * plane : 0));
+    const float *g = dout;
+    for (int l0 = top, k = 0; l0 >= 0; l0 -= kMaxDepth, ++k) {
+        float *to = l0 == 0 ? din : between + (k & 1) * plane;
+        mesh_backward_launch(mesh_chunk(m, l0), l0 == 0 ? in : stack + (l0 - 1) * plane, stack + l0 * plane, g, to,
+                             l0 == 0 && accumulate, w + size_t(l0) * 2 * m.W, partials, grad + size_t(l0) * 2 * m.W,
+                             rows, stream);
+        g = to;
+    }
 }
 
 void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream) {

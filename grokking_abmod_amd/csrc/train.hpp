@@ -11,19 +11,25 @@
 
 namespace meshgpt::kern::train {
 
-constexpr int kMaxDepth = 16;       // mesh layers per stack (weight gradients stay in registers)
+constexpr int kMaxDepth = 16;       // mesh layers per kernel launch (weight gradients stay in registers)
 constexpr int kMaxWidth = 1024;     // one thread per channel
 constexpr int kMaxHeadWidth = 1024; // wave-per-row kernels keep up to 16 dims a lane
 
+// A mesh stack of `depth` layers; the kernels run it kMaxDepth layers at a
+// time, each launch on the layers from layer0 (absolute: the butterfly stride
+// of layer l is 1 << (l % log2w)), its top layer linear only when it is the
+// stack's last.
 struct Mesh {
     int W, depth, butterfly, log2w;
+    int layer0 = 0, linear_top = 1;
 };
 
 // stack[l] (rows x W, l < depth) = output of mesh layer l on `in`
 // (reference.rs:422-453): z = x[c] w_self + x[(c + s) % W] w_partner, ELU on
 // all layers but the last.
 void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream);
-// Scratch floats mesh_backward needs for `rows` rows.
+// Scratch floats mesh_backward needs for `rows` rows: the partial sums, and for
+// stacks deeper than kMaxDepth the gradient rows between launches.
 size_t mesh_partial_floats(const Mesh &m, int rows);
 // Backward of mesh_forward: dout is d loss / d stack[depth - 1]; din (when not
 // null) receives d loss / d in (added to what it holds when accumulate); the

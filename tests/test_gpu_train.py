@@ -111,6 +111,37 @@ def test_loss_and_gradients_match_the_oracle(cfg, cases):
                 assert abs(model.cross_entropy(x, targets, s) - loss) <= 1e-6 * (1 + abs(loss))
 
 
+# Stacks deeper than the 16 layers of one kernel launch, in the wave (width
+# <= 128) and the LDS (wider) mesh kernels, both connectivities, the mesh
+# embedding included.
+DEEP = [
+    dict(vocab_size=7, context=3, width=8, heads=2, layers=1, attention_mesh_depth=32, ffn_mesh_depth=20),
+    dict(vocab_size=7, context=3, width=8, heads=2, layers=1, attention_mesh_depth=17, ffn_mesh_depth=33,
+         embedding=1, connectivity=1),
+    dict(vocab_size=7, context=3, width=128, heads=2, layers=1, attention_mesh_depth=20, ffn_mesh_depth=17,
+         embedding=1),
+    dict(vocab_size=9, context=3, width=256, heads=4, layers=1, attention_mesh_depth=18, ffn_mesh_depth=40,
+         embedding=1, connectivity=1),
+]
+
+
+@pytest.mark.parametrize("cfg", DEEP, ids=[_ids(c) for c in DEEP])
+def test_deep_stacks_match_the_oracle(cfg):
+    """At the seeded initialisation a deep stack's gradient all but vanishes, so
+    the weights are drawn from U(-1.3, 1.3) instead: every layer carries a
+    gradient of order 1e-3..1."""
+    g, o = configs_for(**cfg)
+    params = np.random.default_rng(3).uniform(-1.3, 1.3, O.parameter_count(o)).astype(np.float32)
+    x, y, _ = batch(cfg["vocab_size"], 2, 3)
+    ref_loss, ref_grad = O.loss_and_gradient(o, params, x, y, 3)
+    assert np.median(np.abs(ref_grad)) > 1e-4
+    with G.MeshGpt(0, g, 7) as model:
+        model.set_parameters(params)
+        loss, grad = model.loss_and_gradient(x, y, 3)
+        assert abs(loss - ref_loss) <= TOL * (1 + abs(ref_loss)), (loss, ref_loss)
+        assert_close(grad, ref_grad, what="deep stack gradient")
+
+
 @pytest.mark.parametrize("setting", [dict(learning_rate=0.002, weight_decay=0.01),
                                      dict(learning_rate=0.001, weight_decay=1.0, beta2=0.98)])
 @pytest.mark.parametrize("frozen", [0, 1])
@@ -213,9 +244,9 @@ def test_training_rejections_carry_the_reference_messages():
         with pytest.raises(G.MeshGptError):
             model.train_batch(x, x, 3, G.AdamW(epsilon=0.0))
         assert np.array_equal(model.parameters(), before)
-    deep, _ = configs_for(vocab_size=7, context=3, width=8, heads=2, layers=1, attention_mesh_depth=17,
-                          ffn_mesh_depth=2)
-    with G.MeshGpt(0, deep, 7) as model:
+    wide, _ = configs_for(vocab_size=7, context=3, width=2048, heads=2, layers=1, attention_mesh_depth=1,
+                          ffn_mesh_depth=1)
+    with G.MeshGpt(0, wide, 7) as model:
         with pytest.raises(G.MeshGptError) as err:
             model.loss_and_gradient(np.zeros(3, np.uint32), np.zeros(3, np.uint32), 3)
         assert err.value.status == G.MG_UNSUPPORTED
