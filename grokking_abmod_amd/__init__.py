@@ -28,7 +28,7 @@ EXPORTS = (
     "mg_checkpoint_parameters", "mg_checkpoint_free", "mg_checkpoint_save", "mg_copy_bandwidth",
     "mg_tokenizer_from_text", "mg_tokenizer_encode", "mg_tokenizer_decode", "mg_sample_logits", "mg_sample_logits_noalloc", "mg_expf",
     "mg_adamw_default", "mg_cross_entropy", "mg_loss_and_gradient", "mg_train_batch",
-    "mg_equation_split", "mg_equation_batch",
+    "mg_equation_split", "mg_equation_batch", "mg_text_batch",
 )
 
 IGNORE_TARGET = 0xFFFFFFFF  # MG_IGNORE_TARGET (src/gpt/mod.rs:26)
@@ -147,6 +147,7 @@ def lib():
         "mg_equation_split": (i, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, u64, _szp, _szp]),
         "mg_equation_batch": (i, [ctypes.c_uint32, ctypes.c_uint32, ctypes.c_double, u64, i, _szp, sz, _u32p,
                                   _u32p]),
+        "mg_text_batch": (i, [_u32p, sz, _cfgp, i, sz, sz, u64, _u32p, _u32p]),
     }
     for name, (res, args) in sigs.items():
         fn = getattr(L, name)
@@ -249,6 +250,18 @@ def equation_batch(indices, validation=False, modulus=97, operation=0, train_fra
     _check(lib().mg_equation_batch(modulus, operation, train_fraction, seed, int(validation),
                                    idx.ctypes.data_as(_szp), idx.size, _p(inputs, _u32p), _p(targets, _u32p)))
     return inputs[:4 * idx.size], targets[:4 * idx.size]
+
+
+def text_batch(tokens, config, validation, sequence, batch, seed):
+    """TextDataset::new + batch (src/gpt/text.rs:63-108): (inputs, targets) of
+    batch windows of sequence tokens from the corpus's 90/10 split."""
+    t = np.ascontiguousarray(tokens, dtype=np.uint32).reshape(-1)
+    n = min(max(sequence * batch, 1), 131072)  # larger batches are rejected before anything is written
+    inputs = np.empty(n, dtype=np.uint32)
+    targets = np.empty_like(inputs)
+    _check(lib().mg_text_batch(_p(t, _u32p), t.size, ctypes.byref(config), int(validation), sequence, batch, seed,
+                               _p(inputs, _u32p), _p(targets, _u32p)))
+    return inputs[:sequence * batch], targets[:sequence * batch]
 
 
 class MeshGpt:

@@ -208,6 +208,16 @@ int mg_equation_batch(uint32_t modulus, uint32_t operation, double train_fractio
     });
 }
 
+int mg_text_batch(const uint32_t *tokens, size_t n_tokens, const mg_config *config, int validation,
+                  size_t sequence, size_t batch, uint64_t seed, uint32_t *inputs, uint32_t *targets) {
+    return guarded([&] {
+        require((tokens != nullptr || n_tokens == 0) && inputs != nullptr && targets != nullptr,
+                "tokens and outputs must not be null");
+        const TextDataset d(std::vector<uint32_t>(tokens, tokens + n_tokens), to_config(config));
+        d.batch(validation != 0, sequence, batch, seed, inputs, targets);
+    });
+}
+
 void mg_adamw_default(mg_adamw *out) {
     if (!out) return;
     const AdamWOptions d;

@@ -12,27 +12,10 @@ namespace meshgpt {
 
 namespace {
 
-const char *form_name(EmbeddingForm f) {
-    static const char *names[] = {"parity",      "circle",    "fourier",   "orthogonal",
-                                  "simplex",     "equiangular", "antipodal", "hypercube",
-                                  "signed-permutations", "sphere"};
-    return names[uint32_t(f)];
-}
-
 size_t bit_length(size_t x) {
     size_t n = 0;
     for (; x; x >>= 1) ++n;
     return n;
-}
-
-// Rust's Display of an f32: the shortest decimal that reads back to the same
-// value, never in exponent form.
-std::string display_f32(float v) {
-    if (std::isnan(v)) return "NaN";
-    if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
-    char buf[96];
-    auto res = std::to_chars(buf, buf + sizeof buf, v, std::chars_format::fixed);
-    return std::string(buf, res.ptr);
 }
 
 bool is_prime(size_t n) {
@@ -117,7 +100,7 @@ void EmbeddingGeometry::validate(const GptConfig &config) const {
     default: break;
     }
     if (!fits)
-        throw Error(std::string(form_name(form)) + " embedding does not fit vocabulary " + std::to_string(v) +
+        throw Error(std::string(name(form)) + " embedding does not fit vocabulary " + std::to_string(v) +
                     ", width " + std::to_string(w) + ", overlap " + display_f32(overlap));
     if (order != EmbeddingOrder::Token) {
         if (modulus < 2 || modulus > 254 || !is_prime(modulus) || v != modulus + 2)

@@ -4,6 +4,7 @@
 #include "meshgpt_types.hpp"
 
 #include <algorithm>
+#include <charconv>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -27,6 +28,37 @@ MeshConnectivity parse_connectivity(const std::string &text) {
     if (text == "neighbor") return MeshConnectivity::Neighbor;
     if (text == "butterfly") return MeshConnectivity::Butterfly;
     throw Error("unknown mesh connectivity: " + text);
+}
+
+namespace {
+const char *const kFormNames[] = {"parity",     "circle",    "fourier",   "orthogonal",          "simplex",
+                                  "equiangular", "antipodal", "hypercube", "signed-permutations", "sphere"};
+const char *const kOrderNames[] = {"token", "residue", "discrete-log"};
+const char *const kNormNames[] = {"none", "unit", "rms"};
+
+template <class E, size_t N>
+E parse_named(const char *const (&names)[N], const std::string &text, const char *type) {
+    for (size_t i = 0; i < N; ++i)
+        if (text == names[i]) return E(i);
+    throw Error(std::string("unknown ") + type + ": " + text);
+}
+}  // namespace
+
+const char *name(EmbeddingForm f) { return kFormNames[uint32_t(f)]; }
+const char *name(EmbeddingOrder o) { return kOrderNames[uint32_t(o)]; }
+const char *name(EmbeddingNorm n) { return kNormNames[uint32_t(n)]; }
+EmbeddingForm parse_form(const std::string &t) { return parse_named<EmbeddingForm>(kFormNames, t, "EmbeddingForm"); }
+EmbeddingOrder parse_order(const std::string &t) {
+    return parse_named<EmbeddingOrder>(kOrderNames, t, "EmbeddingOrder");
+}
+EmbeddingNorm parse_norm(const std::string &t) { return parse_named<EmbeddingNorm>(kNormNames, t, "EmbeddingNorm"); }
+
+std::string display_f32(float v) {
+    if (std::isnan(v)) return "NaN";
+    if (std::isinf(v)) return v > 0 ? "inf" : "-inf";
+    char buf[96];
+    auto res = std::to_chars(buf, buf + sizeof buf, v, std::chars_format::fixed);
+    return std::string(buf, res.ptr);
 }
 
 static size_t ilog2(size_t x) {
@@ -83,6 +115,37 @@ void AdamWOptions::validate() const {
         !(beta1 >= 0.0f && beta1 < 1.0f) || !fin(beta2) || !(beta2 >= 0.0f && beta2 < 1.0f) || !fin(epsilon) ||
         epsilon <= 0.0f)
         throw Error("AdamW requires finite positive learning rate/epsilon, nonnegative decay, and betas in [0, 1)");
+}
+
+void GptTrainOptions::validate() const {
+    if (steps == 0 || report_every == 0) throw Error("steps and report_every must be positive");
+    if (!std::isfinite(learning_rate) || learning_rate <= 0.0f || !std::isfinite(weight_decay) || weight_decay < 0.0f)
+        throw Error("learning_rate must be positive and weight_decay nonnegative; both must be finite");
+}
+
+TextDataset::TextDataset(const std::vector<uint32_t> &tokens, const GptConfig &config) {
+    config.validate();
+    for (uint32_t id : tokens)
+        if (id >= config.vocab_size) throw Error("dataset has invalid token IDs");
+    const size_t split = tokens.size() * 9 / 10;
+    if (split <= config.context || tokens.size() - split <= config.context)
+        throw Error("corpus is too short for a 90/10 split at this context length");
+    training_.assign(tokens.begin(), tokens.begin() + split);
+    validation_.assign(tokens.begin() + split, tokens.end());
+}
+
+void TextDataset::batch(bool validation, size_t sequence, size_t batch, uint64_t seed, uint32_t *inputs,
+                        uint32_t *targets) const {
+    const std::vector<uint32_t> &corpus = validation ? validation_ : training_;
+    if (sequence == 0 || sequence >= corpus.size() || batch == 0 || batch > kMaxRows / sequence)
+        throw Error("invalid dataset batch dimensions");
+    Random random(seed);
+    for (size_t b = 0; b < batch; ++b) {
+        // An f32 product truncated toward zero, as the reference's `as usize`.
+        const size_t start = size_t(random.unit() * float(corpus.size() - sequence));
+        std::copy_n(corpus.begin() + start, sequence, inputs + b * sequence);
+        std::copy_n(corpus.begin() + start + 1, sequence, targets + b * sequence);
+    }
 }
 
 void GptConfig::validate_tokens(const uint32_t *tokens, size_t n, size_t sequence) const {

@@ -64,6 +64,18 @@ enum class EmbeddingForm : uint32_t {
 enum class EmbeddingOrder : uint32_t { Token = 0, Residue, DiscreteLog };
 enum class EmbeddingNorm : uint32_t { None = 0, Unit, Rms };
 
+// Their names and parsers (geometry.rs:8-46): "unknown EmbeddingForm: X" etc.
+const char *name(EmbeddingForm f);
+const char *name(EmbeddingOrder o);
+const char *name(EmbeddingNorm n);
+EmbeddingForm parse_form(const std::string &text);
+EmbeddingOrder parse_order(const std::string &text);
+EmbeddingNorm parse_norm(const std::string &text);
+
+// Rust's Display of an f32: the shortest decimal that reads back to the same
+// value, never in exponent form.
+std::string display_f32(float v);
+
 struct GptConfig;
 
 // EmbeddingGeometry (geometry.rs:49-81); defaults keep the signed parity codes.
@@ -75,6 +87,15 @@ struct AdamWOptions {
     float beta2 = 0.999f;
     float epsilon = 1e-8f;
     void validate() const;  // config.rs:278-295
+};
+
+// GptTrainOptions (config.rs:297-333): the `mesh-gpt train` loop's settings.
+struct GptTrainOptions {
+    size_t steps = 1000;
+    float learning_rate = 0.003f;
+    float weight_decay = 0.01f;
+    size_t report_every = 100;
+    void validate() const;
 };
 
 struct EmbeddingGeometry {
@@ -169,6 +190,20 @@ struct EquationDataset {
     static EquationDataset build(size_t modulus, uint32_t operation, double train_fraction, uint64_t seed);
     // inputs and targets of 4 * n rows for the split's equations `indices`
     void batch(bool validation, const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets) const;
+};
+// TextDataset (text.rs:58-108): a tokenised corpus split 90/10 into training
+// and validation; a batch is `batch` windows of `sequence` tokens at seeded
+// starts, targets shifted by one.
+class TextDataset {
+  public:
+    TextDataset(const std::vector<uint32_t> &tokens, const GptConfig &config);
+    void batch(bool validation, size_t sequence, size_t batch, uint64_t seed, uint32_t *inputs,
+               uint32_t *targets) const;
+    size_t training_size() const { return training_.size(); }
+    size_t validation_size() const { return validation_.size(); }
+
+  private:
+    std::vector<uint32_t> training_, validation_;
 };
 // The smallest primitive root of a prime (geometry.rs:166-184).
 size_t primitive_root(size_t prime);

@@ -139,6 +139,13 @@ int mg_equation_split(uint32_t modulus, uint32_t operation, double train_fractio
  * and targets (MG_IGNORE_TARGET but the answer) for the split's equations. */
 int mg_equation_batch(uint32_t modulus, uint32_t operation, double train_fraction, uint64_t seed, int validation,
                       const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets);
+/* TextDataset::new + batch (src/gpt/text.rs:63-108): the corpus `tokens` split
+ * 90/10 (checked against `config`'s vocabulary and context), then `batch`
+ * windows of `sequence` tokens from the training (validation = 0) or
+ * validation split at starts drawn from `seed`; targets are the inputs shifted
+ * by one.  inputs and targets hold batch * sequence tokens each. */
+int mg_text_batch(const uint32_t *tokens, size_t n_tokens, const mg_config *config, int validation,
+                  size_t sequence, size_t batch, uint64_t seed, uint32_t *inputs, uint32_t *targets);
 /* SpecializedMeshGpt::token_embeddings (gpu.rs:2056-2068): vocab_size x width. */
 int mg_token_embeddings(mg_model *model, float *out, size_t n);
 /* SpecializedMeshGpt::hidden_states (gpu.rs:2070-2092): n x width. */

@@ -291,3 +291,91 @@ def test_reference_default_training_run():
         assert abs(train - expected[step]["train"]) <= bound, (step, train, expected[step])
         assert abs(valid - expected[step]["validation"]) <= bound, (step, valid, expected[step])
     assert abs(reports[1000][0] - 1.70316) <= 1e-2 and abs(reports[1000][1] - 1.91340) <= 1e-2
+
+
+def test_cli_train_default_run(tmp_path):
+    """`mesh-gpt train` with every default (src/bin/mesh-gpt.rs:173-299) on the
+    demo corpus: its stdout lines, loss.csv, geometry.txt, run.txt, checkpoint
+    and sample.txt.  The reports are those of the same loop run through the
+    library (the golden trajectory and the published step 0 / 1000, as in
+    test_reference_default_training_run), and the checkpoint holds exactly the
+    weights that loop produces."""
+    import json
+    import os
+    import re
+    import subprocess
+
+    here = os.path.dirname(os.path.abspath(__file__))
+    corpus = os.path.join(here, "golden", "mesh-gpt-demo.txt")
+    out = tmp_path / "run"
+    res = subprocess.run([G.CLI_PATH, "train", "--dataset", corpus, "--output", str(out)], capture_output=True,
+                         text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    head, sep, rest = res.stdout.partition(f"Saved checkpoint to {out / 'model.bin'}\n\n")
+    assert sep and rest.endswith("\n")
+    lines = head.splitlines()
+    assert lines[0] == "Mesh GPT: blocks=2, width=32, heads=4, context=32, vocabulary=26, parameters=3072"
+    assert lines[1] == ("Meshes: Q/K/V/output depth=4, FFN depth=6; embeddings=mesh, form=parity, norm=none, "
+                        "protected=0; RoPE=true, QK-Norm=true, XSA=true")
+    pattern = re.compile(r"step +(\d+): train CE=(\d+\.\d{5}), validation CE=(\d+\.\d{5}), perplexity=(\d+\.\d{3})$")
+    reports = {}
+    for line in lines[2:13]:
+        m = pattern.match(line)
+        assert m and len(line.split(":")[0]) == len("step ") + 6, line
+        reports[int(m.group(1))] = tuple(float(v) for v in m.groups()[1:])
+    assert sorted(reports) == list(range(0, 1001, 100))
+    assert re.fullmatch(r"Training time: \d+\.\d{3} s", lines[13]) and len(lines) == 14
+    with open(os.path.join(here, "golden", "demo_training.json")) as f:
+        expected = {r["step"]: r for r in json.load(f)["reports"]}
+    for step, (train, valid, ppl) in reports.items():
+        bound = 1e-4 if step <= 300 else 5e-3
+        assert abs(train - expected[step]["train"]) <= bound + 5e-6, (step, train)
+        assert abs(valid - expected[step]["validation"]) <= bound + 5e-6, (step, valid)
+        assert abs(ppl - np.exp(valid)) <= 2e-4 * ppl
+    # docs/mesh-gpt.md:264-266
+    assert abs(reports[0][0] - 3.38668) <= 1e-5 and abs(reports[0][1] - 3.37963) <= 1e-5
+    assert abs(reports[1000][0] - 1.70316) <= 1e-2 and abs(reports[1000][1] - 1.91340) <= 1e-2
+
+    rows = (out / "loss.csv").read_text().splitlines()
+    assert rows[0] == "step,train_cross_entropy,validation_cross_entropy,validation_perplexity"
+    csv = {int(r.split(",")[0]): [float(v) for v in r.split(",")[1:]] for r in rows[1:]}
+    assert sorted(csv) == sorted(reports)
+    for step, (train, valid, ppl) in csv.items():
+        assert abs(train - reports[step][0]) <= 5e-6 and abs(valid - reports[step][1]) <= 5e-6
+        assert abs(ppl - np.exp(valid)) <= 1e-8 * ppl
+
+    assert (out / "geometry.txt").read_text() == (
+        "embedding_form=parity\nembedding_order=token\nembedding_frequency=1\nembedding_harmonics=1\n"
+        "equiangular_overlap=0\nembedding_norm=none\nfreeze_embedding=false\npreserve_features=0\n"
+        "geometry_modulus=0\ngeometry_seed=0\nrope=true\nqk_norm_enabled=true\nxsa_enabled=true\n"
+        "geometry_supplies_arithmetic_order=false\n")
+    run = dict(line.split("=", 1) for line in (out / "run.txt").read_text().splitlines())
+    fixed = dict(attention="xsa", positions="slice_rope", rope_base="10000", normalization="pre_rmsnorm",
+                 rmsnorm_epsilon="1e-5", rmsnorm_affine="false", qk_norm="per_head_rmsnorm", bias="false",
+                 embeddings="mesh", token_codes="signed_binary_parity_radix",
+                 embedding_depth="attention_mesh_depth", head="tied_mesh_embeddings", all_parameters="mesh_edges",
+                 dataset=corpus, seed="7", steps="1000", batch="8", width="32", heads="4", layers="2", context="32",
+                 attention_mesh_depth="4", ffn_mesh_depth="6", parameters="3072", learning_rate="0.003",
+                 weight_decay="0.01")
+    for key, value in fixed.items():
+        assert run.pop(key) == value, key
+    assert abs(float(run.pop("initial_validation_cross_entropy")) - csv[0][1]) <= 1e-9
+    assert abs(float(run.pop("final_validation_cross_entropy")) - csv[1000][1]) <= 1e-9
+    assert float(run.pop("training_seconds")) > 0 and not run
+
+    # The same loop through the library: batches from the product's TextDataset
+    # (checked against the oracle's on the CPU), seeds 7 + step.
+    saved = G.Checkpoint.load(str(out / "model.bin"))
+    cfg = G.GptConfig(vocab_size=26)
+    assert saved.config == cfg
+    text = open(corpus, encoding="utf-8").read()
+    tokenizer = G.CharacterTokenizer.from_text(text)
+    assert G.CharacterTokenizer(saved.characters) == tokenizer
+    tokens = np.array(tokenizer.encode(text), dtype=np.uint32)
+    with G.MeshGpt(0, cfg, 7) as model:
+        for step in range(1, 1001):
+            x, y = G.text_batch(tokens, cfg, False, 32, 8, 7 + step)
+            model.train_batch(x, y, 32)
+        assert np.array_equal(model.parameters().view(np.uint32), saved.parameters.view(np.uint32))
+        sample = model.generate(tokenizer.characters, "the little robot ", 240, 0.7, 7)
+    assert (out / "sample.txt").read_text(encoding="utf-8") == sample == rest[:-1]

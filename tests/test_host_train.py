@@ -1,12 +1,17 @@
 """Host-side pieces of the training path (no GPU): the equation dataset the
-training benchmark and the grok evaluation feed (src/gpt/grokking.rs:116-258)
-and the AdamW defaults (src/gpt/config.rs:258-276), through the C ABI.
+training benchmark and the grok evaluation feed (src/gpt/grokking.rs:116-258),
+the text dataset of `mesh-gpt train` (src/gpt/text.rs:58-108), the AdamW
+defaults (src/gpt/config.rs:258-276) and the `mesh-gpt train` rejections that
+come before any device work (src/bin/mesh-gpt.rs:173-184, geometry.rs:24-55).
 
-The dataset is checked against the oracle's restatement, which the published
-step-0 cross-entropies pin (tests/test_oracle.py), for every operation; the
-split sizes are the published 4704 / 4705 (docs/grokking.md:14-15).
+The datasets are checked against the oracle's restatements, which the
+published step-0 cross-entropies pin (tests/test_oracle.py), for every
+operation; the split sizes are the published 4704 / 4705
+(docs/grokking.md:14-15).
 """
 import ctypes
+import os
+import subprocess
 
 import numpy as np
 import pytest
@@ -66,3 +71,94 @@ def test_adamw_defaults():
     a = G.AdamW()
     assert (a.learning_rate, a.weight_decay, a.beta1, a.beta2, a.epsilon) == tuple(
         float(np.float32(v)) for v in (0.003, 0.01, 0.9, 0.999, 1e-8))
+
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+CORPUS = os.path.join(ROOT, "tests", "golden", "mesh-gpt-demo.txt")
+
+
+def demo_tokens():
+    with open(CORPUS, encoding="utf-8") as f:
+        text = f.read()
+    chars = sorted(set(text))
+    index = {ch: i for i, ch in enumerate(chars)}
+    return np.array([index[ch] for ch in text], dtype=np.uint32), len(chars)
+
+
+@pytest.mark.parametrize("validation", [False, True])
+@pytest.mark.parametrize("sequence,batch,seed", [(32, 8, 7), (32, 8, 101), (5, 3, 2 ** 64 - 1), (1, 40, 12345)])
+def test_text_batches_equal_the_oracle(validation, sequence, batch, seed):
+    tokens, V = demo_tokens()
+    cfg = G.GptConfig(vocab_size=V, context=32)
+    x, y = G.text_batch(tokens, cfg, validation, sequence, batch, seed)
+    want_x, want_y = O.text_batch(tokens, validation, sequence, batch, seed)
+    assert np.array_equal(x, want_x) and np.array_equal(y, want_y)
+    # Windows stay inside their split and targets are the next tokens.
+    split = tokens.size * 9 // 10
+    corpus = tokens[split:] if validation else tokens[:split]
+    for b in range(batch):
+        row = x[b * sequence:(b + 1) * sequence]
+        starts = [i for i in range(corpus.size - sequence) if np.array_equal(corpus[i:i + sequence], row)]
+        assert any(np.array_equal(corpus[i + 1:i + sequence + 1], y[b * sequence:(b + 1) * sequence])
+                   for i in starts)
+
+
+def test_text_dataset_rejections_carry_the_reference_messages():
+    tokens, V = demo_tokens()
+    cfg = G.GptConfig(vocab_size=V, context=32)
+    cases = [
+        (lambda: G.text_batch(tokens, G.GptConfig(vocab_size=V - 1, context=32), False, 32, 8, 7),
+         "dataset has invalid token IDs"),
+        (lambda: G.text_batch(tokens[:300], cfg, False, 32, 8, 7),
+         "corpus is too short for a 90/10 split at this context length"),
+        (lambda: G.text_batch(tokens, cfg, False, 0, 8, 7), "invalid dataset batch dimensions"),
+        (lambda: G.text_batch(tokens, cfg, False, 32, 0, 7), "invalid dataset batch dimensions"),
+        (lambda: G.text_batch(tokens, cfg, False, 32, 4097, 7), "invalid dataset batch dimensions"),
+        (lambda: G.text_batch(tokens, cfg, True, tokens.size - tokens.size * 9 // 10, 1, 7),
+         "invalid dataset batch dimensions"),
+        (lambda: G.text_batch(tokens, G.GptConfig(vocab_size=V, context=32, heads=3), False, 32, 8, 7),
+         "heads must be in 1..64 and divide width"),
+    ]
+    for call, message in cases:
+        with pytest.raises(G.MeshGptError) as err:
+            call()
+        assert message in str(err.value)
+
+
+def cli(*args):
+    return subprocess.run([G.CLI_PATH, *args], capture_output=True, text=True, timeout=60)
+
+
+@pytest.mark.parametrize("args,message", [
+    (["--steps", "0"], "steps and report_every must be positive"),
+    (["--report-every", "0"], "steps and report_every must be positive"),
+    (["--learning-rate", "0"], "learning_rate must be positive and weight_decay nonnegative; both must be finite"),
+    (["--weight-decay", "-1"], "learning_rate must be positive and weight_decay nonnegative; both must be finite"),
+    (["--learning-rate", "inf"], "learning_rate must be positive and weight_decay nonnegative; both must be finite"),
+    (["--prompt", ""], "generation prompt must not be empty"),
+    (["--temperature", "-1"], "temperature must be finite and nonnegative"),
+    (["--heads", "3"], "heads must be in 1..64 and divide width"),
+    (["--context", "5000"], "context must be in 1..4096"),
+    (["--rope", "2"], "--rope requires 0 or 1"),
+    (["--qk-norm", "x"], "invalid value for --qk-norm: x"),
+    (["--embedding-form", "cube"], "unknown EmbeddingForm: cube"),
+    (["--embedding-order", "x"], "unknown EmbeddingOrder: x"),
+    (["--embedding-norm", "l2"], "unknown EmbeddingNorm: l2"),
+    (["--embedding-norm"], "missing value for --embedding-norm"),
+    (["--unknown"], "unknown option: --unknown; use --help"),
+])
+def test_cli_train_rejections(args, message):
+    """Each is raised before any device work, so no GPU is needed."""
+    res = cli("train", "--dataset", CORPUS, *args)
+    assert res.returncode == 1 and res.stdout == ""
+    assert res.stderr == f'Error: "{message}"\n'
+
+
+def test_cli_help_lists_the_training_and_geometry_flags():
+    res = cli("--help")
+    assert res.returncode == 0
+    for flag in ("--steps", "--learning-rate", "--weight-decay", "--report-every", "--embedding-form",
+                 "--embedding-order", "--embedding-frequency", "--embedding-harmonics", "--equiangular-overlap",
+                 "--embedding-norm", "--freeze-embedding", "--preserve-features", "--geometry-seed", "--rope",
+                 "--qk-norm", "--xsa"):
+        assert flag in res.stdout, flag
