@@ -574,7 +574,8 @@ struct MeshGpt::Impl {
         size_t n1, inv1, qs, ks, vs, qr, kr, qinv, kinv, y, lse, z, ps, xm, inv2, n2, fs;
     };
     struct TrainPlan {
-        size_t es, eg, er, x, invf, nf, et, logits, dlogits, loss, dx, dn, dq, dk, dv, dy, dt, dsum, dE, total;
+        size_t es, eg, er, x, invf, nf, et, logits, dlogits, loss, dx, dn, dnk, dnv, dq, dk, dv, dy, dt, dsum, dE,
+            total;
         std::vector<TrainBlock> blocks;
     };
 
@@ -621,6 +622,8 @@ struct MeshGpt::Impl {
         p.loss = take(R);
         p.dx = take(RW);
         p.dn = take(RW);
+        p.dnk = take(RW);
+        p.dnv = take(RW);
         p.dq = take(RW);
         p.dk = take(RW);
         p.dv = take(RW);
@@ -660,7 +663,7 @@ struct MeshGpt::Impl {
         const T::Mesh mf{W, int(cfg.ffn_mesh_depth), shape.butterfly, shape.log2w};
         const size_t P = layout.count();
         bool grown = tact.ensure(train_plan(n).total * 4);
-        grown |= tpart.ensure(std::max({T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
+        grown |= tpart.ensure(std::max({3 * T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
                                         T::mesh_partial_floats(ma, V), T::embedding_partial_floats(R, W, V)}) *
                               4);
         grown |= tgrad.ensure(P * 4);
@@ -729,28 +732,34 @@ struct MeshGpt::Impl {
         T::gather(Ev, tok, at(p.x), R, W, stream);
         auto X = [&](int b) { return at(p.x) + size_t(b) * RW; };
         auto last = [&](size_t o, int depth) { return at(o) + size_t(depth - 1) * RW; };
+        T::rmsnorm_forward(X(0), at(p.blocks[0].n1), at(p.blocks[0].inv1), R, W, 1, stream);
         for (int b = 0; b < L; ++b) {
             const TrainBlock &k = p.blocks[b];
             const Block &g = layout.blocks[b];
-            T::rmsnorm_forward(X(b), at(k.n1), at(k.inv1), R, W, 1, stream);
-            T::mesh_forward(ma, at(k.n1), at(k.qs), w + group(g.query), R, stream);
-            T::mesh_forward(ma, at(k.n1), at(k.ks), w + group(g.key), R, stream);
-            T::mesh_forward(ma, at(k.n1), at(k.vs), w + group(g.value), R, stream);
-            // reference.rs:174-193: QK-Norm, then RoPE, each when switched on
-            T::qk_forward(last(k.qs, A), at(k.qr), at(k.qinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
-            T::qk_forward(last(k.ks, A), at(k.kr), at(k.kinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+            // Q, K and V of n1 in one launch, then QK-Norm and RoPE of q and k
+            // in one (reference.rs:174-193, each when switched on).
+            const float *n1 = at(k.n1);
+            const float *qkv_in[3] = {n1, n1, n1}, *qkv_w[3] = {w + group(g.query), w + group(g.key),
+                                                                  w + group(g.value)};
+            float *qkv[3] = {at(k.qs), at(k.ks), at(k.vs)};
+            T::mesh_forward_set(ma, 3, qkv_in, qkv, qkv_w, R, stream);
+            const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)};
+            float *qk_out[2] = {at(k.qr), at(k.kr)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
+            T::qk_forward(2, qk_pre, qk_out, qk_inv, table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
             T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), R, seq, W, H, stream);
             if (cfg.xsa)
                 T::xsa_forward(at(k.y), last(k.vs, A), at(k.z), R, W, H, stream);
             else
                 T::copy(at(k.y), at(k.z), RW, stream);
             T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);
-            T::add(X(b), last(k.ps, A), at(k.xm), RW, stream);
-            T::rmsnorm_forward(at(k.xm), at(k.n2), at(k.inv2), R, W, 1, stream);
+            // xm = x_b + proj, n2 = rmsnorm(xm); x_{b+1} = xm + ffn, normalised
+            // by the next block (or the final norm) in the same launch.
+            T::add_rmsnorm_forward(X(b), last(k.ps, A), at(k.xm), at(k.n2), at(k.inv2), R, W, stream);
             T::mesh_forward(mf, at(k.n2), at(k.fs), w + group(g.ffn), R, stream);
-            T::add(at(k.xm), last(k.fs, F), X(b + 1), RW, stream);
+            const bool top = b + 1 == L;
+            T::add_rmsnorm_forward(at(k.xm), last(k.fs, F), X(b + 1), at(top ? p.nf : p.blocks[b + 1].n1),
+                                   at(top ? p.invf : p.blocks[b + 1].inv1), R, W, stream);
         }
-        T::rmsnorm_forward(X(L), at(p.nf), at(p.invf), R, W, 1, stream);
         T::head_logits(at(p.nf), Ev, at(p.et), at(p.logits), R, W, V, stream);
         T::cross_entropy(at(p.logits), ttgt.as<uint32_t>(), at(p.dlogits), at(p.loss), R, V, sc, stream);
         if (!backward) return;
@@ -777,16 +786,20 @@ struct MeshGpt::Impl {
             T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dy, dq, dk, dv, at(p.dsum),
                                   R, seq, W, H, stream);
             if (cfg.rope || cfg.qk_norm) {
-                T::qk_backward(dq, last(k.qs, A), at(k.qinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
-                T::qk_backward(dk, last(k.ks, A), at(k.kinv), table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+                float *qk_g[2] = {dq, dk};
+                const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
+                T::qk_backward(2, qk_g, qk_pre, qk_inv, table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
             }
-            T::mesh_backward(ma, at(k.n1), at(k.qs), dq, dn, false, w + group(g.query), part, grad + group(g.query),
-                             R, stream);
-            T::mesh_backward(ma, at(k.n1), at(k.ks), dk, dn, true, w + group(g.key), part, grad + group(g.key), R,
-                             stream);
-            T::mesh_backward(ma, at(k.n1), at(k.vs), dv, dn, true, w + group(g.value), part, grad + group(g.value),
-                             R, stream);
-            T::rmsnorm_backward(X(b), at(k.inv1), dn, dx, true, R, W, 1, stream);
+            // The Q, K and V meshes' backward in one launch, each into its own
+            // rows; the norm's backward adds them (in that order).
+            const float *n1 = at(k.n1);
+            const float *qkv_in[3] = {n1, n1, n1}, *qkv[3] = {at(k.qs), at(k.ks), at(k.vs)};
+            const float *qkv_dout[3] = {dq, dk, dv};
+            const float *qkv_w[3] = {w + group(g.query), w + group(g.key), w + group(g.value)};
+            float *qkv_din[3] = {dn, at(p.dnk), at(p.dnv)};
+            float *qkv_grad[3] = {grad + group(g.query), grad + group(g.key), grad + group(g.value)};
+            T::mesh_backward_set(ma, 3, qkv_in, qkv, qkv_dout, qkv_din, false, qkv_w, part, qkv_grad, R, stream);
+            T::rmsnorm_backward_sum3(X(b), at(k.inv1), dn, at(p.dnk), at(p.dnv), dx, true, R, W, stream);
         }
         // The tied vectors collect the head's gradient and the gathered rows'.
         T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), part, R, W, V, stream);

@@ -18,6 +18,29 @@
 namespace meshgpt::kern::train {
 namespace {
 
+// Up to kMaxSet stacks of one shape in one launch, stack blockIdx.y reading
+// its own input and weights.
+struct MeshSet {
+    const float *in[kMaxSet];
+    float *stack[kMaxSet];
+    const float *w[kMaxSet];
+};
+struct MeshGradSet {
+    const float *in[kMaxSet], *stack[kMaxSet], *dout[kMaxSet], *w[kMaxSet];
+    float *din[kMaxSet], *partials[kMaxSet];
+};
+struct ReduceSet {
+    const float *part[kMaxSet];
+    float *out[kMaxSet];
+};
+// QK-Norm and RoPE of q and k in one launch: out[i] (the gradient rows, in
+// place, for the backward) from the pre-norm rows pre[i], factors inv[i].
+struct QkSet {
+    const float *pre[kMaxSet];
+    float *out[kMaxSet];
+    float *inv[kMaxSet];
+};
+
 constexpr float kRmsEps = 1e-5f;                                         // src/gpt/mod.rs:38
 constexpr float kXsaFloor = float(double(1e-12f) * double(1e-12f));      // XSA_EPSILON^2
 constexpr int kThreads = 256;
@@ -38,10 +61,11 @@ unsigned blocks_for(size_t n, int threads = kThreads) { return unsigned((n + thr
 
 // ---- mesh stacks
 
-__global__ void __launch_bounds__(kMaxWidth) mesh_forward_kernel(Mesh m, const float *__restrict__ in,
-                                                                 float *__restrict__ stack,
-                                                                 const float *__restrict__ w, int rows) {
+__global__ void __launch_bounds__(kMaxWidth) mesh_forward_kernel(Mesh m, MeshSet set, int rows) {
     extern __shared__ float buf[];  // two rows: the layer's input and output
+    const float *__restrict__ in = set.in[blockIdx.y];
+    float *__restrict__ stack = set.stack[blockIdx.y];
+    const float *__restrict__ w = set.w[blockIdx.y];
     const int c = threadIdx.x, W = m.W;
     for (int r = blockIdx.x; r < rows; r += gridDim.x) {
         float *cur = buf, *nxt = buf + W;
@@ -74,12 +98,15 @@ __host__ __device__ inline int mesh_rpb(int W) { return kMaxWidth / mesh_sub(W);
 // c of it carries d loss / d (channel c) down the layers and adds its two
 // weights' gradients over its rows in registers.  At the end the sub-blocks'
 // sums are added in LDS (in sub-block order) into the workgroup's partial.
-__global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const float *__restrict__ in,
-                                                                  const float *__restrict__ stack,
-                                                                  const float *__restrict__ dout, float *din,
-                                                                  int accumulate, const float *__restrict__ w,
-                                                                  float *__restrict__ partials, int rows) {
+__global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, MeshGradSet set, int accumulate,
+                                                                  int rows) {
     extern __shared__ float lds[];  // RPB rows of dz, then RPB x W x 2 sums
+    const float *__restrict__ in = set.in[blockIdx.y];
+    const float *__restrict__ stack = set.stack[blockIdx.y];
+    const float *__restrict__ dout = set.dout[blockIdx.y];
+    float *din = set.din[blockIdx.y];
+    const float *__restrict__ w = set.w[blockIdx.y];
+    float *__restrict__ partials = set.partials[blockIdx.y];
     const int W = m.W, depth = m.depth, SUB = mesh_sub(W), RPB = mesh_rpb(W);
     const int sub = threadIdx.x / SUB, c = threadIdx.x % SUB;
     float *dz_row = lds + sub * W;
@@ -151,9 +178,10 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, const 
 // out[i] = sum over g < groups of part[g * n + i], in g order per wave and
 // the waves' sums in wave order: 64 outputs per workgroup, wave k of its 16
 // adding groups k, k + 16, ...
-__global__ void __launch_bounds__(1024) reduce_groups_kernel(const float *__restrict__ part, int groups, int n,
-                                                            float *__restrict__ out) {
+__global__ void __launch_bounds__(1024) reduce_groups_kernel(ReduceSet set, int groups, int n) {
     __shared__ float sums[16][64];
+    const float *__restrict__ part = set.part[blockIdx.y];
+    float *__restrict__ out = set.out[blockIdx.y];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = blockIdx.x * 64 + lane;
     float acc = 0.0f;
     if (i < n)
@@ -201,9 +229,10 @@ __device__ __forceinline__ void channel_shift(const float (&x)[CPL], int d, int 
 constexpr int kMeshWaveRows = 2;  // rows per wave of the wave-per-row mesh backward
 
 template <int CPL>
-__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, const float *__restrict__ in,
-                                                              float *__restrict__ stack, const float *__restrict__ w,
-                                                              int rows) {
+__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, int rows) {
+    const float *__restrict__ in = set.in[blockIdx.y];
+    float *__restrict__ stack = set.stack[blockIdx.y];
+    const float *__restrict__ w = set.w[blockIdx.y];
     const int lane = threadIdx.x & 63, W = m.W;
     const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), waves = gridDim.x * (kThreads / 64);
     // The stack's weights of this lane's channels, loaded once.
@@ -240,12 +269,14 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, const floa
 // adds the weights' gradients in registers; the workgroup's waves add theirs
 // in LDS (in wave order) into the workgroup's partial.
 template <int CPL>
-__global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, const float *__restrict__ in,
-                                                               const float *__restrict__ stack,
-                                                               const float *__restrict__ dout, float *din,
-                                                               int accumulate, const float *__restrict__ w,
-                                                               float *__restrict__ partials, int rows) {
+__global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradSet set, int accumulate, int rows) {
     extern __shared__ float sums[];  // (kThreads / 64) x depth x W x 2
+    const float *__restrict__ in = set.in[blockIdx.y];
+    const float *__restrict__ stack = set.stack[blockIdx.y];
+    const float *__restrict__ dout = set.dout[blockIdx.y];
+    float *din = set.din[blockIdx.y];
+    const float *__restrict__ w = set.w[blockIdx.y];
+    float *__restrict__ partials = set.partials[blockIdx.y];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, W = m.W, depth = m.depth;
     const int wave = blockIdx.x * (kThreads / 64) + wv, waves = gridDim.x * (kThreads / 64);
     float gs[kMaxDepth][CPL], gp[kMaxDepth][CPL];
@@ -337,51 +368,52 @@ int mesh_wave_groups(int rows) {
 
 // ---- norms (one wave per (row, group))
 
-__global__ void __launch_bounds__(kThreads) rmsnorm_forward_kernel(const float *__restrict__ x, float *y,
+// With RES the normalised row is x + b, which is also stored to `sum` (the
+// residual add of the block fused into the norm that follows it).
+template <bool RES>
+__global__ void __launch_bounds__(kThreads) rmsnorm_forward_kernel(const float *__restrict__ x,
+                                                                   const float *__restrict__ b, float *sum, float *y,
                                                                    float *__restrict__ inv, int n_groups, int gw) {
     const int wave = (blockIdx.x * kThreads + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (wave >= n_groups) return;
-    const float *xs = x + size_t(wave) * gw;
+    const size_t o = size_t(wave) * gw;
+    auto value = [&](int i) { return RES ? x[o + i] + b[o + i] : x[o + i]; };
     float acc = 0.0f;
-    for (int i = lane; i < gw; i += 64) acc = fmaf(xs[i], xs[i], acc);
+    for (int i = lane; i < gw; i += 64) {
+        const float v = value(i);
+        acc = fmaf(v, v, acc);
+    }
     const float iv = rsqrtf(wave_sum(acc) * (1.0f / float(gw)) + kRmsEps);
-    for (int i = lane; i < gw; i += 64) y[size_t(wave) * gw + i] = xs[i] * iv;
+    for (int i = lane; i < gw; i += 64) {
+        const float v = value(i);
+        if (RES) sum[o + i] = v;
+        y[o + i] = v * iv;
+    }
     if (lane == 0) inv[wave] = iv;
 }
 
+// dy is the sum of NDY gradients, added in order (dy0 + dy1) + dy2.
+template <int NDY>
 __global__ void __launch_bounds__(kThreads) rmsnorm_backward_kernel(const float *__restrict__ x,
-                                                                    const float *__restrict__ inv, const float *dy,
-                                                                    float *dx, int accumulate, int n_groups, int gw) {
+                                                                    const float *__restrict__ inv, const float *dy0,
+                                                                    const float *dy1, const float *dy2, float *dx,
+                                                                    int accumulate, int n_groups, int gw) {
     const int wave = (blockIdx.x * kThreads + threadIdx.x) >> 6, lane = threadIdx.x & 63;
     if (wave >= n_groups) return;
     const size_t o = size_t(wave) * gw;
+    auto grad = [&](int i) {
+        float g = dy0[o + i];
+        if (NDY > 1) g += dy1[o + i];
+        if (NDY > 2) g += dy2[o + i];
+        return g;
+    };
     float acc = 0.0f;
-    for (int i = lane; i < gw; i += 64) acc = fmaf(dy[o + i], x[o + i], acc);
+    for (int i = lane; i < gw; i += 64) acc = fmaf(grad(i), x[o + i], acc);
     const float iv = inv[wave];
     const float k = wave_sum(acc) * iv * iv * iv * (1.0f / float(gw));
     for (int i = lane; i < gw; i += 64) {
-        const float d = iv * dy[o + i] - x[o + i] * k;
+        const float d = iv * grad(i) - x[o + i] * k;
         dx[o + i] = accumulate ? dx[o + i] + d : d;
-    }
-}
-
-// ---- RoPE (one thread per (row, head, pair))
-
-__global__ void __launch_bounds__(kThreads) rope_kernel(float *x, const float2 *__restrict__ table, int rows,
-                                                        int sequence, int W, int H, int inverse) {
-    const int hd = W / H, half = hd / 2;
-    const int i = blockIdx.x * kThreads + threadIdx.x;
-    if (i >= rows * H * half) return;
-    const int r = i / (H * half), rest = i % (H * half), h = rest / half, pair = rest % half;
-    const float2 cs = table[size_t(r % sequence) * half + pair];
-    float *row = x + size_t(r) * W + h * hd;
-    const float a = row[pair], b = row[pair + half];
-    if (inverse) {
-        row[pair] = a * cs.x + b * cs.y;
-        row[pair + half] = b * cs.x - a * cs.y;
-    } else {
-        row[pair] = a * cs.x - b * cs.y;
-        row[pair + half] = b * cs.x + a * cs.y;
     }
 }
 
@@ -576,10 +608,11 @@ __device__ __forceinline__ int row_wave() { return int((blockIdx.x * kThreads + 
 // QK-Norm (per-head RMSNorm) then RoPE of row r, head h, in place; inv keeps
 // the norm's factor (reference.rs:174-193, 392-409, 462-482).
 template <int EPL>
-__global__ void __launch_bounds__(kThreads) qk_forward_kernel(float *x, const float *__restrict__ pre,
-                                                              float *__restrict__ inv, const float2 *__restrict__ table,
-                                                              int rows, int sequence, int W, int H, int norm,
-                                                              int rotate) {
+__global__ void __launch_bounds__(kThreads) qk_forward_kernel(QkSet set, const float2 *__restrict__ table, int rows,
+                                                              int sequence, int W, int H, int norm, int rotate) {
+    float *x = set.out[blockIdx.y];
+    const float *__restrict__ pre = set.pre[blockIdx.y];
+    float *__restrict__ inv = set.inv[blockIdx.y];
     const int t = row_wave(), lane = threadIdx.x & 63;
     if (t >= rows * H) return;
     const int r = t / H, h = t % H, hd = W / H, half = hd / 2;
@@ -607,10 +640,11 @@ __global__ void __launch_bounds__(kThreads) qk_forward_kernel(float *x, const fl
 // Its backward in place on g: the transposed rotation, then the norm's
 // backward against the pre-norm rows `pre`.
 template <int EPL>
-__global__ void __launch_bounds__(kThreads) qk_backward_kernel(float *g, const float *__restrict__ pre,
-                                                               const float *__restrict__ inv,
-                                                               const float2 *__restrict__ table, int rows,
+__global__ void __launch_bounds__(kThreads) qk_backward_kernel(QkSet set, const float2 *__restrict__ table, int rows,
                                                                int sequence, int W, int H, int norm, int rotate) {
+    float *g = set.out[blockIdx.y];
+    const float *__restrict__ pre = set.pre[blockIdx.y];
+    const float *__restrict__ inv = set.inv[blockIdx.y];
     const int t = row_wave(), lane = threadIdx.x & 63;
     if (t >= rows * H) return;
     const int r = t / H, h = t % H, hd = W / H, half = hd / 2;
@@ -864,11 +898,6 @@ __global__ void __launch_bounds__(kThreads) gather_kernel(const float *__restric
     x[i] = E[size_t(tokens[r]) * W + c];
 }
 
-__global__ void __launch_bounds__(kThreads) add_kernel(const float *a, const float *b, float *out, size_t n) {
-    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i < n) out[i] = a[i] + b[i];
-}
-
 __global__ void __launch_bounds__(kThreads) fill_kernel(float *p, float v, size_t n) {
     const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
     if (i < n) p[i] = v;
@@ -1032,23 +1061,6 @@ void by_head_width(int hd, F &&f) {
 
 }  // namespace
 
-// One launch over at most kMaxDepth layers.
-void mesh_forward_launch(const Mesh &m, const float *in, float *stack, const float *w, int rows,
-                         hipStream_t stream) {
-    if (const int cpl = mesh_wave_cpl(m.W)) {
-        const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)));
-        if (cpl == 1)
-            hipLaunchKernelGGL(mesh_forward_wave<1>, grid, dim3(kThreads), 0, stream, m, in, stack, w, rows);
-        else
-            hipLaunchKernelGGL(mesh_forward_wave<2>, grid, dim3(kThreads), 0, stream, m, in, stack, w, rows);
-        return;
-    }
-    const int threads = block_for(m.W);
-    const unsigned grid = unsigned(std::min(rows, 2048));
-    hipLaunchKernelGGL(mesh_forward_kernel, dim3(grid), dim3(threads), 2 * m.W * sizeof(float), stream, m, in,
-                       stack, w, rows);
-}
-
 // Layers [l0, l0 + kMaxDepth) of m as one launch's stack.
 Mesh mesh_chunk(const Mesh &m, int l0) {
     Mesh c = m;
@@ -1058,11 +1070,33 @@ Mesh mesh_chunk(const Mesh &m, int l0) {
     return c;
 }
 
-void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
+void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
+                      int rows, hipStream_t stream) {
     const size_t plane = size_t(rows) * m.W;
-    for (int l0 = 0; l0 < m.depth; l0 += kMaxDepth)
-        mesh_forward_launch(mesh_chunk(m, l0), l0 == 0 ? in : stack + (l0 - 1) * plane, stack + l0 * plane,
-                            w + size_t(l0) * 2 * m.W, rows, stream);
+    for (int l0 = 0; l0 < m.depth; l0 += kMaxDepth) {
+        const Mesh c = mesh_chunk(m, l0);
+        MeshSet set{};
+        for (int i = 0; i < count; ++i) {
+            set.in[i] = l0 == 0 ? in[i] : stack[i] + (l0 - 1) * plane;
+            set.stack[i] = stack[i] + l0 * plane;
+            set.w[i] = w[i] + size_t(l0) * 2 * m.W;
+        }
+        if (const int cpl = mesh_wave_cpl(m.W)) {
+            const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)), unsigned(count));
+            if (cpl == 1)
+                hipLaunchKernelGGL(mesh_forward_wave<1>, grid, dim3(kThreads), 0, stream, c, set, rows);
+            else
+                hipLaunchKernelGGL(mesh_forward_wave<2>, grid, dim3(kThreads), 0, stream, c, set, rows);
+        } else {
+            const dim3 grid(unsigned(std::min(rows, 2048)), unsigned(count));
+            hipLaunchKernelGGL(mesh_forward_kernel, grid, dim3(block_for(m.W)), 2 * m.W * sizeof(float), stream, c,
+                               set, rows);
+        }
+    }
+}
+
+void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
+    mesh_forward_set(m, 1, &in, &stack, &w, rows, stream);
 }
 
 size_t mesh_partial_floats(const Mesh &m, int rows) {
@@ -1071,64 +1105,82 @@ size_t mesh_partial_floats(const Mesh &m, int rows) {
     return m.depth > kMaxDepth ? partial + 2 * size_t(rows) * m.W : partial;
 }
 
-// One launch over at most kMaxDepth layers, then the reduction of its partials.
-void mesh_backward_launch(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
-                          bool accumulate, const float *w, float *partials, float *grad, int rows,
-                          hipStream_t stream) {
-    const int n = m.depth * m.W * 2;
-    int groups;
-    if (const int cpl = mesh_wave_cpl(m.W)) {
-        groups = mesh_wave_groups(rows);
-        const size_t lds = size_t(kThreads / 64) * n * sizeof(float);
-        if (cpl == 1)
-            hipLaunchKernelGGL(mesh_backward_wave<1>, dim3(groups), dim3(kThreads), lds, stream, m, in, stack, dout,
-                               din, int(accumulate), w, partials, rows);
-        else
-            hipLaunchKernelGGL(mesh_backward_wave<2>, dim3(groups), dim3(kThreads), lds, stream, m, in, stack, dout,
-                               din, int(accumulate), w, partials, rows);
-    } else {
-        groups = mesh_groups(m, rows);
-        const int rpb = mesh_rpb(m.W);
-        hipLaunchKernelGGL(mesh_backward_kernel, dim3(groups), dim3(kMaxWidth), size_t(3) * rpb * m.W * sizeof(float),
-                           stream, m, in, stack, dout, din, int(accumulate), w, partials, rows);
+// Each stack of the set works in its own mesh_partial_floats of `partials`:
+// the partial sums, then (deep stacks) the two planes of gradient rows that
+// carry d loss down from one launch of kMaxDepth layers to the next.
+void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
+                       const float *const *dout, float *const *din, bool accumulate, const float *const *w,
+                       float *partials, float *const *grad, int rows, hipStream_t stream) {
+    const size_t plane = size_t(rows) * m.W, per = mesh_partial_floats(m, rows);
+    const int top = (m.depth - 1) / kMaxDepth * kMaxDepth;
+    const float *g[kMaxSet] = {};
+    for (int i = 0; i < count; ++i) g[i] = dout[i];
+    for (int l0 = top, k = 0; l0 >= 0; l0 -= kMaxDepth, ++k) {
+        const Mesh c = mesh_chunk(m, l0);
+        MeshGradSet set{};
+        ReduceSet red{};
+        for (int i = 0; i < count; ++i) {
+            float *base = partials + i * per, *between = base + (per - (top > 0 ? 2 * plane : 0));
+            float *to = l0 == 0 ? din[i] : between + (k & 1) * plane;
+            set.in[i] = l0 == 0 ? in[i] : stack[i] + (l0 - 1) * plane;
+            set.stack[i] = stack[i] + l0 * plane;
+            set.dout[i] = g[i];
+            set.din[i] = to;
+            set.w[i] = w[i] + size_t(l0) * 2 * m.W;
+            set.partials[i] = base;
+            red.part[i] = base;
+            red.out[i] = grad[i] + size_t(l0) * 2 * m.W;
+            g[i] = to;
+        }
+        const int acc = l0 == 0 && accumulate, n = c.depth * m.W * 2;
+        int groups;
+        if (const int cpl = mesh_wave_cpl(m.W)) {
+            groups = mesh_wave_groups(rows);
+            const size_t lds = size_t(kThreads / 64) * n * sizeof(float);
+            const dim3 grid{unsigned(groups), unsigned(count)};
+            if (cpl == 1)
+                hipLaunchKernelGGL(mesh_backward_wave<1>, grid, dim3(kThreads), lds, stream, c, set, acc, rows);
+            else
+                hipLaunchKernelGGL(mesh_backward_wave<2>, grid, dim3(kThreads), lds, stream, c, set, acc, rows);
+        } else {
+            groups = mesh_groups(c, rows);
+            const int rpb = mesh_rpb(m.W);
+            hipLaunchKernelGGL(mesh_backward_kernel, dim3(unsigned(groups), unsigned(count)), dim3(kMaxWidth),
+                               size_t(3) * rpb * m.W * sizeof(float), stream, c, set, acc, rows);
+        }
+        hipLaunchKernelGGL(reduce_groups_kernel, dim3(unsigned((n + 63) / 64), unsigned(count)), dim3(1024), 0,
+                           stream, red, groups, n);
     }
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3((n + 63) / 64), dim3(1024), 0, stream, partials, groups, n, grad);
 }
 
-// Deep stacks go down kMaxDepth layers a launch, from the top; the gradient
-// rows between launches alternate between two planes after the partial sums.
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
                    bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream) {
-    const size_t plane = size_t(rows) * m.W;
-    const int top = (m.depth - 1) / kMaxDepth * kMaxDepth;
-    float *between = partials + (mesh_partial_floats(m, rows) - (top > 0 ? 2 * plane : 0));
-    const float *g = dout;
-    for (int l0 = top, k = 0; l0 >= 0; l0 -= kMaxDepth, ++k) {
-        float *to = l0 == 0 ? din : between + (k & 1) * plane;
-        mesh_backward_launch(mesh_chunk(m, l0), l0 == 0 ? in : stack + (l0 - 1) * plane, stack + l0 * plane, g, to,
-                             l0 == 0 && accumulate, w + size_t(l0) * 2 * m.W, partials, grad + size_t(l0) * 2 * m.W,
-                             rows, stream);
-        g = to;
-    }
+    mesh_backward_set(m, 1, &in, &stack, &dout, &din, accumulate, &w, partials, &grad, rows, stream);
 }
 
 void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream) {
     const size_t n = size_t(rows) * groups;
-    hipLaunchKernelGGL(rmsnorm_forward_kernel, dim3(blocks_for(n * 64)), dim3(kThreads), 0, stream, x, y, inv,
-                       int(n), W / groups);
+    hipLaunchKernelGGL(rmsnorm_forward_kernel<false>, dim3(blocks_for(n * 64)), dim3(kThreads), 0, stream, x,
+                       nullptr, nullptr, y, inv, int(n), W / groups);
+}
+
+void add_rmsnorm_forward(const float *a, const float *b, float *sum, float *y, float *inv, int rows, int W,
+                         hipStream_t stream) {
+    hipLaunchKernelGGL(rmsnorm_forward_kernel<true>, dim3(blocks_for(size_t(rows) * 64)), dim3(kThreads), 0, stream,
+                       a, b, sum, y, inv, rows, W);
 }
 
 void rmsnorm_backward(const float *x, const float *inv, const float *dy, float *dx, bool accumulate, int rows,
                       int W, int groups, hipStream_t stream) {
     const size_t n = size_t(rows) * groups;
-    hipLaunchKernelGGL(rmsnorm_backward_kernel, dim3(blocks_for(n * 64)), dim3(kThreads), 0, stream, x, inv, dy, dx,
-                       int(accumulate), int(n), W / groups);
+    hipLaunchKernelGGL(rmsnorm_backward_kernel<1>, dim3(blocks_for(n * 64)), dim3(kThreads), 0, stream, x, inv, dy,
+                       nullptr, nullptr, dx, int(accumulate), int(n), W / groups);
 }
 
-void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, bool inverse, hipStream_t stream) {
-    const size_t n = size_t(rows) * H * (W / H / 2);
-    hipLaunchKernelGGL(rope_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, x, table, rows, sequence, W, H,
-                       int(inverse));
+void rmsnorm_backward_sum3(const float *x, const float *inv, const float *dy0, const float *dy1, const float *dy2,
+                           float *dx, bool accumulate, int rows, int W, hipStream_t stream) {
+    hipLaunchKernelGGL(rmsnorm_backward_kernel<3>, dim3(blocks_for(size_t(rows) * 64)), dim3(kThreads), 0, stream,
+                       x, inv, dy0, dy1, dy2, dx, int(accumulate), rows, W);
 }
 
 void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
@@ -1186,21 +1238,33 @@ void xsa_backward(const float *y, const float *v, const float *dz, float *dy, fl
     });
 }
 
-void qk_forward(const float *pre, float *out, float *inv, const float2 *table, int rows, int sequence, int W, int H,
-                bool norm, bool rotate, hipStream_t stream) {
+void qk_forward(int count, const float *const *pre, float *const *out, float *const *inv, const float2 *table,
+                int rows, int sequence, int W, int H, bool norm, bool rotate, hipStream_t stream) {
+    QkSet set{};
+    for (int i = 0; i < count; ++i) {
+        set.pre[i] = pre[i];
+        set.out[i] = out[i];
+        set.inv[i] = inv[i];
+    }
     by_lanes(W / H, [&](auto e) {
-        hipLaunchKernelGGL(qk_forward_kernel<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
-                           dim3(kThreads), 0, stream, out, pre, inv, table, rows, sequence, W, H, int(norm),
-                           int(rotate));
+        hipLaunchKernelGGL(qk_forward_kernel<decltype(e)::value>,
+                           dim3(blocks_for(size_t(rows) * H * 64), unsigned(count)), dim3(kThreads), 0, stream, set,
+                           table, rows, sequence, W, H, int(norm), int(rotate));
     });
 }
 
-void qk_backward(float *g, const float *pre, const float *inv, const float2 *table, int rows, int sequence, int W,
-                 int H, bool norm, bool rotate, hipStream_t stream) {
+void qk_backward(int count, float *const *g, const float *const *pre, const float *const *inv, const float2 *table,
+                 int rows, int sequence, int W, int H, bool norm, bool rotate, hipStream_t stream) {
+    QkSet set{};
+    for (int i = 0; i < count; ++i) {
+        set.pre[i] = pre[i];
+        set.out[i] = g[i];
+        set.inv[i] = const_cast<float *>(inv[i]);  // read only in the backward
+    }
     by_lanes(W / H, [&](auto e) {
-        hipLaunchKernelGGL(qk_backward_kernel<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
-                           dim3(kThreads), 0, stream, g, pre, inv, table, rows, sequence, W, H, int(norm),
-                           int(rotate));
+        hipLaunchKernelGGL(qk_backward_kernel<decltype(e)::value>,
+                           dim3(blocks_for(size_t(rows) * H * 64), unsigned(count)), dim3(kThreads), 0, stream, set,
+                           table, rows, sequence, W, H, int(norm), int(rotate));
     });
 }
 
@@ -1219,10 +1283,6 @@ void geometry_backward(const float *raw, const float *rinv, float *g, int V, int
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream) {
     hipLaunchKernelGGL(gather_kernel, dim3(blocks_for(size_t(rows) * W)), dim3(kThreads), 0, stream, E, tokens, x,
                        rows, W);
-}
-
-void add(const float *a, const float *b, float *out, size_t n, hipStream_t stream) {
-    hipLaunchKernelGGL(add_kernel, dim3(blocks_for(n)), dim3(kThreads), 0, stream, a, b, out, n);
 }
 
 void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
@@ -1261,7 +1321,10 @@ void embedding_gradient(const float *dlogits, const float *n, const uint32_t *to
     const int chunks = (rows + kEmbeddingChunk - 1) / kEmbeddingChunk, nvw = V * W;
     hipLaunchKernelGGL(embedding_gradient_kernel, dim3(blocks_for(size_t(nvw)), chunks), dim3(kThreads), 0, stream,
                        dlogits, n, tokens, dx, partials, rows, W, V);
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, partials, chunks, nvw, dE);
+    ReduceSet red{};
+    red.part[0] = partials;
+    red.out[0] = dE;
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, red, chunks, nvw);
 }
 
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,

@@ -14,6 +14,7 @@ namespace meshgpt::kern::train {
 constexpr int kMaxDepth = 16;       // mesh layers per kernel launch (weight gradients stay in registers)
 constexpr int kMaxWidth = 1024;     // one thread per channel
 constexpr int kMaxHeadWidth = 1024; // wave-per-row kernels keep up to 16 dims a lane
+constexpr int kMaxSet = 3;          // stacks (or heads' q and k) sharing one launch
 
 // A mesh stack of `depth` layers; the kernels run it kMaxDepth layers at a
 // time, each launch on the layers from layer0 (absolute: the butterfly stride
@@ -37,27 +38,39 @@ size_t mesh_partial_floats(const Mesh &m, int rows);
 // Deterministic: per-workgroup partial sums in `partials`, then one reduction.
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
                    bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream);
+// `count` (<= kMaxSet) stacks of the same shape at once, stack i on in[i] with
+// weights w[i] (the Q, K and V meshes of a block); the backward needs count x
+// mesh_partial_floats of `partials`, and its din[i] must be distinct rows.
+void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
+                      int rows, hipStream_t stream);
+void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
+                       const float *const *dout, float *const *din, bool accumulate, const float *const *w,
+                       float *partials, float *const *grad, int rows, hipStream_t stream);
 
 // RMSNorm over `groups` equal groups of each row (reference.rs:392-409):
 // y = x / sqrt(mean(x^2) + 1e-5); inv[row * groups + g] keeps the factor.
 void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream);
+// The residual add and the RMSNorm after it (whole rows): sum = a + b, y its norm.
+void add_rmsnorm_forward(const float *a, const float *b, float *sum, float *y, float *inv, int rows, int W,
+                         hipStream_t stream);
 // dx = inv dy - x inv^3 (dy . x) / n per group (dx may alias dy; added to
 // dx's contents when accumulate, then it must not alias).
 void rmsnorm_backward(const float *x, const float *inv, const float *dy, float *dx, bool accumulate, int rows,
                       int W, int groups, hipStream_t stream);
+// The same over whole rows with dy = (dy0 + dy1) + dy2 (the Q, K and V meshes'
+// gradients of one input).
+void rmsnorm_backward_sum3(const float *x, const float *inv, const float *dy0, const float *dy1, const float *dy2,
+                           float *dx, bool accumulate, int rows, int W, hipStream_t stream);
 
-// Slice RoPE in place (reference.rs:462-482) at position r % sequence, from
-// the (cos, sin) table [position][hd / 2]; inverse = the transposed rotation
-// (its backward).
-void rope(float *x, const float2 *table, int rows, int sequence, int W, int H, bool inverse, hipStream_t stream);
-
-// QK-Norm (when norm) then RoPE (when rotate) of the rows `pre` into `out`
-// (reference.rs:174-193); inv (rows x H) keeps the norm's factors.
-void qk_forward(const float *pre, float *out, float *inv, const float2 *table, int rows, int sequence, int W, int H,
-                bool norm, bool rotate, hipStream_t stream);
-// Its backward in place on g (d loss / d out -> d loss / d pre).
-void qk_backward(float *g, const float *pre, const float *inv, const float2 *table, int rows, int sequence, int W,
-                 int H, bool norm, bool rotate, hipStream_t stream);
+// QK-Norm (when norm) then slice RoPE (when rotate; reference.rs:462-482, at
+// position r % sequence from the (cos, sin) table [position][hd / 2]) of the
+// rows pre[i] into out[i] for i < count (q and k in one launch;
+// reference.rs:174-193); inv[i] (rows x H) keeps the norm's factors.
+void qk_forward(int count, const float *const *pre, float *const *out, float *const *inv, const float2 *table,
+                int rows, int sequence, int W, int H, bool norm, bool rotate, hipStream_t stream);
+// Its backward in place on g[i] (d loss / d out -> d loss / d pre).
+void qk_backward(int count, float *const *g, const float *const *pre, const float *const *inv, const float2 *table,
+                 int rows, int sequence, int W, int H, bool norm, bool rotate, hipStream_t stream);
 
 // Causal softmax attention per (sequence, head) (reference.rs:510-554);
 // lse[r * H + h] = max + ln(sum) of the row's scaled scores.
@@ -85,8 +98,6 @@ void geometry_backward(const float *raw, const float *rinv, float *g, int V, int
 
 // x[r] = E[tokens[r]]
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream);
-// out = a + b (elementwise, n floats; out may alias a)
-void add(const float *a, const float *b, float *out, size_t n, hipStream_t stream);
 // logits[r][t] = n[r] . E[t]; Et (W x V floats) receives E transposed.
 void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
                  hipStream_t stream);
