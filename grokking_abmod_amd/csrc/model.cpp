@@ -46,6 +46,32 @@ struct DevBuf {
     }
 };
 
+// Page-locked host memory (hipHostMalloc) for the training step's uploads and
+// its loss, so that each is one DMA copy.
+struct PinnedBuf {
+    void *p = nullptr;
+    size_t bytes = 0;
+    PinnedBuf() = default;
+    PinnedBuf(const PinnedBuf &) = delete;
+    PinnedBuf &operator=(const PinnedBuf &) = delete;
+    ~PinnedBuf() { release(); }
+    void release() {
+        if (p) (void)hipHostFree(p);
+        p = nullptr;
+        bytes = 0;
+    }
+    void ensure(size_t n) {
+        if (n <= bytes && p) return;
+        release();
+        check(hipHostMalloc(&p, std::max<size_t>(n, 256), hipHostMallocDefault), "hipHostMalloc");
+        bytes = std::max<size_t>(n, 256);
+    }
+    template <class T>
+    T *as() const {
+        return static_cast<T *>(p);
+    }
+};
+
 int floor_log2(size_t x) {
     int r = 0;
     while (x >>= 1) ++r;
@@ -121,7 +147,12 @@ struct MeshGpt::Impl {
     // Training (gpu.rs:1915-2003): the activations of the last forward, the
     // gradient, AdamW's moments and the running powers of its betas (reset
     // with the weights, gpu.rs:1856-1872).
-    DevBuf tact, tgrad, tm, tv, tpart, ttok, ttgt, thyper;
+    // Training: activations, gradient, AdamW moments, reduction scratch, and
+    // the step's inputs (StepScalars, then the n tokens, then the n targets)
+    // with their pinned host staging (the same layout, then the n row losses).
+    DevBuf tact, tgrad, tm, tv, tpart, tin;
+    PinnedBuf tstage;
+    static constexpr size_t kTrainTokensAt = 256;
     kern::train::StepScalars hyper{};  // host copy uploaded before each step (kept alive for the async copy)
     float beta1_power = 1.0f, beta2_power = 1.0f;
     bool derived_stale = false;  // E and the decode tables lag the weights
@@ -667,9 +698,9 @@ struct MeshGpt::Impl {
                                         T::mesh_partial_floats(ma, V), T::embedding_partial_floats(R, W, V)}) *
                               4);
         grown |= tgrad.ensure(P * 4);
-        grown |= ttok.ensure(n * 4);
-        grown |= ttgt.ensure(n * 4);
-        grown |= thyper.ensure(sizeof(T::StepScalars));
+        static_assert(sizeof(T::StepScalars) <= kTrainTokensAt, "step scalars precede the tokens");
+        grown |= tin.ensure(kTrainTokensAt + 8 * n);
+        tstage.ensure(kTrainTokensAt + 12 * n);
         if (tm.ensure(P * 4) | tv.ensure(P * 4)) {
             grown = true;
             check(hipMemsetAsync(tm.p, 0, tm.bytes, stream), "clear moments");
@@ -688,10 +719,13 @@ struct MeshGpt::Impl {
     // Uploads a step's inputs, targets and scalars (outside any graph).
     void train_upload(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t supervised, float c1,
                       float c2) {
-        check(hipMemcpyAsync(ttok.p, inputs, n * 4, hipMemcpyHostToDevice, stream), "upload inputs");
-        check(hipMemcpyAsync(ttgt.p, targets, n * 4, hipMemcpyHostToDevice, stream), "upload targets");
+        // The previous step's copies are complete: each step ends with a sync.
         hyper = kern::train::StepScalars{c1, c2, 1.0f / float(supervised), 0};
-        check(hipMemcpyAsync(thyper.p, &hyper, sizeof(hyper), hipMemcpyHostToDevice, stream), "upload scalars");
+        char *h = tstage.as<char>();
+        std::memcpy(h, &hyper, sizeof(hyper));
+        std::memcpy(h + kTrainTokensAt, inputs, n * 4);
+        std::memcpy(h + kTrainTokensAt + 4 * n, targets, n * 4);
+        check(hipMemcpyAsync(tin.p, h, kTrainTokensAt + 8 * n, hipMemcpyHostToDevice, stream), "upload batch");
     }
 
     // The training forward over n rows (reference.rs:104-228) keeping every
@@ -707,9 +741,9 @@ struct MeshGpt::Impl {
         const T::Mesh ma{W, A, shape.butterfly, shape.log2w}, mf{W, F, shape.butterfly, shape.log2w};
         float *act = tact.as<float>(), *part = tpart.as<float>(), *grad = tgrad.as<float>();
         const float *w = params.as<float>();
-        const uint32_t *tok = ttok.as<uint32_t>();
+        const uint32_t *tok = train_tokens(), *tgt = tok + n;
         const float2 *table = rope.as<float2>();
-        auto *sc = thyper.as<T::StepScalars>();
+        auto *sc = tin.as<T::StepScalars>();
         auto at = [&](size_t o) { return act + o; };
         auto group = [&](size_t id) { return layout.groups[id].offset; };
         const size_t emb = group(layout.embedding);
@@ -746,11 +780,8 @@ struct MeshGpt::Impl {
             const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)};
             float *qk_out[2] = {at(k.qr), at(k.kr)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
             T::qk_forward(2, qk_pre, qk_out, qk_inv, table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
-            T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), R, seq, W, H, stream);
-            if (cfg.xsa)
-                T::xsa_forward(at(k.y), last(k.vs, A), at(k.z), R, W, H, stream);
-            else
-                T::copy(at(k.y), at(k.z), RW, stream);
+            T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.z), at(k.lse), R, seq, W, H,
+                                 cfg.xsa, stream);
             T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);
             // xm = x_b + proj, n2 = rmsnorm(xm); x_{b+1} = xm + ffn, normalised
             // by the next block (or the final norm) in the same launch.
@@ -761,7 +792,7 @@ struct MeshGpt::Impl {
                                    at(top ? p.invf : p.blocks[b + 1].inv1), R, W, stream);
         }
         T::head_logits(at(p.nf), Ev, at(p.et), at(p.logits), R, W, V, stream);
-        T::cross_entropy(at(p.logits), ttgt.as<uint32_t>(), at(p.dlogits), at(p.loss), R, V, sc, stream);
+        T::cross_entropy(at(p.logits), tgt, at(p.dlogits), at(p.loss), R, V, sc, stream);
         if (!backward) return;
 
         float *dx = at(p.dx), *dn = at(p.dn), *dq = at(p.dq), *dk = at(p.dk), *dv = at(p.dv);
@@ -777,14 +808,8 @@ struct MeshGpt::Impl {
             T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
             T::mesh_backward(ma, at(k.z), at(k.ps), dx, dt, false, w + group(g.projection), part,
                              grad + group(g.projection), R, stream);
-            if (cfg.xsa) {
-                T::xsa_backward(at(k.y), last(k.vs, A), dt, dy, dv, R, W, H, stream);
-            } else {
-                T::copy(dt, dy, RW, stream);
-                T::fill(dv, 0.0f, RW, stream);
-            }
-            T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dy, dq, dk, dv, at(p.dsum),
-                                  R, seq, W, H, stream);
+            T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dt, dy, dq, dk, dv,
+                                  at(p.dsum), R, seq, W, H, cfg.xsa, stream);
             if (cfg.rope || cfg.qk_norm) {
                 float *qk_g[2] = {dq, dk};
                 const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
@@ -820,15 +845,16 @@ struct MeshGpt::Impl {
     }
 
     // gpu.rs:2296-2313: the per-row f32 losses summed in f64 on the host.
+    const uint32_t *train_tokens() const { return reinterpret_cast<const uint32_t *>(tin.as<char>() + kTrainTokensAt); }
+
     double train_loss(size_t n, size_t supervised) {
-        std::vector<float> rows(n);
-        check(hipMemcpyAsync(rows.data(), tact.as<float>() + train_plan(n).loss, n * 4, hipMemcpyDeviceToHost,
-                             stream),
+        float *rows = reinterpret_cast<float *>(tstage.as<char>() + kTrainTokensAt + 8 * n);
+        check(hipMemcpyAsync(rows, tact.as<float>() + train_plan(n).loss, n * 4, hipMemcpyDeviceToHost, stream),
               "download loss");
         sync();
-        validate_finite(rows.data(), rows.size(), "cross-entropy");
+        validate_finite(rows, n, "cross-entropy");
         double total = 0.0;
-        for (float v : rows) total += double(v);
+        for (size_t i = 0; i < n; ++i) total += double(rows[i]);
         return total / double(supervised);
     }
 
@@ -869,7 +895,7 @@ struct MeshGpt::Impl {
             const size_t begin = cfg.geometry.frozen ? cfg.embedding_parameter_count() : 0;
             kern::train::adam(params.as<float>(), tm.as<float>(), tv.as<float>(), tgrad.as<float>(), begin,
                               layout.count(), {o.learning_rate, o.weight_decay, o.beta1, o.beta2, o.epsilon},
-                              thyper.as<kern::train::StepScalars>(), stream);
+                              tin.as<kern::train::StepScalars>(), stream);
         };
         if (use_graph) {
             if (!texec || !(key == tkey)) {

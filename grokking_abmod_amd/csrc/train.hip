@@ -672,12 +672,49 @@ __global__ void __launch_bounds__(kThreads) qk_backward_kernel(QkSet set, const 
 }
 
 // Causal attention for short sequences: one wave per query row and head.
+// XSA of one (row, head) in a wave's lanes (reference.rs:577-603): y minus
+// its component along u = v / max(|v|, 1e-12), in place.
 template <int EPL>
+__device__ __forceinline__ void lanes_xsa(float (&yv)[EPL], const float (&v)[EPL]) {
+    float u[EPL];
+    const float inv = rsqrtf(fmaxf(lanes_dot(v, v), kXsaFloor));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) u[e] = v[e] * inv;
+    const float s = lanes_dot(yv, u);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) yv[e] -= s * u[e];
+}
+
+// Its backward from g = d loss / d z: g becomes d loss / d y = g - (g.u) u,
+// and dv = inv (du - u (u.du)) above the norm floor (inv du below it) with
+// du = -((y.u) g + (g.u) y).
+template <int EPL>
+__device__ __forceinline__ void lanes_xsa_backward(const float (&yv)[EPL], const float (&v)[EPL], float (&g)[EPL],
+                                                   float (&dv)[EPL]) {
+    float u[EPL];
+    const float sq = lanes_dot(v, v), inv = rsqrtf(fmaxf(sq, kXsaFloor));
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) u[e] = v[e] * inv;
+    const float s = lanes_dot(yv, u), tg = lanes_dot(g, u);
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        dv[e] = -(s * g[e] + tg * yv[e]);
+        g[e] = g[e] - tg * u[e];
+    }
+    const float udu = sq >= kXsaFloor ? lanes_dot(u, dv) : 0.0f;
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) dv[e] = inv * (dv[e] - u[e] * udu);
+}
+
+// Causal attention of one (row, head) per wave, then (XSA) the exclusive
+// projection against the row's own value: y and z = xsa(y) (or y) stored.
+template <int EPL, bool XSA>
 __global__ void __launch_bounds__(kThreads) attention_forward_wave(const float *__restrict__ q,
                                                                    const float *__restrict__ k,
                                                                    const float *__restrict__ v, float *__restrict__ y,
-                                                                   float *__restrict__ lse, int rows, int sequence,
-                                                                   int W, int H, float scale) {
+                                                                   float *__restrict__ z, float *__restrict__ lse,
+                                                                   int rows, int sequence, int W, int H,
+                                                                   float scale) {
     const int t = row_wave(), lane = threadIdx.x & 63;
     if (t >= rows * H) return;
     const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
@@ -698,15 +735,26 @@ __global__ void __launch_bounds__(kThreads) attention_forward_wave(const float *
     const float il = 1.0f / l;
 #pragma unroll
     for (int e = 0; e < EPL; ++e) acc[e] *= il;
-    lanes_store(y + size_t(r) * W + h * hd, hd, lane, acc);
+    const size_t o = size_t(r) * W + h * hd;
+    lanes_store(y + o, hd, lane, acc);
     if (lane == 0) lse[t] = m + logf(l);
+    if (XSA) {
+        float vs[EPL];
+        lanes_load(v + o, hd, lane, vs);
+        lanes_xsa(acc, vs);
+    }
+    lanes_store(z + o, hd, lane, acc);
 }
 
-template <int EPL>
+// From dz = d loss / d z: (XSA) its backward first, storing dy and the XSA's
+// part of dv; without XSA dy is dz and dv starts at zero.  Then dq and the
+// row's dy . y (dsum), which the key-side kernel needs.
+template <int EPL, bool XSA>
 __global__ void __launch_bounds__(kThreads) attention_dq_wave(const float *__restrict__ q, const float *__restrict__ k,
                                                               const float *__restrict__ v, const float *__restrict__ y,
                                                               const float *__restrict__ lse,
-                                                              const float *__restrict__ dy, float *__restrict__ dq,
+                                                              const float *__restrict__ dz, float *__restrict__ dy,
+                                                              float *__restrict__ dv, float *__restrict__ dq,
                                                               float *__restrict__ dsum, int rows, int sequence, int W,
                                                               int H, float scale) {
     const int t = row_wave(), lane = threadIdx.x & 63;
@@ -715,8 +763,16 @@ __global__ void __launch_bounds__(kThreads) attention_dq_wave(const float *__res
     const size_t o = size_t(r) * W + h * hd;
     float qr[EPL], g[EPL], yv[EPL], acc[EPL] = {};
     lanes_load(q + o, hd, lane, qr);
-    lanes_load(dy + o, hd, lane, g);
+    lanes_load(dz + o, hd, lane, g);
     lanes_load(y + o, hd, lane, yv);
+    float dvs[EPL] = {};
+    if (XSA) {
+        float vs[EPL];
+        lanes_load(v + o, hd, lane, vs);
+        lanes_xsa_backward(yv, vs, g, dvs);
+        lanes_store(dy + o, hd, lane, g);
+    }
+    lanes_store(dv + o, hd, lane, dvs);
     const float D = lanes_dot(g, yv), L = lse[t];
     for (int j = 0; j <= pos; ++j) {
         float kr[EPL], vr[EPL];
@@ -778,20 +834,13 @@ __global__ void __launch_bounds__(kThreads) xsa_forward_wave(const float *__rest
     if (t >= rows * H) return;
     const int hd = W / H;
     const size_t o = size_t(t / H) * W + (t % H) * hd;
-    float yv[EPL], u[EPL];
+    float yv[EPL], vs[EPL];
     lanes_load(y + o, hd, lane, yv);
-    lanes_load(v + o, hd, lane, u);
-    const float inv = rsqrtf(fmaxf(lanes_dot(u, u), kXsaFloor));
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) u[e] *= inv;
-    const float s = lanes_dot(yv, u);
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) yv[e] -= s * u[e];
+    lanes_load(v + o, hd, lane, vs);
+    lanes_xsa(yv, vs);
     lanes_store(z + o, hd, lane, yv);
 }
 
-// dy = dz - (dz.u) u;  du = -((y.u) dz + (dz.u) y);  dv = inv (du - u (u.du))
-// above the norm floor, inv du below it.
 template <int EPL>
 __global__ void __launch_bounds__(kThreads) xsa_backward_wave(const float *__restrict__ y, const float *__restrict__ v,
                                                               const float *__restrict__ dz, float *__restrict__ dy,
@@ -800,25 +849,13 @@ __global__ void __launch_bounds__(kThreads) xsa_backward_wave(const float *__res
     if (t >= rows * H) return;
     const int hd = W / H;
     const size_t o = size_t(t / H) * W + (t % H) * hd;
-    float yv[EPL], u[EPL], g[EPL];
+    float yv[EPL], vs[EPL], g[EPL], d[EPL];
     lanes_load(y + o, hd, lane, yv);
-    lanes_load(v + o, hd, lane, u);
+    lanes_load(v + o, hd, lane, vs);
     lanes_load(dz + o, hd, lane, g);
-    const float sq = lanes_dot(u, u), inv = rsqrtf(fmaxf(sq, kXsaFloor));
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) u[e] *= inv;
-    const float s = lanes_dot(yv, u), tg = lanes_dot(g, u);
-    float du[EPL], gy[EPL];
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) {
-        du[e] = -(s * g[e] + tg * yv[e]);
-        gy[e] = g[e] - tg * u[e];
-    }
-    const float udu = sq >= kXsaFloor ? lanes_dot(u, du) : 0.0f;
-#pragma unroll
-    for (int e = 0; e < EPL; ++e) du[e] = inv * (du[e] - u[e] * udu);
-    lanes_store(dy + o, hd, lane, gy);
-    lanes_store(dv + o, hd, lane, du);
+    lanes_xsa_backward(yv, vs, g, d);
+    lanes_store(dy + o, hd, lane, g);
+    lanes_store(dv + o, hd, lane, d);
 }
 
 template <class F>
@@ -1183,13 +1220,19 @@ void rmsnorm_backward_sum3(const float *x, const float *inv, const float *dy0, c
                        x, inv, dy0, dy1, dy2, dx, int(accumulate), rows, W);
 }
 
-void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
-                       int sequence, int W, int H, hipStream_t stream) {
+void attention_forward(const float *q, const float *k, const float *v, float *y, float *z, float *lse, int rows,
+                       int sequence, int W, int H, bool xsa, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
     if (sequence <= kWaveAttentionMax || W / H > 128) {
         by_lanes(W / H, [&](auto e) {
-            hipLaunchKernelGGL(attention_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
-                               dim3(kThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
+            constexpr int EPL = decltype(e)::value;
+            const dim3 grid(blocks_for(size_t(rows) * H * 64));
+            if (xsa)
+                hipLaunchKernelGGL((attention_forward_wave<EPL, true>), grid, dim3(kThreads), 0, stream, q, k, v, y,
+                                   z, lse, rows, sequence, W, H, scale);
+            else
+                hipLaunchKernelGGL((attention_forward_wave<EPL, false>), grid, dim3(kThreads), 0, stream, q, k, v, y,
+                                   z, lse, rows, sequence, W, H, scale);
         });
         return;
     }
@@ -1197,44 +1240,51 @@ void attention_forward(const float *q, const float *k, const float *v, float *y,
         hipLaunchKernelGGL(attention_forward_kernel<decltype(hd)::value>, dim3(blocks_for(size_t(rows) * H, kRowThreads)),
                            dim3(kRowThreads), 0, stream, q, k, v, y, lse, rows, sequence, W, H, scale);
     });
+    if (xsa) {
+        by_lanes(W / H, [&](auto e) {
+            hipLaunchKernelGGL(xsa_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
+                               dim3(kThreads), 0, stream, y, v, z, rows, W, H);
+        });
+    } else {
+        copy(y, z, size_t(rows) * W, stream);
+    }
 }
 
 void attention_backward(const float *q, const float *k, const float *v, const float *y, const float *lse,
-                        const float *dy, float *dq, float *dk, float *dv, float *dsum, int rows, int sequence, int W,
-                        int H, hipStream_t stream) {
+                        const float *dz, float *dy, float *dq, float *dk, float *dv, float *dsum, int rows,
+                        int sequence, int W, int H, bool xsa, hipStream_t stream) {
     const float scale = float(1.0 / std::sqrt(double(W / H)));
+    // Without XSA the attention's output gradient is dz itself.
+    const float *g = xsa ? dy : dz;
     if (sequence <= kWaveAttentionMax || W / H > 128) {
         by_lanes(W / H, [&](auto e) {
             constexpr int EPL = decltype(e)::value;
             const dim3 grid(blocks_for(size_t(rows) * H * 64));
-            hipLaunchKernelGGL(attention_dq_wave<EPL>, grid, dim3(kThreads), 0, stream, q, k, v, y, lse, dy, dq, dsum,
-                               rows, sequence, W, H, scale);
-            hipLaunchKernelGGL(attention_dkv_wave<EPL>, grid, dim3(kThreads), 0, stream, q, k, v, lse, dy, dsum, dk, dv,
+            if (xsa)
+                hipLaunchKernelGGL((attention_dq_wave<EPL, true>), grid, dim3(kThreads), 0, stream, q, k, v, y, lse,
+                                   dz, dy, dv, dq, dsum, rows, sequence, W, H, scale);
+            else
+                hipLaunchKernelGGL((attention_dq_wave<EPL, false>), grid, dim3(kThreads), 0, stream, q, k, v, y, lse,
+                                   dz, dy, dv, dq, dsum, rows, sequence, W, H, scale);
+            hipLaunchKernelGGL(attention_dkv_wave<EPL>, grid, dim3(kThreads), 0, stream, q, k, v, lse, g, dsum, dk, dv,
                                rows, sequence, W, H, scale);
         });
         return;
     }
+    if (xsa) {
+        by_lanes(W / H, [&](auto e) {
+            hipLaunchKernelGGL(xsa_backward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
+                               dim3(kThreads), 0, stream, y, v, dz, dy, dv, rows, W, H);
+        });
+    } else {
+        fill(dv, 0.0f, size_t(rows) * W, stream);
+    }
     by_head_width(W / H, [&](auto hd) {
         constexpr int HD = decltype(hd)::value;
         hipLaunchKernelGGL(attention_dq_kernel<HD>, dim3(blocks_for(size_t(rows) * H, kRowThreads)), dim3(kRowThreads), 0, stream, q,
-                           k, v, y, lse, dy, dq, dsum, rows, sequence, W, H, scale);
+                           k, v, y, lse, g, dq, dsum, rows, sequence, W, H, scale);
         hipLaunchKernelGGL(attention_dkv_kernel<HD>, dim3(blocks_for(size_t(rows) * H, kRowThreads)), dim3(kRowThreads), 0, stream,
-                           q, k, v, lse, dy, dsum, dk, dv, rows, sequence, W, H, scale);
-    });
-}
-
-void xsa_forward(const float *y, const float *v, float *z, int rows, int W, int H, hipStream_t stream) {
-    by_lanes(W / H, [&](auto e) {
-        hipLaunchKernelGGL(xsa_forward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
-                           dim3(kThreads), 0, stream, y, v, z, rows, W, H);
-    });
-}
-
-void xsa_backward(const float *y, const float *v, const float *dz, float *dy, float *dv, int rows, int W, int H,
-                  hipStream_t stream) {
-    by_lanes(W / H, [&](auto e) {
-        hipLaunchKernelGGL(xsa_backward_wave<decltype(e)::value>, dim3(blocks_for(size_t(rows) * H * 64)),
-                           dim3(kThreads), 0, stream, y, v, dz, dy, dv, rows, W, H);
+                           q, k, v, lse, g, dsum, dk, dv, rows, sequence, W, H, scale);
     });
 }
 

@@ -72,20 +72,18 @@ void qk_forward(int count, const float *const *pre, float *const *out, float *co
 void qk_backward(int count, float *const *g, const float *const *pre, const float *const *inv, const float2 *table,
                  int rows, int sequence, int W, int H, bool norm, bool rotate, hipStream_t stream);
 
-// Causal softmax attention per (sequence, head) (reference.rs:510-554);
-// lse[r * H + h] = max + ln(sum) of the row's scaled scores.
-void attention_forward(const float *q, const float *k, const float *v, float *y, float *lse, int rows,
-                       int sequence, int W, int H, hipStream_t stream);
-// Its backward: dq and dk written, dv added to; dsum (rows x H) is scratch.
+// Causal softmax attention per (sequence, head) (reference.rs:510-554) into y,
+// then z = XSA(y) (reference.rs:577-603: y - (y.u) u, u = v / max(|v|, 1e-12)
+// per head) when xsa, else z = y; lse[r * H + h] = max + ln(sum) of the row's
+// scaled scores.
+void attention_forward(const float *q, const float *k, const float *v, float *y, float *z, float *lse, int rows,
+                       int sequence, int W, int H, bool xsa, hipStream_t stream);
+// Its backward from dz = d loss / d z: dq and dk written, dv written (XSA's
+// part and attention's); dy (rows x W) receives d loss / d y when xsa; dsum
+// (rows x H) is scratch.
 void attention_backward(const float *q, const float *k, const float *v, const float *y, const float *lse,
-                        const float *dy, float *dq, float *dk, float *dv, float *dsum, int rows, int sequence,
-                        int W, int H, hipStream_t stream);
-
-// XSA (reference.rs:577-603): z = y - (y.u) u, u = v / max(|v|, 1e-12) per head.
-void xsa_forward(const float *y, const float *v, float *z, int rows, int W, int H, hipStream_t stream);
-// Its backward: dy and dv written.
-void xsa_backward(const float *y, const float *v, const float *dz, float *dy, float *dv, int rows, int W, int H,
-                  hipStream_t stream);
+                        const float *dz, float *dy, float *dq, float *dk, float *dv, float *dsum, int rows,
+                        int sequence, int W, int H, bool xsa, hipStream_t stream);
 
 // The embedding geometry (reference.rs:130-149) on V raw token rows: scaled to
 // `radius` when normalize (rinv[t] keeps 1 / max(|row|, 1e-12)), then the first
