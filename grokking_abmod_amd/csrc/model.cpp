@@ -605,7 +605,7 @@ struct MeshGpt::Impl {
         size_t n1, inv1, qs, ks, vs, qr, kr, qinv, kinv, y, lse, z, ps, xm, inv2, n2, fs;
     };
     struct TrainPlan {
-        size_t es, eg, er, x, invf, nf, et, logits, dlogits, loss, dx, dn, dnk, dnv, dq, dk, dv, dy, dt, dsum, dE,
+        size_t es, eg, er, x, invf, nf, logits, dlogits, loss, dx, dn, dnk, dnv, dq, dk, dv, dy, dt, dsum, dE,
             total;
         std::vector<TrainBlock> blocks;
     };
@@ -647,7 +647,6 @@ struct MeshGpt::Impl {
         }
         p.invf = take(R);
         p.nf = take(RW);
-        p.et = take(V * W);
         p.logits = take(R * V);
         p.dlogits = take(R * V);
         p.loss = take(R);
@@ -791,7 +790,7 @@ struct MeshGpt::Impl {
             T::add_rmsnorm_forward(at(k.xm), last(k.fs, F), X(b + 1), at(top ? p.nf : p.blocks[b + 1].n1),
                                    at(top ? p.invf : p.blocks[b + 1].inv1), R, W, stream);
         }
-        T::head_logits(at(p.nf), Ev, at(p.et), at(p.logits), R, W, V, stream);
+        T::head_logits(at(p.nf), Ev, at(p.logits), R, W, V, stream);
         T::cross_entropy(at(p.logits), tgt, at(p.dlogits), at(p.loss), R, V, sc, stream);
         if (!backward) return;
 

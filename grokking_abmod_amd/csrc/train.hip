@@ -945,40 +945,7 @@ __global__ void __launch_bounds__(kThreads) copy_kernel(const float *__restrict_
     if (i < n) b[i] = a[i];
 }
 
-// logits[r][t] = n[r] . E[t] with E given transposed (Et[c][t]): a workgroup
-// stages kHeadRows rows of n in LDS; thread t of it takes token t0 + t for
-// all of them, reading each Et value once, coalesced across threads.
-constexpr int kHeadRows = 16;
 
-__global__ void __launch_bounds__(kThreads) head_logits_kernel(const float *__restrict__ n,
-                                                               const float *__restrict__ Et,
-                                                               float *__restrict__ logits, int rows, int W, int V) {
-    extern __shared__ float nr[];  // kHeadRows x W
-    const int r0 = blockIdx.x * kHeadRows, t = blockIdx.y * kThreads + threadIdx.x;
-    for (int i = threadIdx.x; i < kHeadRows * W; i += kThreads) {
-        const int r = r0 + i / W;
-        nr[i] = r < rows ? n[size_t(r) * W + i % W] : 0.0f;
-    }
-    __syncthreads();
-    if (t >= V) return;
-    float acc[kHeadRows] = {};
-    for (int c = 0; c < W; ++c) {
-        const float e = Et[size_t(c) * V + t];
-#pragma unroll
-        for (int k = 0; k < kHeadRows; ++k) acc[k] = fmaf(nr[k * W + c], e, acc[k]);
-    }
-#pragma unroll
-    for (int k = 0; k < kHeadRows; ++k)
-        if (r0 + k < rows) logits[size_t(r0 + k) * V + t] = acc[k];
-}
-
-__global__ void __launch_bounds__(kThreads) transpose_kernel(const float *__restrict__ E, float *__restrict__ Et,
-                                                             int V, int W) {
-    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= size_t(V) * W) return;
-    const size_t c = i / V, t = i % V;
-    Et[i] = E[t * W + c];
-}
 
 // One wave per row: the maximum and the sum over the vocabulary by wave
 // reductions (the loss kernel of gpu.rs:949-994 sums sequentially; the
@@ -1013,55 +980,68 @@ __global__ void __launch_bounds__(kThreads) cross_entropy_kernel(const float *__
         out[t] = (expf(row[t] - maximum) / sum - (uint32_t(t) == target ? 1.0f : 0.0f)) * scale;
 }
 
-// dn[r][c] = sum_t dlogits[r][t] E[t][c]: a workgroup takes kHeadRows rows and
-// channels c0 + threadIdx.x; the rows' gradients pass through LDS in chunks of
-// kThreads tokens, and each E value loaded serves all the rows.
-__global__ void __launch_bounds__(kThreads) head_backward_kernel(const float *__restrict__ dlogits,
-                                                                 const float *__restrict__ E, float *__restrict__ dn,
-                                                                 int rows, int W, int V) {
-    __shared__ float g[kHeadRows][kThreads];
-    const int r0 = blockIdx.x * kHeadRows, c = blockIdx.y * kThreads + threadIdx.x;
-    float acc[kHeadRows] = {};
-    for (int t0 = 0; t0 < V; t0 += kThreads) {
-        const int nt = min(kThreads, V - t0);
-        __syncthreads();
-        for (int k = 0; k < kHeadRows; ++k)
-            g[k][threadIdx.x] = r0 + k < rows && int(threadIdx.x) < nt ? dlogits[size_t(r0 + k) * V + t0 + threadIdx.x]
-                                                                        : 0.0f;
-        __syncthreads();
-        if (c < W)
-            for (int t = 0; t < nt; ++t) {
-                const float e = E[size_t(t0 + t) * W + c];
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+// C = A B, one 16 x 16 tile of C per wave on v_mfma_f32_16x16x4f32 (FP32
+// products and sums).  At step s of each 16-wide slice of K, lane l supplies
+// A[l % 16][k] and B[k][l % 16] for k = 4 (l / 16) + s, and it holds
+// C[4 (l / 16) + j][l % 16] in element j.  A[m][k] is A[m lda + k] (AK) or
+// A[k lda + m]; B[k][n] is B[n ldb + k] (BK) or B[k ldb + n].  blockIdx.y
+// takes the K slice [y kspan, (y + 1) kspan) and writes C + y cstride.  With
+// `tokens` (the embedding gradient: M = vocabulary, K = rows, N = W), each row
+// r of the slice also adds dx[r][n] to C[tokens[r]][n].
+template <bool AK, bool BK>
+__global__ void __launch_bounds__(kThreads) gemm_tile_kernel(const float *__restrict__ A, int lda,
+                                                             const float *__restrict__ B, int ldb,
+                                                             float *__restrict__ C, int ldc, size_t cstride, int M,
+                                                             int N, int K, int kspan, const uint32_t *__restrict__ tokens,
+                                                             const float *__restrict__ dx) {
+    const int tiles_n = (N + 15) / 16, tiles = (M + 15) / 16 * tiles_n;
+    const int wave = int(blockIdx.x) * (kThreads / 64) + int(threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (wave >= tiles) return;
+    const int m0 = wave / tiles_n * 16, n0 = wave % tiles_n * 16, i = lane & 15, g = lane >> 4;
+    const int m = m0 + i, n = n0 + i, kb = int(blockIdx.y) * kspan, ke = min(K, kb + kspan);
+    v4f acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int k0 = kb; k0 < ke; k0 += 16) {
+        float a[4], b[4];
 #pragma unroll
-                for (int k = 0; k < kHeadRows; ++k) acc[k] = fmaf(g[k][t], e, acc[k]);
-            }
+        for (int s = 0; s < 4; ++s) {
+            const int k = k0 + 4 * g + s;
+            const bool ok = k < ke;
+            a[s] = ok && m < M ? (AK ? A[size_t(m) * lda + k] : A[size_t(k) * lda + m]) : 0.0f;
+            b[s] = ok && n < N ? (BK ? B[size_t(n) * ldb + k] : B[size_t(k) * ldb + n]) : 0.0f;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[s], b[s], acc, 0, 0, 0);
     }
-    if (c >= W) return;
+    if (tokens) {
+        for (int r = kb; r < ke; ++r) {
+            const int t = int(tokens[r]) - m0;  // the same for every lane
+            if (t < 0 || t >= 16 || (t >> 2) != g || n >= N) continue;
+            const float d = dx[size_t(r) * N + n];
 #pragma unroll
-    for (int k = 0; k < kHeadRows; ++k)
-        if (r0 + k < rows) dn[size_t(r0 + k) * W + c] = acc[k];
+            for (int j = 0; j < 4; ++j)
+                if ((t & 3) == j) acc[j] += d;
+        }
+    }
+    float *out = C + size_t(blockIdx.y) * cstride;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = m0 + 4 * g + j;
+        if (row < M && n < N) out[size_t(row) * ldc + n] = acc[j];
+    }
 }
 
-// Partial sums of dE over chunk blockIdx.y of kEmbeddingChunk rows:
-// part[chunk][t][c] = sum_r dlogits[r][t] n[r][c] + (rows of token t) dx[r][c].
-constexpr int kEmbeddingChunk = 32;
+// Rows of the embedding gradient's K slices (one partial per slice).
+constexpr int kEmbeddingSpan = 64;
 
-__global__ void __launch_bounds__(kThreads) embedding_gradient_kernel(const float *__restrict__ dlogits,
-                                                                      const float *__restrict__ n,
-                                                                      const uint32_t *__restrict__ tokens,
-                                                                      const float *__restrict__ dx,
-                                                                      float *__restrict__ part, int rows, int W,
-                                                                      int V) {
-    const size_t i = size_t(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= size_t(V) * W) return;
-    const size_t t = i / W, c = i % W;
-    const int r0 = blockIdx.y * kEmbeddingChunk, r1 = min(rows, r0 + kEmbeddingChunk);
-    float acc = 0.0f;
-    for (int r = r0; r < r1; ++r) {
-        acc = fmaf(dlogits[size_t(r) * V + t], n[size_t(r) * W + c], acc);
-        if (tokens[r] == t) acc += dx[size_t(r) * W + c];
-    }
-    part[size_t(blockIdx.y) * V * W + i] = acc;
+template <bool AK, bool BK>
+void gemm_tiles(const float *A, int lda, const float *B, int ldb, float *C, int ldc, size_t cstride, int M, int N,
+                int K, int kspan, const uint32_t *tokens, const float *dx, hipStream_t stream) {
+    const int tiles = (M + 15) / 16 * ((N + 15) / 16), splits = (K + kspan - 1) / kspan;
+    const dim3 grid(unsigned((tiles + kThreads / 64 - 1) / (kThreads / 64)), unsigned(std::max(splits, 1)));
+    hipLaunchKernelGGL((gemm_tile_kernel<AK, BK>), grid, dim3(kThreads), 0, stream, A, lda, B, ldb, C, ldc, cstride,
+                       M, N, K, kspan, tokens, dx);
 }
 
 __global__ void __launch_bounds__(kThreads) adam_kernel(float *__restrict__ params, float *__restrict__ m,
@@ -1335,12 +1315,8 @@ void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, h
                        rows, W);
 }
 
-void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
-                 hipStream_t stream) {
-    hipLaunchKernelGGL(transpose_kernel, dim3(blocks_for(size_t(V) * W)), dim3(kThreads), 0, stream, E, Et, V, W);
-    const dim3 grid(unsigned((rows + kHeadRows - 1) / kHeadRows), blocks_for(V));
-    hipLaunchKernelGGL(head_logits_kernel, grid, dim3(kThreads), size_t(kHeadRows) * W * sizeof(float), stream, n, Et,
-                       logits, rows, W, V);
+void head_logits(const float *n, const float *E, float *logits, int rows, int W, int V, hipStream_t stream) {
+    gemm_tiles<true, true>(n, W, E, W, logits, V, 0, rows, V, W, W, nullptr, nullptr, stream);
 }
 
 void cross_entropy(const float *logits, const uint32_t *targets, float *dlogits, float *loss, int rows, int V,
@@ -1358,23 +1334,22 @@ void copy(const float *a, float *b, size_t n, hipStream_t stream) {
 }
 
 void head_backward(const float *dlogits, const float *E, float *dn, int rows, int W, int V, hipStream_t stream) {
-    const dim3 grid(unsigned((rows + kHeadRows - 1) / kHeadRows), blocks_for(W));
-    hipLaunchKernelGGL(head_backward_kernel, grid, dim3(kThreads), 0, stream, dlogits, E, dn, rows, W, V);
+    gemm_tiles<true, false>(dlogits, V, E, W, dn, W, 0, rows, W, V, V, nullptr, nullptr, stream);
 }
 
 size_t embedding_partial_floats(int rows, int W, int V) {
-    return size_t((rows + kEmbeddingChunk - 1) / kEmbeddingChunk) * V * W;
+    return size_t((rows + kEmbeddingSpan - 1) / kEmbeddingSpan) * V * W;
 }
 
 void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
                         float *partials, int rows, int W, int V, hipStream_t stream) {
-    const int chunks = (rows + kEmbeddingChunk - 1) / kEmbeddingChunk, nvw = V * W;
-    hipLaunchKernelGGL(embedding_gradient_kernel, dim3(blocks_for(size_t(nvw)), chunks), dim3(kThreads), 0, stream,
-                       dlogits, n, tokens, dx, partials, rows, W, V);
+    const int splits = (rows + kEmbeddingSpan - 1) / kEmbeddingSpan, nvw = V * W;
+    gemm_tiles<false, false>(dlogits, V, n, W, partials, W, size_t(nvw), V, W, rows, kEmbeddingSpan, tokens, dx,
+                             stream);
     ReduceSet red{};
     red.part[0] = partials;
     red.out[0] = dE;
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, red, chunks, nvw);
+    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, red, splits, nvw);
 }
 
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,

@@ -96,9 +96,10 @@ void geometry_backward(const float *raw, const float *rinv, float *g, int V, int
 
 // x[r] = E[tokens[r]]
 void gather(const float *E, const uint32_t *tokens, float *x, int rows, int W, hipStream_t stream);
-// logits[r][t] = n[r] . E[t]; Et (W x V floats) receives E transposed.
-void head_logits(const float *n, const float *E, float *Et, float *logits, int rows, int W, int V,
-                 hipStream_t stream);
+// logits[r][t] = n[r] . E[t] (FP32 matrix cores; each dot product's terms are
+// added in another order than the reference's sequential sum, within f32
+// rounding of it).
+void head_logits(const float *n, const float *E, float *logits, int rows, int W, int V, hipStream_t stream);
 // A training step's scalars in device memory, written before each step, so
 // that a captured step replays with new values: the AdamW bias corrections
 // 1 - beta^t, 1 / (supervised rows), and a flag the loss kernel raises on a
@@ -118,8 +119,9 @@ void copy(const float *a, float *b, size_t n, hipStream_t stream);
 // dn[r][c] = sum_t dlogits[r][t] E[t][c]
 void head_backward(const float *dlogits, const float *E, float *dn, int rows, int W, int V, hipStream_t stream);
 // dE[t][c] = sum_r dlogits[r][t] n[r][c] + sum over rows r of token t of dx[r][c],
-// by chunks of rows into `partials` (embedding_partial_floats), then one
-// deterministic reduction.
+// by slices of 64 rows into `partials` (embedding_partial_floats), then one
+// deterministic reduction.  These products, like head_backward's, run on the
+// FP32 matrix cores.
 size_t embedding_partial_floats(int rows, int W, int V);
 void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
                         float *partials, int rows, int W, int V, hipStream_t stream);
