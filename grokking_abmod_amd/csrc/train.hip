@@ -203,25 +203,55 @@ int mesh_groups(const Mesh &m, int rows) {
 // ---- mesh stacks of width <= 64 or 128: one wave per row, channel
 // lane + 64 j in register j, partners by lane shuffles (no barriers).
 
+// Lane l gets v of lane (l + 1) mod 64 (DPP wave_rol:1) or of lane (l - 1)
+// mod 64 (DPP wave_ror:1): no LDS round trip.
+__device__ __forceinline__ float lanes_rol1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x134, 0xf, 0xf, false));
+}
+__device__ __forceinline__ float lanes_ror1(float v) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x13C, 0xf, 0xf, false));
+}
+
 // out[j] = the value of channel (lane + 64 j + d) mod W, for 0 <= d < W.
+// Width 128 (CPL 2): a shift by 64 + d' renames the registers and shifts by
+// d'; for d' < 64 every lane reads lane (lane + d') mod 64, whose lanes below
+// d' offer their other register (their readers wrapped past lane 63), one lane
+// read per register, a DPP rotation for d' = 1 or 63 (the neighbour mesh and
+// its backward).
 template <int CPL>
 __device__ __forceinline__ void channel_shift(const float (&x)[CPL], int d, int W, int lane, float (&out)[CPL]) {
+    static_assert(CPL == 1 || CPL == 2, "wave mesh kernels take widths up to 128");
     if constexpr (CPL == 1) {
-        int src = lane + d;
-        if (src >= W) src -= W;
-        out[0] = __shfl(x[0], src & 63, 64);
+        if (W == 64 && d == 1) {
+            out[0] = lanes_rol1(x[0]);
+        } else if (W == 64 && d == 63) {
+            out[0] = lanes_ror1(x[0]);
+        } else {
+            int src = lane + d;
+            if (src >= W) src -= W;
+            out[0] = __shfl(x[0], src & 63, 64);
+        }
     } else {
-#pragma unroll
-        for (int j = 0; j < CPL; ++j) {
-            int t = lane + 64 * j + d;
-            if (t >= W) t -= W;
-            float v = 0.0f;
-#pragma unroll
-            for (int k = 0; k < CPL; ++k) {
-                const float u = __shfl(x[k], t & 63, 64);
-                if ((t >> 6) == k) v = u;
-            }
-            out[j] = v;
+        const bool swap = d >= 64;
+        const float y0 = swap ? x[1] : x[0], y1 = swap ? x[0] : x[1];
+        d &= 63;
+        if (d == 0) {
+            out[0] = y0;
+            out[1] = y1;
+            return;
+        }
+        const bool next = lane < d;
+        const float o0 = next ? y1 : y0, o1 = next ? y0 : y1;
+        if (d == 1) {
+            out[0] = lanes_rol1(o0);
+            out[1] = lanes_rol1(o1);
+        } else if (d == 63) {
+            out[0] = lanes_ror1(o0);
+            out[1] = lanes_ror1(o1);
+        } else {
+            const int src = (lane + d) & 63;
+            out[0] = __shfl(o0, src, 64);
+            out[1] = __shfl(o1, src, 64);
         }
     }
 }
