@@ -3613,9 +3613,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
 // head of another, and the mesh teams, whose phase is the longer one on the
 // chain, keep a CU to themselves.  (Measured on config 3 at batch 32: 59.5 us
 // per step, against 62.3 with pairs in plain order and 61.7 with each team
-// beside a head of its own sequence.)  Any other placement only costs speed:
-// every role of a sequence stays on one XCD, and the map is a bijection of
-// [0, K).
+// beside a head of its own sequence.)  Of a pair, the workgroup dispatched
+// first runs faster (the wave scheduler favours older waves): sequences 0 and
+// 2 of an XCD, always first, finish the 512-step launch of config 3 ~11 %
+// before sequences 1 and 3.  Mixing the two places within each sequence was
+// slower still (518k against 538k tokens/s): a sequence then waits every
+// layer for its slowest head.  Any other placement only costs speed: every
+// role of a sequence stays on one XCD, and the map is a bijection of [0, K).
 __host__ __device__ inline void persistent_role(int k, int K, int C, int R, int &q, int &r) {
     const int P = K - C, Q = K / R, H = R - 3;
     if (P <= 0 || 2 * P > Q * H || Q < 2 || C < P) {
