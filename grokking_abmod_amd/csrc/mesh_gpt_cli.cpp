@@ -264,7 +264,9 @@ int train(Options &o, const std::string &checkpoint) {
     if (o.prompt.empty()) throw Error("generation prompt must not be empty");
     tokenizer.encode(o.prompt);
     const TextDataset dataset(tokenizer.encode(text), config);
-    const size_t C = config.context, rows = C * o.batch;
+    const size_t C = config.context;
+    if (o.batch == 0 || o.batch > kMaxRows / C) throw Error("invalid dataset batch dimensions");
+    const size_t rows = C * o.batch;
     std::vector<uint32_t> ex(rows), ey(rows), x(rows), y(rows);
     dataset.batch(true, C, o.batch, 101, ex.data(), ey.data());
     MeshGpt model(int(o.device), config, o.seed);

@@ -142,7 +142,11 @@ void TextDataset::batch(bool validation, size_t sequence, size_t batch, uint64_t
     Random random(seed);
     for (size_t b = 0; b < batch; ++b) {
         // An f32 product truncated toward zero, as the reference's `as usize`.
+        // Beyond 2^24 windows the product can round up to the last start,
+        // whose target would lie past the corpus (the reference's slice
+        // panics there); that is an error here.
         const size_t start = size_t(random.unit() * float(corpus.size() - sequence));
+        if (start + sequence >= corpus.size()) throw Error("invalid dataset batch dimensions");
         std::copy_n(corpus.begin() + start, sequence, inputs + b * sequence);
         std::copy_n(corpus.begin() + start + 1, sequence, targets + b * sequence);
     }

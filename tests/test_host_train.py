@@ -146,6 +146,8 @@ def cli(*args):
     (["--embedding-norm", "l2"], "unknown EmbeddingNorm: l2"),
     (["--embedding-norm"], "missing value for --embedding-norm"),
     (["--unknown"], "unknown option: --unknown; use --help"),
+    (["--batch", "5000"], "invalid dataset batch dimensions"),
+    (["--batch", "0"], "invalid dataset batch dimensions"),
 ])
 def test_cli_train_rejections(args, message):
     """Each is raised before any device work, so no GPU is needed."""
