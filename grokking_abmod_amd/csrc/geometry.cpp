@@ -159,6 +159,7 @@ EquationDataset EquationDataset::build(size_t modulus, uint32_t operation, doubl
         throw Error("train fraction must be finite and strictly between 0 and 1");
     EquationDataset d;
     d.modulus = modulus;
+    d.operation = operation;
     d.residue_tokens = residue_permutation(modulus, seed);
     std::vector<Equation> all;
     for (size_t a = 0; a < modulus; ++a)
@@ -186,6 +187,15 @@ void EquationDataset::batch(bool validation, const size_t *indices, size_t n, ui
         std::copy(row, row + 4, inputs + 4 * i);
         std::copy(want, want + 4, targets + 4 * i);
     }
+}
+
+CharacterTokenizer EquationDataset::tokenizer() const {
+    std::vector<uint32_t> characters(modulus + 2, uint32_t(' '));
+    for (size_t r = 0; r < residue_tokens.size(); ++r) characters[residue_tokens[r]] = 0xE000u + uint32_t(r);
+    static const uint32_t symbols[] = {'+', '*', '-', '/'};  // ModularOperation::symbol
+    characters[modulus] = operation < 4 ? symbols[operation] : 0x2218u;
+    characters[modulus + 1] = uint32_t('=');
+    return CharacterTokenizer::from_characters(characters);
 }
 
 size_t primitive_root(size_t prime) {

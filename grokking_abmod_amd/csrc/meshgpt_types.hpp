@@ -77,6 +77,7 @@ EmbeddingNorm parse_norm(const std::string &text);
 std::string display_f32(float v);
 
 struct GptConfig;
+class CharacterTokenizer;
 
 // EmbeddingGeometry (geometry.rs:49-81); defaults keep the signed parity codes.
 // AdamWOptions (config.rs:258-276) with its defaults.
@@ -190,6 +191,10 @@ struct EquationDataset {
     static EquationDataset build(size_t modulus, uint32_t operation, double train_fraction, uint64_t seed);
     // inputs and targets of 4 * n rows for the split's equations `indices`
     void batch(bool validation, const size_t *indices, size_t n, uint32_t *inputs, uint32_t *targets) const;
+    // The dataset's tokenizer (grokking.rs:146-157): residue r's token is the
+    // private-use character U+E000 + r, then the operation's symbol and '='.
+    CharacterTokenizer tokenizer() const;
+    uint32_t operation = 0;
 };
 // TextDataset (text.rs:58-108): a tokenised corpus split 90/10 into training
 // and validation; a batch is `batch` windows of `sequence` tokens at seeded

@@ -844,6 +844,15 @@ struct MeshGpt::Impl {
     }
 
     // gpu.rs:2296-2313: the per-row f32 losses summed in f64 on the host.
+    size_t allocated_device_bytes() const {
+        size_t total = 0;
+        for (const DevBuf *b : {&params, &codes, &E, &Et, &rope, &wdec, &Edec, &q0, &kc, &vc, &dx, &dx2, &dxn, &dq,
+                                &part, &dtokens, &dlen, &drng, &dlogits, &dflags, &drng_start, &pxch, &pabort, &wx,
+                                &wxn, &wq, &wy, &wtok, &wlogits, &wk, &wv, &tact, &tgrad, &tm, &tv, &tpart, &tin})
+            total += b->bytes;
+        return total;
+    }
+
     const uint32_t *train_tokens() const { return reinterpret_cast<const uint32_t *>(tin.as<char>() + kTrainTokensAt); }
 
     double train_loss(size_t n, size_t supervised) {
@@ -1217,6 +1226,8 @@ double MeshGpt::train_batch(const uint32_t *inputs, const uint32_t *targets, siz
                             const AdamWOptions &options) {
     return impl_->train_batch(inputs, targets, n, sequence, options);
 }
+
+size_t MeshGpt::allocated_device_bytes() const { return impl_->allocated_device_bytes(); }
 
 std::vector<float> MeshGpt::hidden_states(const uint32_t *tokens, size_t n, size_t sequence) {
     return impl_->hidden_states(tokens, n, sequence);

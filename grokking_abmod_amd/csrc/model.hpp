@@ -40,6 +40,8 @@ class MeshGpt {
                              std::vector<float> &gradient);
     double train_batch(const uint32_t *inputs, const uint32_t *targets, size_t n, size_t sequence,
                        const AdamWOptions &options);
+    // Bytes of device memory the model holds (gpu.rs allocated_device_bytes).
+    size_t allocated_device_bytes() const;
     // gpu.rs:2006-2053 on text; batch rows b use seed + b.
     std::string generate(const CharacterTokenizer &tokenizer, const std::string &prompt, size_t count,
                          float temperature, uint64_t seed);

@@ -379,3 +379,67 @@ def test_cli_train_default_run(tmp_path):
         assert np.array_equal(model.parameters().view(np.uint32), saved.parameters.view(np.uint32))
         sample = model.generate(tokenizer.characters, "the little robot ", 240, 0.7, 7)
     assert (out / "sample.txt").read_text(encoding="utf-8") == sample == rest[:-1]
+
+
+def test_bench_binary_reference_protocol(tmp_path):
+    """mesh-gpt-bench with the reference's documented command
+    (docs/cuda-performance.md:25-28, two trials here): each trial restores the
+    seeded weights, so both print the same losses, and those are the losses of
+    the same protocol run through the library (bench.py's training figure);
+    timings.csv, run.txt and the first trial's model.bin hold what they should,
+    the checkpoint with the equation dataset's tokenizer (grokking.rs:146-157)."""
+    import os
+    import re
+    import subprocess
+
+    bench = os.path.join(os.path.dirname(G.CLI_PATH), "mesh-gpt-bench")
+    out = tmp_path / "bench"
+    res = subprocess.run([bench, "--steps", "30", "--warmup", "10", "--trials", "2", "--output", str(out)],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    lines = res.stdout.splitlines()
+    pat = re.compile(r"trial (\d): (\d+\.\d{3}) ms/update; (\d+) tokens/s; CE (\d+\.\d{5}) -> (\d+\.\d{5})$")
+    m1, m2 = pat.match(lines[0]), pat.match(lines[2])
+    assert m1 and m2 and re.fullmatch(r"device buffers: \d+\.\d MiB", lines[1]) and len(lines) == 3, lines
+    assert m1.group(4, 5) == m2.group(4, 5)
+
+    cfg = G.GptConfig(vocab_size=99, context=4, width=128, heads=4, layers=2)
+    n_train, _ = G.equation_split()
+    x, y = G.equation_batch(np.arange(512) % n_train)
+    opts = G.AdamW(learning_rate=0.001, weight_decay=1.0, beta2=0.98)
+    with G.MeshGpt(0, cfg, 7) as model:
+        for _ in range(10):
+            model.train_batch(x, y, 4, opts)
+        losses = [model.train_batch(x, y, 4, opts) for _ in range(30)]
+        params = model.parameters()
+    assert m1.group(4) == f"{losses[0]:.5f}" and m1.group(5) == f"{losses[-1]:.5f}"
+
+    rows = (out / "timings.csv").read_text().splitlines()
+    assert rows[0] == "trial,steps,total_ms,ms_per_step,first_loss,last_loss,weight_l2" and len(rows) == 3
+    t1 = rows[1].split(",")
+    assert t1[:2] == ["1", "30"] and abs(float(t1[4]) - losses[0]) <= 1e-9 and abs(float(t1[5]) - losses[-1]) <= 1e-9
+    assert abs(float(t1[6]) - np.sqrt(np.sum(params.astype(np.float64) ** 2))) <= 1e-6
+    run = dict(line.split("=", 1) for line in (out / "run.txt").read_text().splitlines())
+    for key, value in dict(precision="fp32", workload="add_mod97", seed="7", width="128", heads="4", layers="2",
+                           attention_mesh_depth="4", ffn_mesh_depth="6", vocabulary="99", context="4", batch="512",
+                           steps="30", warmup="10", trials="2", learning_rate="0.001", weight_decay="1",
+                           betas="0.9,0.98", timing="end_to_end_wall_clock",
+                           final_parameter_download="included").items():
+        assert run[key] == value, key
+    assert int(run["allocated_device_bytes"]) > 0
+
+    saved = G.Checkpoint.load(str(out / "model.bin"))
+    assert saved.config == cfg
+    assert np.array_equal(saved.parameters.view(np.uint32), params.view(np.uint32))
+    perm, _, _ = __import__("test_host_train").oracle_equations(97, 0, 0.5, 7)
+    want = [" "] * 99
+    for residue, token in enumerate(perm):
+        want[token] = chr(0xE000 + residue)
+    want[97], want[98] = "+", "="
+    assert G.CharacterTokenizer(saved.characters) == G.CharacterTokenizer(want)
+
+    # Other contexts take the cyclic next-token workload (mesh-gpt-bench.rs:140-149).
+    res = subprocess.run([bench, "--context", "8", "--batch", "16", "--steps", "2", "--warmup", "1", "--trials", "1",
+                          "--output", str(tmp_path / "cyclic")], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    assert "workload=cyclic_next_token" in (tmp_path / "cyclic" / "run.txt").read_text()

@@ -164,3 +164,32 @@ def test_cli_help_lists_the_training_and_geometry_flags():
                  "--embedding-norm", "--freeze-embedding", "--preserve-features", "--geometry-seed", "--rope",
                  "--qk-norm", "--xsa"):
         assert flag in res.stdout, flag
+
+
+BENCH_PATH = os.path.join(os.path.dirname(G.CLI_PATH), "mesh-gpt-bench")
+
+
+@pytest.mark.parametrize("args,message", [
+    (["--steps", "0"], "steps/trials/batch must be positive, with at most 131072 token rows"),
+    (["--trials", "0"], "steps/trials/batch must be positive, with at most 131072 token rows"),
+    (["--batch", "40000"], "steps/trials/batch must be positive, with at most 131072 token rows"),
+    (["--heads", "16", "--width", "128"], "benchmark requires width <=1024 and <=8 heads"),
+    (["--width", "2048", "--heads", "8"], "benchmark requires width <=1024 and <=8 heads"),
+    (["--context", "256", "--width", "256"], "benchmark context must be <=128, or <=4096 with width <=128"),
+    (["--heads", "3"], "heads must be in 1..64 and divide width"),
+    (["--steps", "x"], "invalid value for --steps: x"),
+    (["--bogus"], "unknown benchmark option: --bogus"),
+])
+def test_bench_binary_rejections(args, message):
+    """mesh-gpt-bench (src/bin/mesh-gpt-bench.rs:29-103) refuses these before any device work."""
+    res = subprocess.run([BENCH_PATH, *args], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 1 and res.stdout == ""
+    assert res.stderr == f'Error: "{message}"\n'
+
+
+def test_bench_binary_help():
+    res = subprocess.run([BENCH_PATH, "--help"], capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0
+    for flag in ("--steps", "--warmup", "--trials", "--batch", "--width", "--heads", "--context", "--layers",
+                 "--attention-depth", "--ffn-depth", "--device", "--output"):
+        assert flag in res.stdout
