@@ -361,7 +361,7 @@ def test_cli_help_and_argument_errors():
     assert r.returncode == 1 and "invalid value for --tokens" in r.stderr
     r = _cli("generate", "--temperature", "-1")
     assert r.returncode == 1 and "temperature must be finite and nonnegative" in r.stderr
-    r = _cli("grok")
+    r = _cli("verify")
     assert r.returncode == 1 and "not part of this build" in r.stderr
     r = _cli("train", "--dataset", "/nonexistent/corpus.txt")
     assert r.returncode == 1 and "cannot open dataset /nonexistent/corpus.txt" in r.stderr

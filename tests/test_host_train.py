@@ -141,9 +141,9 @@ def cli(*args):
     (["--context", "5000"], "context must be in 1..4096"),
     (["--rope", "2"], "--rope requires 0 or 1"),
     (["--qk-norm", "x"], "invalid value for --qk-norm: x"),
-    (["--embedding-form", "cube"], "unknown EmbeddingForm: cube"),
-    (["--embedding-order", "x"], "unknown EmbeddingOrder: x"),
-    (["--embedding-norm", "l2"], "unknown EmbeddingNorm: l2"),
+    (["--embedding-form", "cube"], "invalid value for --embedding-form: cube"),
+    (["--embedding-order", "x"], "invalid value for --embedding-order: x"),
+    (["--embedding-norm", "l2"], "invalid value for --embedding-norm: l2"),
     (["--embedding-norm"], "missing value for --embedding-norm"),
     (["--unknown"], "unknown option: --unknown; use --help"),
     (["--batch", "5000"], "invalid dataset batch dimensions"),
@@ -193,3 +193,40 @@ def test_bench_binary_help():
     for flag in ("--steps", "--warmup", "--trials", "--batch", "--width", "--heads", "--context", "--layers",
                  "--attention-depth", "--ffn-depth", "--device", "--output"):
         assert flag in res.stdout
+
+
+@pytest.mark.parametrize("args,message", [
+    (["--steps", "5", "--epochs", "1"], "choose either --epochs or --steps"),
+    (["--operation", "pow"], "invalid value for --operation: pow"),
+    (["--modulus", "96"], "modulus must be a prime in 2..254 (two vocabulary slots are reserved)"),
+    (["--train-fraction", "1"], "train fraction must be finite and strictly between 0 and 1"),
+    (["--report-every", "0"], "steps, report interval, and evaluation batch must be positive"),
+    (["--eval-batch", "0"], "steps, report interval, and evaluation batch must be positive"),
+    (["--init-gain", "0"], "initialization gains must be finite and positive"),
+    (["--embedding-output-gain", "nan"], "initialization gains must be finite and positive"),
+    (["--workspace-cache", "4"], "workspace capacity must be in 1..3"),
+    (["--stop-validation-accuracy", "1.5"], "validation stop accuracy must be in (0, 1]"),
+    (["--qk-signs", "2"], "Q/K sign initialization must be 0 or 1"),
+    (["--learning-rate", "0"],
+     "AdamW requires finite positive learning rate/epsilon, nonnegative decay, and betas in [0, 1)"),
+    (["--embedding-init-unit"],
+     "initial unit normalization requires table embeddings, embedding-norm none, and no protected features"),
+    (["--batch", "5000"], "invalid equation minibatch size"),
+    (["--width", "2048"], "grokking requires width <=1024"),
+    (["--embedding-form", "cube"], "invalid value for --embedding-form: cube"),
+    (["--bogus"], "unknown grok option: --bogus; use grok --help"),
+])
+def test_cli_grok_rejections(args, message):
+    """`mesh-gpt grok` (src/bin/mesh-gpt/grokking.rs:44-218) refuses these before any device work."""
+    res = cli("grok", *args)
+    assert res.returncode == 1 and res.stdout == ""
+    assert res.stderr == f'Error: "{message}"\n'
+
+
+def test_cli_grok_help():
+    res = cli("grok", "--help")
+    assert res.returncode == 0
+    for flag in ("--operation", "--modulus", "--train-fraction", "--epochs", "--stop-validation-accuracy",
+                 "--eval-batch", "--workspace-cache", "--init-gain", "--embedding-output-gain",
+                 "--embedding-init-unit", "--qk-signs", "--embedding-form", "--xsa"):
+        assert flag in res.stdout, flag
