@@ -540,3 +540,50 @@ def test_cli_grok_published_1000_updates(tmp_path):
     assert lines[2] == "step       0: train CE=7.41967 accuracy=0.00%; validation CE=7.43258 accuracy=0.00%"
     assert lines[3] == "step    1000: train CE=4.58679 accuracy=1.28%; validation CE=4.59957 accuracy=0.83%"
     assert lines[-1] == "Stopped after 1000 updates: update_budget"
+
+
+def test_cli_grok_initialisation_controls(tmp_path):
+    """grok's initialisation controls (src/bin/mesh-gpt/grokking.rs:221-283),
+    all at once: every mesh edge scaled by --init-gain, the embedding mesh's
+    final layer by --embedding-output-gain, the final Q and K mesh rows by
+    seeded signs (their own SplitMix64 stream), the table taken from the
+    adjusted mesh's vectors, and each table row normalised once.  The
+    step-zero checkpoint holds exactly that, restated here from the oracle's
+    seeded initialisation and token vectors."""
+    import subprocess
+
+    out = tmp_path / "grok"
+    res = subprocess.run([G.CLI_PATH, "grok", "--steps", "1", "--report-every", "1", "--init-gain", "1.5",
+                          "--embedding-output-gain", "0.5", "--qk-signs", "1", "--embedding", "table",
+                          "--embedding-init-unit", "--output", str(out)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    W, A, F, L, V = 128, 4, 6, 2, 99
+    mesh = O.config(vocab_size=V, context=4, width=W, heads=4, layers=L)
+    p = O.initialize(mesh, 7) * np.float32(1.5)
+    emb = 2 * W * A
+    p[emb - 2 * W:emb] *= np.float32(0.5)
+    mask = (1 << 64) - 1
+    state = 7 ^ 0x514B5349474E5331
+    block = 2 * W * (4 * A + F)
+    for b in range(L):
+        for proj in range(2):
+            end = emb + b * block + (proj + 1) * emb
+            for i in range(end - 2 * W, end, 2):
+                state = (state + 0x9E3779B97F4A7C15) & mask
+                z = state
+                z = ((z ^ (z >> 30)) * 0xBF58476D1CE4E5B9) & mask
+                z = ((z ^ (z >> 27)) * 0x94D049BB133111EB) & mask
+                z ^= z >> 31
+                if z >> 63:
+                    p[i] = -p[i]
+                    p[i + 1] = -p[i + 1]
+    table = O.token_embeddings(mesh, p)
+    table = (table / np.sqrt(np.sum(table ** 2, axis=1, keepdims=True))).astype(np.float32)
+    saved = G.Checkpoint.load(str(out / "initial-model.bin"))
+    assert saved.parameters.size == V * W + p.size - emb
+    np.testing.assert_allclose(saved.parameters[:V * W].reshape(V, W), table, rtol=0, atol=2e-7)
+    assert np.array_equal(saved.parameters[V * W:].view(np.uint32), p[emb:].view(np.uint32))
+    run = dict(line.split("=", 1) for line in (out / "run.txt").read_text().splitlines())
+    assert (run["initialization_gain"], run["embedding_output_gain"], run["qk_signs"], run["embedding_init_unit"],
+            run["embeddings"], run["all_parameters"]) == ("1.5", "0.5", "1", "true", "table",
+                                                            "mesh_edges_and_token_table")
