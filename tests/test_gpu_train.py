@@ -587,3 +587,32 @@ def test_cli_grok_initialisation_controls(tmp_path):
     assert (run["initialization_gain"], run["embedding_output_gain"], run["qk_signs"], run["embedding_init_unit"],
             run["embeddings"], run["all_parameters"]) == ("1.5", "0.5", "1", "true", "table",
                                                             "mesh_edges_and_token_table")
+
+
+def test_cli_grok_stop_rule_and_epoch_tails(tmp_path):
+    """--stop-validation-accuracy ends at the first report whose complete
+    validation split reaches the target, else the budget runs out
+    (grokking.rs:386-422); examples seen count short epoch tails
+    (mod 5 at fraction 0.8: 20 training equations, batches of 6, so epochs
+    of 6 + 6 + 6 + 2)."""
+    import subprocess
+
+    out = tmp_path / "grok"
+    res = subprocess.run([G.CLI_PATH, "grok", "--modulus", "5", "--train-fraction", "0.8", "--batch", "6",
+                          "--steps", "400", "--report-every", "4", "--stop-validation-accuracy", "0.4",
+                          "--output", str(out)], capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    rows = [r.split(",") for r in (out / "loss.csv").read_text().splitlines()[1:]]
+    steps = [int(r[0]) for r in rows]
+    assert steps == list(range(0, 4 * len(rows), 4))
+    for r in rows:  # four updates per epoch of 20 equations
+        step, seen = int(r[0]), int(r[1])
+        assert seen == 20 * (step // 4) and int(r[2]) == step // 4 and int(r[3]) == 0
+    reached = [i for i, r in enumerate(rows) if float(r[7]) >= 0.4]
+    run = dict(line.split("=", 1) for line in (out / "run.txt").read_text().splitlines())
+    if reached:
+        assert reached[0] == len(rows) - 1 and run["stop_reason"] == "validation_accuracy"
+        assert res.stdout.splitlines()[-1] == f"Stopped after {steps[-1]} updates: validation_accuracy"
+    else:
+        assert steps[-1] == 400 and run["stop_reason"] == "update_budget"
+    assert run["completed_steps"] == str(steps[-1]) and run["steps_per_epoch"] == "4"
