@@ -688,14 +688,9 @@ struct MeshGpt::Impl {
     // reallocation invalidates the captured step.
     void train_prepare(size_t n) {
         namespace T = kern::train;
-        const int R = int(n), W = int(cfg.width), V = int(cfg.vocab_size);
-        const T::Mesh ma{W, int(cfg.attention_mesh_depth), shape.butterfly, shape.log2w};
-        const T::Mesh mf{W, int(cfg.ffn_mesh_depth), shape.butterfly, shape.log2w};
         const size_t P = layout.count();
         bool grown = tact.ensure(train_plan(n).total * 4);
-        grown |= tpart.ensure(std::max({3 * T::mesh_partial_floats(ma, R), T::mesh_partial_floats(mf, R),
-                                        T::mesh_partial_floats(ma, V), T::embedding_partial_floats(R, W, V)}) *
-                              4);
+        grown |= tpart.ensure(train_partial_floats(n) * 4);
         grown |= tgrad.ensure(P * 4);
         static_assert(sizeof(T::StepScalars) <= kTrainTokensAt, "step scalars precede the tokens");
         grown |= tin.ensure(kTrainTokensAt + 8 * n);
@@ -706,6 +701,19 @@ struct MeshGpt::Impl {
             check(hipMemsetAsync(tv.p, 0, tv.bytes, stream), "clear moments");
         }
         if (grown) drop_train_graph();
+    }
+
+    // The backward's reduction scratch: a region for each mesh stack's partial
+    // sums (their reductions run together at the end), then the embedding
+    // gradient's.
+    size_t train_partial_floats(size_t n) const {
+        namespace T = kern::train;
+        const int R = int(n), W = int(cfg.width), V = int(cfg.vocab_size);
+        const T::Mesh ma{W, int(cfg.attention_mesh_depth), shape.butterfly, shape.log2w};
+        const T::Mesh mf{W, int(cfg.ffn_mesh_depth), shape.butterfly, shape.log2w};
+        size_t total = cfg.layers * (4 * T::mesh_partial_floats(ma, R) + T::mesh_partial_floats(mf, R));
+        if (cfg.embedding == TokenEmbedding::Mesh) total += T::mesh_partial_floats(ma, V);
+        return total + T::embedding_partial_floats(R, W, V);
     }
 
     void drop_train_graph() {
@@ -796,17 +804,31 @@ struct MeshGpt::Impl {
 
         float *dx = at(p.dx), *dn = at(p.dn), *dq = at(p.dq), *dk = at(p.dk), *dv = at(p.dv);
         float *dy = at(p.dy), *dt = at(p.dt);
+        // Each stack's partial sums get their own region of the scratch, and
+        // all their reductions run in one launch at the end.
+        std::vector<T::GradReduce> reductions;
+        float *scratch = part;
+        auto region = [&](size_t floats) {
+            float *r = scratch;
+            scratch += floats;
+            return r;
+        };
+        auto mesh_backward = [&](const T::Mesh &m, const float *in, const float *stack, const float *dout,
+                                 float *din, size_t wo, int rows) {
+            const float *wp = w + wo;
+            float *gp = grad + wo;
+            T::mesh_backward_set(m, 1, &in, &stack, &dout, &din, false, &wp, region(T::mesh_partial_floats(m, rows)),
+                                 &gp, rows, stream, &reductions);
+        };
         T::head_backward(at(p.dlogits), Ev, dn, R, W, V, stream);
         T::rmsnorm_backward(X(L), at(p.invf), dn, dx, false, R, W, 1, stream);
         for (int b = L - 1; b >= 0; --b) {
             const TrainBlock &k = p.blocks[b];
             const Block &g = layout.blocks[b];
             // x_{b+1} = xm + ffn(rmsnorm(xm)); xm = x_b + proj(attention)
-            T::mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, false, w + group(g.ffn), part, grad + group(g.ffn), R,
-                             stream);
+            mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, group(g.ffn), R);
             T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
-            T::mesh_backward(ma, at(k.z), at(k.ps), dx, dt, false, w + group(g.projection), part,
-                             grad + group(g.projection), R, stream);
+            mesh_backward(ma, at(k.z), at(k.ps), dx, dt, group(g.projection), R);
             T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dt, dy, dq, dk, dv,
                                   at(p.dsum), R, seq, W, H, cfg.xsa, stream);
             if (cfg.rope || cfg.qk_norm) {
@@ -822,17 +844,19 @@ struct MeshGpt::Impl {
             const float *qkv_w[3] = {w + group(g.query), w + group(g.key), w + group(g.value)};
             float *qkv_din[3] = {dn, at(p.dnk), at(p.dnv)};
             float *qkv_grad[3] = {grad + group(g.query), grad + group(g.key), grad + group(g.value)};
-            T::mesh_backward_set(ma, 3, qkv_in, qkv, qkv_dout, qkv_din, false, qkv_w, part, qkv_grad, R, stream);
+            T::mesh_backward_set(ma, 3, qkv_in, qkv, qkv_dout, qkv_din, false, qkv_w,
+                                 region(3 * T::mesh_partial_floats(ma, R)), qkv_grad, R, stream, &reductions);
             T::rmsnorm_backward_sum3(X(b), at(k.inv1), dn, at(p.dnk), at(p.dnv), dx, true, R, W, stream);
         }
         // The tied vectors collect the head's gradient and the gathered rows'.
-        T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), part, R, W, V, stream);
+        T::embedding_gradient(at(p.dlogits), at(p.nf), tok, dx, at(p.dE), region(T::embedding_partial_floats(R, W, V)),
+                              R, W, V, stream);
         if (geometry) T::geometry_backward(Eraw, at(p.er), at(p.dE), V, W, radius, normalize, preserve, stream);
         if (cfg.embedding == TokenEmbedding::Mesh)
-            T::mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, false, w + emb, part, grad + emb, V,
-                             stream);
+            mesh_backward(ma, codes.as<float>(), at(p.es), at(p.dE), nullptr, emb, V);
         else
             T::copy(at(p.dE), grad + emb, size_t(V) * W, stream);
+        T::reduce_gradients(reductions.data(), reductions.size(), stream);
         // config.rs:490-500: the frozen embedding group, and the final mesh rows
         // that write protected residual coordinates.
         if (cfg.geometry.frozen) T::fill(grad + emb, 0.0f, cfg.embedding_parameter_count(), stream);

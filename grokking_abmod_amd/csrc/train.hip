@@ -29,9 +29,13 @@ struct MeshGradSet {
     const float *in[kMaxSet], *stack[kMaxSet], *dout[kMaxSet], *w[kMaxSet];
     float *din[kMaxSet], *partials[kMaxSet];
 };
+// Up to kMaxReduce reductions in one launch, reduction blockIdx.y summing
+// groups[y] partial rows of n[y] floats.
+constexpr int kMaxReduce = 8;
 struct ReduceSet {
-    const float *part[kMaxSet];
-    float *out[kMaxSet];
+    const float *part[kMaxReduce];
+    float *out[kMaxReduce];
+    int groups[kMaxReduce], n[kMaxReduce];
 };
 // QK-Norm and RoPE of q and k in one launch: out[i] (the gradient rows, in
 // place, for the backward) from the pre-norm rows pre[i], factors inv[i].
@@ -178,10 +182,12 @@ __global__ void __launch_bounds__(kMaxWidth) mesh_backward_kernel(Mesh m, MeshGr
 // out[i] = sum over g < groups of part[g * n + i], in g order per wave and
 // the waves' sums in wave order: 64 outputs per workgroup, wave k of its 16
 // adding groups k, k + 16, ...
-__global__ void __launch_bounds__(1024) reduce_groups_kernel(ReduceSet set, int groups, int n) {
+__global__ void __launch_bounds__(1024) reduce_groups_kernel(ReduceSet set) {
     __shared__ float sums[16][64];
     const float *__restrict__ part = set.part[blockIdx.y];
     float *__restrict__ out = set.out[blockIdx.y];
+    const int groups = set.groups[blockIdx.y], n = set.n[blockIdx.y];
+    if (int(blockIdx.x) * 64 >= n) return;  // the whole workgroup: a shorter reduction of the set
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, i = blockIdx.x * 64 + lane;
     float acc = 0.0f;
     if (i < n)
@@ -1108,6 +1114,22 @@ void by_head_width(int hd, F &&f) {
 
 }  // namespace
 
+void reduce_gradients(const GradReduce *r, size_t count, hipStream_t stream) {
+    for (size_t b = 0; b < count; b += kMaxReduce) {
+        ReduceSet set{};
+        int most = 0, k = 0;
+        for (; k < kMaxReduce && b + k < count; ++k) {
+            set.part[k] = r[b + k].part;
+            set.out[k] = r[b + k].out;
+            set.groups[k] = r[b + k].groups;
+            set.n[k] = r[b + k].n;
+            most = std::max(most, r[b + k].n);
+        }
+        hipLaunchKernelGGL(reduce_groups_kernel, dim3(unsigned((most + 63) / 64), unsigned(k)), dim3(1024), 0, stream,
+                           set);
+    }
+}
+
 // Layers [l0, l0 + kMaxDepth) of m as one launch's stack.
 Mesh mesh_chunk(const Mesh &m, int l0) {
     Mesh c = m;
@@ -1157,7 +1179,8 @@ size_t mesh_partial_floats(const Mesh &m, int rows) {
 // carry d loss down from one launch of kMaxDepth layers to the next.
 void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
                        const float *const *dout, float *const *din, bool accumulate, const float *const *w,
-                       float *partials, float *const *grad, int rows, hipStream_t stream) {
+                       float *partials, float *const *grad, int rows, hipStream_t stream,
+                       std::vector<GradReduce> *deferred) {
     const size_t plane = size_t(rows) * m.W, per = mesh_partial_floats(m, rows);
     const int top = (m.depth - 1) / kMaxDepth * kMaxDepth;
     const float *g[kMaxSet] = {};
@@ -1165,7 +1188,7 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
     for (int l0 = top, k = 0; l0 >= 0; l0 -= kMaxDepth, ++k) {
         const Mesh c = mesh_chunk(m, l0);
         MeshGradSet set{};
-        ReduceSet red{};
+        GradReduce red[kMaxSet];
         for (int i = 0; i < count; ++i) {
             float *base = partials + i * per, *between = base + (per - (top > 0 ? 2 * plane : 0));
             float *to = l0 == 0 ? din[i] : between + (k & 1) * plane;
@@ -1175,8 +1198,8 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
             set.din[i] = to;
             set.w[i] = w[i] + size_t(l0) * 2 * m.W;
             set.partials[i] = base;
-            red.part[i] = base;
-            red.out[i] = grad[i] + size_t(l0) * 2 * m.W;
+            red[i].part = base;
+            red[i].out = grad[i] + size_t(l0) * 2 * m.W;
             g[i] = to;
         }
         const int acc = l0 == 0 && accumulate, n = c.depth * m.W * 2;
@@ -1195,14 +1218,22 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
             hipLaunchKernelGGL(mesh_backward_kernel, dim3(unsigned(groups), unsigned(count)), dim3(kMaxWidth),
                                size_t(3) * rpb * m.W * sizeof(float), stream, c, set, acc, rows);
         }
-        hipLaunchKernelGGL(reduce_groups_kernel, dim3(unsigned((n + 63) / 64), unsigned(count)), dim3(1024), 0,
-                           stream, red, groups, n);
+        for (int i = 0; i < count; ++i) {
+            red[i].groups = groups;
+            red[i].n = n;
+        }
+        // A single launch's sums can wait for the caller's combined reduction;
+        // a deep stack's partials are reused by its next launch.
+        if (deferred && top == 0)
+            deferred->insert(deferred->end(), red, red + count);
+        else
+            reduce_gradients(red, size_t(count), stream);
     }
 }
 
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
                    bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream) {
-    mesh_backward_set(m, 1, &in, &stack, &dout, &din, accumulate, &w, partials, &grad, rows, stream);
+    mesh_backward_set(m, 1, &in, &stack, &dout, &din, accumulate, &w, partials, &grad, rows, stream, nullptr);
 }
 
 void rmsnorm_forward(const float *x, float *y, float *inv, int rows, int W, int groups, hipStream_t stream) {
@@ -1376,10 +1407,8 @@ void embedding_gradient(const float *dlogits, const float *n, const uint32_t *to
     const int splits = (rows + kEmbeddingSpan - 1) / kEmbeddingSpan, nvw = V * W;
     gemm_tiles<false, false>(dlogits, V, n, W, partials, W, size_t(nvw), V, W, rows, kEmbeddingSpan, tokens, dx,
                              stream);
-    ReduceSet red{};
-    red.part[0] = partials;
-    red.out[0] = dE;
-    hipLaunchKernelGGL(reduce_groups_kernel, dim3((nvw + 63) / 64), dim3(1024), 0, stream, red, splits, nvw);
+    const GradReduce red{partials, dE, splits, nvw};
+    reduce_gradients(&red, 1, stream);
 }
 
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,

@@ -8,6 +8,7 @@
 
 #include <cstddef>
 #include <cstdint>
+#include <vector>
 
 namespace meshgpt::kern::train {
 
@@ -38,14 +39,26 @@ size_t mesh_partial_floats(const Mesh &m, int rows);
 // Deterministic: per-workgroup partial sums in `partials`, then one reduction.
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,
                    bool accumulate, const float *w, float *partials, float *grad, int rows, hipStream_t stream);
+// A weight gradient's last step: out[i] = the sum over `groups` partial rows
+// of n floats at part, in a fixed order.
+struct GradReduce {
+    const float *part;
+    float *out;
+    int groups, n;
+};
+// Runs reductions, up to eight a launch.
+void reduce_gradients(const GradReduce *r, size_t count, hipStream_t stream);
 // `count` (<= kMaxSet) stacks of the same shape at once, stack i on in[i] with
 // weights w[i] (the Q, K and V meshes of a block); the backward needs count x
 // mesh_partial_floats of `partials`, and its din[i] must be distinct rows.
+// With `deferred`, a stack of at most kMaxDepth layers appends its
+// reductions there (its partials must then stay untouched until they run).
 void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
                       int rows, hipStream_t stream);
 void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
                        const float *const *dout, float *const *din, bool accumulate, const float *const *w,
-                       float *partials, float *const *grad, int rows, hipStream_t stream);
+                       float *partials, float *const *grad, int rows, hipStream_t stream,
+                       std::vector<GradReduce> *deferred);
 
 // RMSNorm over `groups` equal groups of each row (reference.rs:392-409):
 // y = x / sqrt(mean(x^2) + 1e-5); inv[row * groups + g] keeps the factor.
