@@ -264,7 +264,9 @@ __device__ __forceinline__ void channel_shift(const float (&x)[CPL], int d, int 
 
 constexpr int kMeshWaveRows = 2;  // rows per wave of the wave-per-row mesh backward
 
-template <int CPL>
+// D: the layers a launch may hold (registers are sized for it; the launch's
+// own depth is at most D).
+template <int CPL, int D>
 __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, int rows) {
     const float *__restrict__ in = set.in[blockIdx.y];
     float *__restrict__ stack = set.stack[blockIdx.y];
@@ -272,9 +274,9 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
     const int lane = threadIdx.x & 63, W = m.W;
     const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6), waves = gridDim.x * (kThreads / 64);
     // The stack's weights of this lane's channels, loaded once.
-    float2 wt[kMaxDepth][CPL];
+    float2 wt[D][CPL];
 #pragma unroll
-    for (int l = 0; l < kMaxDepth; ++l)
+    for (int l = 0; l < D; ++l)
 #pragma unroll
         for (int j = 0; j < CPL; ++j)
             wt[l][j] = l < m.depth && lane + 64 * j < W
@@ -285,7 +287,7 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
 #pragma unroll
         for (int j = 0; j < CPL; ++j) x[j] = lane + 64 * j < W ? in[size_t(r) * W + lane + 64 * j] : 0.0f;
 #pragma unroll
-        for (int l = 0; l < kMaxDepth; ++l) {
+        for (int l = 0; l < D; ++l) {
             if (l >= m.depth) continue;
             float p[CPL];
             channel_shift(x, stride_of(m, l), W, lane, p);
@@ -301,10 +303,34 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
     }
 }
 
-// Each wave carries d loss / d (its row) down the layers, row after row, and
-// adds the weights' gradients in registers; the workgroup's waves add theirs
-// in LDS (in wave order) into the workgroup's partial.
-template <int CPL>
+// One row's layer inputs and outputs in a wave's registers (the backward's
+// operands, loaded at once so that the layer chain waits only on lane shifts).
+template <int CPL, int D>
+struct MeshRowSaved {
+    float g[CPL], xin[D][CPL], act[D][CPL];
+    __device__ __forceinline__ void load(const Mesh &m, const float *__restrict__ in, const float *__restrict__ stack,
+                                         const float *__restrict__ dout, int r, int rows, int lane) {
+        const int W = m.W;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) g[j] = lane + 64 * j < W ? dout[size_t(r) * W + lane + 64 * j] : 0.0f;
+#pragma unroll
+        for (int l = 0; l < D; ++l)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                const bool ok = l < m.depth && c < W;
+                const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
+                xin[l][j] = ok ? x[c] : 0.0f;
+                act[l][j] = ok && elu_layer(m, l) ? stack[(size_t(l) * rows + r) * W + c] : 0.0f;
+            }
+    }
+};
+
+// Each wave carries d loss / d (its row) down the layers, row after row (the
+// next row's operands loading during the current row's chain), and adds the
+// weights' gradients in registers; the workgroup's waves add theirs in LDS
+// (in wave order) into the workgroup's partial.
+template <int CPL, int D>
 __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradSet set, int accumulate, int rows) {
     extern __shared__ float sums[];  // (kThreads / 64) x depth x W x 2
     const float *__restrict__ in = set.in[blockIdx.y];
@@ -315,42 +341,41 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradS
     float *__restrict__ partials = set.partials[blockIdx.y];
     const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6, W = m.W, depth = m.depth;
     const int wave = blockIdx.x * (kThreads / 64) + wv, waves = gridDim.x * (kThreads / 64);
-    float gs[kMaxDepth][CPL], gp[kMaxDepth][CPL];
+    // The weights of this lane's channels, loaded once, off the layer chain.
+    float2 wt[D][CPL];
 #pragma unroll
-    for (int l = 0; l < kMaxDepth; ++l)
+    for (int l = 0; l < D; ++l)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j)
+            wt[l][j] = l < depth && lane + 64 * j < W
+                           ? reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W)[lane + 64 * j]
+                           : make_float2(0.0f, 0.0f);
+    float gs[D][CPL], gp[D][CPL];
+#pragma unroll
+    for (int l = 0; l < D; ++l)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) gs[l][j] = gp[l][j] = 0.0f;
+    MeshRowSaved<CPL, D> cur;
+    if (wave < rows) cur.load(m, in, stack, dout, wave, rows, lane);
     for (int r = wave; r < rows; r += waves) {
+        MeshRowSaved<CPL, D> next;
+        if (r + waves < rows) next.load(m, in, stack, dout, r + waves, rows, lane);
         float g[CPL];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) g[j] = lane + 64 * j < W ? dout[size_t(r) * W + lane + 64 * j] : 0.0f;
-        // Every layer's input and output of this row, loaded at once: the
-        // layer chain below waits only on lane shuffles.
-        float xin[kMaxDepth][CPL], act[kMaxDepth][CPL];
+        for (int j = 0; j < CPL; ++j) g[j] = cur.g[j];
 #pragma unroll
-        for (int l = 0; l < kMaxDepth; ++l)
-#pragma unroll
-            for (int j = 0; j < CPL; ++j) {
-                const int c = lane + 64 * j;
-                const bool ok = l < depth && c < W;
-                const float *x = l == 0 ? in + size_t(r) * W : stack + (size_t(l - 1) * rows + r) * W;
-                xin[l][j] = ok ? x[c] : 0.0f;
-                act[l][j] = ok && elu_layer(m, l) ? stack[(size_t(l) * rows + r) * W + c] : 0.0f;
-            }
-#pragma unroll
-        for (int l = kMaxDepth - 1; l >= 0; --l) {
+        for (int l = D - 1; l >= 0; --l) {
             if (l >= depth) continue;
             const int s = stride_of(m, l);
-            const float2 *wl = reinterpret_cast<const float2 *>(w + size_t(l) * 2 * W);
             float x[CPL], xp[CPL], dz[CPL], t[CPL], back[CPL];
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const int c = lane + 64 * j;
-                x[j] = xin[l][j];
+                x[j] = cur.xin[l][j];
                 // ELU'(z) from its output a: 1 for a >= 0, else exp(z) = a + 1.
-                const float d = act[l][j] < 0.0f ? g[j] * (act[l][j] + 1.0f) : g[j];
+                const float d = cur.act[l][j] < 0.0f ? g[j] * (cur.act[l][j] + 1.0f) : g[j];
                 dz[j] = c < W ? d : 0.0f;
-                t[j] = c < W ? dz[j] * wl[c].y : 0.0f;
+                t[j] = dz[j] * wt[l][j].y;
             }
             channel_shift(x, s, W, lane, xp);
             // Channel c feeds itself and channel c - s: its input gradient is
@@ -361,7 +386,7 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradS
                 const int c = lane + 64 * j;
                 gs[l][j] = fmaf(dz[j], x[j], gs[l][j]);
                 gp[l][j] = fmaf(dz[j], xp[j], gp[l][j]);
-                g[j] = c < W ? dz[j] * wl[c].x + back[j] : 0.0f;
+                g[j] = c < W ? dz[j] * wt[l][j].x + back[j] : 0.0f;
             }
         }
         if (din) {
@@ -373,9 +398,10 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradS
                 din[i] = accumulate ? din[i] + g[j] : g[j];
             }
         }
+        cur = next;
     }
 #pragma unroll
-    for (int l = 0; l < kMaxDepth; ++l) {
+    for (int l = 0; l < D; ++l) {
         if (l >= depth) continue;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
@@ -1114,6 +1140,24 @@ void by_head_width(int hd, F &&f) {
 
 }  // namespace
 
+// f(channels a lane, layers a launch holds) for the wave mesh kernels: 4, 8 or
+// 16 layers, the fewest that hold `depth`.
+template <class F>
+void by_wave_shape(int cpl, int depth, F &&f) {
+    auto layers = [&](auto C) {
+        if (depth <= 4)
+            f(C, std::integral_constant<int, 4>{});
+        else if (depth <= 8)
+            f(C, std::integral_constant<int, 8>{});
+        else
+            f(C, std::integral_constant<int, kMaxDepth>{});
+    };
+    if (cpl == 1)
+        layers(std::integral_constant<int, 1>{});
+    else
+        layers(std::integral_constant<int, 2>{});
+}
+
 void reduce_gradients(const GradReduce *r, size_t count, hipStream_t stream) {
     for (size_t b = 0; b < count; b += kMaxReduce) {
         ReduceSet set{};
@@ -1152,10 +1196,10 @@ void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *c
         }
         if (const int cpl = mesh_wave_cpl(m.W)) {
             const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)), unsigned(count));
-            if (cpl == 1)
-                hipLaunchKernelGGL(mesh_forward_wave<1>, grid, dim3(kThreads), 0, stream, c, set, rows);
-            else
-                hipLaunchKernelGGL(mesh_forward_wave<2>, grid, dim3(kThreads), 0, stream, c, set, rows);
+            by_wave_shape(cpl, c.depth, [&](auto C, auto D) {
+                hipLaunchKernelGGL((mesh_forward_wave<decltype(C)::value, decltype(D)::value>), grid, dim3(kThreads), 0,
+                                   stream, c, set, rows);
+            });
         } else {
             const dim3 grid(unsigned(std::min(rows, 2048)), unsigned(count));
             hipLaunchKernelGGL(mesh_forward_kernel, grid, dim3(block_for(m.W)), 2 * m.W * sizeof(float), stream, c,
@@ -1208,10 +1252,10 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
             groups = mesh_wave_groups(rows);
             const size_t lds = size_t(kThreads / 64) * n * sizeof(float);
             const dim3 grid{unsigned(groups), unsigned(count)};
-            if (cpl == 1)
-                hipLaunchKernelGGL(mesh_backward_wave<1>, grid, dim3(kThreads), lds, stream, c, set, acc, rows);
-            else
-                hipLaunchKernelGGL(mesh_backward_wave<2>, grid, dim3(kThreads), lds, stream, c, set, acc, rows);
+            by_wave_shape(cpl, c.depth, [&](auto C, auto D) {
+                hipLaunchKernelGGL((mesh_backward_wave<decltype(C)::value, decltype(D)::value>), grid, dim3(kThreads),
+                                   lds, stream, c, set, acc, rows);
+            });
         } else {
             groups = mesh_groups(c, rows);
             const int rpb = mesh_rpb(m.W);
