@@ -773,31 +773,34 @@ struct MeshGpt::Impl {
         T::gather(Ev, tok, at(p.x), R, W, stream);
         auto X = [&](int b) { return at(p.x) + size_t(b) * RW; };
         auto last = [&](size_t o, int depth) { return at(o) + size_t(depth - 1) * RW; };
-        T::rmsnorm_forward(X(0), at(p.blocks[0].n1), at(p.blocks[0].inv1), R, W, 1, stream);
         for (int b = 0; b < L; ++b) {
             const TrainBlock &k = p.blocks[b];
             const Block &g = layout.blocks[b];
-            // Q, K and V of n1 in one launch, then QK-Norm and RoPE of q and k
-            // in one (reference.rs:174-193, each when switched on).
-            const float *n1 = at(k.n1);
-            const float *qkv_in[3] = {n1, n1, n1}, *qkv_w[3] = {w + group(g.query), w + group(g.key),
-                                                                  w + group(g.value)};
+            // n1 = rmsnorm(x_b), x_b = xm + ffn of the block below (its residual
+            // add and this norm are formed in front of the meshes), then Q, K
+            // and V of n1 in one launch, then QK-Norm and RoPE of q and k in
+            // one (reference.rs:174-193, each when switched on).
+            const float *qkv_w[3] = {w + group(g.query), w + group(g.key), w + group(g.value)};
             float *qkv[3] = {at(k.qs), at(k.ks), at(k.vs)};
-            T::mesh_forward_set(ma, 3, qkv_in, qkv, qkv_w, R, stream);
+            const T::NormIn n1 = b == 0 ? T::NormIn{X(0), nullptr, nullptr, at(k.n1), at(k.inv1)}
+                                        : T::NormIn{at(p.blocks[b - 1].xm), last(p.blocks[b - 1].fs, F), X(b),
+                                                    at(k.n1), at(k.inv1)};
+            T::norm_mesh_forward_set(ma, 3, n1, qkv, qkv_w, R, stream);
             const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)};
             float *qk_out[2] = {at(k.qr), at(k.kr)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
             T::qk_forward(2, qk_pre, qk_out, qk_inv, table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
             T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.z), at(k.lse), R, seq, W, H,
                                  cfg.xsa, stream);
             T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);
-            // xm = x_b + proj, n2 = rmsnorm(xm); x_{b+1} = xm + ffn, normalised
-            // by the next block (or the final norm) in the same launch.
-            T::add_rmsnorm_forward(X(b), last(k.ps, A), at(k.xm), at(k.n2), at(k.inv2), R, W, stream);
-            T::mesh_forward(mf, at(k.n2), at(k.fs), w + group(g.ffn), R, stream);
-            const bool top = b + 1 == L;
-            T::add_rmsnorm_forward(at(k.xm), last(k.fs, F), X(b + 1), at(top ? p.nf : p.blocks[b + 1].n1),
-                                   at(top ? p.invf : p.blocks[b + 1].inv1), R, W, stream);
+            // xm = x_b + proj and n2 = rmsnorm(xm), formed in front of the FFN mesh.
+            float *fs = at(k.fs);
+            const float *wf = w + group(g.ffn);
+            T::norm_mesh_forward_set(mf, 1, T::NormIn{X(b), last(k.ps, A), at(k.xm), at(k.n2), at(k.inv2)}, &fs, &wf,
+                                     R, stream);
         }
+        // x_L = xm + ffn of the top block, and the final norm.
+        T::add_rmsnorm_forward(at(p.blocks[L - 1].xm), last(p.blocks[L - 1].fs, F), X(L), at(p.nf), at(p.invf), R, W,
+                               stream);
         T::head_logits(at(p.nf), Ev, at(p.logits), R, W, V, stream);
         T::cross_entropy(at(p.logits), tgt, at(p.dlogits), at(p.loss), R, V, sc, stream);
         if (!backward) return;
@@ -826,8 +829,9 @@ struct MeshGpt::Impl {
             const TrainBlock &k = p.blocks[b];
             const Block &g = layout.blocks[b];
             // x_{b+1} = xm + ffn(rmsnorm(xm)); xm = x_b + proj(attention)
-            mesh_backward(mf, at(k.n2), at(k.fs), dx, dn, group(g.ffn), R);
-            T::rmsnorm_backward(at(k.xm), at(k.inv2), dn, dx, true, R, W, 1, stream);
+            T::mesh_backward_norm(mf, at(k.n2), at(k.fs), dx, T::NormGrad{at(k.xm), at(k.inv2), dx}, dn,
+                                  w + group(g.ffn), region(T::mesh_partial_floats(mf, R)), grad + group(g.ffn), R,
+                                  stream, &reductions);
             mesh_backward(ma, at(k.z), at(k.ps), dx, dt, group(g.projection), R);
             T::attention_backward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.lse), dt, dy, dq, dk, dv,
                                   at(p.dsum), R, seq, W, H, cfg.xsa, stream);

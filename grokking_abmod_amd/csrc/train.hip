@@ -29,9 +29,10 @@ struct MeshGradSet {
     const float *in[kMaxSet], *stack[kMaxSet], *dout[kMaxSet], *w[kMaxSet];
     float *din[kMaxSet], *partials[kMaxSet];
 };
+
 // Up to kMaxReduce reductions in one launch, reduction blockIdx.y summing
 // groups[y] partial rows of n[y] floats.
-constexpr int kMaxReduce = 8;
+constexpr int kMaxReduce = 16;
 struct ReduceSet {
     const float *part[kMaxReduce];
     float *out[kMaxReduce];
@@ -266,8 +267,11 @@ constexpr int kMeshWaveRows = 2;  // rows per wave of the wave-per-row mesh back
 
 // D: the layers a launch may hold (registers are sized for it; the launch's
 // own depth is at most D).
-template <int CPL, int D>
-__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, int rows) {
+// With NORM the stacks' input is RMSNorm(a + b) (b optional) of each row,
+// formed here with the arithmetic of rmsnorm_forward_kernel; stack 0 stores the
+// sum, the normalised row and its factor.
+template <int CPL, int D, bool NORM>
+__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, NormIn ni, int rows) {
     const float *__restrict__ in = set.in[blockIdx.y];
     float *__restrict__ stack = set.stack[blockIdx.y];
     const float *__restrict__ w = set.w[blockIdx.y];
@@ -284,8 +288,29 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
                            : make_float2(0.0f, 0.0f);
     for (int r = wave; r < rows; r += waves) {
         float x[CPL];
+        if constexpr (NORM) {
+            const bool first = blockIdx.y == 0;
+            float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x[j] = lane + 64 * j < W ? in[size_t(r) * W + lane + 64 * j] : 0.0f;
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                const size_t i = size_t(r) * W + c;
+                x[j] = c < W ? (ni.b ? ni.a[i] + ni.b[i] : ni.a[i]) : 0.0f;
+                acc = fmaf(x[j], x[j], acc);
+                if (first && ni.b && c < W) ni.sum[i] = x[j];
+            }
+            const float iv = rsqrtf(wave_sum(acc) * (1.0f / float(W)) + kRmsEps);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                x[j] *= iv;
+                if (first && c < W) ni.n[size_t(r) * W + c] = x[j];
+            }
+            if (first && lane == 0) ni.inv[r] = iv;
+        } else {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[j] = lane + 64 * j < W ? in[size_t(r) * W + lane + 64 * j] : 0.0f;
+        }
 #pragma unroll
         for (int l = 0; l < D; ++l) {
             if (l >= m.depth) continue;
@@ -305,14 +330,20 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
 
 // One row's layer inputs and outputs in a wave's registers (the backward's
 // operands, loaded at once so that the layer chain waits only on lane shifts).
-template <int CPL, int D>
+template <int CPL, int D, bool NORMB>
 struct MeshRowSaved {
     float g[CPL], xin[D][CPL], act[D][CPL];
+    float xr[NORMB ? CPL : 1], iv = 0.0f;  // the norm's input row and factor (NORMB)
     __device__ __forceinline__ void load(const Mesh &m, const float *__restrict__ in, const float *__restrict__ stack,
-                                         const float *__restrict__ dout, int r, int rows, int lane) {
+                                         const float *dout, const NormGrad &ng, int r, int rows, int lane) {
         const int W = m.W;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) g[j] = lane + 64 * j < W ? dout[size_t(r) * W + lane + 64 * j] : 0.0f;
+        if constexpr (NORMB) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) xr[j] = lane + 64 * j < W ? ng.x[size_t(r) * W + lane + 64 * j] : 0.0f;
+            iv = ng.inv[r];
+        }
 #pragma unroll
         for (int l = 0; l < D; ++l)
 #pragma unroll
@@ -330,12 +361,16 @@ struct MeshRowSaved {
 // next row's operands loading during the current row's chain), and adds the
 // weights' gradients in registers; the workgroup's waves add theirs in LDS
 // (in wave order) into the workgroup's partial.
-template <int CPL, int D>
-__global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradSet set, int accumulate, int rows) {
+// With NORMB the input gradient goes on through the RMSNorm in front of the
+// stack (rmsnorm_backward_kernel's arithmetic): dx += iv g - x iv^3 (g . x) / W.
+template <int CPL, int D, bool NORMB>
+__global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradSet set, NormGrad ng, int accumulate,
+                                                               int rows) {
     extern __shared__ float sums[];  // (kThreads / 64) x depth x W x 2
     const float *__restrict__ in = set.in[blockIdx.y];
     const float *__restrict__ stack = set.stack[blockIdx.y];
-    const float *__restrict__ dout = set.dout[blockIdx.y];
+    // dout may be the rows NORMB adds to (each row is read before it is written).
+    const float *dout = set.dout[blockIdx.y];
     float *din = set.din[blockIdx.y];
     const float *__restrict__ w = set.w[blockIdx.y];
     float *__restrict__ partials = set.partials[blockIdx.y];
@@ -355,11 +390,11 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradS
     for (int l = 0; l < D; ++l)
 #pragma unroll
         for (int j = 0; j < CPL; ++j) gs[l][j] = gp[l][j] = 0.0f;
-    MeshRowSaved<CPL, D> cur;
-    if (wave < rows) cur.load(m, in, stack, dout, wave, rows, lane);
+    MeshRowSaved<CPL, D, NORMB> cur;
+    if (wave < rows) cur.load(m, in, stack, dout, ng, wave, rows, lane);
     for (int r = wave; r < rows; r += waves) {
-        MeshRowSaved<CPL, D> next;
-        if (r + waves < rows) next.load(m, in, stack, dout, r + waves, rows, lane);
+        MeshRowSaved<CPL, D, NORMB> next;
+        if (r + waves < rows) next.load(m, in, stack, dout, ng, r + waves, rows, lane);
         float g[CPL];
 #pragma unroll
         for (int j = 0; j < CPL; ++j) g[j] = cur.g[j];
@@ -389,7 +424,19 @@ __global__ void __launch_bounds__(kThreads) mesh_backward_wave(Mesh m, MeshGradS
                 g[j] = c < W ? dz[j] * wt[l][j].x + back[j] : 0.0f;
             }
         }
-        if (din) {
+        if constexpr (NORMB) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) acc = fmaf(g[j], cur.xr[j], acc);
+            const float iv = cur.iv, k = wave_sum(acc) * iv * iv * iv * (1.0f / float(W));
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const int c = lane + 64 * j;
+                if (c >= W) continue;
+                const size_t i = size_t(r) * W + c;
+                ng.dx[i] += iv * g[j] - cur.xr[j] * k;
+            }
+        } else if (din) {
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const int c = lane + 64 * j;
@@ -1183,8 +1230,12 @@ Mesh mesh_chunk(const Mesh &m, int l0) {
     return c;
 }
 
-void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
-                      int rows, hipStream_t stream) {
+// The wave kernels can put the norm in front of a stack of at most kMaxDepth
+// layers in its own launch; every other case takes the norm's own launch.
+bool norm_fuses(const Mesh &m) { return mesh_wave_cpl(m.W) != 0 && m.depth <= kMaxDepth; }
+
+void mesh_forward_impl(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
+                       const NormIn *ni, int rows, hipStream_t stream) {
     const size_t plane = size_t(rows) * m.W;
     for (int l0 = 0; l0 < m.depth; l0 += kMaxDepth) {
         const Mesh c = mesh_chunk(m, l0);
@@ -1196,9 +1247,15 @@ void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *c
         }
         if (const int cpl = mesh_wave_cpl(m.W)) {
             const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)), unsigned(count));
+            const NormIn none{};
             by_wave_shape(cpl, c.depth, [&](auto C, auto D) {
-                hipLaunchKernelGGL((mesh_forward_wave<decltype(C)::value, decltype(D)::value>), grid, dim3(kThreads), 0,
-                                   stream, c, set, rows);
+                constexpr int CC = decltype(C)::value, DD = decltype(D)::value;
+                if (ni)
+                    hipLaunchKernelGGL((mesh_forward_wave<CC, DD, true>), grid, dim3(kThreads), 0, stream, c, set, *ni,
+                                       rows);
+                else
+                    hipLaunchKernelGGL((mesh_forward_wave<CC, DD, false>), grid, dim3(kThreads), 0, stream, c, set,
+                                       none, rows);
             });
         } else {
             const dim3 grid(unsigned(std::min(rows, 2048)), unsigned(count));
@@ -1206,6 +1263,26 @@ void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *c
                                set, rows);
         }
     }
+}
+
+void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
+                      int rows, hipStream_t stream) {
+    mesh_forward_impl(m, count, in, stack, w, nullptr, rows, stream);
+}
+
+void norm_mesh_forward_set(const Mesh &m, int count, const NormIn &ni, float *const *stack, const float *const *w,
+                           int rows, hipStream_t stream) {
+    const float *in[kMaxSet];
+    for (int i = 0; i < count; ++i) in[i] = ni.n;
+    if (norm_fuses(m)) {
+        mesh_forward_impl(m, count, in, stack, w, &ni, rows, stream);
+        return;
+    }
+    if (ni.b)
+        add_rmsnorm_forward(ni.a, ni.b, ni.sum, ni.n, ni.inv, rows, m.W, stream);
+    else
+        rmsnorm_forward(ni.a, ni.n, ni.inv, rows, m.W, 1, stream);
+    mesh_forward_impl(m, count, in, stack, w, nullptr, rows, stream);
 }
 
 void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {
@@ -1221,10 +1298,10 @@ size_t mesh_partial_floats(const Mesh &m, int rows) {
 // Each stack of the set works in its own mesh_partial_floats of `partials`:
 // the partial sums, then (deep stacks) the two planes of gradient rows that
 // carry d loss down from one launch of kMaxDepth layers to the next.
-void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
-                       const float *const *dout, float *const *din, bool accumulate, const float *const *w,
-                       float *partials, float *const *grad, int rows, hipStream_t stream,
-                       std::vector<GradReduce> *deferred) {
+void mesh_backward_impl(const Mesh &m, int count, const float *const *in, const float *const *stack,
+                        const float *const *dout, float *const *din, bool accumulate, const float *const *w,
+                        float *partials, float *const *grad, const NormGrad *ng, int rows, hipStream_t stream,
+                        std::vector<GradReduce> *deferred) {
     const size_t plane = size_t(rows) * m.W, per = mesh_partial_floats(m, rows);
     const int top = (m.depth - 1) / kMaxDepth * kMaxDepth;
     const float *g[kMaxSet] = {};
@@ -1252,9 +1329,15 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
             groups = mesh_wave_groups(rows);
             const size_t lds = size_t(kThreads / 64) * n * sizeof(float);
             const dim3 grid{unsigned(groups), unsigned(count)};
+            const NormGrad none{};
             by_wave_shape(cpl, c.depth, [&](auto C, auto D) {
-                hipLaunchKernelGGL((mesh_backward_wave<decltype(C)::value, decltype(D)::value>), grid, dim3(kThreads),
-                                   lds, stream, c, set, acc, rows);
+                constexpr int CC = decltype(C)::value, DD = decltype(D)::value;
+                if (ng)
+                    hipLaunchKernelGGL((mesh_backward_wave<CC, DD, true>), grid, dim3(kThreads), lds, stream, c, set,
+                                       *ng, acc, rows);
+                else
+                    hipLaunchKernelGGL((mesh_backward_wave<CC, DD, false>), grid, dim3(kThreads), lds, stream, c, set,
+                                       none, acc, rows);
             });
         } else {
             groups = mesh_groups(c, rows);
@@ -1273,6 +1356,26 @@ void mesh_backward_set(const Mesh &m, int count, const float *const *in, const f
         else
             reduce_gradients(red, size_t(count), stream);
     }
+}
+
+void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
+                       const float *const *dout, float *const *din, bool accumulate, const float *const *w,
+                       float *partials, float *const *grad, int rows, hipStream_t stream,
+                       std::vector<GradReduce> *deferred) {
+    mesh_backward_impl(m, count, in, stack, dout, din, accumulate, w, partials, grad, nullptr, rows, stream, deferred);
+}
+
+void mesh_backward_norm(const Mesh &m, const float *in, const float *stack, const float *dout, const NormGrad &ng,
+                        float *scratch, const float *w, float *partials, float *grad, int rows, hipStream_t stream,
+                        std::vector<GradReduce> *deferred) {
+    if (norm_fuses(m)) {
+        float *none = nullptr;
+        mesh_backward_impl(m, 1, &in, &stack, &dout, &none, false, &w, partials, &grad, &ng, rows, stream, deferred);
+        return;
+    }
+    mesh_backward_impl(m, 1, &in, &stack, &dout, &scratch, false, &w, partials, &grad, nullptr, rows, stream,
+                       deferred);
+    rmsnorm_backward(ng.x, ng.inv, scratch, ng.dx, true, rows, m.W, 1, stream);
 }
 
 void mesh_backward(const Mesh &m, const float *in, const float *stack, const float *dout, float *din,

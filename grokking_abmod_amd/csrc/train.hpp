@@ -46,7 +46,7 @@ struct GradReduce {
     float *out;
     int groups, n;
 };
-// Runs reductions, up to eight a launch.
+// Runs reductions, up to sixteen a launch.
 void reduce_gradients(const GradReduce *r, size_t count, hipStream_t stream);
 // `count` (<= kMaxSet) stacks of the same shape at once, stack i on in[i] with
 // weights w[i] (the Q, K and V meshes of a block); the backward needs count x
@@ -55,6 +55,25 @@ void reduce_gradients(const GradReduce *r, size_t count, hipStream_t stream);
 // reductions there (its partials must then stay untouched until they run).
 void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
                       int rows, hipStream_t stream);
+// The RMSNorm (and residual add) in front of a stack set: x = a (+ b, stored to
+// sum), n = x / sqrt(mean(x^2) + 1e-5) stored with its factor inv, and the
+// stacks run on n; in the wave kernels all in one launch.
+struct NormIn {
+    const float *a, *b;
+    float *sum, *n, *inv;
+};
+void norm_mesh_forward_set(const Mesh &m, int count, const NormIn &ni, float *const *stack, const float *const *w,
+                           int rows, hipStream_t stream);
+// The backward of one stack whose input is RMSNorm(x): its input gradient goes
+// through the norm's backward into dx (added); `scratch` (rows x W) holds it
+// in between when the two are separate launches.
+struct NormGrad {
+    const float *x, *inv;
+    float *dx;
+};
+void mesh_backward_norm(const Mesh &m, const float *in, const float *stack, const float *dout, const NormGrad &ng,
+                        float *scratch, const float *w, float *partials, float *grad, int rows, hipStream_t stream,
+                        std::vector<GradReduce> *deferred);
 void mesh_backward_set(const Mesh &m, int count, const float *const *in, const float *const *stack,
                        const float *const *dout, float *const *din, bool accumulate, const float *const *w,
                        float *partials, float *const *grad, int rows, hipStream_t stream,
