@@ -936,6 +936,86 @@ __global__ void __launch_bounds__(kThreads) attention_dkv_wave(const float *__re
     lanes_store(dv + o, hd, lane, old);
 }
 
+// The whole attention backward of short sequences in one launch: waves of
+// blockIdx.y = 0 take a query row each (dq, as attention_dq_wave), waves of
+// blockIdx.y = 1 a key row each (dk and dv, as attention_dkv_wave), which
+// form each later query's XSA backward and dy . y themselves instead of
+// waiting for the query waves: the same arithmetic on the same operands.
+template <int EPL, bool XSA>
+__global__ void __launch_bounds__(kThreads) attention_backward_wave(const float *__restrict__ q,
+                                                                    const float *__restrict__ k,
+                                                                    const float *__restrict__ v,
+                                                                    const float *__restrict__ y,
+                                                                    const float *__restrict__ lse,
+                                                                    const float *__restrict__ dz,
+                                                                    float *__restrict__ dq, float *__restrict__ dk,
+                                                                    float *__restrict__ dv, int rows, int sequence,
+                                                                    int W, int H, float scale) {
+    const int t = row_wave(), lane = threadIdx.x & 63;
+    if (t >= rows * H) return;
+    const int r = t / H, h = t % H, hd = W / H, pos = r % sequence, first = r - pos;
+    // d loss / d y of row i (XSA's backward when on) and its dy . y.
+    auto output_grad = [&](int i, float (&g)[EPL], float (&dvs)[EPL]) {
+        const size_t oi = size_t(i) * W + h * hd;
+        float yv[EPL];
+        lanes_load(dz + oi, hd, lane, g);
+        lanes_load(y + oi, hd, lane, yv);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) dvs[e] = 0.0f;
+        if (XSA) {
+            float vs[EPL];
+            lanes_load(v + oi, hd, lane, vs);
+            lanes_xsa_backward(yv, vs, g, dvs);
+        }
+        return lanes_dot(g, yv);
+    };
+    const size_t o = size_t(r) * W + h * hd;
+    if (blockIdx.y == 0) {
+        float qr[EPL], g[EPL], dvs[EPL], acc[EPL] = {};
+        lanes_load(q + o, hd, lane, qr);
+        const float D = output_grad(r, g, dvs), L = lse[t];
+        for (int j = 0; j <= pos; ++j) {
+            float kr[EPL], vr[EPL];
+            lanes_load(k + size_t(first + j) * W + h * hd, hd, lane, kr);
+            lanes_load(v + size_t(first + j) * W + h * hd, hd, lane, vr);
+            const float ds = expf(lanes_dot(qr, kr) * scale - L) * (lanes_dot(g, vr) - D);
+#pragma unroll
+            for (int e = 0; e < EPL; ++e) acc[e] = fmaf(ds, kr[e], acc[e]);
+        }
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) acc[e] *= scale;
+        lanes_store(dq + o, hd, lane, acc);
+        return;
+    }
+    const int last = first + sequence;
+    float kr[EPL], vr[EPL], ak[EPL] = {}, av[EPL] = {}, own[EPL];
+    lanes_load(k + o, hd, lane, kr);
+    lanes_load(v + o, hd, lane, vr);
+    {
+        float g[EPL];
+        output_grad(r, g, own);  // this row's own XSA part of dv
+    }
+    for (int i = r; i < last; ++i) {
+        float qi[EPL], gi[EPL], unused[EPL];
+        lanes_load(q + size_t(i) * W + h * hd, hd, lane, qi);
+        const float D = output_grad(i, gi, unused);
+        const float p = expf(lanes_dot(qi, kr) * scale - lse[size_t(i) * H + h]);
+        const float ds = p * (lanes_dot(gi, vr) - D);
+#pragma unroll
+        for (int e = 0; e < EPL; ++e) {
+            av[e] = fmaf(p, gi[e], av[e]);
+            ak[e] = fmaf(ds, qi[e], ak[e]);
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < EPL; ++e) {
+        ak[e] *= scale;
+        own[e] += av[e];
+    }
+    lanes_store(dk + o, hd, lane, ak);
+    lanes_store(dv + o, hd, lane, own);
+}
+
 template <int EPL>
 __global__ void __launch_bounds__(kThreads) xsa_forward_wave(const float *__restrict__ y, const float *__restrict__ v,
                                                              float *__restrict__ z, int rows, int W, int H) {
@@ -985,6 +1065,9 @@ void by_lanes(int hd, F &&f) {
 // ones the thread-per-row kernels, whose key loops do 64 rows' work per wave
 // (head widths up to 128; wider heads always take the wave kernels).
 constexpr int kWaveAttentionMax = 64;
+// Sequences up to this length run the attention backward as one launch, whose
+// key waves redo the later queries' XSA backward (a few rows each).
+constexpr int kMergedBackwardMax = 8;
 
 // ---- embedding geometry (reference.rs:130-149): rows scaled to the radius,
 // then protected coordinates replaced by their codes.  One wave per token.
@@ -1444,6 +1527,19 @@ void attention_backward(const float *q, const float *k, const float *v, const fl
     const float scale = float(1.0 / std::sqrt(double(W / H)));
     // Without XSA the attention's output gradient is dz itself.
     const float *g = xsa ? dy : dz;
+    if (sequence <= kMergedBackwardMax) {
+        by_lanes(W / H, [&](auto e) {
+            constexpr int EPL = decltype(e)::value;
+            const dim3 grid(blocks_for(size_t(rows) * H * 64), 2);
+            if (xsa)
+                hipLaunchKernelGGL((attention_backward_wave<EPL, true>), grid, dim3(kThreads), 0, stream, q, k, v, y,
+                                   lse, dz, dq, dk, dv, rows, sequence, W, H, scale);
+            else
+                hipLaunchKernelGGL((attention_backward_wave<EPL, false>), grid, dim3(kThreads), 0, stream, q, k, v, y,
+                                   lse, dz, dq, dk, dv, rows, sequence, W, H, scale);
+        });
+        return;
+    }
     if (sequence <= kWaveAttentionMax || W / H > 128) {
         by_lanes(W / H, [&](auto e) {
             constexpr int EPL = decltype(e)::value;

@@ -111,8 +111,8 @@ void qk_backward(int count, float *const *g, const float *const *pre, const floa
 void attention_forward(const float *q, const float *k, const float *v, float *y, float *z, float *lse, int rows,
                        int sequence, int W, int H, bool xsa, hipStream_t stream);
 // Its backward from dz = d loss / d z: dq and dk written, dv written (XSA's
-// part and attention's); dy (rows x W) receives d loss / d y when xsa; dsum
-// (rows x H) is scratch.
+// part and attention's); dy (rows x W) and dsum (rows x H) are scratch.
+// Sequences of at most 8 rows take one launch for all of it.
 void attention_backward(const float *q, const float *k, const float *v, const float *y, const float *lse,
                         const float *dz, float *dy, float *dq, float *dk, float *dv, float *dsum, int rows,
                         int sequence, int W, int H, bool xsa, hipStream_t stream);
