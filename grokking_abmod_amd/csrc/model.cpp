@@ -785,10 +785,8 @@ struct MeshGpt::Impl {
             const T::NormIn n1 = b == 0 ? T::NormIn{X(0), nullptr, nullptr, at(k.n1), at(k.inv1)}
                                         : T::NormIn{at(p.blocks[b - 1].xm), last(p.blocks[b - 1].fs, F), X(b),
                                                     at(k.n1), at(k.inv1)};
-            T::norm_mesh_forward_set(ma, 3, n1, qkv, qkv_w, R, stream);
-            const float *qk_pre[2] = {last(k.qs, A), last(k.ks, A)};
-            float *qk_out[2] = {at(k.qr), at(k.kr)}, *qk_inv[2] = {at(k.qinv), at(k.kinv)};
-            T::qk_forward(2, qk_pre, qk_out, qk_inv, table, R, seq, W, H, cfg.qk_norm, cfg.rope, stream);
+            const T::QkOut qk{{at(k.qr), at(k.kr)}, {at(k.qinv), at(k.kinv)}, table, seq, H, cfg.qk_norm, cfg.rope};
+            T::norm_mesh_forward_qkv(ma, n1, qkv, qkv_w, qk, R, stream);
             T::attention_forward(at(k.qr), at(k.kr), last(k.vs, A), at(k.y), at(k.z), at(k.lse), R, seq, W, H,
                                  cfg.xsa, stream);
             T::mesh_forward(ma, at(k.z), at(k.ps), w + group(g.projection), R, stream);

@@ -270,8 +270,13 @@ constexpr int kMeshWaveRows = 2;  // rows per wave of the wave-per-row mesh back
 // With NORM the stacks' input is RMSNorm(a + b) (b optional) of each row,
 // formed here with the arithmetic of rmsnorm_forward_kernel; stack 0 stores the
 // sum, the normalised row and its factor.
+// With qk.out[0] set, stacks 0 and 1 (Q and K) also get QK-Norm and slice RoPE
+// of their last layer, per head of hd = W / H lanes (hd a power of two up to
+// 64 within a register, or all 128 channels), stored to qk.out[y] with the
+// norm factors in qk.inv[y] (qk_forward_kernel's operations; the head sums
+// by lane exchanges).
 template <int CPL, int D, bool NORM>
-__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, NormIn ni, int rows) {
+__global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet set, NormIn ni, QkOut qk, int rows) {
     const float *__restrict__ in = set.in[blockIdx.y];
     float *__restrict__ stack = set.stack[blockIdx.y];
     const float *__restrict__ w = set.w[blockIdx.y];
@@ -324,6 +329,53 @@ __global__ void __launch_bounds__(kThreads) mesh_forward_wave(Mesh m, MeshSet se
                 x[j] = z;
                 if (c < W) stack[(size_t(l) * rows + r) * W + c] = z;
             }
+        }
+        if (qk.out[0] && blockIdx.y < 2) {
+            const int y = blockIdx.y, hd = W / qk.H, half = hd / 2;
+            if (qk.norm) {
+                float sq[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) sq[j] = x[j] * x[j];
+                if (hd <= 64) {
+                    for (int off = hd / 2; off >= 1; off >>= 1)
+#pragma unroll
+                        for (int j = 0; j < CPL; ++j) sq[j] += __shfl_xor(sq[j], off, 64);
+                } else {
+                    float t = 0.0f;
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) t += sq[j];
+                    for (int off = 32; off >= 1; off >>= 1) t += __shfl_xor(t, off, 64);
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) sq[j] = t;
+                }
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const int c = lane + 64 * j;
+                    const float iv = rsqrtf(sq[j] * (1.0f / float(hd)) + kRmsEps);
+                    x[j] *= iv;
+                    if (c < W && c % hd == 0) qk.inv[y][size_t(r) * qk.H + c / hd] = iv;
+                }
+            }
+            if (qk.rotate) {
+                float o[CPL];
+                if (hd <= 64) {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) o[j] = __shfl_xor(x[j], half, 64);
+                } else {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) o[j] = x[(j + 1) % CPL];
+                }
+                const float2 *row = qk.table + size_t(r % qk.sequence) * half;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const int d = (lane + 64 * j) % hd;
+                    const float2 cs = row[d < half ? d : d - half];
+                    x[j] = d < half ? x[j] * cs.x - o[j] * cs.y : x[j] * cs.x + o[j] * cs.y;
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (lane + 64 * j < W) qk.out[y][size_t(r) * W + lane + 64 * j] = x[j];
         }
     }
 }
@@ -1318,7 +1370,7 @@ Mesh mesh_chunk(const Mesh &m, int l0) {
 bool norm_fuses(const Mesh &m) { return mesh_wave_cpl(m.W) != 0 && m.depth <= kMaxDepth; }
 
 void mesh_forward_impl(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
-                       const NormIn *ni, int rows, hipStream_t stream) {
+                       const NormIn *ni, const QkOut *qk, int rows, hipStream_t stream) {
     const size_t plane = size_t(rows) * m.W;
     for (int l0 = 0; l0 < m.depth; l0 += kMaxDepth) {
         const Mesh c = mesh_chunk(m, l0);
@@ -1331,14 +1383,17 @@ void mesh_forward_impl(const Mesh &m, int count, const float *const *in, float *
         if (const int cpl = mesh_wave_cpl(m.W)) {
             const dim3 grid(unsigned((rows + kThreads / 64 - 1) / (kThreads / 64)), unsigned(count));
             const NormIn none{};
+            const QkOut noqk{};
+            // Only the launch with the stacks' last layers forms q and k.
+            const QkOut &tail = qk && l0 + c.depth == m.depth ? *qk : noqk;
             by_wave_shape(cpl, c.depth, [&](auto C, auto D) {
                 constexpr int CC = decltype(C)::value, DD = decltype(D)::value;
                 if (ni)
                     hipLaunchKernelGGL((mesh_forward_wave<CC, DD, true>), grid, dim3(kThreads), 0, stream, c, set, *ni,
-                                       rows);
+                                       tail, rows);
                 else
                     hipLaunchKernelGGL((mesh_forward_wave<CC, DD, false>), grid, dim3(kThreads), 0, stream, c, set,
-                                       none, rows);
+                                       none, tail, rows);
             });
         } else {
             const dim3 grid(unsigned(std::min(rows, 2048)), unsigned(count));
@@ -1350,7 +1405,7 @@ void mesh_forward_impl(const Mesh &m, int count, const float *const *in, float *
 
 void mesh_forward_set(const Mesh &m, int count, const float *const *in, float *const *stack, const float *const *w,
                       int rows, hipStream_t stream) {
-    mesh_forward_impl(m, count, in, stack, w, nullptr, rows, stream);
+    mesh_forward_impl(m, count, in, stack, w, nullptr, nullptr, rows, stream);
 }
 
 void norm_mesh_forward_set(const Mesh &m, int count, const NormIn &ni, float *const *stack, const float *const *w,
@@ -1358,14 +1413,29 @@ void norm_mesh_forward_set(const Mesh &m, int count, const NormIn &ni, float *co
     const float *in[kMaxSet];
     for (int i = 0; i < count; ++i) in[i] = ni.n;
     if (norm_fuses(m)) {
-        mesh_forward_impl(m, count, in, stack, w, &ni, rows, stream);
+        mesh_forward_impl(m, count, in, stack, w, &ni, nullptr, rows, stream);
         return;
     }
     if (ni.b)
         add_rmsnorm_forward(ni.a, ni.b, ni.sum, ni.n, ni.inv, rows, m.W, stream);
     else
         rmsnorm_forward(ni.a, ni.n, ni.inv, rows, m.W, 1, stream);
-    mesh_forward_impl(m, count, in, stack, w, nullptr, rows, stream);
+    mesh_forward_impl(m, count, in, stack, w, nullptr, nullptr, rows, stream);
+}
+
+void norm_mesh_forward_qkv(const Mesh &m, const NormIn &ni, float *const *stack, const float *const *w,
+                           const QkOut &qk, int rows, hipStream_t stream) {
+    const int hd = m.W / qk.H;
+    const bool pow2 = hd >= 2 && (hd & (hd - 1)) == 0;
+    if (norm_fuses(m) && pow2 && (hd <= 64 || hd == 128)) {
+        const float *in[3] = {ni.n, ni.n, ni.n};
+        mesh_forward_impl(m, 3, in, stack, w, &ni, &qk, rows, stream);
+        return;
+    }
+    norm_mesh_forward_set(m, 3, ni, stack, w, rows, stream);
+    const size_t last = size_t(m.depth - 1) * rows * m.W;
+    const float *pre[2] = {stack[0] + last, stack[1] + last};
+    qk_forward(2, pre, qk.out, qk.inv, qk.table, rows, qk.sequence, m.W, qk.H, qk.norm, qk.rotate, stream);
 }
 
 void mesh_forward(const Mesh &m, const float *in, float *stack, const float *w, int rows, hipStream_t stream) {

@@ -64,6 +64,18 @@ struct NormIn {
 };
 void norm_mesh_forward_set(const Mesh &m, int count, const NormIn &ni, float *const *stack, const float *const *w,
                            int rows, hipStream_t stream);
+// The Q, K and V stacks on RMSNorm(a + b), then QK-Norm (when norm) and slice
+// RoPE (when rotate) of Q's and K's last layer into out[0], out[1] with the
+// norm factors in inv (as qk_forward); one launch where the wave kernels
+// allow it.
+struct QkOut {
+    float *out[2];
+    float *inv[2];
+    const float2 *table;
+    int sequence, H, norm, rotate;
+};
+void norm_mesh_forward_qkv(const Mesh &m, const NormIn &ni, float *const *stack, const float *const *w,
+                           const QkOut &qk, int rows, hipStream_t stream);
 // The backward of one stack whose input is RMSNorm(x): its input gradient goes
 // through the norm's backward into dx (added); `scratch` (rows x W) holds it
 // in between when the two are separate launches.
