@@ -561,10 +561,43 @@ struct MeshGpt::Impl {
         activate();
         ensure_derived();
         const size_t out_rows = last_only ? n / sequence : n;
-        forward_rows(tokens, n, sequence, out_rows);
-        kern::head(shape, wxn.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
-                   last_only ? int(sequence) - 1 : 0, Et.as<float>(), vpad, wlogits.as<float>(), head_rows(),
-                   stream);
+        namespace T = kern::train;
+        if (T::short_forward_fits(int(cfg.width), int(cfg.heads), cfg.vocab_size, int(sequence))) {
+            // Sequences of up to 16 rows: the whole forward and the head in one
+            // launch, a workgroup per sequence.
+            ensure_workspace(n, out_rows, true);
+            check(hipMemcpyAsync(wtok.p, tokens, n * 4, hipMemcpyHostToDevice, stream), "upload tokens");
+            mark_call(0);
+            T::ShortForward a{};
+            a.E = E.as<float>();
+            a.Et = Et.as<float>();
+            a.vpad = vpad;
+            a.w = params.as<float>();
+            a.tokens = wtok.as<uint32_t>();
+            a.table = rope.as<float2>();
+            a.logits = wlogits.as<float>();
+            a.block0 = layout.groups[layout.blocks[0].query].offset;
+            a.W = int(cfg.width);
+            a.H = int(cfg.heads);
+            a.L = int(cfg.layers);
+            a.A = int(cfg.attention_mesh_depth);
+            a.F = int(cfg.ffn_mesh_depth);
+            a.V = int(cfg.vocab_size);
+            a.sequence = int(sequence);
+            a.butterfly = shape.butterfly;
+            a.log2w = shape.log2w;
+            a.rope = cfg.rope;
+            a.qk_norm = cfg.qk_norm;
+            a.xsa = cfg.xsa;
+            a.last_only = last_only;
+            a.scale = float(1.0 / std::sqrt(double(cfg.width / cfg.heads)));
+            T::short_forward(a, int(n / sequence), stream);
+        } else {
+            forward_rows(tokens, n, sequence, out_rows);
+            kern::head(shape, wxn.as<float>(), int(out_rows), last_only ? int(sequence) : 1,
+                       last_only ? int(sequence) - 1 : 0, Et.as<float>(), vpad, wlogits.as<float>(), head_rows(),
+                       stream);
+        }
         mark_call(1);
         std::vector<float> out(out_rows * cfg.vocab_size);
         check(hipMemcpyAsync(out.data(), wlogits.p, out.size() * 4, hipMemcpyDeviceToHost, stream),

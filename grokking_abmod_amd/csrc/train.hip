@@ -1320,6 +1320,281 @@ void by_head_width(int hd, F &&f) {
         f(std::integral_constant<int, 128>{});
 }
 
+// ---- the forward of short sequences: a workgroup holds R sequences, one wave
+// per position holding that position's row of each (W <= 128, channel
+// lane + 64 j in register j); the rows stay in registers through every block,
+// the sequences' keys and values meet in LDS, and only the logits leave.
+
+// ELU (reference.rs:325-332) with exp(z) - 1 from the hardware exp2 on the
+// negative branch: its absolute error (~1e-7 near 0) is one f32 rounding of the
+// row values, far below the logit tolerance, where the library expm1 is a long
+// dependent chain on every mesh layer.
+__device__ __forceinline__ float elu_exp2(float z) {
+    return z >= 0.0f ? z : __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f;
+}
+
+// Sum over the aligned groups of hd lanes (hd a power of two up to 64), or over
+// both registers and the wave when hd = 128: every lane of a head gets its sum
+// (DPP moves within 16-lane rows, lane shuffles across them).
+template <int CPL>
+__device__ __forceinline__ void head_sums(float (&v)[CPL], int hd) {
+    if (hd > 64) {
+        float t = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) t += v[j];
+        t = wave_sum(t);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) v[j] = t;
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        switch (hd) {
+            case 2: v[j] = group_sum<2>(v[j]); break;
+            case 4: v[j] = group_sum<4>(v[j]); break;
+            case 8: v[j] = group_sum<8>(v[j]); break;
+            case 16: v[j] = group_sum<16>(v[j]); break;
+            case 32: v[j] = group_sum<32>(v[j]); break;
+            default: v[j] = group_sum<64>(v[j]); break;
+        }
+    }
+}
+
+// One mesh stack (reference.rs:422-453) on the wave's R rows, in place: layer l
+// reads its weights at w + l * 2W, the next layer's loading during this one.
+// BF: butterfly strides (a lane exchange per distance), else neighbour
+// connectivity, whose constant stride keeps the code small enough for the
+// instruction cache.
+template <int CPL, int R, bool BF>
+__device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__restrict__ w, int depth,
+                                           const Mesh &m, int lane) {
+    const int W = m.W;
+    float2 cur[CPL], nxt[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+        cur[j] = lane + 64 * j < W ? reinterpret_cast<const float2 *>(w)[lane + 64 * j] : make_float2(0.0f, 0.0f);
+        nxt[j] = cur[j];
+    }
+#pragma nounroll
+    for (int l = 0; l < depth; ++l) {
+        if (l + 1 < depth) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                nxt[j] = lane + 64 * j < W ? reinterpret_cast<const float2 *>(w + size_t(l + 1) * 2 * W)[lane + 64 * j]
+                                           : make_float2(0.0f, 0.0f);
+        }
+        const int d = BF ? 1 << (l % m.log2w) : 1;
+        const bool last = l + 1 == depth;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            float p[CPL];
+            channel_shift(x[i], d, W, lane, p);
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                const float z = x[i][j] * cur[j].x + p[j] * cur[j].y;
+                x[i][j] = last ? z : elu_exp2(z);
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) cur[j] = nxt[j];
+    }
+}
+
+// RMSNorm of each of the wave's rows (reference.rs:392-409).
+template <int CPL, int R>
+__device__ __forceinline__ void wave_rmsnorm(const float (&x)[R][CPL], float (&n)[R][CPL], int W) {
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) acc = fmaf(x[i][j], x[i][j], acc);
+        const float iv = rsqrtf(wave_sum(acc) * (1.0f / float(W)) + kRmsEps);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) n[i][j] = x[i][j] * iv;
+    }
+}
+
+template <int CPL, int R, bool BF>
+__global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int sequences) {
+    // keys, values and final rows, each [R][sequence][W]
+    extern __shared__ float lds[];
+    const int W = a.W, lane = threadIdx.x & 63, pos = threadIdx.x >> 6, S = a.sequence;
+    const int hd = W / a.H, half = hd / 2, slab = R * S * W;
+    const float scale2 = a.scale * 1.4426950408889634f;
+    float *keys = lds, *values = lds + slab, *finals = lds + 2 * slab;
+    const Mesh m{W, 0, a.butterfly, a.log2w};
+    // Sequence i of the workgroup; past the last one a workgroup recomputes the
+    // last and stores nothing for it.
+    const int s0 = blockIdx.x * R, valid = min(R, sequences - s0);
+    float x[R][CPL];
+#pragma unroll
+    for (int i = 0; i < R; ++i) {
+        const uint32_t tok = a.tokens[size_t(s0 + min(i, valid - 1)) * S + pos];
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[i][j] = lane + 64 * j < W ? a.E[size_t(tok) * W + lane + 64 * j] : 0.0f;
+    }
+    const size_t gA = 2 * size_t(W) * a.A, gF = 2 * size_t(W) * a.F;
+    for (int b = 0; b < a.L; ++b) {
+        const float *wb = a.w + a.block0 + size_t(b) * (4 * gA + gF);
+        float q[R][CPL], k[R][CPL], v[R][CPL];
+        wave_rmsnorm(x, q, W);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) k[i][j] = v[i][j] = q[i][j];
+        wave_stack<CPL, R, BF>(q, wb, a.A, m, lane);
+        wave_stack<CPL, R, BF>(k, wb + gA, a.A, m, lane);
+        wave_stack<CPL, R, BF>(v, wb + 2 * gA, a.A, m, lane);
+        // QK-Norm, then slice RoPE at this row's position (reference.rs:174-193).
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+            if (a.qk_norm) {
+                float sq[CPL], sk[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    sq[j] = q[i][j] * q[i][j];
+                    sk[j] = k[i][j] * k[i][j];
+                }
+                head_sums(sq, hd);
+                head_sums(sk, hd);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    q[i][j] *= rsqrtf(sq[j] * (1.0f / float(hd)) + kRmsEps);
+                    k[i][j] *= rsqrtf(sk[j] * (1.0f / float(hd)) + kRmsEps);
+                }
+            }
+            if (a.rope) {
+                float oq[CPL], ok[CPL];
+                if (hd <= 64) {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) {
+                        oq[j] = __shfl_xor(q[i][j], half, 64);
+                        ok[j] = __shfl_xor(k[i][j], half, 64);
+                    }
+                } else {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) {
+                        oq[j] = q[i][(j + 1) % CPL];
+                        ok[j] = k[i][(j + 1) % CPL];
+                    }
+                }
+                const float2 *tr = a.table + size_t(pos) * half;
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    const int d = (lane + 64 * j) % hd;
+                    const float2 cs = tr[d < half ? d : d - half];
+                    q[i][j] = d < half ? q[i][j] * cs.x - oq[j] * cs.y : q[i][j] * cs.x + oq[j] * cs.y;
+                    k[i][j] = d < half ? k[i][j] * cs.x - ok[j] * cs.y : k[i][j] * cs.x + ok[j] * cs.y;
+                }
+            }
+        }
+        __syncthreads();  // the previous block's readers of keys and values are done
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (lane + 64 * j < W) {
+                    keys[(i * S + pos) * W + lane + 64 * j] = k[i][j];
+                    values[(i * S + pos) * W + lane + 64 * j] = v[i][j];
+                }
+        __syncthreads();
+        // Causal softmax attention over keys 0..pos per head (reference.rs:510-554),
+        // the maximum and sum carried along the keys.
+        float y[R][CPL], mx[R][CPL], sum[R][CPL];
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+                y[i][j] = sum[i][j] = 0.0f;
+                mx[i][j] = -INFINITY;
+            }
+        for (int t = 0; t <= pos; ++t) {
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+                const float *kr = keys + (i * S + t) * W, *vr = values + (i * S + t) * W;
+                float sv[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) sv[j] = lane + 64 * j < W ? q[i][j] * kr[lane + 64 * j] : 0.0f;
+                head_sums(sv, hd);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    // Scores in log2 units: exp is the hardware exp2 (relative
+                    // error ~1e-7 for the scores' range).
+                    const float sc = sv[j] * scale2, top = fmaxf(mx[i][j], sc);
+                    const float c = __builtin_amdgcn_exp2f(mx[i][j] - top), e = __builtin_amdgcn_exp2f(sc - top);
+                    sum[i][j] = fmaf(sum[i][j], c, e);
+                    y[i][j] = fmaf(y[i][j], c, e * (lane + 64 * j < W ? vr[lane + 64 * j] : 0.0f));
+                    mx[i][j] = top;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) y[i][j] /= sum[i][j];
+            // XSA against the row's own value (reference.rs:577-603).
+            if (a.xsa) {
+                float vv[CPL], yu[CPL];
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) vv[j] = v[i][j] * v[i][j];
+                head_sums(vv, hd);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    v[i][j] *= rsqrtf(fmaxf(vv[j], kXsaFloor));
+                    yu[j] = y[i][j] * v[i][j];
+                }
+                head_sums(yu, hd);
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) y[i][j] -= yu[j] * v[i][j];
+            }
+        }
+        wave_stack<CPL, R, BF>(y, wb + 3 * gA, a.A, m, lane);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[i][j] += y[i][j];
+        wave_rmsnorm(x, y, W);
+        wave_stack<CPL, R, BF>(y, wb + 4 * gA, a.F, m, lane);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x[i][j] += y[i][j];
+    }
+    // The tied head (reference.rs:218-226) on the final norm of the rows asked for.
+    if (!a.last_only || pos == S - 1) {
+        float nf[R][CPL];
+        wave_rmsnorm(x, nf, W);
+#pragma unroll
+        for (int i = 0; i < R; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j)
+                if (lane + 64 * j < W) finals[(i * S + pos) * W + lane + 64 * j] = nf[i][j];
+    }
+    __syncthreads();
+    // Every thread of the workgroup on (row, token) pairs, consecutive tokens
+    // on consecutive lanes: the reads of Et[c][t] are coalesced, the final
+    // rows' are LDS broadcasts.
+    const int first = a.last_only ? S - 1 : 0, per = S - first, n = valid * per * a.V;
+    float *lo = a.logits + size_t(s0) * per * a.V;
+    for (int e = threadIdx.x; e < n; e += blockDim.x) {
+        const int r = e / a.V, t = e - r * a.V, i = r / per;
+        const float *fr = finals + (i * S + first + r - i * per) * W;
+        float acc = 0.0f;
+        // The column's values 32 at a time, so that the loads overlap (32-bit
+        // offsets from the uniform base: Et holds under 2^31 floats); the
+        // terms still add in channel order.
+        for (int c0 = 0; c0 < W; c0 += 32) {
+            float ev[32];
+#pragma unroll
+            for (int u = 0; u < 32; ++u) ev[u] = c0 + u < W ? a.Et[unsigned((c0 + u) * a.vpad + t)] : 0.0f;
+#pragma unroll
+            for (int u = 0; u < 32; ++u)
+                if (c0 + u < W) acc = fmaf(fr[c0 + u], ev[u], acc);
+        }
+        lo[e] = acc;
+    }
+}
+
 }  // namespace
 
 // f(channels a lane, layers a launch holds) for the wave mesh kernels: 4, 8 or
@@ -1722,6 +1997,32 @@ void embedding_gradient(const float *dlogits, const float *n, const uint32_t *to
                              stream);
     const GradReduce red{partials, dE, splits, nvw};
     reduce_gradients(&red, 1, stream);
+}
+
+bool short_forward_fits(int W, int H, size_t V, int sequence) {
+    const int hd = W / H;
+    return mesh_wave_cpl(W) != 0 && sequence >= 1 && sequence <= kShortRows && hd >= 2 && (hd & (hd - 1)) == 0 &&
+           (hd <= 64 || hd == 128) && size_t(W) * (V + 3) < (size_t(1) << 31);
+}
+
+void short_forward(const ShortForward &a, int sequences, hipStream_t stream) {
+    // Sequences a workgroup holds: 4 up to 4 rows, 2 up to 8, else 1 (LDS at
+    // most 3 x 16 rows x 128 floats).
+    const int R = a.sequence <= 4 ? 4 : (a.sequence <= 8 ? 2 : 1);
+    const size_t lds = size_t(3) * R * a.sequence * a.W * sizeof(float);
+    const dim3 grid{unsigned((sequences + R - 1) / R)}, block{unsigned(64 * a.sequence)};
+    using Kernel = void (*)(ShortForward, int);
+    const bool one = mesh_wave_cpl(a.W) == 1;
+    Kernel kernel;
+    if (a.butterfly)
+        kernel = R == 4   ? (one ? short_forward_kernel<1, 4, true> : short_forward_kernel<2, 4, true>)
+                 : R == 2 ? (one ? short_forward_kernel<1, 2, true> : short_forward_kernel<2, 2, true>)
+                          : (one ? short_forward_kernel<1, 1, true> : short_forward_kernel<2, 1, true>);
+    else
+        kernel = R == 4   ? (one ? short_forward_kernel<1, 4, false> : short_forward_kernel<2, 4, false>)
+                 : R == 2 ? (one ? short_forward_kernel<1, 2, false> : short_forward_kernel<2, 2, false>)
+                          : (one ? short_forward_kernel<1, 1, false> : short_forward_kernel<2, 1, false>);
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, a, sequences);
 }
 
 void adam(float *params, float *m, float *v, const float *grad, size_t begin, size_t end, const AdamW &o,

@@ -170,6 +170,25 @@ size_t embedding_partial_floats(int rows, int W, int V);
 void embedding_gradient(const float *dlogits, const float *n, const uint32_t *tokens, const float *dx, float *dE,
                         float *partials, int rows, int W, int V, hipStream_t stream);
 
+// The forward of short sequences for inference (logits only): one workgroup
+// per sequence of at most kShortRows rows, one wave per row, W <= 128 and head
+// widths a power of two up to 64 (or 128); E the effective token vectors
+// (V x W), Et the same transposed, w the parameters with block 0's query group
+// at block0, table the RoPE (cos, sin) pairs [position][hd / 2].  logits: one
+// row per sequence (last_only) or per row.
+constexpr int kShortRows = 16;
+struct ShortForward {
+    const float *E, *Et, *w;  // Et: E transposed, [W][vpad]
+    const uint32_t *tokens;
+    const float2 *table;
+    float *logits;
+    size_t block0;
+    int W, H, L, A, F, V, vpad, sequence, butterfly, log2w, rope, qk_norm, xsa, last_only;
+    float scale;  // 1 / sqrt(W / H)
+};
+bool short_forward_fits(int W, int H, size_t V, int sequence);
+void short_forward(const ShortForward &a, int sequences, hipStream_t stream);
+
 struct AdamW {
     float learning_rate, weight_decay, beta1, beta2, epsilon;
 };

@@ -381,3 +381,31 @@ def test_mshgpt09_ablations_match_oracle(kw):
         for b in range(2):
             assert_close(last[b], O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], what=f"decode seq {b}")
             check_trajectory(o, params, prompts[b], got[b], 0.0, 3 + b, _device_last(model))
+
+
+# The one-launch forward of sequences of up to 16 rows (a workgroup holds 4, 2
+# or 1 of them by length, and the count need not divide by it): lengths across
+# those cases, ragged counts, head widths 2 to 128, both connectivities and
+# embeddings, all-row and last-row logits, a vocabulary beyond the workgroup.
+SHORT = [
+    (dict(vocab_size=11, context=16, width=128, heads=1, layers=2, attention_mesh_depth=3, ffn_mesh_depth=2),
+     (1, 4, 5, 8, 9, 16)),
+    (dict(vocab_size=67, context=16, width=64, heads=1, layers=1, attention_mesh_depth=2, ffn_mesh_depth=3,
+          connectivity=1), (2, 7, 12)),
+    (dict(vocab_size=300, context=16, width=16, heads=8, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2,
+          embedding=1), (3, 6, 16)),
+]
+
+
+@pytest.mark.parametrize("cfg,lengths", SHORT, ids=[_ids(c) for c, _ in SHORT])
+def test_short_sequence_forward_matches_oracle(cfg, lengths):
+    g, o = configs_for(**cfg)
+    params = O.initialize(o, 5)
+    with G.MeshGpt(0, g, 5) as model:
+        for n in lengths:
+            for batch in (1, 3, 7):
+                x = G.random_prompts(cfg["vocab_size"], batch, n, n + batch).reshape(-1)
+                expected = O.logits(o, params, x, n)
+                assert_close(model.logits(x, n), expected, what=f"logits batch={batch} n={n}")
+                assert_close(model.logits(x, n, last_only=True), expected.reshape(batch, n, -1)[:, -1],
+                             what=f"last-row logits batch={batch} n={n}")
