@@ -1325,12 +1325,13 @@ void by_head_width(int hd, F &&f) {
 // lane + 64 j in register j); the rows stay in registers through every block,
 // the sequences' keys and values meet in LDS, and only the logits leave.
 
-// ELU (reference.rs:325-332) with exp(z) - 1 from the hardware exp2 on the
-// negative branch: its absolute error (~1e-7 near 0) is one f32 rounding of the
-// row values, far below the logit tolerance, where the library expm1 is a long
-// dependent chain on every mesh layer.
+// ELU (reference.rs:325-332) as the median of z, u = exp(z) - 1 and 0: for
+// z < 0, z < u < 0; for z >= 0, 0 <= z <= u (both up to u's rounding).  u comes
+// from the hardware exp2, so the result is off by at most ~1e-7 (one rounding
+// of 1 + u) near 0, far below the logit tolerance, where the library expm1 and
+// a branch select cost several instructions more on every mesh layer.
 __device__ __forceinline__ float elu_exp2(float z) {
-    return z >= 0.0f ? z : __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f;
+    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
 }
 
 // Sum over the aligned groups of hd lanes (hd a power of two up to 64), or over
