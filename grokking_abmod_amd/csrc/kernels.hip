@@ -111,12 +111,14 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
-// ELU of reference.rs:325-332.  The negative branch is exp(z) - 1 from the
-// hardware exp2: its absolute error (~1e-7 for z near 0) is that of one f32
-// rounding of the row values, far below the logit tolerance; the library
-// expm1 costs a long dependent chain on every mesh layer.
+// ELU of reference.rs:325-332 as the median of z, u = exp(z) - 1 and 0: for
+// z < 0, z < u < 0; for z >= 0, 0 <= z <= u (both up to u's rounding).  u comes
+// from the hardware exp2: the absolute error (~1e-7 for z near 0) is that of
+// one f32 rounding of the row values, far below the logit tolerance, where the
+// library expm1 and a branch select cost several instructions more on every
+// mesh layer.
 __device__ __forceinline__ float elu(float z) {
-    return z >= 0.0f ? z : __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f;
+    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
 }
 
 // Flat LDS index -> (row, column) for rows of length W.

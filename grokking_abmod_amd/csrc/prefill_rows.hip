@@ -29,7 +29,8 @@ constexpr float kEps = 1e-5f;  // src/gpt/mod.rs:38
 constexpr float kXsaNormFloor = float(double(1e-12f) * double(1e-12f));
 
 __device__ __forceinline__ float elu_f(float z) {
-    return z >= 0.0f ? z : __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f;
+    // the median of z, exp(z) - 1 and 0 (kernels.hip's elu)
+    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
 }
 
 template <int W>
