@@ -1334,11 +1334,34 @@ __device__ __forceinline__ float elu_exp2(float z) {
     return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
 }
 
-// Sum over the aligned groups of hd lanes (hd a power of two up to 64), or over
-// both registers and the wave when hd = 128: every lane of a head gets its sum
-// (DPP moves within 16-lane rows, lane shuffles across them).
-template <int CPL>
+// The channel of a lane's register j: lane + 64 j, or 2 lane + j when IL (the
+// interleaved order of width 128 with neighbour connectivity: channel c + 1 of
+// register 0 is register 1 of the same lane, that of register 1 is register 0
+// one lane up, wrapping at lane 63 to channel 0, so the mesh shift needs no
+// select).
+template <bool IL>
+__device__ __forceinline__ int short_channel(int lane, int j) { return IL ? 2 * lane + j : lane + 64 * j; }
+
+// Sum over the channels of each head of hd channels, left in all of them: the
+// aligned groups of hd lanes (hd a power of two up to 64), or both registers
+// and the wave when hd = 128; when IL, both registers of hd / 2 lanes (DPP
+// moves within 16-lane rows, lane shuffles across them).
+template <bool IL, int CPL>
 __device__ __forceinline__ void head_sums(float (&v)[CPL], int hd) {
+    if constexpr (IL) {
+        float t = v[0] + v[1];
+        switch (hd) {
+            case 2: break;
+            case 4: t = group_sum<2>(t); break;
+            case 8: t = group_sum<4>(t); break;
+            case 16: t = group_sum<8>(t); break;
+            case 32: t = group_sum<16>(t); break;
+            case 64: t = group_sum<32>(t); break;
+            default: t = wave_sum(t); break;
+        }
+        v[0] = v[1] = t;
+        return;
+    }
     if (hd > 64) {
         float t = 0.0f;
 #pragma unroll
@@ -1366,30 +1389,37 @@ __device__ __forceinline__ void head_sums(float (&v)[CPL], int hd) {
 // BF: butterfly strides (a lane exchange per distance), else neighbour
 // connectivity, whose constant stride keeps the code small enough for the
 // instruction cache.
-template <int CPL, int R, bool BF>
+template <int CPL, int R, bool BF, bool IL>
 __device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__restrict__ w, int depth,
                                            const Mesh &m, int lane) {
     const int W = m.W;
     float2 cur[CPL], nxt[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        cur[j] = lane + 64 * j < W ? reinterpret_cast<const float2 *>(w)[lane + 64 * j] : make_float2(0.0f, 0.0f);
+        const int c = short_channel<IL>(lane, j);
+        cur[j] = c < W ? reinterpret_cast<const float2 *>(w)[c] : make_float2(0.0f, 0.0f);
         nxt[j] = cur[j];
     }
 #pragma nounroll
     for (int l = 0; l < depth; ++l) {
         if (l + 1 < depth) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j)
-                nxt[j] = lane + 64 * j < W ? reinterpret_cast<const float2 *>(w + size_t(l + 1) * 2 * W)[lane + 64 * j]
-                                           : make_float2(0.0f, 0.0f);
+            for (int j = 0; j < CPL; ++j) {
+                const int c = short_channel<IL>(lane, j);
+                nxt[j] = c < W ? reinterpret_cast<const float2 *>(w + size_t(l + 1) * 2 * W)[c] : make_float2(0.0f, 0.0f);
+            }
         }
         const int d = BF ? 1 << (l % m.log2w) : 1;
         const bool last = l + 1 == depth;
 #pragma unroll
         for (int i = 0; i < R; ++i) {
             float p[CPL];
-            channel_shift(x[i], d, W, lane, p);
+            if constexpr (IL) {
+                p[0] = x[i][1];
+                p[1] = lanes_rol1(x[i][0]);
+            } else {
+                channel_shift(x[i], d, W, lane, p);
+            }
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const float z = x[i][j] * cur[j].x + p[j] * cur[j].y;
@@ -1422,6 +1452,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
     const int W = a.W, lane = threadIdx.x & 63, pos = threadIdx.x >> 6, S = a.sequence;
     const int hd = W / a.H, half = hd / 2, slab = R * S * W;
     const float scale2 = a.scale * 1.4426950408889634f;
+    constexpr bool IL = CPL == 2 && !BF;
     float *keys = lds, *values = lds + slab, *finals = lds + 2 * slab;
     const Mesh m{W, 0, a.butterfly, a.log2w};
     // Sequence i of the workgroup; past the last one a workgroup recomputes the
@@ -1432,7 +1463,10 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
     for (int i = 0; i < R; ++i) {
         const uint32_t tok = a.tokens[size_t(s0 + min(i, valid - 1)) * S + pos];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) x[i][j] = lane + 64 * j < W ? a.E[size_t(tok) * W + lane + 64 * j] : 0.0f;
+        for (int j = 0; j < CPL; ++j) {
+            const int c = short_channel<IL>(lane, j);
+            x[i][j] = c < W ? a.E[size_t(tok) * W + c] : 0.0f;
+        }
     }
     const size_t gA = 2 * size_t(W) * a.A, gF = 2 * size_t(W) * a.F;
     for (int b = 0; b < a.L; ++b) {
@@ -1443,9 +1477,9 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j) k[i][j] = v[i][j] = q[i][j];
-        wave_stack<CPL, R, BF>(q, wb, a.A, m, lane);
-        wave_stack<CPL, R, BF>(k, wb + gA, a.A, m, lane);
-        wave_stack<CPL, R, BF>(v, wb + 2 * gA, a.A, m, lane);
+        wave_stack<CPL, R, BF, IL>(q, wb, a.A, m, lane);
+        wave_stack<CPL, R, BF, IL>(k, wb + gA, a.A, m, lane);
+        wave_stack<CPL, R, BF, IL>(v, wb + 2 * gA, a.A, m, lane);
         // QK-Norm, then slice RoPE at this row's position (reference.rs:174-193).
 #pragma unroll
         for (int i = 0; i < R; ++i) {
@@ -1456,8 +1490,8 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                     sq[j] = q[i][j] * q[i][j];
                     sk[j] = k[i][j] * k[i][j];
                 }
-                head_sums(sq, hd);
-                head_sums(sk, hd);
+                head_sums<IL>(sq, hd);
+                head_sums<IL>(sk, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     q[i][j] *= rsqrtf(sq[j] * (1.0f / float(hd)) + kRmsEps);
@@ -1466,7 +1500,19 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
             }
             if (a.rope) {
                 float oq[CPL], ok[CPL];
-                if (hd <= 64) {
+                if (IL && half == 1) {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) {
+                        oq[j] = q[i][(j + 1) % CPL];
+                        ok[j] = k[i][(j + 1) % CPL];
+                    }
+                } else if (IL) {
+#pragma unroll
+                    for (int j = 0; j < CPL; ++j) {
+                        oq[j] = __shfl_xor(q[i][j], half / 2, 64);
+                        ok[j] = __shfl_xor(k[i][j], half / 2, 64);
+                    }
+                } else if (hd <= 64) {
 #pragma unroll
                     for (int j = 0; j < CPL; ++j) {
                         oq[j] = __shfl_xor(q[i][j], half, 64);
@@ -1482,7 +1528,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 const float2 *tr = a.table + size_t(pos) * half;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
-                    const int d = (lane + 64 * j) % hd;
+                    const int d = short_channel<IL>(lane, j) % hd;
                     const float2 cs = tr[d < half ? d : d - half];
                     q[i][j] = d < half ? q[i][j] * cs.x - oq[j] * cs.y : q[i][j] * cs.x + oq[j] * cs.y;
                     k[i][j] = d < half ? k[i][j] * cs.x - ok[j] * cs.y : k[i][j] * cs.x + ok[j] * cs.y;
@@ -1494,9 +1540,9 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
-                if (lane + 64 * j < W) {
-                    keys[(i * S + pos) * W + lane + 64 * j] = k[i][j];
-                    values[(i * S + pos) * W + lane + 64 * j] = v[i][j];
+                if (short_channel<IL>(lane, j) < W) {
+                    keys[(i * S + pos) * W + short_channel<IL>(lane, j)] = k[i][j];
+                    values[(i * S + pos) * W + short_channel<IL>(lane, j)] = v[i][j];
                 }
         __syncthreads();
         // Causal softmax attention over keys 0..pos per head (reference.rs:510-554),
@@ -1515,8 +1561,8 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 const float *kr = keys + (i * S + t) * W, *vr = values + (i * S + t) * W;
                 float sv[CPL];
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) sv[j] = lane + 64 * j < W ? q[i][j] * kr[lane + 64 * j] : 0.0f;
-                head_sums(sv, hd);
+                for (int j = 0; j < CPL; ++j) sv[j] = short_channel<IL>(lane, j) < W ? q[i][j] * kr[short_channel<IL>(lane, j)] : 0.0f;
+                head_sums<IL>(sv, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     // Scores in log2 units: exp is the hardware exp2 (relative
@@ -1524,7 +1570,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                     const float sc = sv[j] * scale2, top = fmaxf(mx[i][j], sc);
                     const float c = __builtin_amdgcn_exp2f(mx[i][j] - top), e = __builtin_amdgcn_exp2f(sc - top);
                     sum[i][j] = fmaf(sum[i][j], c, e);
-                    y[i][j] = fmaf(y[i][j], c, e * (lane + 64 * j < W ? vr[lane + 64 * j] : 0.0f));
+                    y[i][j] = fmaf(y[i][j], c, e * (short_channel<IL>(lane, j) < W ? vr[short_channel<IL>(lane, j)] : 0.0f));
                     mx[i][j] = top;
                 }
             }
@@ -1538,24 +1584,24 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 float vv[CPL], yu[CPL];
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) vv[j] = v[i][j] * v[i][j];
-                head_sums(vv, hd);
+                head_sums<IL>(vv, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     v[i][j] *= rsqrtf(fmaxf(vv[j], kXsaFloor));
                     yu[j] = y[i][j] * v[i][j];
                 }
-                head_sums(yu, hd);
+                head_sums<IL>(yu, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) y[i][j] -= yu[j] * v[i][j];
             }
         }
-        wave_stack<CPL, R, BF>(y, wb + 3 * gA, a.A, m, lane);
+        wave_stack<CPL, R, BF, IL>(y, wb + 3 * gA, a.A, m, lane);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j) x[i][j] += y[i][j];
         wave_rmsnorm(x, y, W);
-        wave_stack<CPL, R, BF>(y, wb + 4 * gA, a.F, m, lane);
+        wave_stack<CPL, R, BF, IL>(y, wb + 4 * gA, a.F, m, lane);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
@@ -1569,7 +1615,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
-                if (lane + 64 * j < W) finals[(i * S + pos) * W + lane + 64 * j] = nf[i][j];
+                if (short_channel<IL>(lane, j) < W) finals[(i * S + pos) * W + short_channel<IL>(lane, j)] = nf[i][j];
     }
     __syncthreads();
     // Every thread of the workgroup on (row, token) pairs, consecutive tokens

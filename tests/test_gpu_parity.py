@@ -394,6 +394,16 @@ SHORT = [
           connectivity=1), (2, 7, 12)),
     (dict(vocab_size=300, context=16, width=16, heads=8, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2,
           embedding=1), (3, 6, 16)),
+    # width 128 with neighbour connectivity keeps channels interleaved (2 lane + j):
+    # head widths 2, 4, 16 and 64 and the ablation switches there
+    (dict(vocab_size=13, context=16, width=128, heads=2, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          qk_norm=0), (3, 6)),
+    (dict(vocab_size=13, context=16, width=128, heads=32, layers=1, attention_mesh_depth=2, ffn_mesh_depth=2,
+          xsa=0), (4, 11)),
+    (dict(vocab_size=13, context=16, width=128, heads=64, layers=1, attention_mesh_depth=1, ffn_mesh_depth=2),
+     (2, 16)),
+    (dict(vocab_size=13, context=16, width=128, heads=8, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2,
+          rope=0), (4,)),
 ]
 
 
