@@ -1321,9 +1321,9 @@ void by_head_width(int hd, F &&f) {
 }
 
 // ---- the forward of short sequences: a workgroup holds R sequences, one wave
-// per position holding that position's row of each (W <= 128, channel
-// lane + 64 j in register j); the rows stay in registers through every block,
-// the sequences' keys and values meet in LDS, and only the logits leave.
+// per position holding that position's row of each (W <= 128, the channel of
+// register j given by short_channel); the rows stay in registers through every
+// block, the sequences' keys and values meet in LDS, and only the logits leave.
 
 // ELU (reference.rs:325-332) as the median of z, u = exp(z) - 1 and 0: for
 // z < 0, z < u < 0; for z >= 0, 0 <= z <= u (both up to u's rounding).  u comes
