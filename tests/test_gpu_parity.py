@@ -404,6 +404,11 @@ SHORT = [
      (2, 16)),
     (dict(vocab_size=13, context=16, width=128, heads=8, layers=2, attention_mesh_depth=2, ffn_mesh_depth=2,
           rope=0), (4,)),
+    # butterfly strides at widths 128 and 32 (lane exchanges, channel lane + 64 j)
+    (dict(vocab_size=13, context=16, width=128, heads=4, layers=2, attention_mesh_depth=9, ffn_mesh_depth=3,
+          connectivity=1), (1, 6, 13)),
+    (dict(vocab_size=13, context=16, width=32, heads=2, layers=1, attention_mesh_depth=6, ffn_mesh_depth=2,
+          connectivity=1, embedding=1), (4, 16)),
 ]
 
 
