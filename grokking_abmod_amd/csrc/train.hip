@@ -1342,6 +1342,11 @@ __device__ __forceinline__ float elu_exp2(float z) {
 template <bool IL>
 __device__ __forceinline__ int short_channel(int lane, int j) { return IL ? 2 * lane + j : lane + 64 * j; }
 
+// Whether channel c holds a value: always at width 128 (two registers a lane),
+// below W at the widths of one register.
+template <int CPL>
+__device__ __forceinline__ bool short_live(int c, int W) { return CPL == 2 || c < W; }
+
 // Sum over the channels of each head of hd channels, left in all of them: the
 // aligned groups of hd lanes (hd a power of two up to 64), or both registers
 // and the wave when hd = 128; when IL, both registers of hd / 2 lanes (DPP
@@ -1397,7 +1402,7 @@ __device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__re
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const int c = short_channel<IL>(lane, j);
-        cur[j] = c < W ? reinterpret_cast<const float2 *>(w)[c] : make_float2(0.0f, 0.0f);
+        cur[j] = short_live<CPL>(c, W) ? reinterpret_cast<const float2 *>(w)[c] : make_float2(0.0f, 0.0f);
         nxt[j] = cur[j];
     }
 #pragma nounroll
@@ -1406,7 +1411,7 @@ __device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__re
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const int c = short_channel<IL>(lane, j);
-                nxt[j] = c < W ? reinterpret_cast<const float2 *>(w + size_t(l + 1) * 2 * W)[c] : make_float2(0.0f, 0.0f);
+                nxt[j] = short_live<CPL>(c, W) ? reinterpret_cast<const float2 *>(w + size_t(l + 1) * 2 * W)[c] : make_float2(0.0f, 0.0f);
             }
         }
         const int d = BF ? 1 << (l % m.log2w) : 1;
@@ -1465,7 +1470,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
             const int c = short_channel<IL>(lane, j);
-            x[i][j] = c < W ? a.E[size_t(tok) * W + c] : 0.0f;
+            x[i][j] = short_live<CPL>(c, W) ? a.E[size_t(tok) * W + c] : 0.0f;
         }
     }
     const size_t gA = 2 * size_t(W) * a.A, gF = 2 * size_t(W) * a.F;
@@ -1540,7 +1545,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
-                if (short_channel<IL>(lane, j) < W) {
+                if (short_live<CPL>(short_channel<IL>(lane, j), W)) {
                     keys[(i * S + pos) * W + short_channel<IL>(lane, j)] = k[i][j];
                     values[(i * S + pos) * W + short_channel<IL>(lane, j)] = v[i][j];
                 }
@@ -1561,7 +1566,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 const float *kr = keys + (i * S + t) * W, *vr = values + (i * S + t) * W;
                 float sv[CPL];
 #pragma unroll
-                for (int j = 0; j < CPL; ++j) sv[j] = short_channel<IL>(lane, j) < W ? q[i][j] * kr[short_channel<IL>(lane, j)] : 0.0f;
+                for (int j = 0; j < CPL; ++j) sv[j] = short_live<CPL>(short_channel<IL>(lane, j), W) ? q[i][j] * kr[short_channel<IL>(lane, j)] : 0.0f;
                 head_sums<IL>(sv, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
@@ -1570,7 +1575,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                     const float sc = sv[j] * scale2, top = fmaxf(mx[i][j], sc);
                     const float c = __builtin_amdgcn_exp2f(mx[i][j] - top), e = __builtin_amdgcn_exp2f(sc - top);
                     sum[i][j] = fmaf(sum[i][j], c, e);
-                    y[i][j] = fmaf(y[i][j], c, e * (short_channel<IL>(lane, j) < W ? vr[short_channel<IL>(lane, j)] : 0.0f));
+                    y[i][j] = fmaf(y[i][j], c, e * (short_live<CPL>(short_channel<IL>(lane, j), W) ? vr[short_channel<IL>(lane, j)] : 0.0f));
                     mx[i][j] = top;
                 }
             }
@@ -1615,7 +1620,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j)
-                if (short_channel<IL>(lane, j) < W) finals[(i * S + pos) * W + short_channel<IL>(lane, j)] = nf[i][j];
+                if (short_live<CPL>(short_channel<IL>(lane, j), W)) finals[(i * S + pos) * W + short_channel<IL>(lane, j)] = nf[i][j];
     }
     __syncthreads();
     // Every thread of the workgroup on (row, token) pairs, consecutive tokens
