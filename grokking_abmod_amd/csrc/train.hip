@@ -1635,13 +1635,15 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         // The column's values 32 at a time, so that the loads overlap (32-bit
         // offsets from the uniform base: Et holds under 2^31 floats); the
         // terms still add in channel order.
-        for (int c0 = 0; c0 < W; c0 += 32) {
+        const int wc = CPL == 2 ? 128 : W;  // a compile-time bound at width 128
+        for (int c0 = 0; c0 < wc; c0 += 32) {
             float ev[32];
 #pragma unroll
-            for (int u = 0; u < 32; ++u) ev[u] = c0 + u < W ? a.Et[unsigned((c0 + u) * a.vpad + t)] : 0.0f;
+            for (int u = 0; u < 32; ++u)
+                ev[u] = short_live<CPL>(c0 + u, wc) ? a.Et[unsigned((c0 + u) * a.vpad + t)] : 0.0f;
 #pragma unroll
             for (int u = 0; u < 32; ++u)
-                if (c0 + u < W) acc = fmaf(fr[c0 + u], ev[u], acc);
+                if (short_live<CPL>(c0 + u, wc)) acc = fmaf(fr[c0 + u], ev[u], acc);
         }
         lo[e] = acc;
     }
