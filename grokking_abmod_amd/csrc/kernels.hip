@@ -111,14 +111,21 @@ __device__ __forceinline__ float group_max(float v) {
     return v;
 }
 
-// ELU of reference.rs:325-332 as the median of z, u = exp(z) - 1 and 0: for
-// z < 0, z < u < 0; for z >= 0, 0 <= z <= u (both up to u's rounding).  u comes
-// from the hardware exp2: the absolute error (~1e-7 for z near 0) is that of
-// one f32 rounding of the row values, far below the logit tolerance, where the
-// library expm1 and a branch select cost several instructions more on every
-// mesh layer.
+// ELU of reference.rs:325-332: max(z, e - 1) with e = exp(z) clamped to
+// [0, 1].  For z >= 0, e = 1 and the maximum is z; for z < 0, e - 1 =
+// exp(z) - 1 lies above z (exp(z) >= 1 + z), so it is the maximum.  e comes
+// from the hardware exp2 with its clamp modifier: the absolute error (~1e-7
+// for z near 0) is that of one f32 rounding of the row values, far below the
+// logit tolerance, where the library expm1 and a branch select cost several
+// instructions more on every mesh layer.  The maximum is IEEE 754-2019's
+// (v_maximum3_f32), which returns NaN when an operand is NaN: a NaN z stays NaN
+// as in the reference (NaN >= 0 is false and exp_m1(NaN) is NaN), while the
+// clamp turns exp2(NaN) into 0 and the older maxNum or med3 forms would have
+// returned the other operand.  z = +inf gives e = 1 and +inf; z = -inf gives
+// e = 0 and -1, both as the reference.
 __device__ __forceinline__ float elu(float z) {
-    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
+    const float e = __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(z * 1.4426950408889634f), 0.0f, 1.0f);
+    return __builtin_elementwise_maximum(z, e - 1.0f);
 }
 
 // Flat LDS index -> (row, column) for rows of length W.
@@ -3690,7 +3697,7 @@ persistent_decode_kernel(PersistArgs a) {
         else
             persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc);
     };
-    if (persistent_handshake(a, far, r))
+    if (!a.agent_scope && persistent_handshake(a, far, r))
         run(PersistXch<true>(a, b, trow));
     else
         run(far);

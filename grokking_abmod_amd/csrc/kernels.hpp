@@ -157,6 +157,11 @@ struct PersistArgs {
     int *abort;           // zero at launch; set when a wait times out
     float scale_log2;     // set by persistent_decode
     int xcd_cus;          // CUs per XCD, set by persistent_decode
+    // Nonzero: every sequence's hand-offs use the agent-scope atomics, as when
+    // its workgroups run on different XCDs, instead of the XCD-local words the
+    // launch's handshake otherwise chooses where it can (for testing that
+    // protocol; MG_PERSIST_AGENT_SCOPE=1).
+    int agent_scope;
     // Optional timeline (nullptr: none): for block k, step t and phase l,
     // trace[((k * steps + t) * (layers + 1) + l) * 2 + {0, 1}] receive the
     // wall clock (100 MHz) when the phase's inputs were ready and when its

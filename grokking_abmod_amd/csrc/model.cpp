@@ -1225,6 +1225,7 @@ struct MeshGpt::Impl {
         a.xstride = xstride;
         a.abort = pabort.as<int>();
         a.trace = trace;
+        a.agent_scope = env_int("MG_PERSIST_AGENT_SCOPE", 0) != 0;
         check(kern::persistent_decode(a, stream), "persistent decode launch");
         sync();
         int aborted = 0;
@@ -1467,12 +1468,21 @@ void sample_logits_noalloc(int device, const float *logits, size_t rows, size_t 
     int count = 0;
     check(hipGetDeviceCount(&count), "hipGetDeviceCount");
     if (device < 0 || device >= count) throw Error("invalid device ordinal", kDeviceError);
+    // The caller's current device is restored on return, also on an error.
+    int caller = 0;
+    check(hipGetDevice(&caller), "hipGetDevice");
+    struct Restore {
+        int device;
+        ~Restore() { (void)hipSetDevice(device); }
+    } restore{caller};
     check(hipSetDevice(device), "hipSetDevice");
     int *counters = nullptr;
     check(kern::noalloc_scratch(device, &counters), "hipGetSymbolAddress(scratch)");
     kern::fill_int(nonfinite, 0, 1, stream);
-    if (rows == 0) return check(hipGetLastError(), "fill launch");
+    check(hipGetLastError(), "flag clear launch");
+    if (rows == 0) return;
     kern::fill_int(counters, 0, int(rows), stream);
+    check(hipGetLastError(), "counter clear launch");
     kern::sample(int(vocab), int(rows), logits, temperature, rng_states, tokens, 1, counters, nonfinite, stream);
     check(hipGetLastError(), "sample launch");
 }

@@ -46,7 +46,6 @@ void fill_int(int *p, int value, int n, hipStream_t stream) {
     if (n <= 0) return;
     const int blocks = (n + 255) / 256 < 1024 ? (n + 255) / 256 : 1024;
     hipLaunchKernelGGL(fill_int_kernel, dim3(blocks), dim3(256), 0, stream, p, value, n);
-    (void)hipGetLastError();
 }
 
 }  // namespace meshgpt::kern

@@ -29,8 +29,10 @@ constexpr float kEps = 1e-5f;  // src/gpt/mod.rs:38
 constexpr float kXsaNormFloor = float(double(1e-12f) * double(1e-12f));
 
 __device__ __forceinline__ float elu_f(float z) {
-    // the median of z, exp(z) - 1 and 0 (kernels.hip's elu)
-    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
+    // max(z, clamp(exp(z), 0, 1) - 1) with the NaN-propagating maximum, which
+    // keeps a NaN z NaN (kernels.hip's elu)
+    const float e = __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(z * 1.4426950408889634f), 0.0f, 1.0f);
+    return __builtin_elementwise_maximum(z, e - 1.0f);
 }
 
 template <int W>

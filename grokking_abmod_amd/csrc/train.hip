@@ -1325,13 +1325,24 @@ void by_head_width(int hd, F &&f) {
 // register j given by short_channel); the rows stay in registers through every
 // block, the sequences' keys and values meet in LDS, and only the logits leave.
 
-// ELU (reference.rs:325-332) as the median of z, u = exp(z) - 1 and 0: for
-// z < 0, z < u < 0; for z >= 0, 0 <= z <= u (both up to u's rounding).  u comes
-// from the hardware exp2, so the result is off by at most ~1e-7 (one rounding
-// of 1 + u) near 0, far below the logit tolerance, where the library expm1 and
-// a branch select cost several instructions more on every mesh layer.
-__device__ __forceinline__ float elu_exp2(float z) {
-    return __builtin_amdgcn_fmed3f(z, __builtin_amdgcn_exp2f(z * 1.4426950408889634f) - 1.0f, 0.0f);
+// The short forward carries every mesh value scaled by K = log2(e): a layer
+// computes t = K z directly from scaled inputs (the mesh is linear in its
+// input up to the ELU), and the ELU in those units is
+//   K ELU(t / K) = max(t, K (clamp(exp2(t), 0, 1) - 1))
+// (reference.rs:325-332): for t >= 0 the clamped exp2 is 1 and the maximum is
+// t; for t < 0, K (2^t - 1) = K (exp(z) - 1) lies above t.  That is one
+// multiply fewer per value than exp2(z K) on unscaled values.  The maximum is
+// IEEE 754-2019's (v_maximum3_f32), which returns NaN when an operand is NaN,
+// so a NaN stays NaN as in the reference (the clamp maps exp2(NaN) to 0, and a
+// maxNum or med3 form would return the other operand); t = +inf stays +inf and
+// t = -inf gives -K, K ELU(-inf).  The hardware exp2's absolute error (~1e-7)
+// is far below the logit tolerance.  The scale enters with the RMSNorm
+// factors in front of the meshes, and leaves in the residual adds, the QK-Norm
+// epsilon (K^2 eps on K-scaled rows) and the XSA floor.
+constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float elu_log2(float t) {
+    const float e = __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(t), 0.0f, 1.0f);
+    return __builtin_elementwise_maximum(t, __builtin_fmaf(e, kLog2e, -kLog2e));
 }
 
 // The channel of a lane's register j: lane + 64 j, or 2 lane + j when IL (the
@@ -1389,8 +1400,9 @@ __device__ __forceinline__ void head_sums(float (&v)[CPL], int hd) {
     }
 }
 
-// One mesh stack (reference.rs:422-453) on the wave's R rows, in place: layer l
-// reads its weights at w + l * 2W, the next layer's loading during this one.
+// One mesh stack (reference.rs:422-453) on the wave's R rows (log2(e)-scaled,
+// elu_log2), in place: layer l reads its weights at w + l * 2W, the next
+// layer's loading during this one.
 // BF: butterfly strides (a lane exchange per distance), else neighbour
 // connectivity, whose constant stride keeps the code small enough for the
 // instruction cache.
@@ -1428,7 +1440,7 @@ __device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__re
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const float z = x[i][j] * cur[j].x + p[j] * cur[j].y;
-                x[i][j] = last ? z : elu_exp2(z);
+                x[i][j] = last ? z : elu_log2(z);
             }
         }
 #pragma unroll
@@ -1436,15 +1448,15 @@ __device__ __forceinline__ void wave_stack(float (&x)[R][CPL], const float *__re
     }
 }
 
-// RMSNorm of each of the wave's rows (reference.rs:392-409).
+// RMSNorm of each of the wave's rows (reference.rs:392-409), times `scale`.
 template <int CPL, int R>
-__device__ __forceinline__ void wave_rmsnorm(const float (&x)[R][CPL], float (&n)[R][CPL], int W) {
+__device__ __forceinline__ void wave_rmsnorm(const float (&x)[R][CPL], float (&n)[R][CPL], int W, float scale) {
 #pragma unroll
     for (int i = 0; i < R; ++i) {
         float acc = 0.0f;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) acc = fmaf(x[i][j], x[i][j], acc);
-        const float iv = rsqrtf(wave_sum(acc) * (1.0f / float(W)) + kRmsEps);
+        const float iv = rsqrtf(wave_sum(acc) * (1.0f / float(W)) + kRmsEps) * scale;
 #pragma unroll
         for (int j = 0; j < CPL; ++j) n[i][j] = x[i][j] * iv;
     }
@@ -1474,15 +1486,23 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
         }
     }
     const size_t gA = 2 * size_t(W) * a.A, gF = 2 * size_t(W) * a.F;
+    // QK-Norm of K-scaled rows q' = K q: q' / sqrt(mean(q'^2) + K^2 eps) is
+    // q / sqrt(mean(q^2) + eps).
+    const float qk_eps = kRmsEps * kLog2e * kLog2e;
     for (int b = 0; b < a.L; ++b) {
         const float *wb = a.w + a.block0 + size_t(b) * (4 * gA + gF);
+        // With last_only, rows before a sequence's last reach the head only
+        // through their keys and values in the last block: those waves run its
+        // K and V meshes and skip the rest (wave-uniform; every barrier is
+        // still reached).
+        const bool tail = a.last_only && b + 1 == a.L && pos + 1 < S;
         float q[R][CPL], k[R][CPL], v[R][CPL];
-        wave_rmsnorm(x, q, W);
+        wave_rmsnorm(x, q, W, kLog2e);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
             for (int j = 0; j < CPL; ++j) k[i][j] = v[i][j] = q[i][j];
-        wave_stack<CPL, R, BF, IL>(q, wb, a.A, m, lane);
+        if (!tail) wave_stack<CPL, R, BF, IL>(q, wb, a.A, m, lane);
         wave_stack<CPL, R, BF, IL>(k, wb + gA, a.A, m, lane);
         wave_stack<CPL, R, BF, IL>(v, wb + 2 * gA, a.A, m, lane);
         // QK-Norm, then slice RoPE at this row's position (reference.rs:174-193).
@@ -1495,12 +1515,18 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                     sq[j] = q[i][j] * q[i][j];
                     sk[j] = k[i][j] * k[i][j];
                 }
-                head_sums<IL>(sq, hd);
+                if (!tail) head_sums<IL>(sq, hd);
                 head_sums<IL>(sk, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
-                    q[i][j] *= rsqrtf(sq[j] * (1.0f / float(hd)) + kRmsEps);
-                    k[i][j] *= rsqrtf(sk[j] * (1.0f / float(hd)) + kRmsEps);
+                    q[i][j] *= rsqrtf(sq[j] * (1.0f / float(hd)) + qk_eps);
+                    k[i][j] *= rsqrtf(sk[j] * (1.0f / float(hd)) + qk_eps);
+                }
+            } else {
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) {
+                    q[i][j] *= kLn2;
+                    k[i][j] *= kLn2;
                 }
             }
             if (a.rope) {
@@ -1550,6 +1576,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                     values[(i * S + pos) * W + short_channel<IL>(lane, j)] = v[i][j];
                 }
         __syncthreads();
+        if (tail) continue;
         // Causal softmax attention over keys 0..pos per head (reference.rs:510-554),
         // the maximum and sum carried along the keys.
         float y[R][CPL], mx[R][CPL], sum[R][CPL];
@@ -1580,11 +1607,14 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 }
             }
         }
+        // The values are K-scaled, so y and the XSA output are too: the
+        // projection mesh takes them as they are.
 #pragma unroll
         for (int i = 0; i < R; ++i) {
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) y[i][j] /= sum[i][j];
-            // XSA against the row's own value (reference.rs:577-603).
+            for (int j = 0; j < CPL; ++j) y[i][j] *= __builtin_amdgcn_rcpf(sum[i][j]);
+            // XSA against the row's own value (reference.rs:577-603); the norm
+            // floor max(|v|, 1e-12) scales with v.
             if (a.xsa) {
                 float vv[CPL], yu[CPL];
 #pragma unroll
@@ -1592,7 +1622,7 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 head_sums<IL>(vv, hd);
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
-                    v[i][j] *= rsqrtf(fmaxf(vv[j], kXsaFloor));
+                    v[i][j] *= rsqrtf(fmaxf(vv[j], kXsaFloor * (kLog2e * kLog2e)));
                     yu[j] = y[i][j] * v[i][j];
                 }
                 head_sums<IL>(yu, hd);
@@ -1604,18 +1634,18 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) x[i][j] += y[i][j];
-        wave_rmsnorm(x, y, W);
+            for (int j = 0; j < CPL; ++j) x[i][j] = fmaf(y[i][j], kLn2, x[i][j]);
+        wave_rmsnorm(x, y, W, kLog2e);
         wave_stack<CPL, R, BF, IL>(y, wb + 4 * gA, a.F, m, lane);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) x[i][j] += y[i][j];
+            for (int j = 0; j < CPL; ++j) x[i][j] = fmaf(y[i][j], kLn2, x[i][j]);
     }
     // The tied head (reference.rs:218-226) on the final norm of the rows asked for.
     if (!a.last_only || pos == S - 1) {
         float nf[R][CPL];
-        wave_rmsnorm(x, nf, W);
+        wave_rmsnorm(x, nf, W, 1.0f);
 #pragma unroll
         for (int i = 0; i < R; ++i)
 #pragma unroll

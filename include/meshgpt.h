@@ -220,7 +220,10 @@ int mg_sample_logits(int device, const float *logits, size_t rows, size_t vocab,
  * counter per row in a fixed array of MG_NOALLOC_MAX_ROWS ints on each GPU,
  * held until the process ends, which every call clears before use.  More rows
  * are rejected with MG_INVALID_ARGUMENT.  Calls that overlap on one GPU share
- * that array and race: order them (one stream, or events). */
+ * that array and race: order them (one stream, or events).  The first call on
+ * a device looks up the array's device address (hipGetSymbolAddress); make it
+ * before capturing a stream.  The calling thread's current device is the same
+ * on return as on entry. */
 #define MG_NOALLOC_MAX_ROWS 65536
 int mg_sample_logits_noalloc(int device, const float *logits, size_t rows, size_t vocab, float temperature,
                              uint64_t *rng_states, uint32_t *tokens, int *nonfinite, void *stream);

@@ -14,6 +14,7 @@ the persistent attention's LDS-ring refills and two-round register tail run;
 the W1024/H16 shape runs past 300 keys through the three-slot ring; config 4
 prefills 8192 tokens and decodes 256 steps past them.
 """
+import json
 import os
 import subprocess
 from concurrent.futures import ThreadPoolExecutor
@@ -112,6 +113,34 @@ def test_config3_full_decode_sampled_matches_oracle(monkeypatch):
                                  expected=expected[b])
 
 
+def test_config3_agent_scope_handoffs_match_xcd_local(monkeypatch):
+    # The persistent kernel's agent-scope hand-off protocol (the one a
+    # sequence falls back to when its workgroups are not all on one XCD),
+    # forced for every sequence with MG_PERSIST_AGENT_SCOPE=1, at config 3's
+    # full batch over 200 sampled steps (T=1, keys 65..264): tokens and
+    # last-step logits bit-equal to the XCD-local words' run (the same
+    # arithmetic in the same order), last-step logits of every sequence equal
+    # to a device re-prefill and of two against the oracle.
+    config = G.named_config("mid")
+    o = oracle_config(config)
+    params = O.initialize(o, 7)
+    prompts = G.random_prompts(256, 32, 64, 7)
+    runs = {}
+    for agent in ("0", "1"):
+        monkeypatch.setenv("MG_PERSIST_AGENT_SCOPE", agent)
+        with G.MeshGpt(0, config, 7, max_batch=32) as model:
+            got = model.generate_tokens(prompts, 200, 1.0, 7)
+            last = model.last_logits(32)
+            runs[agent] = (got, last)
+            if agent == "1":
+                assert_close(last, reprefill_last(model, got[:, :-1]), what="agent-scope decode vs re-prefill")
+                refs = parallel(lambda b: O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], range(2))
+                for b in range(2):
+                    assert_close(last[b], refs[b], what=f"agent-scope step-200 logits, sequence {b}")
+    assert np.array_equal(runs["0"][0], runs["1"][0])
+    assert np.array_equal(runs["0"][1], runs["1"][1])
+
+
 def test_config3_decode_segments_continue_one_launch():
     # Four persistent launches (150 + 150 + 150 + 61 steps after the prefill's
     # token) produce exactly the tokens of one 511-step launch, and each
@@ -193,6 +222,28 @@ def test_config4_long_context_full_size(monkeypatch):
             runs[disable] = got
 
 
+@pytest.mark.parametrize("mfma", ["1", "0"], ids=["mfma", "valu"])
+def test_config4_full_prefill_matches_oracle_fixture(mfma, monkeypatch):
+    # Config 4's 8192-token prefill against the f64 oracle: the last-row
+    # logits of benchmark prompt 0 cut at 1024, 4096 and 8192 tokens
+    # (tests/golden/config4_prefill.json, written by make_config4_prefill.py
+    # from one oracle forward over all 8192 rows), on the matrix-core flash
+    # attention and on the VALU flash kernel.  At 8192 keys the f32 softmax
+    # sums differ most from f64; the bound stays TOL * (1 + |ref|).
+    with open(os.path.join(ROOT, "tests", "golden", "config4_prefill.json")) as f:
+        fixture = json.load(f)
+    config = G.named_config("long")
+    assert fixture["config"] == config.as_dict()
+    prompt = G.random_prompts(256, 8, 8192, 7)[0]
+    assert fixture["prompt_sha"] == int(np.bitwise_xor.reduce(
+        prompt.astype(np.uint64) * (np.arange(8192, dtype=np.uint64) + 1)))
+    monkeypatch.setenv("MG_DISABLE_MFMA_PREFILL", "0" if mfma == "1" else "1")
+    with G.MeshGpt(0, config, 7) as model:
+        for n, row in fixture["rows"].items():
+            got = model.logits(prompt[:int(n)], int(n), last_only=True)[0]
+            assert_close(got, np.array(row), what=f"config-4 prefill of {n} tokens, last row")
+
+
 def test_config4_shape_against_oracle():
     # Config 4's model (W512 L4, context 8448) on a length the oracle covers:
     # one 1024-token prompt and 16 greedy steps.
@@ -208,27 +259,34 @@ def test_config4_shape_against_oracle():
         check_trajectory(o, params, prompt, got, 0.0, 7, last_row_logits(model), expected=expected)
 
 
+@pytest.mark.timeout(900)
 def test_config5_high_batch_full_size():
-    # Config 5: batch 256, W1024 L12 H16x64, context 2048 (a 48 GiB KV cache),
-    # 128-token prompts, 16 greedy steps on the per-phase kernels (4864
-    # workgroups exceed co-residency, so no persistent launch), in two slices
-    # of 128 sequences on two streams.  One sequence of each slice against
-    # the oracle; all 256 against a device re-prefill.
+    # Config 5 exactly: batch 256, W1024 L12 H16x64, context 2048 (a 48 GiB KV
+    # cache), 128-token prompts, all 1024 greedy steps (positions 128..1151)
+    # on the per-phase kernels (4864 workgroups exceed co-residency, so no
+    # persistent launch), in two slices of 128 sequences on two streams.  The
+    # last step's logits of all 256 sequences against a device re-prefill of
+    # their 1151 tokens (in chunks within the 131072-row limit), and sequence
+    # 0's trajectory and last-step logits against the oracle (its cached
+    # decode, and its full forward over the device's tokens).
     config = G.named_config("high")
     o = oracle_config(config)
     params = O.initialize(o, 7)
     prompts = G.random_prompts(256, 256, 128, 7)
-    checked = (0, 200)
-    expected = parallel(lambda b: O.generate(o, params, prompts[b], 16, 0.0, 7 + b, cached=True), checked)
-    with G.MeshGpt(0, config, 7, max_batch=256) as model:
-        got = model.generate_tokens(prompts, 16, 0.0, 7)
-        last = model.last_logits(256)
-        assert_close(last, reprefill_last(model, got[:, :-1]), what="config-5 decode vs re-prefill")
-        refs = parallel(lambda b: O.logits(o, params, got[b, :-1], got.shape[1] - 1)[-1], checked)
-        for i, b in enumerate(checked):
-            assert_close(last[b], refs[i], what=f"config-5 logits, sequence {b}")
-            check_trajectory(o, params, prompts[b], got[b], 0.0, 7 + b, last_row_logits(model),
-                             expected=expected[i])
+    with ThreadPoolExecutor(2) as ex:
+        expected = ex.submit(O.generate, o, params, prompts[0], 1024, 0.0, 7, True)
+        with G.MeshGpt(0, config, 7, max_batch=256) as model:
+            got = model.generate_tokens(prompts, 1024, 0.0, 7)
+            assert got.shape == (256, 1152)
+            assert np.array_equal(got[:, :128], prompts)
+            ref = ex.submit(lambda: O.logits(o, params, got[0, :-1], 1151)[-1])
+            last = model.last_logits(256)
+            for b0 in range(0, 256, 96):
+                assert_close(last[b0:b0 + 96], reprefill_last(model, got[b0:b0 + 96, :-1]),
+                             what=f"config-5 step-1024 logits vs re-prefill, sequences {b0}..")
+            assert_close(last[0], ref.result(), what="config-5 step-1024 logits, sequence 0")
+            check_trajectory(o, params, prompts[0], got[0], 0.0, 7, last_row_logits(model),
+                             expected=expected.result())
 
 
 @pytest.mark.parametrize("temperature,graph", [(0.0, True), (1.0, True), (1.0, False)])

@@ -141,6 +141,52 @@ def test_zero_embedding_gives_zero_logits():
                 assert np.array_equal(model.logits([0, 1, 2, 3, 4, 0], 3), np.zeros((6, 5), np.float32))
 
 
+def _overflowing_v_mesh(o, params):
+    """Block 0's V mesh with every weight 3e38: its rows overflow to +inf in f32
+    (and, after 8 ELU layers of growth by 6e38, in the f64 oracle too).  XSA
+    then divides inf by inf, so every head's output is NaN, and the projection
+    mesh's ELU layers must carry the NaN on (reference.rs:325-332: NaN >= 0 is
+    false and exp_m1(NaN) is NaN) so that the logits are non-finite."""
+    bad = params.copy()
+    start = O.group_offsets(o)[1 + 2]  # embedding mesh, then block 0's q, k, v
+    size = 2 * o.width * o.attention_mesh_depth
+    bad[start:start + size] = 3e38
+    return bad
+
+
+@pytest.mark.parametrize("shape", ["W512-A9", "W128-A9-short"])
+def test_nan_inside_a_mesh_reaches_the_logits(shape, monkeypatch):
+    """A NaN born inside the model (inf / inf in XSA) must make the logits
+    non-finite on every path, prefill (register-tile and short-sequence
+    kernels), the persistent decode and the per-phase decode, so that the
+    calls return MG_NONFINITE as the reference's "logits must contain only
+    finite values" (gpu.rs:1903-1913).  The f64 oracle's logits are non-finite
+    for the same weights."""
+    if shape == "W512-A9":
+        kw = dict(vocab_size=256, context=128, width=512, heads=8, layers=2, attention_mesh_depth=9,
+                  ffn_mesh_depth=9, connectivity=1)
+        n = 64
+    else:
+        kw = dict(vocab_size=64, context=64, width=128, heads=4, layers=2, attention_mesh_depth=9,
+                  ffn_mesh_depth=9, connectivity=1)
+        n = 8
+    g, o = configs_for(**kw)
+    bad = _overflowing_v_mesh(o, O.initialize(o, 7))
+    tokens = G.random_prompts(kw["vocab_size"], 2, n, 7)
+    assert not np.isfinite(O.logits(o, bad, tokens[0], n)).all()
+    for disable in ("0", "1"):
+        monkeypatch.setenv("MG_DISABLE_PERSISTENT", disable)
+        with G.MeshGpt(0, g, 7, max_batch=2) as model:
+            model.set_parameters(bad)
+            for last_only in (False, True):
+                with pytest.raises(G.MeshGptError, match="logits must contain only finite values") as err:
+                    model.logits(tokens.reshape(-1), n, last_only=last_only)
+                assert err.value.status == G.MG_NONFINITE
+            with pytest.raises(G.MeshGptError) as err:
+                model.generate_tokens(tokens, 4, 0.0, 7)
+            assert err.value.status == G.MG_NONFINITE, str(err.value)
+
+
 def _device_last(model):
     return lambda window: model.logits(window, len(window), last_only=True)[0]
 

@@ -174,6 +174,51 @@ def test_adamw_steps(setting, frozen):
                 assert np.array_equal(got[:skip], before[:skip])
 
 
+def test_nonfinite_step_changes_nothing():
+    """A step whose loss is not finite stops before AdamW (gpu.rs:2296-2313):
+    train_batch raises MG_NONFINITE with the weights, the moments and the step
+    count as they were, so the next (finite) steps update exactly as f32 AdamW
+    from step 1 on.  The weights make the loss depend on the batch: block 0's V
+    mesh scales channel 0 by 3e38 in each of its two ELU layers, so a token
+    whose normalised row has n_0 > 0 overflows to inf there (NaN after XSA,
+    NaN loss), while a token with n_0 < 0 saturates at ELU = -1 (finite, with a
+    zero gradient through that path).  The failing step is replayed from the
+    same captured graph as the good ones."""
+    cfg = dict(vocab_size=7, context=3, width=8, heads=2, layers=1, attention_mesh_depth=3, ffn_mesh_depth=2)
+    g, _ = configs_for(**cfg)
+    W, A = 8, 3
+    v_mesh = 2 * W * A * 3  # after the embedding, Q and K meshes (config.rs:367-396)
+    setting = dict(learning_rate=0.002, weight_decay=0.01)
+    opts = G.AdamW(**setting)
+    with G.MeshGpt(0, g, 7) as model:
+        params = model.parameters()
+        for layer in (0, 1):
+            params[v_mesh + layer * 2 * W] = 3e38  # channel 0: self weight
+            params[v_mesh + layer * 2 * W + 1] = 0.0  # and no partner
+        model.set_parameters(params)
+        E = model.token_embeddings()
+        up = [t for t in range(7) if E[t, 0] > 1e-3]
+        down = [t for t in range(7) if E[t, 0] < -1e-3]
+        assert up and len(down) >= 2, E[:, 0]
+        bad_x = np.array([down[0], up[0], down[1]], np.uint32)
+        good_x = np.array([down[0], down[1], down[0]], np.uint32)
+        y = np.array([1, 2, 3], np.uint32)
+        cpu = O.Adam(params, **setting)
+        for step in range(3):
+            before = model.parameters()
+            with pytest.raises(G.MeshGptError) as err:
+                model.train_batch(bad_x, y, 3, opts)
+            assert err.value.status == G.MG_NONFINITE
+            assert "finite" in str(err.value)
+            assert np.array_equal(model.parameters(), before), f"step {step}: a failed step moved the weights"
+            loss, grad = model.loss_and_gradient(good_x, y, 3)
+            assert np.isfinite(loss) and np.isfinite(grad).all()
+            want = cpu.step(grad).copy()
+            model.train_batch(good_x, y, 3, opts)
+            np.testing.assert_allclose(model.parameters(), want, rtol=2e-6, atol=1e-9,
+                                       err_msg=f"step {step}: the update after a failed step")
+
+
 @pytest.mark.parametrize("geometry", [{}, dict(normalization=2), dict(preserve_features=2)],
                          ids=["default", "normalised", "protected"])
 def test_training_then_inference_uses_the_new_weights(geometry):
