@@ -1653,29 +1653,71 @@ __global__ void __launch_bounds__(1024) short_forward_kernel(ShortForward a, int
                 if (short_live<CPL>(short_channel<IL>(lane, j), W)) finals[(i * S + pos) * W + short_channel<IL>(lane, j)] = nf[i][j];
     }
     __syncthreads();
-    // Every thread of the workgroup on (row, token) pairs, consecutive tokens
-    // on consecutive lanes: the reads of Et[c][t] are coalesced, the final
-    // rows' are LDS broadcasts.
-    const int first = a.last_only ? S - 1 : 0, per = S - first, n = valid * per * a.V;
+    // The tied head over the rows asked for (at most R * S <= 16): work items
+    // pair a run of 64 tokens, one a lane (the reads of Et[c][t] coalesced,
+    // each from a uniform column base plus the lane's token), with a group of
+    // up to 4 rows, whose channels are LDS broadcasts shared by the lane's
+    // tokens; the waves take the items in turn.  Rows go in groups of 4, or of
+    // fewer when that would leave waves idle.  Each logit adds its terms in
+    // channel order (reference.rs:218-226).
+    const int first = a.last_only ? S - 1 : 0, per = S - first, nrow = valid * per;
+    const int chunks = (a.V + 63) / 64;
+    int G = 4;
+    while (G > 1 && chunks * ((nrow + G - 1) / G) < S) G >>= 1;
+    const int items = chunks * ((nrow + G - 1) / G);
     float *lo = a.logits + size_t(s0) * per * a.V;
-    for (int e = threadIdx.x; e < n; e += blockDim.x) {
-        const int r = e / a.V, t = e - r * a.V, i = r / per;
-        const float *fr = finals + (i * S + first + r - i * per) * W;
-        float acc = 0.0f;
-        // The column's values 32 at a time, so that the loads overlap (32-bit
-        // offsets from the uniform base: Et holds under 2^31 floats); the
-        // terms still add in channel order.
-        const int wc = CPL == 2 ? 128 : W;  // a compile-time bound at width 128
-        for (int c0 = 0; c0 < wc; c0 += 32) {
-            float ev[32];
+    // One item: rows r0 .. r0 + gn - 1 (gn <= GG; the rows past them repeat
+    // the last one and are not stored) for the lane's token.
+    auto item = [&](auto GGC, int chunk, int r0, int gn) {
+        constexpr int GG = decltype(GGC)::value;
+        const int t = chunk * 64 + lane, tt = min(t, a.V - 1);  // lanes past V compute a copy
+        const float *fr[GG];
 #pragma unroll
-            for (int u = 0; u < 32; ++u)
-                ev[u] = short_live<CPL>(c0 + u, wc) ? a.Et[unsigned((c0 + u) * a.vpad + t)] : 0.0f;
-#pragma unroll
-            for (int u = 0; u < 32; ++u)
-                if (short_live<CPL>(c0 + u, wc)) acc = fmaf(fr[c0 + u], ev[u], acc);
+        for (int k = 0; k < GG; ++k) {
+            const int r = r0 + min(k, gn - 1), i = r / per;
+            fr[k] = finals + (i * S + first + r - i * per) * W;
         }
-        lo[e] = acc;
+        float acc[GG];
+#pragma unroll
+        for (int k = 0; k < GG; ++k) acc[k] = 0.0f;
+        if constexpr (CPL == 2) {
+            // Width 128: channels four at a time (one LDS read per row), 32
+            // column loads in flight.
+#pragma unroll 8
+            for (int c = 0; c < 128; c += 4) {
+                float e[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) e[u] = (a.Et + size_t(c + u) * a.vpad)[tt];
+#pragma unroll
+                for (int k = 0; k < GG; ++k) {
+                    const float4 f = *reinterpret_cast<const float4 *>(fr[k] + c);
+                    acc[k] = fmaf(f.x, e[0], acc[k]);
+                    acc[k] = fmaf(f.y, e[1], acc[k]);
+                    acc[k] = fmaf(f.z, e[2], acc[k]);
+                    acc[k] = fmaf(f.w, e[3], acc[k]);
+                }
+            }
+        } else {
+            for (int c = 0; c < W; ++c) {
+                const float e = (a.Et + size_t(c) * a.vpad)[tt];
+#pragma unroll
+                for (int k = 0; k < GG; ++k) acc[k] = fmaf(fr[k][c], e, acc[k]);
+            }
+        }
+        if (t < a.V) {
+#pragma unroll
+            for (int k = 0; k < GG; ++k)
+                if (k < gn) lo[size_t(r0 + k) * a.V + t] = acc[k];
+        }
+    };
+    for (int it = pos; it < items; it += S) {
+        const int chunk = it % chunks, r0 = it / chunks * G, gn = min(G, nrow - r0);
+        if (G == 4)
+            item(std::integral_constant<int, 4>{}, chunk, r0, gn);
+        else if (G == 2)
+            item(std::integral_constant<int, 2>{}, chunk, r0, gn);
+        else
+            item(std::integral_constant<int, 1>{}, chunk, r0, gn);
     }
 }
 
