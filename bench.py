@@ -20,8 +20,11 @@ short-context end), config 1 at batch 1, config 2's single 9409-row prefill,
 config 4's 8192-token prefill and long-context decode, config 5's batch-256
 decode, the training step on the reference's training benchmark
 (mesh-gpt-bench defaults, ms per AdamW update against its published 5.759 ms),
-the measured copy bandwidth of the box, HBM traffic from rocprofv3 counters,
-and the CPU baseline (the f64 oracle on one core, a bounded sample).
+config 3 with BASELINE.json's N(0, 0.5) weights, the measured copy bandwidth of
+the box, HBM traffic from rocprofv3 counters, and the CPU baselines: the
+KV-cached f32 decode on the host's threads (config 3's whole workload, a
+config-5 sample), the f64 oracle's KV-cached decode on one core, and the
+reference's full-window semantics on one core (config 1).
 """
 import argparse
 import ctypes
@@ -114,14 +117,54 @@ def cpu_name():
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(config, prompts, steps, temperature, budget_s):
-    """The f64 oracle's KV-cached decode on one host core over whole sequences
-    of the workload (prompt, then all decode steps), until budget_s is spent."""
+def host_threads():
+    """The host threads the CPU baselines use: OMP_NUM_THREADS when set (the
+    GPU box sets it to its CPU share, 16), else the cores this process may run
+    on, at most 16."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    return max(1, min(16, len(os.sched_getaffinity(0))))
+
+
+def oracle_config(config):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib as O
 
-    o = O.config(**{k: v for k, v in config.as_dict().items() if k != "long_context"})
+    return O, O.config(**{k: v for k, v in config.as_dict().items() if k != "long_context"})
+
+
+def cpu_f32_mode(name, prompts, steps, temperature, threads, sample):
+    """cpu-f32-kv: the KV-cached f32 decode of oracle/cpu_f32_decode.c, one
+    sequence a thread on `threads` host threads; decode steps only."""
+    config = G.named_config(name)
+    O, o = oracle_config(config)
     params = O.initialize(o, 7)
+    _, seconds = O.cpu_generate_f32(o, params, prompts, steps, temperature, 7, threads)
+    tokens = prompts.shape[0] * steps
+    return {"mode": "cpu-f32-kv", "workload": name, "value": round(tokens / seconds, 1), "unit": "tokens/s",
+            "cores": threads, "cpu": cpu_name(), "sample": sample,
+            "us_per_decode_step": round(1e6 * seconds / steps, 1)}
+
+
+def cpu_baseline(config, prompts, steps, temperature, budget_s):
+    """The CPU baselines, timed on this host (bench.py's cpu_baseline leg).
+    `value` is cpu-f32-kv on config 3's whole workload (all 32 sequences, all
+    512 steps, on host_threads() threads); `modes` adds cpu-f32-kv on a
+    config-5 sample, the f64 oracle's KV-cached decode on one core (whole
+    config-3 sequences within budget_s), and the reference's own semantics on
+    one core (the f64 oracle recomputing the whole window for every token, as
+    gpu.rs:2025-2027 and reference.rs:49-59 do) over config 1's whole run."""
+    O, o = oracle_config(config)
+    params = O.initialize(o, 7)
+    threads = host_threads()
+    modes = [cpu_f32_mode("mid", prompts, steps, temperature, threads,
+                          f"config 3: all {prompts.shape[0]} sequences, {prompts.shape[1]}-token prompts then all "
+                          f"{steps} decode steps at T={temperature}; decode time only")]
+    high = G.random_prompts(256, 256, 128, 7)[:32]
+    modes.append(cpu_f32_mode("high", high, 64, 0.0, threads,
+                              "config 5: 32 of its 256 sequences (two per thread), 128-token prompts then 64 "
+                              "greedy decode steps (positions 128..191); decode time only"))
     tokens, seconds, done = 0, 0.0, 0
     for b in range(prompts.shape[0]):
         t0 = time.perf_counter()
@@ -134,66 +177,24 @@ def cpu_baseline(config, prompts, steps, temperature, budget_s):
         done += 1
         if t2 - t0 + seconds > budget_s:
             break
-    return {
-        "value": round(tokens / seconds, 2),
-        "unit": "tokens/s",
-        "cores": 1,
-        "kind": "port",
-        "sample": f"{done} of {prompts.shape[0]} sequences, each its {prompts.shape[1]}-token prompt "
-                  f"then {steps} decode steps; decode time only; f64 KV-cached oracle; {cpu_name()}",
-    }
-
-
-def pmc_traffic(args):
-    """HBM bytes of one bench-step launch, from two rocprofv3 --pmc runs of a
-    child process (FETCH_SIZE, then WRITE_SIZE), each scaled by the same
-    counter on a plain copy kernel of known size.  Every run's return code is
-    reported; a failed run is not repeated."""
-    rocprof = "/opt/rocm/bin/rocprofv3"
-    report = {"runs": []}
-    if not os.path.exists(rocprof):
-        report["error"] = "rocprofv3 not found"
-        return report
-    import csv
-
-    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
-        out = tempfile.mkdtemp(prefix="mg_pmc_")
-        cmd = ["timeout", "-s", "KILL", "90", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
-               "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe"]
-        res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
-        hits, copy = [], []
-        for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
-            with open(path) as f:
-                for row in csv.DictReader(f):
-                    name = row.get("Kernel_Name", "")
-                    value = float(row.get("Counter_Value", "nan"))
-                    if KERNEL in name and "<4, 2, 16, 9, 64>" in name:
-                        hits.append(value)
-                    elif "calibration_copy" in name:
-                        copy.append(value)
-        # rocprofv3 can end with a segmentation fault after its tool
-        # finalisation when the program made cooperative launches; the
-        # counter file is complete by then, so the rows decide.
-        report["runs"].append({"counter": counter, "rc": res.returncode, "kernel_rows": len(hits),
-                               "copy_rows": len(copy)})
-        if not hits or not copy:
-            report["error"] = f"{counter}: no counter rows (rc {res.returncode}): {res.stderr[-300:]}"
-            return report
-        factor = (PROBE_COPY_BYTES / 1024.0) / float(np.mean(copy))
-        report[counter] = float(np.mean(hits)) * factor * 1024.0
-        report[counter + "_factor"] = factor
-    return report
-
-
-def probe():
-    """Child process under rocprofv3 --pmc: one bench step (the prefill, then
-    the 512-step decode launch) and one plain copy of known size."""
-    config = G.named_config("mid")
-    prompts = G.random_prompts(256, 32, 64, 7)
-    with G.MeshGpt(0, config, 7, max_batch=32) as model:
-        model.prefill(prompts, 1.0, 7, reserve=64 + 1 + DECODE_STEPS)
-        model.decode(DECODE_STEPS)
-    G.calibration_copy(PROBE_COPY_BYTES)
+    modes.append({"mode": "oracle-f64-kv", "workload": "mid", "value": round(tokens / seconds, 2),
+                  "unit": "tokens/s", "cores": 1, "cpu": cpu_name(),
+                  "sample": f"config 3: {done} of {prompts.shape[0]} sequences, each its {prompts.shape[1]}-token "
+                            f"prompt then {steps} decode steps; decode time only"})
+    tiny = G.named_config("tiny")
+    Ot, ot = oracle_config(tiny)
+    tp = G.random_prompts(64, 1, 16, 7)[0]
+    t0 = time.perf_counter()
+    Ot.generate(ot, Ot.initialize(ot, 7), tp, 128, 0.0, 7, cached=False)
+    seconds1 = time.perf_counter() - t0
+    modes.append({"mode": "oracle-f64-window", "workload": "tiny", "value": round(128 / seconds1, 1),
+                  "unit": "tokens/s", "cores": 1, "cpu": cpu_name(),
+                  "us_per_token": round(1e6 * seconds1 / 128, 1),
+                  "sample": "config 1: the whole run, a 16-token prompt then 128 greedy tokens, each from a "
+                            "full-window f64 forward (the reference's generate semantics, no KV cache)"})
+    first = modes[0]
+    return {"value": first["value"], "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"cpu-f32-kv, {first['sample']}; {cpu_name()}", "modes": modes}
 
 
 def batch1_figure(hip, steps=128):
@@ -262,9 +263,9 @@ def long_figure(hip, decode_steps=256):
             "decode_hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
-def high_figure(hip, decode_steps=64):
-    """batch 256, W1024 L12, 128-token prompts, greedy decode
-    (the first 64 of its 1024 steps)."""
+def high_figure(hip, decode_steps=1024):
+    """batch 256, W1024 L12, 128-token prompts, all 1024
+    greedy decode steps (positions 128..1151)."""
     config = G.named_config("high")
     prompts = G.random_prompts(256, 256, 128, 7)
     with G.MeshGpt(0, config, 7, max_batch=256) as model:
@@ -280,6 +281,29 @@ def high_figure(hip, decode_steps=64):
             "decode_tokens_per_s": round(256 * decode_steps / (ms / 1000.0), 1),
             "decode_us_per_step": round(1000.0 * ms / decode_steps, 2),
             "decode_hbm_frac": round(nbytes / (ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def normal_figure(hip, timed=2):
+    """Config 3 as the headline (batch 32, 64-token prompts, 512 decode steps
+    at T=1) with BASELINE.json's N(0, 0.5) weights (mg_normal_parameters, seed
+    7) instead of the reference's seeded initialisation."""
+    config = G.named_config("mid")
+    prompts = G.random_prompts(config.vocab_size, 32, 64, 7)
+    with G.MeshGpt(0, config, 7, max_batch=32) as model:
+        model.set_parameters(G.normal_parameters(config, 7, 0.5))
+        model.prefill(prompts, 1.0, 7, reserve=64 + 1 + DECODE_STEPS)
+        model.decode(DECODE_STEPS)  # warm-up
+        ms = []
+        for _ in range(timed):
+            model.rewind()
+            ms.append(timed_decode(hip, model, DECODE_STEPS))
+    avg = float(np.mean(ms))
+    nbytes = decode_bytes(config, 32, 64, DECODE_STEPS)
+    return {"workload": "config 3 with N(0, 0.5) weights (sigma 0.5, the reference's Box-Muller draw on "
+                        "Random::new(7)): batch 32, 64-token prompts, 512 decode steps at T=1",
+            "tokens_per_s": round(32 * DECODE_STEPS / (avg / 1000.0), 1),
+            "us_per_decode_step": round(1000.0 * avg / DECODE_STEPS, 2),
+            "hbm_frac": round(nbytes / (avg / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4)}
 
 
 def training_figure(steps=30, warmup=10, trials=3):
@@ -331,7 +355,8 @@ def main():
     parser.add_argument("--no-cpu", action="store_true")
     parser.add_argument("--no-pmc", action="store_true")
     parser.add_argument("--no-extra", action="store_true", help="config 3 only")
-    parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5", "training"],
+    parser.add_argument("--only", choices=["batch1", "config2", "config4", "config5", "normal", "training",
+                                           "cpu"],
                         help="print only that figure (for profiling one workload)")
     parser.add_argument("--calibrate", action="store_true",
                         help="with --only: a plain copy of 256 MiB after the figure (the scale of counter runs)")
@@ -349,9 +374,12 @@ def main():
         sys.exit("--steps must be at least 1")
 
     if args.only:
+        mid = G.named_config("mid")
         figures = {"batch1": lambda: batch1_figure(Hip()), "config2": symbolic_figure,
                    "config4": lambda: long_figure(Hip()), "config5": lambda: high_figure(Hip()),
-                   "training": training_figure}
+                   "normal": lambda: normal_figure(Hip()), "training": training_figure,
+                   "cpu": lambda: cpu_baseline(mid, G.random_prompts(256, 32, 64, 7), DECODE_STEPS, 1.0,
+                                               args.cpu_budget)}
         print(json.dumps({args.only: figures[args.only]()}))
         if args.calibrate:
             G.calibration_copy(PROBE_COPY_BYTES)
@@ -438,6 +466,7 @@ def main():
         result["config2"] = symbolic_figure()
         result["config4"] = long_figure(hip)
         result["config5"] = high_figure(hip)
+        result["config3_normal_init"] = normal_figure(hip)
         result["training"] = training_figure()
     # Measured copy roofline of this box (read + write bytes of a plain copy kernel).
     result["copy_gbps"] = round(G.copy_bandwidth(1 << 30, 10), 1)

@@ -20,7 +20,7 @@ MG_OK, MG_INVALID_ARGUMENT, MG_OUT_OF_MEMORY, MG_DEVICE_ERROR, MG_NONFINITE, MG_
 # Every function include/meshgpt.h declares.
 EXPORTS = (
     "mg_last_error", "mg_config_default", "mg_config_validate", "mg_parameter_count",
-    "mg_initial_parameters", "mg_token_codes", "mg_model_create", "mg_model_destroy",
+    "mg_initial_parameters", "mg_normal_parameters", "mg_token_codes", "mg_model_create", "mg_model_destroy",
     "mg_model_config", "mg_parameters", "mg_set_parameters", "mg_logits", "mg_token_embeddings",
     "mg_hidden_states", "mg_generate", "mg_generate_text", "mg_prefill", "mg_decode",
     "mg_decode_rewind", "mg_last_call_ms", "mg_decode_profiled", "mg_decode_traced", "mg_sequence_length", "mg_read_tokens", "mg_last_logits",
@@ -106,6 +106,7 @@ def lib():
         "mg_config_validate": (i, [_cfgp]),
         "mg_parameter_count": (i, [_cfgp, _szp]),
         "mg_initial_parameters": (i, [_cfgp, u64, _f32p, sz]),
+        "mg_normal_parameters": (i, [_cfgp, u64, f, _f32p, sz]),
         "mg_token_codes": (i, [_cfgp, _f32p, sz]),
         "mg_model_create": (i, [i, _cfgp, u64, sz, ctypes.POINTER(vp)]),
         "mg_model_destroy": (None, [vp]),
@@ -187,6 +188,14 @@ def parameter_count(config):
 def initial_parameters(config, seed):
     out = np.empty(parameter_count(config), dtype=np.float32)
     _check(lib().mg_initial_parameters(ctypes.byref(config), seed, _p(out, _f32p), out.size))
+    return out
+
+
+def normal_parameters(config, seed, sigma=0.5):
+    """mg_normal_parameters: N(0, sigma^2) weights, the reference's Box-Muller
+    draw on Random::new(seed) (src/simple/numerical.rs:163-167)."""
+    out = np.empty(parameter_count(config), dtype=np.float32)
+    _check(lib().mg_normal_parameters(ctypes.byref(config), seed, sigma, _p(out, _f32p), out.size))
     return out
 
 

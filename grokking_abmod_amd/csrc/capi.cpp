@@ -143,6 +143,14 @@ int mg_initial_parameters(const mg_config *config, uint64_t seed, float *out, si
     return guarded([&] { copy_out(to_config(config).initial_parameters(seed), out, n); });
 }
 
+int mg_normal_parameters(const mg_config *config, uint64_t seed, float sigma, float *out, size_t n) {
+    return guarded([&] {
+        GptConfig g = to_config(config);
+        g.validate();
+        copy_out(Layout::build(g).initialize_normal(g, seed, sigma), out, n);
+    });
+}
+
 int mg_token_codes(const mg_config *config, float *out, size_t n) {
     return guarded([&] {
         GptConfig g = to_config(config);

@@ -41,6 +41,9 @@ struct Options {
     float temperature = 0.7f;
     std::string synthetic;
     size_t random_prompt = 0;
+    std::string prompt_file;
+    std::string init = "reference";
+    float init_sigma = 0.5f;
     bool help = false;
 };
 
@@ -215,6 +218,9 @@ Options parse(int argc, char **argv) {
         else if (flag == "--temperature") o.temperature = value<float>(it, end, flag);
         else if (flag == "--config") o.synthetic = value<std::string>(it, end, flag);
         else if (flag == "--random-prompt") o.random_prompt = value<size_t>(it, end, flag);
+        else if (flag == "--prompt-file") o.prompt_file = value<std::string>(it, end, flag);
+        else if (flag == "--init") o.init = value<std::string>(it, end, flag);
+        else if (flag == "--init-sigma") o.init_sigma = value<float>(it, end, flag);
         else if (flag == "--help" || flag == "-h") o.help = true;
         else throw Error("unknown option: " + flag + "; use --help");
     }
@@ -264,7 +270,40 @@ const char *kHelp =
     "--seed N              Initialization/data/sampling seed (default: 7)\n"
     "--device N            HIP device ordinal (default: 0)\n"
     "--config NAME         generate: synthetic seeded model: tiny, symbolic, mid, long or high\n"
-    "--random-prompt LEN   With --config: LEN seeded uniform token ids as the prompt\n";
+    "--random-prompt LEN   With --config: LEN seeded uniform token ids as the prompt\n"
+    "--prompt-file PATH    generate: read the prefix from PATH; with --batch N, N lines of\n"
+    "                      equal token length, one prompt per sequence\n"
+    "--init NAME           init and generate --config: reference (default, the seeded\n"
+    "                      initialisation) or normal (N(0, sigma^2) weights)\n"
+    "--init-sigma X        Standard deviation of --init normal (default: 0.5)\n";
+
+// The weights of a synthetic model or a new checkpoint: the reference's
+// seeded initialisation (config.rs:443-449), or N(0, sigma^2) weights drawn
+// with the reference's Box-Muller normal (src/simple/numerical.rs:163-167).
+std::vector<float> initial_weights(const GptConfig &config, const Options &o) {
+    if (o.init == "reference") return config.initial_parameters(o.seed);
+    if (o.init == "normal") return Layout::build(config).initialize_normal(config, o.seed, o.init_sigma);
+    throw Error("unknown initialisation: " + o.init + "; use reference or normal");
+}
+
+// --prompt-file: the whole file is the prompt, or with --batch one line per
+// sequence (the line breaks are not part of the prompts).
+std::vector<std::string> prompt_lines(const Options &o) {
+    const std::string text = read_file(o.prompt_file);
+    if (!o.batch_set) return {text};
+    std::vector<std::string> lines;
+    size_t start = 0;
+    while (start < text.size()) {
+        size_t stop = text.find('\n', start);
+        if (stop == std::string::npos) stop = text.size();
+        lines.push_back(text.substr(start, stop - start));
+        start = stop + 1;
+    }
+    if (lines.size() != o.batch)
+        throw Error("prompt file must hold one line per sequence (" + std::to_string(o.batch) + "), found " +
+                    std::to_string(lines.size()));
+    return lines;
+}
 
 // report (mesh-gpt.rs:289-299): one stdout line and one loss.csv row.
 void report(std::ofstream &history, size_t step, double train, double validation) {
@@ -857,7 +896,7 @@ int run(int argc, char **argv) {
             std::vector<uint32_t> chars(config.vocab_size);
             for (size_t i = 0; i < chars.size(); ++i) chars[i] = uint32_t(config.vocab_size == 64 ? 0x20 + i : i);
             tokenizer = CharacterTokenizer::from_characters(chars);
-            parameters = config.initial_parameters(o.seed);
+            parameters = initial_weights(config, o);
             if (o.random_prompt) {
                 Random r(o.seed);
                 for (size_t i = 0; i < o.batch * o.random_prompt; ++i)
@@ -871,9 +910,22 @@ int run(int argc, char **argv) {
         }
         MeshGpt model(int(o.device), config, o.seed, o.batch);
         model.set_parameters(parameters.data(), parameters.size());
+        std::vector<std::string> texts;
+        if (!o.prompt_file.empty() && prompt.empty()) texts = prompt_lines(o);
         if (prompt.empty() && !o.batch_set) {
-            std::cout << model.generate(tokenizer, o.prompt, o.tokens, o.temperature, o.seed) << "\n";
+            const std::string &text = texts.empty() ? o.prompt : texts[0];
+            std::cout << model.generate(tokenizer, text, o.tokens, o.temperature, o.seed) << "\n";
             return 0;
+        }
+        if (prompt.empty() && !texts.empty()) {
+            size_t p = 0;
+            for (size_t b = 0; b < o.batch; ++b) {
+                std::vector<uint32_t> one = tokenizer.encode(texts[b]);
+                if (one.empty()) throw Error("generation prompt must not be empty");
+                if (b > 0 && one.size() != p) throw Error("batched prompts must have equal token lengths");
+                p = one.size();
+                prompt.insert(prompt.end(), one.begin(), one.end());
+            }
         }
         if (prompt.empty()) {
             std::vector<uint32_t> one = tokenizer.encode(o.prompt);
@@ -898,7 +950,7 @@ int run(int argc, char **argv) {
         ck.tokenizer = CharacterTokenizer::from_text(text);
         ck.config = o.config;
         ck.config.vocab_size = ck.tokenizer.vocab_size();
-        ck.parameters = ck.config.initial_parameters(o.seed);
+        ck.parameters = initial_weights(ck.config, o);
         ck.save(checkpoint);
         std::cout << "Saved seed-" << o.seed << " checkpoint to " << checkpoint << "\n";
         return 0;

@@ -227,6 +227,24 @@ std::vector<float> Layout::initialize(const GptConfig &config, uint64_t seed) co
     return parameters;
 }
 
+std::vector<float> Layout::initialize_normal(const GptConfig &config, uint64_t seed, float sigma) const {
+    if (!std::isfinite(sigma) || sigma < 0.0f) throw Error("normal initialisation needs a finite nonnegative sigma");
+    Random random(seed);
+    std::vector<float> parameters(count());
+    for (float &value : parameters) {
+        const double u1 = double(random.unit()), u2 = double(random.unit());
+        const double radius = std::sqrt(-2.0 * std::log(1.0 - u1));
+        const double angle = 6.283185307179586 * u2;  // f64 TAU
+        value = float(radius * std::cos(angle)) * sigma;
+    }
+    for (size_t id = 0; id < groups.size(); ++id) {
+        const auto [begin, end] = constrained_range(config, id);
+        std::fill(parameters.begin() + groups[id].offset + begin, parameters.begin() + groups[id].offset + end,
+                  0.0f);
+    }
+    return parameters;
+}
+
 std::pair<size_t, size_t> Layout::constrained_range(const GptConfig &config, size_t id) const {
     if (config.geometry.preserve_features == 0) return {0, 0};
     for (const Block &b : blocks)

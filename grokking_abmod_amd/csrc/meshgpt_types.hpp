@@ -165,6 +165,13 @@ struct Layout {
     static Layout build(const GptConfig &config);
     size_t count() const;
     std::vector<float> initialize(const GptConfig &config, uint64_t seed) const;
+    // Weights drawn from N(0, sigma^2) (BASELINE.json's synthetic workloads;
+    // config.rs has no such initialiser): parameter i in flat order (group,
+    // layer, channel, self then partner) is sigma times the reference's
+    // Box-Muller draw from Random::new(seed) (src/simple/numerical.rs:163-167:
+    // two unit() draws, sqrt(-2 ln(1 - u1)) cos(2 pi u2) in f64, rounded to
+    // f32), multiplied in f32; protected rows stay zero as in initialize.
+    std::vector<float> initialize_normal(const GptConfig &config, uint64_t seed, float sigma) const;
     // The final mesh rows that write protected residual coordinates
     // (config.rs:461-474): [begin, end) within group `id`.
     std::pair<size_t, size_t> constrained_range(const GptConfig &config, size_t id) const;

@@ -82,6 +82,13 @@ int mg_config_validate(const mg_config *config);
 int mg_parameter_count(const mg_config *config, size_t *out);
 /* GptConfig::initial_parameters (config.rs:187-190); out holds parameter_count floats. */
 int mg_initial_parameters(const mg_config *config, uint64_t seed, float *out, size_t n);
+/* No counterpart in config.rs: the N(0, sigma^2) weights of BASELINE.json's
+ * synthetic workloads (sigma 0.5 there).  Parameter i, in the flat order of
+ * mg_initial_parameters, is sigma times one draw of the reference's Box-Muller
+ * normal (src/simple/numerical.rs:163-167) from Random::new(seed) (two unit()
+ * draws per parameter); the protected rows of a geometry with
+ * preserve_features stay zero.  out holds parameter_count floats. */
+int mg_normal_parameters(const mg_config *config, uint64_t seed, float sigma, float *out, size_t n);
 /* GptConfig::fixed_token_codes (config.rs:205-208); out is vocab_size x width. */
 int mg_token_codes(const mg_config *config, float *out, size_t n);
 

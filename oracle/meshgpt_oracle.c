@@ -512,6 +512,31 @@ void og_initialize(const og_config *c, uint64_t seed, float *out) {
     free(tmp);
 }
 
+/* N(0, sigma^2) weights (BASELINE.json's synthetic workloads; config.rs has
+ * no such initialiser): parameter i in flat order is sigma times the
+ * reference's Box-Muller draw (src/simple/numerical.rs:163-167), u1 and u2
+ * two unit() draws of Random::new(seed), sqrt(-2 ln(1 - u1)) cos(tau u2) in
+ * f64 rounded to f32, times sigma in f32; protected rows are zeroed as in
+ * og_initialize. */
+void og_initialize_normal(const og_config *c, uint64_t seed, float sigma, float *out) {
+    uint64_t state = seed;
+    size_t n = og_parameter_count(c);
+    for (size_t i = 0; i < n; ++i) {
+        double u1 = (double)og_rng_unit(&state), u2 = (double)og_rng_unit(&state);
+        double radius = sqrt(-2.0 * log(1.0 - u1));
+        out[i] = (float)(radius * cos(6.283185307179586 * u2)) * sigma;
+    }
+    size_t ngroups = 1 + 5 * (size_t)c->layers;
+    size_t *offsets = (size_t *)malloc(sizeof(size_t) * ngroups);
+    og_group_offsets(c, offsets);
+    for (size_t g = 0; g < ngroups; ++g) {
+        size_t begin, end;
+        og_constrained_range(c, g, &begin, &end);
+        for (size_t i = begin; i < end; ++i) out[offsets[g] + i] = 0.0f;
+    }
+    free(offsets);
+}
+
 /* ------------------------------------------------------------ operators */
 
 /* Tape::dot: products first, then a left fold starting at the first product
@@ -606,10 +631,13 @@ static void attention_row(const double *query, const double *k, const double *v,
         }
         double reciprocal = 1.0 / sum;
         for (size_t j = 0; j <= position; ++j) scores[j] = scores[j] * reciprocal;
-        for (size_t ch = b; ch < b + hw; ++ch) {
-            double total = scores[0] * v[ch];
-            for (size_t j = 1; j <= position; ++j) total = total + scores[j] * v[j * width + ch];
-            out[ch] = total;
+        /* Each channel's total is the left fold over j in order; the loops run
+         * j outermost so that the value rows are read contiguously (the same
+         * operations, in the same order, per channel). */
+        for (size_t ch = b; ch < b + hw; ++ch) out[ch] = scores[0] * v[ch];
+        for (size_t j = 1; j <= position; ++j) {
+            const double s = scores[j], *vj = v + j * width;
+            for (size_t ch = b; ch < b + hw; ++ch) out[ch] = out[ch] + s * vj[ch];
         }
     }
 }

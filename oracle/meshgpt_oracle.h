@@ -64,6 +64,7 @@ size_t og_embedding_parameter_count(const og_config *c);
 void og_group_offsets(const og_config *c, size_t *offsets /* 1+5L */);
 uint32_t og_stride(const og_config *c, uint32_t layer);
 void og_initialize(const og_config *c, uint64_t seed, float *out);
+void og_initialize_normal(const og_config *c, uint64_t seed, float sigma, float *out);
 /* fixed token codes, V x W (config.rs:552-591, geometry.rs:186-325) */
 void og_token_codes(const og_config *c, float *out);
 /* grokking.rs:260-271 (modulus entries) and geometry.rs:166-184 */
@@ -135,6 +136,17 @@ int og_equations(uint32_t modulus, uint32_t operation, double train_fraction, ui
                  size_t *n_train, size_t *n_valid);
 /* row_metrics of src/bin/mesh-gpt/grokking.rs:544-557 on one f32 row */
 double og_row_metrics(const float *row, size_t vocab, size_t target, size_t *prediction);
+
+/* ---- CPU baseline (bench.py's cpu_baseline leg; cpu_f32_decode.c) ----
+ * KV-cached f32 decode on `threads` OpenMP threads, one sequence a thread:
+ * prompts B x P, then `steps` decode steps (the forward of the last token and
+ * the draw of the next, seed + b per sequence, og_sample's arithmetic);
+ * out: B x (P + steps + 1) tokens; decode_seconds: wall time of the steps.
+ * Returns nonzero for shapes it does not take (geometric forms, embedding
+ * normalisation, protected coordinates, P + steps beyond the context). */
+int cb_generate_f32(const og_config *c, const float *params, const uint32_t *prompts, size_t B, size_t P,
+                    size_t steps, float temperature, uint64_t seed, int threads, uint32_t *out,
+                    double *decode_seconds);
 
 #ifdef __cplusplus
 }

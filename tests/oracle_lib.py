@@ -57,8 +57,13 @@ def lib():
             "og_parameter_count": (ctypes.c_size_t, [cp]),
             "og_embedding_parameter_count": (ctypes.c_size_t, [cp]),
             "og_group_offsets": (None, [cp, _szp]),
+            "og_constrained_range": (None, [cp, ctypes.c_size_t, _szp, _szp]),
             "og_stride": (ctypes.c_uint32, [cp, ctypes.c_uint32]),
             "og_initialize": (None, [cp, ctypes.c_uint64, _f32p]),
+            "og_initialize_normal": (None, [cp, ctypes.c_uint64, ctypes.c_float, _f32p]),
+            "cb_generate_f32": (ctypes.c_int, [cp, _f32p, _u32p, ctypes.c_size_t, ctypes.c_size_t, ctypes.c_size_t,
+                                               ctypes.c_float, ctypes.c_uint64, ctypes.c_int, _u32p,
+                                               ctypes.POINTER(ctypes.c_double)]),
             "og_token_codes": (None, [cp, _f32p]),
             "og_residue_permutation": (None, [ctypes.c_uint32, ctypes.c_uint64, _u32p]),
             "og_primitive_root": (ctypes.c_uint32, [ctypes.c_uint32]),
@@ -139,6 +144,12 @@ def stride(c, layer):
 def initialize(c, seed):
     out = np.zeros(parameter_count(c), dtype=np.float32)
     lib().og_initialize(ctypes.byref(c), seed, ptr(out, _f32p))
+    return out
+
+
+def initialize_normal(c, seed, sigma=0.5):
+    out = np.zeros(parameter_count(c), dtype=np.float32)
+    lib().og_initialize_normal(ctypes.byref(c), seed, sigma, ptr(out, _f32p))
     return out
 
 
@@ -280,6 +291,21 @@ def generate(c, params, prompt, count, temperature, seed, cached=False):
     if rc:
         raise ValueError("oracle rejected the generation request")
     return out
+
+
+def cpu_generate_f32(c, params, prompts, steps, temperature, seed, threads):
+    """The CPU baseline (cpu_f32_decode.c): KV-cached f32 decode of the
+    (B, P) prompts on `threads` threads; returns (tokens B x (P + steps + 1),
+    seconds of the decode steps)."""
+    params, prompts = f32(params), np.ascontiguousarray(prompts, dtype=np.uint32)
+    B, P = prompts.shape
+    out = np.zeros((B, P + steps + 1), dtype=np.uint32)
+    seconds = ctypes.c_double()
+    rc = lib().cb_generate_f32(ctypes.byref(c), ptr(params, _f32p), ptr(prompts, _u32p), B, P, steps, temperature,
+                               seed, threads, ptr(out, _u32p), ctypes.byref(seconds))
+    if rc:
+        raise ValueError("the CPU baseline does not take this shape")
+    return out, seconds.value
 
 
 def sample(logits_f32, temperature, rng_state):

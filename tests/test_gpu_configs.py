@@ -141,6 +141,37 @@ def test_config3_agent_scope_handoffs_match_xcd_local(monkeypatch):
     assert np.array_equal(runs["0"][1], runs["1"][1])
 
 
+@pytest.mark.parametrize("name,batch,prompt,steps,temperature,checked", [
+    ("tiny", 1, 16, 128, 0.0, 1), ("mid", 32, 64, 512, 0.0, 4), ("mid", 32, 64, 512, 1.0, 4)],
+    ids=["config1-greedy", "config3-greedy", "config3-T1"])
+def test_normal_weights_decode_matches_oracle(name, batch, prompt, steps, temperature, checked):
+    # BASELINE.json's N(0, 0.5) weights (mg_normal_parameters, seed 7, the
+    # reference's Box-Muller draw) at configs 1 and 3: trajectories of
+    # `checked` sequences against the oracle's decode on the same weights,
+    # last-step logits of two against the oracle and of all against a device
+    # re-prefill.
+    config = G.named_config(name)
+    o = oracle_config(config)
+    params = O.initialize_normal(o, 7, 0.5)
+    prompts = G.random_prompts(config.vocab_size, batch, prompt, 7)
+    expected = parallel(lambda b: O.generate(o, params, prompts[b], steps, temperature, 7 + b, cached=True),
+                        range(checked))
+    with G.MeshGpt(0, config, 7, max_batch=batch) as model:
+        weights = G.normal_parameters(config, 7, 0.5)
+        assert np.array_equal(weights, params)
+        model.set_parameters(weights)
+        got = model.generate_tokens(prompts, steps, temperature, 7)
+        last = model.last_logits(batch)
+        n = got.shape[1] - 1
+        refs = parallel(lambda b: O.logits(o, params, got[b, :-1], n)[-1], range(min(2, checked)))
+        for b, ref in enumerate(refs):
+            assert_close(last[b], ref, what=f"{name} N(0, 0.5) last-step logits, sequence {b}")
+        assert_close(last, reprefill_last(model, got[:, :-1]), what=f"{name} N(0, 0.5) decode vs re-prefill")
+        for b in range(checked):
+            check_trajectory(o, params, prompts[b], got[b], temperature, 7 + b, last_row_logits(model),
+                             expected=expected[b])
+
+
 def test_config3_decode_segments_continue_one_launch():
     # Four persistent launches (150 + 150 + 150 + 61 steps after the prefill's
     # token) produce exactly the tokens of one 511-step launch, and each
@@ -403,6 +434,63 @@ def test_cli_init_then_generate_matches_oracle(tmp_path):
         with G.MeshGpt(0, g, 7) as model:
             model.set_parameters(saved.parameters)
             check_trajectory(o, params, ids, got, T, 7, last_row_logits(model), cached=False)
+
+
+def test_cli_prompt_file_and_normal_init(tmp_path):
+    # generate --prompt-file: with --batch, one prompt per line (equal token
+    # lengths), sequence b sampled with seed + b; without, the whole file is the
+    # prompt, as --prompt.  generate --config tiny --init normal: the N(0, 0.5)
+    # model.  Each output against the oracle's trajectory.
+    cli = G.CLI_PATH
+    checkpoint = str(tmp_path / "model.bin")
+    corpus = os.path.join(ROOT, "tests", "golden", "mesh-gpt-demo.txt")
+    res = subprocess.run([cli, "init", "--dataset", corpus, "--checkpoint", checkpoint],
+                         capture_output=True, text=True, timeout=60)
+    assert res.returncode == 0, res.stderr
+    saved = G.Checkpoint.load(checkpoint)
+    tokenizer = G.CharacterTokenizer(saved.characters)
+    o = oracle_config(saved.config)
+    params = O.initialize(o, 7)
+    lines = ["the little robot ", "a quiet dog sang "]
+    batch_file, one_file = tmp_path / "prompts.txt", tmp_path / "prompt.txt"
+    batch_file.write_text("\n".join(lines) + "\n")
+    one_file.write_text(lines[1])
+    with G.MeshGpt(0, saved.config, 7) as model:
+        model.set_parameters(saved.parameters)
+        for path, extra, texts in ((batch_file, ["--batch", "2"], lines), (one_file, [], lines[1:])):
+            res = subprocess.run([cli, "generate", "--checkpoint", checkpoint, "--prompt-file", str(path),
+                                  "--tokens", "24", "--temperature", "0.8"] + extra,
+                                 capture_output=True, text=True, timeout=120)
+            assert res.returncode == 0, res.stderr
+            outs = res.stdout.split("\n")[:-1]
+            assert len(outs) == len(texts)
+            for b, (text, out) in enumerate(zip(texts, outs)):
+                assert out.startswith(text)
+                ids = np.array(tokenizer.encode(text), dtype=np.uint32)
+                got = np.array(tokenizer.encode(out), dtype=np.uint32)
+                check_trajectory(o, params, ids, got, 0.8, 7 + b, last_row_logits(model), cached=False)
+    bad = tmp_path / "bad.txt"
+    bad.write_text("the little robot \nshort\n")
+    res = subprocess.run([cli, "generate", "--checkpoint", checkpoint, "--prompt-file", str(bad), "--batch", "2"],
+                         capture_output=True, text=True, timeout=60)
+    assert res.returncode == 1 and "batched prompts must have equal token lengths" in res.stderr
+    res = subprocess.run([cli, "generate", "--checkpoint", checkpoint, "--prompt-file", str(bad), "--batch", "3"],
+                         capture_output=True, text=True, timeout=60)
+    assert res.returncode == 1 and "prompt file must hold one line per sequence (3), found 2" in res.stderr
+    # A synthetic model with N(0, 0.5) weights and a seeded random prompt.
+    tiny = G.named_config("tiny")
+    ot = oracle_config(tiny)
+    res = subprocess.run([cli, "generate", "--config", "tiny", "--init", "normal", "--random-prompt", "16",
+                          "--batch", "1", "--tokens", "32", "--temperature", "0"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 0, res.stderr
+    chars = [0x20 + i for i in range(64)]
+    got = np.array([chars.index(ord(ch)) for ch in res.stdout[:-1]], dtype=np.uint32)
+    prompt = G.random_prompts(64, 1, 16, 7)[0]
+    weights = O.initialize_normal(ot, 7, 0.5)
+    with G.MeshGpt(0, tiny, 7) as model:
+        model.set_parameters(weights)
+        check_trajectory(ot, weights, prompt, got, 0.0, 7, last_row_logits(model))
 
 
 MFMA_SHAPES = [

@@ -163,6 +163,23 @@ def test_initial_parameters_and_codes_bit_equal_oracle(kw):
     assert np.array_equal(G.token_codes(g), O.token_codes(o))
 
 
+@pytest.mark.parametrize("kw", [
+    dict(vocab_size=64, width=128, heads=4, layers=2, attention_mesh_depth=7, ffn_mesh_depth=7, connectivity=1),
+    dict(vocab_size=256, width=512, heads=8, layers=6, attention_mesh_depth=9, ffn_mesh_depth=9, connectivity=1),
+    dict(vocab_size=99, width=16, attention_mesh_depth=6, embedding=1),
+    dict(vocab_size=16, width=32, heads=4, layers=2, preserve_features=3),
+])
+def test_normal_parameters_bit_equal_oracle(kw):
+    # mg_normal_parameters (N(0, sigma^2) weights) equals the oracle's
+    # restatement to the bit, for several seeds and sigmas.
+    g, o = G.GptConfig(**kw), O.config(**kw)
+    for seed, sigma in ((7, 0.5), (0, 1.0), (2**64 - 1, 0.125)):
+        assert np.array_equal(G.normal_parameters(g, seed, sigma).view(np.uint32),
+                              O.initialize_normal(o, seed, sigma).view(np.uint32))
+    with pytest.raises(G.MeshGptError, match="finite nonnegative sigma"):
+        G.normal_parameters(g, 7, -1.0)
+
+
 def test_parameter_counts_of_the_benchmark_configs():
     # 2W(A + L(4A + F)) for the five workloads
     expected = dict(tiny=19712, symbolic=12288, mid=285696, long=193536, high=1249280)
@@ -384,3 +401,14 @@ def test_cli_init_writes_reference_checkpoint(tmp_path):
     assert open(tmp_path / "b.bin", "rb").read(8) == b"MSHGPT08"
     r = _cli("init", "--dataset", DEMO, "--checkpoint", str(tmp_path / "c.bin"), "--connectivity", "Butterfly")
     assert r.returncode == 1
+    # --init normal: N(0, 0.5^2) weights, the oracle's draw to the bit.
+    r = _cli("init", "--dataset", DEMO, "--checkpoint", str(tmp_path / "n.bin"), "--init", "normal")
+    assert r.returncode == 0, r.stderr
+    ck = G.Checkpoint.load(str(tmp_path / "n.bin"))
+    assert np.array_equal(ck.parameters, O.initialize_normal(o, 7, 0.5))
+    r = _cli("init", "--dataset", DEMO, "--checkpoint", str(tmp_path / "s.bin"), "--init", "normal",
+             "--init-sigma", "2", "--seed", "9")
+    assert r.returncode == 0, r.stderr
+    assert np.array_equal(G.Checkpoint.load(str(tmp_path / "s.bin")).parameters, O.initialize_normal(o, 9, 2.0))
+    r = _cli("init", "--dataset", DEMO, "--checkpoint", str(tmp_path / "u.bin"), "--init", "uniform")
+    assert r.returncode == 1 and "unknown initialisation: uniform; use reference or normal" in r.stderr
