@@ -197,6 +197,58 @@ def cpu_baseline(config, prompts, steps, temperature, budget_s):
             "sample": f"cpu-f32-kv, {first['sample']}; {cpu_name()}", "modes": modes}
 
 
+def pmc_traffic(args):
+    """HBM bytes of one bench-step launch, from two rocprofv3 --pmc runs of a
+    child process (FETCH_SIZE, then WRITE_SIZE), each scaled by the same
+    counter on a plain copy kernel of known size.  Every run's return code is
+    reported; a failed run is not repeated."""
+    rocprof = "/opt/rocm/bin/rocprofv3"
+    report = {"runs": []}
+    if not os.path.exists(rocprof):
+        report["error"] = "rocprofv3 not found"
+        return report
+    import csv
+
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        out = tempfile.mkdtemp(prefix="mg_pmc_")
+        cmd = ["timeout", "-s", "KILL", "90", rocprof, "--pmc", counter, "-d", out, "-o", "pmc",
+               "--output-format", "csv", "--", sys.executable, os.path.abspath(__file__), "--probe"]
+        res = subprocess.run(cmd, cwd="/tmp", capture_output=True, text=True)
+        hits, copy = [], []
+        for path in glob.glob(os.path.join(out, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    name = row.get("Kernel_Name", "")
+                    value = float(row.get("Counter_Value", "nan"))
+                    if KERNEL in name and "<4, 2, 16, 9, 64>" in name:
+                        hits.append(value)
+                    elif "calibration_copy" in name:
+                        copy.append(value)
+        # rocprofv3 can end with a segmentation fault after its tool
+        # finalisation when the program made cooperative launches; the
+        # counter file is complete by then, so the rows decide.
+        report["runs"].append({"counter": counter, "rc": res.returncode, "kernel_rows": len(hits),
+                               "copy_rows": len(copy)})
+        if not hits or not copy:
+            report["error"] = f"{counter}: no counter rows (rc {res.returncode}): {res.stderr[-300:]}"
+            return report
+        factor = (PROBE_COPY_BYTES / 1024.0) / float(np.mean(copy))
+        report[counter] = float(np.mean(hits)) * factor * 1024.0
+        report[counter + "_factor"] = factor
+    return report
+
+
+def probe():
+    """Child process under rocprofv3 --pmc: one bench step (the prefill, then
+    the 512-step decode launch) and one plain copy of known size."""
+    config = G.named_config("mid")
+    prompts = G.random_prompts(256, 32, 64, 7)
+    with G.MeshGpt(0, config, 7, max_batch=32) as model:
+        model.prefill(prompts, 1.0, 7, reserve=64 + 1 + DECODE_STEPS)
+        model.decode(DECODE_STEPS)
+    G.calibration_copy(PROBE_COPY_BYTES)
+
+
 def batch1_figure(hip, steps=128):
     """batch 1, 16-token prompt, greedy decode 128 tokens."""
     config = G.named_config("tiny")

@@ -1195,8 +1195,12 @@ struct MeshGpt::Impl {
     }
 
     // `steps` decode steps in one launch of the persistent kernel (the caller
-    // checked decodable(steps) and persistent_usable()).
-    void persistent(size_t steps, uint64_t *trace = nullptr) {
+    // checked decodable(steps) and persistent_usable()).  Returns false, with
+    // nothing changed, when the runtime refuses the cooperative launch: it
+    // does while another process on the GPU holds the device's cooperative
+    // launch resources (hipErrorIllegalState), or when the blocks cannot all
+    // be resident; the caller then runs the per-phase kernels.
+    bool persistent(size_t steps, uint64_t *trace = nullptr) {
         const size_t xstride = kern::persistent_exchange_words(shape);
         check(hipMemsetAsync(pxch.p, 0, batch * xstride * 8, stream), "clear exchange words");
         check(hipMemsetAsync(pabort.p, 0, 4, stream), "clear abort");
@@ -1226,7 +1230,12 @@ struct MeshGpt::Impl {
         a.abort = pabort.as<int>();
         a.trace = trace;
         a.agent_scope = env_int("MG_PERSIST_AGENT_SCOPE", 0) != 0;
-        check(kern::persistent_decode(a, stream), "persistent decode launch");
+        const hipError_t launched = kern::persistent_decode(a, stream);
+        if (launched == hipErrorIllegalState || launched == hipErrorCooperativeLaunchTooLarge) {
+            (void)hipGetLastError();  // the refusal is not a device error
+            return false;
+        }
+        check(launched, "persistent decode launch");
         sync();
         int aborted = 0;
         check(hipMemcpy(&aborted, pabort.p, 4, hipMemcpyDeviceToHost), "download abort flag");
@@ -1236,6 +1245,7 @@ struct MeshGpt::Impl {
         }
         cached = length + steps - 1;
         length += steps;
+        return true;
     }
 };
 
@@ -1302,10 +1312,9 @@ void MeshGpt::generate_tokens(const uint32_t *prompts, size_t batch, size_t prom
         m.step();  // the prompt's prefill and the first token
         ++done;
     }
-    if (done < count && m.decodable(count - done) && m.persistent_usable() && m.persistent_preferred(count - done)) {
-        m.persistent(count - done);
+    if (done < count && m.decodable(count - done) && m.persistent_usable() && m.persistent_preferred(count - done) &&
+        m.persistent(count - done))
         done = count;
-    }
     for (; done < count; ++done) m.step();
     m.finish();
     m.read_tokens(out, batch, prompt_len + count);
@@ -1355,8 +1364,7 @@ void MeshGpt::decode(size_t steps) {
     if (!m.decodable(steps))
         throw Error("decode steps need a prefilled batch and must stay within the context and reserve");
     m.activate();
-    if (m.persistent_usable() && m.persistent_preferred(steps)) {
-        m.persistent(steps);
+    if (m.persistent_usable() && m.persistent_preferred(steps) && m.persistent(steps)) {
         m.finish();
         return;
     }
@@ -1403,7 +1411,10 @@ std::vector<uint64_t> MeshGpt::decode_traced(size_t steps) {
     DevBuf trace;
     trace.ensure(n * 8);
     check(hipMemsetAsync(trace.p, 0, n * 8, m.stream), "clear trace");
-    m.persistent(steps, trace.as<uint64_t>());
+    if (!m.persistent(steps, trace.as<uint64_t>()))
+        throw Error("the runtime refused the persistent decode kernel's cooperative launch (another process may "
+                    "hold the GPU's cooperative launch resources)",
+                    kDeviceError);
     m.finish();
     std::vector<uint64_t> out(n);
     check(hipMemcpy(out.data(), trace.p, n * 8, hipMemcpyDeviceToHost), "download trace");

@@ -462,8 +462,15 @@ def test_cli_prompt_file_and_normal_init(tmp_path):
                                   "--tokens", "24", "--temperature", "0.8"] + extra,
                                  capture_output=True, text=True, timeout=120)
             assert res.returncode == 0, res.stderr
-            outs = res.stdout.split("\n")[:-1]
-            assert len(outs) == len(texts)
+            # Each sequence prints its prompt and 24 generated characters (one
+            # a token; the corpus has a newline character), then a newline.
+            outs, at = [], 0
+            for text in texts:
+                n = len(text) + 24
+                outs.append(res.stdout[at:at + n])
+                assert res.stdout[at + n] == "\n"
+                at += n + 1
+            assert at == len(res.stdout)
             for b, (text, out) in enumerate(zip(texts, outs)):
                 assert out.startswith(text)
                 ids = np.array(tokenizer.encode(text), dtype=np.uint32)
@@ -478,18 +485,25 @@ def test_cli_prompt_file_and_normal_init(tmp_path):
                          capture_output=True, text=True, timeout=60)
     assert res.returncode == 1 and "prompt file must hold one line per sequence (3), found 2" in res.stderr
     # A synthetic model with N(0, 0.5) weights and a seeded random prompt.
+    # This process decodes it first with the persistent kernel, whose
+    # cooperative launch holds the GPU's cooperative launch resources for the
+    # rest of the process; the CLI's own cooperative launch is then refused
+    # (hipErrorIllegalState) and it must fall back to the per-phase kernels,
+    # with the same tokens.
     tiny = G.named_config("tiny")
     ot = oracle_config(tiny)
-    res = subprocess.run([cli, "generate", "--config", "tiny", "--init", "normal", "--random-prompt", "16",
-                          "--batch", "1", "--tokens", "32", "--temperature", "0"],
-                         capture_output=True, text=True, timeout=120)
-    assert res.returncode == 0, res.stderr
-    chars = [0x20 + i for i in range(64)]
-    got = np.array([chars.index(ord(ch)) for ch in res.stdout[:-1]], dtype=np.uint32)
     prompt = G.random_prompts(64, 1, 16, 7)[0]
     weights = O.initialize_normal(ot, 7, 0.5)
     with G.MeshGpt(0, tiny, 7) as model:
         model.set_parameters(weights)
+        here = model.generate_tokens(prompt[None, :], 32, 0.0, 7)[0]
+        res = subprocess.run([cli, "generate", "--config", "tiny", "--init", "normal", "--random-prompt", "16",
+                              "--batch", "1", "--tokens", "32", "--temperature", "0"],
+                             capture_output=True, text=True, timeout=120)
+        assert res.returncode == 0, res.stderr
+        chars = [0x20 + i for i in range(64)]
+        got = np.array([chars.index(ord(ch)) for ch in res.stdout[:-1]], dtype=np.uint32)
+        assert np.array_equal(got, here)
         check_trajectory(ot, weights, prompt, got, 0.0, 7, last_row_logits(model))
 
 
