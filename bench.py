@@ -13,7 +13,9 @@ device copies: mg_decode_rewind), so every step decodes the same 16384 tokens
 from inputs resident in HBM.  `value` is tokens/s over the K timed steps by
 the host clock between device synchronisations; the roofline divides the
 algorithmic HBM bytes of one launch by the launch's average duration from HIP
-events recorded on the model's stream around it.
+events that the library records on the model's stream right before and after
+the kernel (mg_last_call_ms); avg_call_us adds the launch and the host's
+return from the call's synchronisation.
 
 Beside the headline: the first 20 decode steps alone (the latency-bound
 short-context end), config 1 at batch 1, config 2's single 9409-row prefill,
@@ -97,13 +99,24 @@ def decode_bytes(config, batch, first, steps):
 
 
 def timed_decode(hip, model, steps):
-    """model.decode(steps) bracketed by HIP events on the model's stream (ms)."""
+    """model.decode(steps) bracketed by HIP events on the model's stream (ms):
+    the call's device work, its launch and the host's return from its
+    synchronisation."""
     stream = model.stream()
     start, stop = hip.event(), hip.event()
     hip.record(start, stream)
     model.decode(steps)
     hip.record(stop, stream)
     return hip.elapsed_ms(start, stop)
+
+
+def timed_launch(hip, model, steps):
+    """(kernel ms, call ms) of model.decode(steps) in one persistent launch:
+    the library's HIP events recorded on the model's stream right before and
+    after the kernel (mg_last_call_ms), and timed_decode's bracket of the
+    whole call."""
+    call = timed_decode(hip, model, steps)
+    return model.last_call_ms(), call
 
 
 def cpu_name():
@@ -450,16 +463,22 @@ def main():
             model.rewind()
             model.decode(DECODE_STEPS)
         hip.synchronize()
-        launch_ms = []
+        launch_ms, call_ms = [], []
         t0 = time.perf_counter()
         for _ in range(args.steps):
             model.rewind()
-            launch_ms.append(timed_decode(hip, model, DECODE_STEPS))
+            kernel, call = timed_launch(hip, model, DECODE_STEPS)
+            launch_ms.append(kernel)
+            call_ms.append(call)
         hip.synchronize()
         wall_s = time.perf_counter() - t0
-        # The latency-bound end alone: the first 20 decode steps.
-        model.rewind()
-        early_ms = timed_decode(hip, model, 20)
+        # The latency-bound end alone: the first 20 decode steps (median of 5 launches).
+        early = []
+        for _ in range(5):
+            model.rewind()
+            early.append(timed_launch(hip, model, 20))
+        early_ms = float(np.median([e[0] for e in early]))
+        early_call_ms = float(np.median([e[1] for e in early]))
 
     avg_ms = float(np.mean(launch_ms))
     launch_bytes = decode_bytes(config, batch, prompt_len, DECODE_STEPS)
@@ -501,12 +520,17 @@ def main():
             "algorithmic_bytes_per_launch": round(launch_bytes),
             "avg_launch_us": round(avg_ms * 1000.0, 1),
             "launch_us": [round(m * 1000.0, 1) for m in launch_ms],
+            "timing": "HIP events recorded by the library on the model's stream right before and after "
+                      "the kernel launch (mg_last_call_ms)",
+            "avg_call_us": round(float(np.mean(call_ms)) * 1000.0, 1),
         },
         "early_slice": {
             "positions": f"{prompt_len}..{prompt_len + 19}",
             "us_per_decode_step": round(1000.0 * early_ms / 20, 2),
             "tokens_per_s": round(batch * 20 / (early_ms / 1000.0), 1),
             "hbm_frac": round(early_bytes / (early_ms / 1000.0) / 1e9 / HBM_PEAK_GBPS, 4),
+            "timing": "kernel events, median of 5 launches of 20 steps",
+            "call_us_per_decode_step": round(1000.0 * early_call_ms / 20, 2),
         },
     }
     if pmc is not None:

@@ -395,7 +395,8 @@ class MeshGpt:
         _check(lib().mg_decode(self._h, steps))
 
     def last_call_ms(self):
-        """Kernel time of the last logits / hidden_states / prefill call (ms)."""
+        """Kernel time of the last logits / hidden_states / prefill call, or
+        of the last persistent decode launch (ms)."""
         ms = ctypes.c_float()
         _check(lib().mg_last_call_ms(self._h, ctypes.byref(ms)))
         return ms.value

@@ -955,10 +955,11 @@ int run(int argc, char **argv) {
         std::cout << "Saved seed-" << o.seed << " checkpoint to " << checkpoint << "\n";
         return 0;
     }
-    if (o.command == "grok-simple" || o.command == "verify")
-        throw Error("the " + o.command +
-                    " command is not part of this build; it provides train, generate and grok (parity checks live "
-                    "in tests/)");
+    if (o.command == "verify")
+        throw Error("the verify command is not part of this CLI, which does not link the CPU oracle: run python "
+                    "tests/verify.py (the reference's model checks, GPU against the oracle)");
+    if (o.command == "grok-simple")
+        throw Error("the grok-simple command is not part of this build; it provides train, generate and grok");
     throw Error("unknown command: " + o.command + "; use train, generate, grok or init");
 }
 

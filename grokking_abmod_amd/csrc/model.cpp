@@ -1031,13 +1031,17 @@ struct MeshGpt::Impl {
     // streams: while one slice's attention streams its keys (memory-bound),
     // another's row blocks run (latency-bound).  Config 5 (batch 256):
     // 1231 us per step in one stream, 1072 in two slices, 1062 in four.
-    // Slices need at least 32 sequences each and the fused head-and-sampler
-    // kernel.  MG_DECODE_SLICES overrides the count (1 = one stream).
+    // Slices need at least 32 sequences each, or 4 once the sequences attend
+    // over 2048 keys or more (config 4, batch 8 at 8192 keys: 248 us per step
+    // in one stream, 237 in two slices), and the fused head-and-sampler
+    // kernel.  MG_DECODE_SLICES overrides the count (1 = one stream),
+    // MG_DECODE_SLICE_MIN the sequences a slice needs.
     int decode_slices() const {
         const int want = std::min(env_int("MG_DECODE_SLICES", 2), kMaxSlices);
         if (kern::head_sample_lds_bytes(shape) > lds_limit) return 1;
+        const size_t least = size_t(env_int("MG_DECODE_SLICE_MIN", length >= 2048 ? 4 : 32));
         for (int n = want; n > 1; --n)
-            if (batch >= size_t(32 * n)) return n;
+            if (batch >= least * n) return n;
         return 1;
     }
 
@@ -1230,13 +1234,18 @@ struct MeshGpt::Impl {
         a.abort = pabort.as<int>();
         a.trace = trace;
         a.agent_scope = env_int("MG_PERSIST_AGENT_SCOPE", 0) != 0;
+        // Events on the stream right around the kernel: last_call_ms() is
+        // the launch's own duration.
+        mark_call(0);
         const hipError_t launched = kern::persistent_decode(a, stream);
         if (launched == hipErrorIllegalState || launched == hipErrorCooperativeLaunchTooLarge) {
             (void)hipGetLastError();  // the refusal is not a device error
             return false;
         }
         check(launched, "persistent decode launch");
+        mark_call(1);
         sync();
+        close_call();
         int aborted = 0;
         check(hipMemcpy(&aborted, pabort.p, 4, hipMemcpyDeviceToHost), "download abort flag");
         if (aborted) {

@@ -195,9 +195,11 @@ int mg_decode_traced(mg_model *model, size_t steps, uint64_t *stamps, size_t n);
  * allocated. */
 int mg_decode_rewind(mg_model *model);
 /* Device time in milliseconds of the kernels of the last mg_logits,
- * mg_hidden_states or mg_prefill call on this model (HIP events on the
+ * mg_hidden_states or mg_prefill call on this model, or of the last
+ * persistent decode launch (mg_decode, mg_generate) (HIP events on the
  * model's stream around its kernels; host copies excluded).  No reference
- * counterpart: it lets a benchmark time a prefill without the PCIe copies. */
+ * counterpart: it lets a benchmark time a prefill without the PCIe copies and
+ * a decode launch without the host's synchronisation. */
 int mg_last_call_ms(mg_model *model, float *ms);
 /* Current tokens per sequence (prompt + generated). */
 int mg_sequence_length(const mg_model *model, size_t *out);

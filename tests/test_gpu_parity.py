@@ -96,6 +96,21 @@ def test_verify_model_logits(cfg, cases):
             assert np.array_equal(full[:2], model.logits([0, 1], 2))
 
 
+def test_verify_command_quick_run():
+    # tests/verify.py, this build's `mesh-gpt verify` (mesh-gpt.rs:624-896),
+    # on its first three models and one geometry: one PASS line each, exit 0.
+    import subprocess
+    import sys
+
+    here = __import__("os").path.dirname(__import__("os").path.abspath(__file__))
+    res = subprocess.run([sys.executable, __import__("os").path.join(here, "verify.py"), "--quick"],
+                         capture_output=True, text=True, timeout=300)
+    assert res.returncode == 0, res.stderr
+    lines = res.stdout.splitlines()
+    assert len(lines) == 4 and all(line.startswith("PASS ") for line in lines), res.stdout
+    assert "AdamW beta2=0.999/0.98/reset, zero-weight behavior" in lines[0]
+
+
 def test_rejections_match_reference_messages():
     g, o = configs_for(vocab_size=5, context=4, width=4, heads=2, layers=1, attention_mesh_depth=2,
                        ffn_mesh_depth=2)

@@ -379,7 +379,7 @@ def test_cli_help_and_argument_errors():
     r = _cli("generate", "--temperature", "-1")
     assert r.returncode == 1 and "temperature must be finite and nonnegative" in r.stderr
     r = _cli("verify")
-    assert r.returncode == 1 and "not part of this build" in r.stderr
+    assert r.returncode == 1 and "run python tests/verify.py" in r.stderr
     r = _cli("train", "--dataset", "/nonexistent/corpus.txt")
     assert r.returncode == 1 and "cannot open dataset /nonexistent/corpus.txt" in r.stderr
 
