@@ -1750,6 +1750,28 @@ __device__ __forceinline__ void load_vec(const float *__restrict__ p, float (&o)
     }
 }
 
+// load_vec with the non-temporal cache policy.
+template <int N>
+__device__ __forceinline__ void load_vec_nt(const float *__restrict__ p, float (&o)[N]) {
+    if constexpr (N % 4 == 0) {
+        typedef float f4 __attribute__((ext_vector_type(4)));
+#pragma unroll
+        for (int i = 0; i < N / 4; ++i) {
+            const f4 t = __builtin_nontemporal_load(reinterpret_cast<const f4 *>(p) + i);
+            o[4 * i] = t.x;
+            o[4 * i + 1] = t.y;
+            o[4 * i + 2] = t.z;
+            o[4 * i + 3] = t.w;
+        }
+    } else {
+        static_assert(N == 2, "vector width");
+        typedef float f2 __attribute__((ext_vector_type(2)));
+        const f2 t = __builtin_nontemporal_load(reinterpret_cast<const f2 *>(p));
+        o[0] = t.x;
+        o[1] = t.y;
+    }
+}
+
 template <int HDP, int TH = 0>
 struct DecodeCfg {
     static constexpr int VEC = HDP <= 4 ? HDP : (HDP / 64 > 4 ? HDP / 64 : 4);  // dims per lane
@@ -1779,6 +1801,17 @@ struct AttnRound {
             const uint32_t at = uint32_t(min(j0 + u * G + int(g), end - 1)) * HDP + d0;
             load_vec<VEC>(kslab + at, k[u]);
             load_vec<VEC>(vslab + at, v[u]);
+        }
+    }
+    // The same with the non-temporal cache policy.
+    __device__ __forceinline__ void load_nt(const float *__restrict__ kslab, const float *__restrict__ vslab, int j0,
+                                            int end) {
+        const uint32_t g = threadIdx.x / LPK, d0 = (threadIdx.x % LPK) * VEC;
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const uint32_t at = uint32_t(min(j0 + u * G + int(g), end - 1)) * HDP + d0;
+            load_vec_nt<VEC>(kslab + at, k[u]);
+            load_vec_nt<VEC>(vslab + at, v[u]);
         }
     }
 };
@@ -1974,7 +2007,7 @@ struct AttnState {
 template <int HDP>
 __device__ __forceinline__ void attn_share(const float *__restrict__ qh, int hd, const float *__restrict__ kslab,
                                            const float *__restrict__ vslab, int start, int end, float scale_log2,
-                                           float *__restrict__ out) {
+                                           float *__restrict__ out, int keep = 1 << 30) {
     using S = AttnState<HDP, 0>;
     using R = typename S::R;
     constexpr int VEC = S::VEC, LPK = S::LPK, G = S::G, U = S::U;
@@ -1992,8 +2025,13 @@ __device__ __forceinline__ void attn_share(const float *__restrict__ qh, int hd,
     for (int e = 0; e < VEC; ++e) qr[e] = d0 + e < hd ? qh[d0 + e] : 0.0f;
     S st;
     for (int j0 = start; j0 < end; j0 += G * U) {
+        // Rows past the first `keep` load with the non-temporal policy
+        // (kv_keep_rows).
         R cur;
-        cur.load(kslab, vslab, j0, end);
+        if (j0 + G * U > keep)
+            cur.load_nt(kslab, vslab, j0, end);
+        else
+            cur.load(kslab, vslab, j0, end);
         st.add(qr, cur, j0, end, scale_log2);
     }
     __shared__ float sm[G], sl[G];
@@ -2023,7 +2061,7 @@ attn_decode_kernel(Shape s, const float *__restrict__ q, KvView kv, const int *_
     const int end = min(start + chunk, keys);
     const size_t slab = size_t(b * s.H + h) * kv.cap * HDP;
     attn_share<HDP>(q + size_t(b) * s.W + h * s.hd, s.hd, kv.k + slab, kv.v + slab, start, end, scale_log2,
-                    part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2));
+                    part + (size_t(b * s.H + h) * nsplit + split) * (HDP + 2), kv.keep);
 }
 
 template <int HDP>
@@ -2829,6 +2867,21 @@ __device__ __forceinline__ void lds_dma16(const float *g, float *l) {
         : "memory");
 }
 
+// lds_dma16 with the non-temporal cache policy.
+__device__ __forceinline__ void lds_dma16_nt(const float *g, float *l) {
+    const uint32_t m = __builtin_amdgcn_readfirstlane(uint32_t(size_t((lds_float *)l)));
+    uint32_t save;
+    asm volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %1\n\t"
+        "s_waitcnt lgkmcnt(0)\n\t"
+        "global_load_lds_dwordx4 %2, off nt\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(save)
+        : "s"(m), "v"(g)
+        : "memory");
+}
+
 template <int N>
 __device__ __forceinline__ void wait_vmem() {
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -2844,9 +2897,20 @@ struct KvRing {
     static constexpr int SLOT = CH * NW * 256;  // floats
     static_assert(VEC == 4, "a lane's part of a row must be one 16-byte load");
     float *buf;  // NS * SLOT floats
-    __device__ void issue(const float *kl, const float *vl, int r, int end, int tid) const {
+    // Rounds that reach past the first `keep` rows load with the
+    // non-temporal policy (kv_keep_rows).
+    __device__ void issue(const float *kl, const float *vl, int r, int end, int tid, int keep = 1 << 30) const {
         const int g = tid / LPK, d0 = (tid % LPK) * VEC, wave = tid >> 6;
         float *slot = buf + (r % NS) * SLOT + wave * 256;
+        if ((r + 1) * G * UL > keep) {
+#pragma unroll
+            for (int u = 0; u < UL; ++u) {
+                const uint32_t at = uint32_t(min(r * G * UL + u * G + g, end - 1)) * HDP + d0;
+                lds_dma16_nt(kl + at, slot + (2 * u) * NW * 256);
+                lds_dma16_nt(vl + at, slot + (2 * u + 1) * NW * 256);
+            }
+            return;
+        }
 #pragma unroll
         for (int u = 0; u < UL; ++u) {
             const uint32_t at = uint32_t(min(r * G * UL + u * G + g, end - 1)) * HDP + d0;
@@ -3457,10 +3521,15 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // Layer 0's first rounds were issued at the end of the previous
             // step (below), before its logits and draw.
             if (l > 0 || step == 0)
-                for (int r = 0; r < min(NS, nring); ++r) ring.issue(kl, vl, r, pos, tid);
+                for (int r = 0; r < min(NS, nring); ++r) ring.issue(kl, vl, r, pos, tid, a.mall_keep);
             R last, last2;
-            if (ntail > 0) last.load(kl, vl, nring * G * U, pos);
-            if (ntail > 1) last2.load(kl, vl, (nring + 1) * G * U, pos);
+            if ((nring + 1) * G * U > a.mall_keep) {
+                if (ntail > 0) last.load_nt(kl, vl, nring * G * U, pos);
+                if (ntail > 1) last2.load_nt(kl, vl, (nring + 1) * G * U, pos);
+            } else {
+                if (ntail > 0) last.load(kl, vl, nring * G * U, pos);
+                if (ntail > 1) last2.load(kl, vl, (nring + 1) * G * U, pos);
+            }
             float qr[VEC], kn[VEC], vn[VEC];
             if (l == 0) {
                 typedef __attribute__((address_space(1))) const float gfloat;
@@ -3534,8 +3603,8 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     R c0, c1;
                     ring.read(r, c0, tid);
                     ring.read(r + 1, c1, tid);
-                    if (r + 2 < nring) ring.issue(kl, vl, r + 2, pos, tid);
-                    if (r + 3 < nring) ring.issue(kl, vl, r + 3, pos, tid);
+                    if (r + 2 < nring) ring.issue(kl, vl, r + 2, pos, tid, a.mall_keep);
+                    if (r + 3 < nring) ring.issue(kl, vl, r + 3, pos, tid, a.mall_keep);
                     st.add2(qr, c0, r * G * U, c1, (r + 1) * G * U, pos, a.scale_log2);
                 }
                 if (r < nring) {
@@ -3549,7 +3618,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     ring.wait(min(NS - 1, nring - 1 - r));
                     R cur;
                     ring.read(r, cur, tid);
-                    if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid);
+                    if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid, a.mall_keep);
                     st.add(qr, cur, r * G * U, pos, a.scale_log2);
                 }
             }
@@ -3605,7 +3674,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             const int p1 = pos + 1, nr1 = (p1 + G * U - 1) / (G * U);
             const int nring1 = nr1 - min(max(nr1 - NS, 0), 2);
             const float *kl0 = a.kc + slab, *vl0 = a.vc + slab;
-            for (int r = 0; r < min(NS, nring1); ++r) ring.issue(kl0, vl0, r, p1, tid);
+            for (int r = 0; r < min(NS, nring1); ++r) ring.issue(kl0, vl0, r, p1, tid, a.mall_keep);
         }
         const Ctx c(m.xch, m.red, tid);
         persistent_head_logits<NW, CPL, GL>(a, c, xc, step, 3 + h, m);
@@ -4140,6 +4209,15 @@ bool persistent_fits(const Shape &s, int batch, int device) {
     if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, f, 64 * row_waves(s.W), 0) != hipSuccess) return false;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess) return false;
     return persistent_blocks(s, batch) <= per_cu * cus;
+}
+
+int kv_keep_rows(const Shape &s, int batch, int layers) {
+    const char *env = std::getenv("MG_MALL_BYTES");
+    const double cache = env && *env ? std::atof(env) : 256.0 * 1024 * 1024;
+    const double per_row = double(batch) * layers * s.H * 2.0 * s.hdp * 4.0;
+    if (per_row <= 0.0) return 1 << 30;
+    const double rows = 0.8 * cache / per_row;
+    return rows >= double(1 << 30) ? 1 << 30 : int(rows);
 }
 
 hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream) {

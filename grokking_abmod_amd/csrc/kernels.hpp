@@ -49,6 +49,9 @@ struct KvView {
     float *k;
     float *v;
     int cap;
+    // Decode attention reads rows past the first `keep` of a slab with the
+    // non-temporal cache policy (kv_keep_rows); prefill ignores it.
+    int keep = 1 << 30;
 };
 
 // One block_kernel launch: the post-attention half of block l-1 (when wproj
@@ -162,6 +165,9 @@ struct PersistArgs {
     // launch's handshake otherwise chooses where it can (for testing that
     // protocol; MG_PERSIST_AGENT_SCOPE=1).
     int agent_scope;
+    // Cached K/V rows at or past this position load with the non-temporal
+    // cache policy (kv_keep_rows).
+    int mall_keep;
     // Optional timeline (nullptr: none): for block k, step t and phase l,
     // trace[((k * steps + t) * (layers + 1) + l) * 2 + {0, 1}] receive the
     // wall clock (100 MHz) when the phase's inputs were ready and when its
@@ -172,6 +178,17 @@ struct PersistArgs {
     uint64_t *trace;
 };
 bool persistent_fits(const Shape &s, int batch, int device);
+// The cached rows of each (sequence, layer, head) that decode attention reads
+// with the default cache policy when `batch` sequences decode: the first rows
+// of every slab, as many as keep about 80 % of the MI355X's 256 MiB memory-side
+// cache (Infinity Cache) for them (MG_MALL_BYTES overrides its size); rows
+// past them load with the non-temporal policy.  Read every step and larger
+// in total than the cache, the cache rows would otherwise be evicted before
+// their reuse by rows read once per step (least recently used replacement
+// over a cyclic pass); kept this way, the prefix stays resident across steps
+// and only the rest streams from HBM (config 3 at batch 32: 27.4 against
+// 30.8 ms per 512-step launch).
+int kv_keep_rows(const Shape &s, int batch, int layers);
 // Exchange words of one sequence: q/k/v of two layer phases, the attention
 // output, the normalised final row, the logits and each workgroup's XCD.
 size_t persistent_exchange_words(const Shape &s);

@@ -539,9 +539,15 @@ struct MeshGpt::Impl {
         }
     }
 
+    // Rows of each cached slab that decode attention reads with the default
+    // cache policy (kern::kv_keep_rows; MG_KV_KEEP_ROWS overrides it).
+    int keep_rows() const {
+        return env_int("MG_KV_KEEP_ROWS", kern::kv_keep_rows(shape, int(std::max<size_t>(batch, 1)), int(cfg.layers)));
+    }
+
     kern::KvView cache_layer(size_t l) const {
         const size_t off = l * layer_cache_elems();
-        return kern::KvView{kc.as<float>() + off, vc.as<float>() + off, int(cfg.context)};
+        return kern::KvView{kc.as<float>() + off, vc.as<float>() + off, int(cfg.context), keep_rows()};
     }
 
     // Forward over a flat batch of sequences with a one-layer KV workspace
@@ -1234,6 +1240,7 @@ struct MeshGpt::Impl {
         a.abort = pabort.as<int>();
         a.trace = trace;
         a.agent_scope = env_int("MG_PERSIST_AGENT_SCOPE", 0) != 0;
+        a.mall_keep = keep_rows();
         // Events on the stream right around the kernel: last_call_ms() is
         // the launch's own duration.
         mark_call(0);
