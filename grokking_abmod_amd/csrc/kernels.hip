@@ -128,6 +128,25 @@ __device__ __forceinline__ float elu(float z) {
     return __builtin_elementwise_maximum(z, e - 1.0f);
 }
 
+// The row meshes (row_layer and the functions built on it) carry their values
+// scaled by log2(e), t = z log2(e): a layer's sum then feeds exp2 directly and
+// the ELU in those units, elu(z) log2(e) = max(t, log2(e) (clamp(exp2(t), 0,
+// 1) - 1)), takes one instruction fewer than elu() on every value of every
+// layer.  NaN and the infinities behave as in elu().  The scale enters with
+// the RMSNorm factor (inv_rms_log2) or one multiply in front of a mesh and
+// leaves in the residual add (an FMA by ln 2) or one multiply after it.
+constexpr float kLog2e = 1.4426950408889634f, kLn2 = 0.6931471805599453f;
+__device__ __forceinline__ float elu_log2(float t) {
+    const float e = __builtin_amdgcn_fmed3f(__builtin_amdgcn_exp2f(t), 0.0f, 1.0f);
+    return __builtin_elementwise_maximum(t, fmaf(e, kLog2e, -kLog2e));
+}
+
+// log2(e) / sqrt(sumsq / W + eps): the RMSNorm factor of a row of W values
+// with sum of squares sumsq, scaled for a row mesh.
+__device__ __forceinline__ float inv_rms_log2(float sumsq, int W) {
+    return rsqrtf(sumsq * (1.0f / (float(W) * kLog2e * kLog2e)) + kRmsEps / (kLog2e * kLog2e));
+}
+
 // Flat LDS index -> (row, column) for rows of length W.
 __device__ __forceinline__ void split_row(int idx, const Shape &s, int &r, int &c) {
     if (s.wshift >= 0) {
@@ -1073,7 +1092,7 @@ __device__ __forceinline__ void row_layer(float (&x)[CPL], const float2 (&w)[CPL
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
         const float z = x[j] * w[j].x + p[j] * w[j].y;
-        x[j] = last ? z : elu(z);
+        x[j] = last ? z : elu_log2(z);
     }
 }
 
@@ -1184,7 +1203,8 @@ struct RowCtx {
     __device__ float *slot(int k) const { return red + k * SLOT; }
 };
 
-// A mesh stack on the row: fixed depth (weights in registers) or any depth.
+// A mesh stack on the row: fixed depth (weights in registers) or any depth;
+// x in and out in the log2(e)-scaled units of row_layer.
 template <int NW, int CPL, int GL, int D>
 __device__ __forceinline__ void row_run_mesh(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], const float2 (&w)[D][CPL],
                                              const float *wg, int depth, const Shape &s, bool fixed) {
@@ -1218,7 +1238,8 @@ __device__ __forceinline__ float row_inv_rms(RowCtx<NW, CPL, GL> &c, const float
     return rsqrtf(row_total<NW>(acc, c.lane, c.wave, c.slot(k)) * (1.0f / float(c.W)) + kRmsEps);
 }
 
-// n = mesh(x * inv_rms(x)) for a compile-time-depth mesh whose first stride
+// n = mesh(x * inv_rms(x)), scaled by log2(e) (elu_log2), for a
+// compile-time-depth mesh whose first stride
 // (1) crosses waves: the row reduction of the RMSNorm and that layer's LDS
 // exchange share one barrier (x is exchanged and each lane scales its partner
 // itself).  Same arithmetic as row_inv_rms, then row_run_mesh on x * inv.
@@ -1243,7 +1264,7 @@ __device__ __forceinline__ void row_rms_mesh(RowCtx<NW, CPL, GL> &c, const float
     float t = 0.0f;
 #pragma unroll
     for (int v = 0; v < NW; ++v) t += red[v];
-    const float inv = rsqrtf(t * (1.0f / float(W)) + kRmsEps);
+    const float inv = inv_rms_log2(t, W);
     // Partner of channel c is c + 1: the next wave, or wave 0 one lane on.
     int w2 = wave + 1, l2 = lane, jc = 0;
     if (w2 >= NW) {
@@ -1259,7 +1280,7 @@ __device__ __forceinline__ void row_rms_mesh(RowCtx<NW, CPL, GL> &c, const float
         const int j2 = j + jc < CPL ? j + jc : 0;
         const float nx = x[j] * inv, np = b[(j2 * NW + w2) * 64 + l2] * inv;
         const float z = nx * w[0][j].x + np * w[0][j].y;
-        n[j] = D == 1 ? z : elu(z);
+        n[j] = D == 1 ? z : elu_log2(z);
     }
     static_for<D>([&](auto U) {
         constexpr int u = decltype(U)::value;
@@ -1276,23 +1297,25 @@ __device__ __forceinline__ void row_post(RowCtx<NW, CPL, GL> &c, float (&x)[CPL]
                                          const float2 (&wf)[D][CPL], const float *gp, const float *gf,
                                          const Shape &s, bool fixed) {
     if constexpr (XSA) row_xsa(c, y, v);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) y[j] *= kLog2e;
     row_run_mesh(c, y, wp, gp, s.A, s, fixed);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) x[j] += y[j];
+    for (int j = 0; j < CPL; ++j) x[j] = fmaf(y[j], kLn2, x[j]);
     if constexpr (NW > 1 && D > 1) {
         if (fixed) {
             row_rms_mesh(c, x, y, wf, 2);
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) x[j] += y[j];
+            for (int j = 0; j < CPL; ++j) x[j] = fmaf(y[j], kLn2, x[j]);
             return;
         }
     }
-    const float inv = row_inv_rms(c, x, 2);
+    const float inv = row_inv_rms(c, x, 2) * kLog2e;
 #pragma unroll
     for (int j = 0; j < CPL; ++j) y[j] = x[j] * inv;
     row_run_mesh(c, y, wf, gf, s.F, s, fixed);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) x[j] += y[j];
+    for (int j = 0; j < CPL; ++j) x[j] = fmaf(y[j], kLn2, x[j]);
 }
 
 // QK-Norm per head, then split-half RoPE (reference.rs:462-482) at the position
@@ -1394,7 +1417,11 @@ row_block_kernel(BlockArgs a) {
     }
     if (!pre) return;
 
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] *= kLog2e;
     row_run_mesh(c, x, wm, wmine, s.A, s, FIXED);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] *= kLn2;
     const size_t cache_row = size_t(seq * s.H) * a.kv_pre.cap + pos;  // + head * cap, then * hdp
     if (team == 2) {
 #pragma unroll
@@ -1937,10 +1964,19 @@ struct AttnState {
             const float M = group_max<G>(mk);
             const float f = exp2_fast(mk - M);
             const float L = group_sum<G>(f * lk);
-            float a = 0.0f;
+            // Four partial sums over the groups k = i (mod 4), added
+            // pairwise: a chain of G/4 + 2 dependent adds instead of G.
+            constexpr int P = G >= 4 ? 4 : G;
+            float part[P];
+#pragma unroll
+            for (int i = 0; i < P; ++i) part[i] = 0.0f;
 #pragma unroll
             for (int kk = 0; kk < G; ++kk)
-                a = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), kk)), ak[kk], a);
+                part[kk % P] = fmaf(__builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, f), kk)),
+                                    ak[kk], part[kk % P]);
+            float a = part[0];
+            if constexpr (P == 4) a = (part[0] + part[1]) + (part[2] + part[3]);
+            else if constexpr (P == 2) a = part[0] + part[1];
             y = lane < HDP ? a * __builtin_amdgcn_rcpf(L) : 0.0f;
         }
         return y;
@@ -2774,6 +2810,7 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 // range), so a broken hand-off ends the launch with an error, not a hang.
 
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
+constexpr uint32_t kPollCheck = 16;        // polls between checks of the abort flag and the clock
 constexpr int kPersistVocab = 1024;        // largest vocabulary of the persistent path
 static_assert(kPersistVocab <= kWaveSampleVocab, "the persistent path draws with the wave sampler");
 
@@ -2815,20 +2852,23 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
     };
     if (!__all(ready())) {
         const uint64_t t0 = wall_clock64();
-        while (true) {
+        for (uint32_t n = 1;; ++n) {
             __builtin_amdgcn_s_sleep(1);
             asm volatile("" ::: "memory");  // the words change under us: load them again
             // Every word again (no per-word branch, whose evaluation would
-            // wait inside the loop), and the abort flag with them: one memory
-            // round trip per poll.
+            // wait inside the loop): one memory round trip per poll.  The
+            // abort flag (an agent-scope load, slower than the words') and
+            // the clock are read every kPollCheck polls only, so they do not
+            // lengthen the polls that find the words.
 #pragma unroll
             for (int i = 0; i < N; ++i) w[i] = get_word(addr(i), local);
-            const int stop = __hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             if (__all(ready())) break;
-            if (stop != 0) break;
-            if (wall_clock64() - t0 > kWaitTicks) {
-                if ((threadIdx.x & 63) == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-                break;
+            if (n % kPollCheck == 0) {
+                if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
+                if (wall_clock64() - t0 > kWaitTicks) {
+                    if ((threadIdx.x & 63) == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                    break;
+                }
             }
         }
     }
@@ -3139,7 +3179,8 @@ __device__ __forceinline__ void load_mesh_far(float2 (&w)[CPL], const float *wg,
     for (int j = 0; j < CPL; ++j) w[j] = __builtin_bit_cast(float2, uint64_t(g[row_of<NW>((c.chan(j) + 2) & (W - 1))]));
 }
 
-// n = mesh(x), or mesh(x * inv_rms(x)) with RMS, for a mesh whose first two
+// n = mesh(x), or mesh(x * inv_rms(x)) with RMS, in the log2(e)-scaled units
+// of row_layer (x itself scaled without RMS), for a mesh whose first two
 // strides cross waves: one LDS exchange serves both layers (each lane reads
 // channels c + 1 .. c + 3 and computes layer 0 of channel c + 2 as well, with
 // its weights w0far), and with RMS the row reduction shares its barrier.  The
@@ -3169,7 +3210,7 @@ __device__ __forceinline__ void row_mesh2(RowCtx<NW, CPL, GL> &c, const float (&
         float t = 0.0f;
 #pragma unroll
         for (int v = 0; v < NW; ++v) t += red[v];
-        inv = rsqrtf(t * (1.0f / float(W)) + kRmsEps);
+        inv = inv_rms_log2(t, W);
     }
     auto scaled = [&](float v) { return RMS ? v * inv : v; };
 #pragma unroll
@@ -3177,9 +3218,9 @@ __device__ __forceinline__ void row_mesh2(RowCtx<NW, CPL, GL> &c, const float (&
         const int ch = c.chan(j);
         const float n0 = scaled(x[j]), n1 = scaled(b[row_of<NW>((ch + 1) & (W - 1))]);
         const float n2 = scaled(b[row_of<NW>((ch + 2) & (W - 1))]), n3 = scaled(b[row_of<NW>((ch + 3) & (W - 1))]);
-        const float z0 = elu(n0 * w[0][j].x + n1 * w[0][j].y);
-        const float z2 = elu(n2 * w0far[j].x + n3 * w0far[j].y);
-        n[j] = elu(z0 * w[1][j].x + z2 * w[1][j].y);
+        const float z0 = elu_log2(n0 * w[0][j].x + n1 * w[0][j].y);
+        const float z2 = elu_log2(n2 * w0far[j].x + n3 * w0far[j].y);
+        n[j] = elu_log2(z0 * w[1][j].x + z2 * w[1][j].y);
     }
     static_for<D>([&](auto U) {
         constexpr int u = decltype(U)::value;
@@ -3194,13 +3235,15 @@ template <int NW, int CPL, int GL, int D>
 __device__ __forceinline__ void team_post_mesh2(RowCtx<NW, CPL, GL> &c, float (&x)[CPL], const float (&y)[CPL],
                                                 const float2 (&wp)[D][CPL], const float2 (&wp2)[CPL],
                                                 const float2 (&wf)[D][CPL], const float2 (&wf2)[CPL]) {
-    float t[CPL];
-    row_mesh2<false>(c, y, t, wp, wp2, 2);
+    float t[CPL], ys[CPL];
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) x[j] += t[j];
+    for (int j = 0; j < CPL; ++j) ys[j] = y[j] * kLog2e;
+    row_mesh2<false>(c, ys, t, wp, wp2, 2);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) x[j] = fmaf(t[j], kLn2, x[j]);
     row_mesh2<true>(c, x, t, wf, wf2, 2);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) x[j] += t[j];
+    for (int j = 0; j < CPL; ++j) x[j] = fmaf(t[j], kLn2, x[j]);
 }
 
 template <int NW, int CPL, int GL, int D>
@@ -3413,14 +3456,14 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
             } else if constexpr (FIXED && NW > 1) {
                 row_rms_mesh(c, x, n, wm, 3);
             } else {
-                const float inv = row_inv_rms(c, x, 3);
+                const float inv = row_inv_rms(c, x, 3) * kLog2e;
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
                 row_run_mesh(c, n, wm, wb + team * gA, s.A, s, FIXED);
             }
             uint64_t *out = xc.qkv(g, team);
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) xc.put(out + c.ridx(j), n[j], g + 1);
+            for (int j = 0; j < CPL; ++j) xc.put(out + c.ridx(j), n[j] * kLn2, g + 1);
             trace_mark(a, xc.row, step, l, 1);
         }
         persistent_last_block<NW, CPL, GL, DEPTH>(a, c, x, xc, step, team, m);
@@ -3515,8 +3558,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             // The first NS rounds load into the ring, and the last two rounds
             // into registers, while the layer's meshes still run (the online
             // softmax takes rounds in any order).
+            // Past layer 0, keys that fit two rounds load straight into
+            // registers (no LDS ring to fill and read); layer 0's rounds load
+            // before the previous step's logits and draw, which need the
+            // registers, so they use the ring.  Either way the rounds are
+            // folded in in the same order.
             const int nr = (pos + G * U - 1) / (G * U);
-            const int ntail = min(max(nr - NS, 0), 2);
+            const int ntail = l > 0 && nr <= 2 ? nr : min(max(nr - NS, 0), 2);
             const int nring = nr - ntail;
             // Layer 0's first rounds were issued at the end of the previous
             // step (below), before its logits and draw.
@@ -3773,8 +3821,8 @@ persistent_decode_kernel(PersistArgs a) {
 }
 
 // Layer-0 table: row (token v, team t) is team t's mesh of block 0 on the
-// RMS-normalised token vector E[v], before QK-norm and RoPE: the arithmetic
-// of a persistent mesh team, so its rows equal what the team would compute.
+// RMS-normalised token vector E[v], before QK-norm and RoPE, with the row
+// meshes' arithmetic (log2(e)-scaled carry) that a persistent mesh team uses.
 template <int NW, int CPL, int GL, int DEPTH>
 __global__ void __launch_bounds__(64 * NW)
 layer0_kernel(Shape s, const float *__restrict__ E, const float *__restrict__ w, size_t block0, float *q0) {
@@ -3792,13 +3840,13 @@ layer0_kernel(Shape s, const float *__restrict__ E, const float *__restrict__ w,
     float x[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) x[j] = E[size_t(v) * W + c.ridx(j)];
-    const float inv = row_inv_rms(c, x, 3);
+    const float inv = row_inv_rms(c, x, 3) * kLog2e;
     float n[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) n[j] = x[j] * inv;
     row_run_mesh(c, n, wr, wm, s.A, s, FIXED);
 #pragma unroll
-    for (int j = 0; j < CPL; ++j) q0[(size_t(v) * 3 + team) * W + c.ridx(j)] = n[j];
+    for (int j = 0; j < CPL; ++j) q0[(size_t(v) * 3 + team) * W + c.ridx(j)] = n[j] * kLn2;
 }
 
 // One workgroup per token row (reference.rs:130-149 with gpu.rs:1261-1333's
