@@ -3521,7 +3521,7 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const floa
 // them load while the inputs are awaited.
 template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
 __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m,
-                                                     const X &xc) {
+                                                     const X &xc, int pair) {
     using Ctx = RowCtx<NW, CPL, GL>;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     using S = AttnState<HDP, 64 * NW, Ring::UL>;
@@ -3540,6 +3540,16 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
         const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
             const int g = step * L + l;
+            // Two workgroups sharing a CU (persistent_role's pairs: the same
+            // head of two sequences) take turns at the front of the wave
+            // arbiter, layer by layer, opposite to each other while their
+            // sequences are at the same layer; by age alone the first
+            // dispatched would always win.  (Measured on config 3: 26.1 ms a
+            // 512-step launch against 26.6, alternating per step 26.3.)
+            if (pair != 0) {
+                if (((g + pair) & 1) != 0) __builtin_amdgcn_s_setprio(1);
+                else __builtin_amdgcn_s_setprio(0);
+            }
             // Lane values are formed per layer from a thread index hidden from
             // the optimiser: hoisted out of the loops they would be spilled, and
             // a spill reload waits for the K/V loads in flight.
@@ -3744,10 +3754,14 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
 // 2 of an XCD, always first, finish the 512-step launch of config 3 ~11 %
 // before sequences 1 and 3.  Mixing the two places within each sequence was
 // slower still (518k against 538k tokens/s): a sequence then waits every
-// layer for its slowest head.  Any other placement only costs speed: every
-// role of a sequence stays on one XCD, and the map is a bijection of [0, K).
-__host__ __device__ inline void persistent_role(int k, int K, int C, int R, int &q, int &r) {
+// layer for its slowest head.  The paired workgroups instead take turns at the
+// front by wave priority (persistent_attention), which narrows the gap.  Any
+// other placement only costs speed: every role of a sequence stays on one
+// XCD, and the map is a bijection of [0, K).  `pair` is 1 for the first
+// workgroup of a pair, 2 for the second and 0 for one that has its CU alone.
+__host__ __device__ inline void persistent_role(int k, int K, int C, int R, int &q, int &r, int &pair) {
     const int P = K - C, Q = K / R, H = R - 3;
+    pair = 0;
     if (P <= 0 || 2 * P > Q * H || Q < 2 || C < P) {
         q = k / R;
         r = k % R;
@@ -3761,10 +3775,12 @@ __host__ __device__ inline void persistent_role(int k, int K, int C, int R, int 
     };
     if (k < P) {
         head_at(2 * k, q, r);
+        pair = 1;
         return;
     }
     if (k >= C && k < C + P) {
         head_at(2 * (k - C) + 1, q, r);
+        pair = 2;
         return;
     }
     // The other roles in (q, r) order over the remaining slots.
@@ -3802,8 +3818,8 @@ persistent_decode_kernel(PersistArgs a) {
     // x + 8q are workgroups x + 8k of XCD x, k given by persistent_role.  (The
     // handshake checks it; any other placement only costs speed.)
     const int R = 3 + a.s.H, x = int(blockIdx.x) % 8, k = int(blockIdx.x) / 8;
-    int q, r;
-    persistent_role(k, int(gridDim.x) / 8, a.xcd_cus, R, q, r);
+    int q, r, pair;
+    persistent_role(k, int(gridDim.x) / 8, a.xcd_cus, R, q, r, pair);
     const int b = x + 8 * q;
     if (b >= a.batch) return;
     const int trow = r < 3 ? 3 * b + r : 3 * a.batch + b * a.s.H + (r - 3);
@@ -3812,7 +3828,7 @@ persistent_decode_kernel(PersistArgs a) {
         if (r < 3)
             persistent_team<NW, CPL, GL, DEPTH, HDP>(a, b, r, m, xc);
         else
-            persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc);
+            persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc, pair);
     };
     if (!a.agent_scope && persistent_handshake(a, far, r))
         run(PersistXch<true>(a, b, trow));
