@@ -2804,10 +2804,20 @@ head_sample_kernel(Shape s, const float *__restrict__ xn, const float *__restric
 // previous value has read it (each rewrite depends, through the chain, on
 // those reads).  The cache rows of a (sequence, head) are written and later
 // read only by that pair's attention workgroup, so its own barriers order
-// them.  Every poll is bounded: after kWaitTicks of wall clock it raises
-// *abort, a poll that sees *abort gives up at once, and the launch then runs
-// to its end on whatever it read (trip counts are fixed and tokens stay in
-// range), so a broken hand-off ends the launch with an error, not a hang.
+// them.  Every poll is bounded: after the launch's wait limit (kWaitTicks
+// unless the host sets another) it raises *abort, a poll that sees *abort
+// gives up soon after, and the launch then runs to its end on whatever it
+// read (trip counts are fixed and tokens stay in range), so a broken
+// hand-off ends the launch with an error, not a hang.
+//
+// Every block must be resident at once.  The launch is an ordinary one (a
+// cooperative launch, which would guarantee it, takes ~12 us longer to start
+// and end): the host launches only when every block fits the GPU at once
+// (persistent_fits), which an otherwise idle GPU then gives.  Should some
+// blocks still have to wait for room (another kernel holding part of the
+// GPU), the resident ones time out and the launch ends with *abort set; the
+// sampler states go to rng_out, not rng, so the host then has the state
+// before the launch and runs the same steps on the per-phase kernels.
 
 constexpr uint64_t kWaitTicks = 20000000;  // 0.2 s of the 100 MHz wall clock
 constexpr uint32_t kPollCheck = 16;        // polls between checks of the abort flag and the clock
@@ -2838,7 +2848,7 @@ __device__ __forceinline__ uint64_t get_word(const uint64_t *p, bool local) {
 // out[i] = the float of the word at addr(i), i < N, once every such word of
 // the wave carries `tag`.
 template <int N, bool LOCAL, class Addr>
-__device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], int *abort) {
+__device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], int *abort, uint64_t wait_ticks) {
     constexpr bool local = LOCAL;
     const uint32_t want = uint32_t(tag);
     uint64_t w[N];
@@ -2852,6 +2862,10 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
     };
     if (!__all(ready())) {
         const uint64_t t0 = wall_clock64();
+        // A limit below the default (a host override, used to force time outs
+        // in tests) is checked on every poll.
+        static_assert((kPollCheck & (kPollCheck - 1)) == 0, "a power of two");
+        const uint32_t check_mask = wait_ticks < kWaitTicks ? 0 : kPollCheck - 1;
         for (uint32_t n = 1;; ++n) {
             __builtin_amdgcn_s_sleep(1);
             asm volatile("" ::: "memory");  // the words change under us: load them again
@@ -2863,9 +2877,9 @@ __device__ __forceinline__ void take_words(Addr addr, int tag, float (&out)[N], 
 #pragma unroll
             for (int i = 0; i < N; ++i) w[i] = get_word(addr(i), local);
             if (__all(ready())) break;
-            if (n % kPollCheck == 0) {
+            if ((n & check_mask) == 0) {
                 if (__hip_atomic_load(abort, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) != 0) break;
-                if (wall_clock64() - t0 > kWaitTicks) {
+                if (wall_clock64() - t0 > wait_ticks) {
                     if ((threadIdx.x & 63) == 0) __hip_atomic_store(abort, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
                     break;
                 }
@@ -3034,8 +3048,9 @@ struct PersistXch {
     uint64_t *base;
     int W, V;
     int row;  // this workgroup's row of the trace (3 * batch teams, then batch * H heads)
+    uint64_t wait;  // a wait's limit (PersistArgs::wait_ticks)
     __device__ PersistXch(const PersistArgs &a, int b, int row_)
-        : base(a.xch + size_t(b) * a.xstride), W(a.s.W), V(a.s.V), row(row_) {}
+        : base(a.xch + size_t(b) * a.xstride), W(a.s.W), V(a.s.V), row(row_), wait(a.wait_ticks) {}
     // q (t = 0), k (1) or v (2) of phase g, double-buffered by phase parity
     __device__ uint64_t *qkv(int g, int t) const { return base + size_t((g & 1) * 3 + t) * W; }
     __device__ uint64_t *y() const { return base + size_t(6) * W; }     // attention output
@@ -3045,7 +3060,7 @@ struct PersistXch {
     __device__ void put(uint64_t *p, float v, int tag) const { put_word(p, v, tag, LOCAL); }
     template <int N, class Addr>
     __device__ void take(Addr addr, int tag, float (&out)[N], int *abort) const {
-        take_words<N, LOCAL>(addr, tag, out, abort);
+        take_words<N, LOCAL>(addr, tag, out, abort, wait);
     }
 };
 
@@ -3476,7 +3491,7 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     }
     if (team == 0 && threadIdx.x == 0) {
         a.len[b] = len;
-        a.rng[b] = rng;
+        a.rng_out[b] = rng;
     }
 }
 
@@ -3799,7 +3814,7 @@ __host__ __device__ inline void persistent_role(int k, int K, int C, int R, int 
 }
 
 // Blocks [0, 3*batch): mesh teams (sequence, team); then (sequence, head)
-// attention blocks.  Needs every block resident at once (cooperative launch).
+// attention blocks.  Needs every block resident at once (see above).
 template <int NW, int CPL, int GL, int DEPTH, int HDP>
 __global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2, 2)))
 persistent_decode_kernel(PersistArgs a) {
@@ -4294,9 +4309,9 @@ hipError_t persistent_decode(const PersistArgs &a, hipStream_t stream) {
         hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess)
         return hipErrorInvalidDevice;
     args.xcd_cus = cus / 8;
+    if (args.wait_ticks == 0) args.wait_ticks = kWaitTicks;
     void *params[] = {&args};
-    return hipLaunchCooperativeKernel(f, dim3(persistent_blocks(a.s, a.batch)), dim3(64 * row_waves(a.s.W)), params, 0,
-                                      stream);
+    return hipLaunchKernel(f, dim3(persistent_blocks(a.s, a.batch)), dim3(64 * row_waves(a.s.W)), params, 0, stream);
 }
 
 size_t persistent_layer0_floats(const Shape &s) { return size_t(s.V) * 3 * s.W; }

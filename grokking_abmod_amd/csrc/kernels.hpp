@@ -151,13 +151,15 @@ struct PersistArgs {
     const float2 *rope;
     uint32_t *tokens;
     int tok_stride;
-    int *len;
-    uint64_t *rng;
+    int *len;             // each sequence's length, written at the end of the launch
+    uint64_t *rng;        // each sequence's sampler state at the start of the launch (read only)
+    uint64_t *rng_out;    // ... and at its end, written by the launch
     float temperature;
     int *flags;           // bit 0: non-finite logits
     uint64_t *xch;        // [batch][xstride] tagged exchange words, zero at launch
     size_t xstride;       // persistent_exchange_words(shape)
     int *abort;           // zero at launch; set when a wait times out
+    uint64_t wait_ticks;  // a wait's limit in 100 MHz wall-clock ticks (kWaitTicks unless overridden)
     float scale_log2;     // set by persistent_decode
     int xcd_cus;          // CUs per XCD, set by persistent_decode
     // Nonzero: every sequence's hand-offs use the agent-scope atomics, as when

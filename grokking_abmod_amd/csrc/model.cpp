@@ -114,6 +114,9 @@ struct MeshGpt::Impl {
     DevBuf kc, vc, dx, dx2, dxn, dq, part, dtokens, dlen, drng, dlogits, dflags;
     // Sampler states and length right after the last prefill (rewind()).
     DevBuf drng_start;
+    // Sampler states a persistent decode launch writes (swapped with drng when
+    // the launch completes).
+    DevBuf drng_next;
     size_t start_length = 0;
     // Persistent decode kernel state: tagged exchange words of every sequence
     // and the abort flag.
@@ -420,11 +423,12 @@ struct MeshGpt::Impl {
             dlen.ensure(batch_cap * 4);
             drng.ensure(batch_cap * 8);
             drng_start.ensure(batch_cap * 8);
+            drng_next.ensure(batch_cap * 8);
             dlogits.ensure(batch_cap * cfg.vocab_size * 4);
             dflags.ensure(4);
             if (persistent_ok) {
                 pxch.ensure(batch_cap * kern::persistent_exchange_words(shape) * 8);
-                pabort.ensure(4);
+                pabort.ensure(8);  // abort flag, then the launch's non-finite flag
             }
         }
         tcap = std::max(t, tcap);
@@ -912,7 +916,7 @@ struct MeshGpt::Impl {
     size_t allocated_device_bytes() const {
         size_t total = 0;
         for (const DevBuf *b : {&params, &codes, &E, &Et, &rope, &wdec, &Edec, &q0, &kc, &vc, &dx, &dx2, &dxn, &dq,
-                                &part, &dtokens, &dlen, &drng, &dlogits, &dflags, &drng_start, &pxch, &pabort, &wx,
+                                &part, &dtokens, &dlen, &drng, &dlogits, &dflags, &drng_start, &drng_next, &pxch, &pabort, &wx,
                                 &wxn, &wq, &wy, &wtok, &wlogits, &wk, &wv, &tact, &tgrad, &tm, &tv, &tpart, &tin})
             total += b->bytes;
         return total;
@@ -1205,15 +1209,22 @@ struct MeshGpt::Impl {
     }
 
     // `steps` decode steps in one launch of the persistent kernel (the caller
-    // checked decodable(steps) and persistent_usable()).  Returns false, with
-    // nothing changed, when the runtime refuses the cooperative launch: it
-    // does while another process on the GPU holds the device's cooperative
-    // launch resources (hipErrorIllegalState), or when the blocks cannot all
-    // be resident; the caller then runs the per-phase kernels.
+    // checked decodable(steps) and persistent_usable(), which includes that
+    // every block fits the GPU at once).  Returns false, with the decode state
+    // as before, when the launch does not complete: the runtime refuses it, or
+    // a hand-off wait times out, which happens when some blocks could not be
+    // resident (another kernel holding part of the GPU).  The caller then runs
+    // the same steps on the per-phase kernels.  The sampler states of the
+    // launch go to drng_next and its non-finite flag to pabort[1], taken over
+    // only when it completes; the token and cache rows past the old length
+    // that a timed-out launch wrote are rewritten by the per-phase steps.
+    // With MG_PERSIST_STRICT=1 a timed-out launch throws instead (tests use
+    // it, so that a broken hand-off is not hidden by the fallback).
+    // MG_PERSIST_WAIT_TICKS sets the waits' limit in 100 MHz ticks.
     bool persistent(size_t steps, uint64_t *trace = nullptr) {
         const size_t xstride = kern::persistent_exchange_words(shape);
         check(hipMemsetAsync(pxch.p, 0, batch * xstride * 8, stream), "clear exchange words");
-        check(hipMemsetAsync(pabort.p, 0, 4, stream), "clear abort");
+        check(hipMemsetAsync(pabort.p, 0, 8, stream), "clear abort and flags");
         kern::PersistArgs a{};
         a.s = shape;
         a.batch = int(batch);
@@ -1233,11 +1244,13 @@ struct MeshGpt::Impl {
         a.tok_stride = int(tcap);
         a.len = dlen.as<int>();
         a.rng = drng.as<uint64_t>();
+        a.rng_out = drng_next.as<uint64_t>();
         a.temperature = temperature;
-        a.flags = dflags.as<int>();
+        a.flags = pabort.as<int>() + 1;
         a.xch = pxch.as<uint64_t>();
         a.xstride = xstride;
         a.abort = pabort.as<int>();
+        a.wait_ticks = uint64_t(std::max(0, env_int("MG_PERSIST_WAIT_TICKS", 0)));
         a.trace = trace;
         a.agent_scope = env_int("MG_PERSIST_AGENT_SCOPE", 0) != 0;
         a.mall_keep = keep_rows();
@@ -1245,7 +1258,8 @@ struct MeshGpt::Impl {
         // the launch's own duration.
         mark_call(0);
         const hipError_t launched = kern::persistent_decode(a, stream);
-        if (launched == hipErrorIllegalState || launched == hipErrorCooperativeLaunchTooLarge) {
+        if (launched == hipErrorOutOfMemory || launched == hipErrorLaunchOutOfResources ||
+            launched == hipErrorCooperativeLaunchTooLarge) {
             (void)hipGetLastError();  // the refusal is not a device error
             return false;
         }
@@ -1253,12 +1267,21 @@ struct MeshGpt::Impl {
         mark_call(1);
         sync();
         close_call();
-        int aborted = 0;
-        check(hipMemcpy(&aborted, pabort.p, 4, hipMemcpyDeviceToHost), "download abort flag");
-        if (aborted) {
-            cached = kNoCache;
-            throw Error("persistent decode kernel timed out waiting on a hand-off", kDeviceError);
+        int status[2] = {0, 0};
+        check(hipMemcpy(status, pabort.p, 8, hipMemcpyDeviceToHost), "download abort flag");
+        if (status[0]) {
+            if (env_int("MG_PERSIST_STRICT", 0)) {
+                cached = kNoCache;
+                throw Error("persistent decode kernel timed out waiting on a hand-off", kDeviceError);
+            }
+            // Every sequence back at the launch's starting length; the sampler
+            // states in drng were not touched.
+            check(hipMemsetD32Async(hipDeviceptr_t(dlen.p), int(length), batch, stream), "restore lengths");
+            return false;
         }
+        std::swap(drng.p, drng_next.p);
+        std::swap(drng.bytes, drng_next.bytes);
+        if (status[1]) check(hipMemsetD32Async(hipDeviceptr_t(dflags.p), 1, 1, stream), "flag non-finite logits");
         cached = length + steps - 1;
         length += steps;
         return true;
@@ -1428,8 +1451,8 @@ std::vector<uint64_t> MeshGpt::decode_traced(size_t steps) {
     trace.ensure(n * 8);
     check(hipMemsetAsync(trace.p, 0, n * 8, m.stream), "clear trace");
     if (!m.persistent(steps, trace.as<uint64_t>()))
-        throw Error("the runtime refused the persistent decode kernel's cooperative launch (another process may "
-                    "hold the GPU's cooperative launch resources)",
+        throw Error("the persistent decode launch did not complete (the runtime refused it, or a hand-off timed out "
+                    "while part of the GPU was busy)",
                     kDeviceError);
     m.finish();
     std::vector<uint64_t> out(n);

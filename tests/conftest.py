@@ -8,6 +8,11 @@ ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 sys.path.insert(0, ROOT)
 sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
 
+# A persistent decode launch whose hand-off times out raises instead of
+# falling back to the per-phase kernels, so that a broken hand-off fails the
+# test that caused it (the fallback has its own test).
+os.environ.setdefault("MG_PERSIST_STRICT", "1")
+
 # Logit tolerance |gpu - oracle| <= TOL * (1 + |oracle|): the north-star bound,
 # five times tighter than the reference's own GPU check (src/bin/mesh-gpt.rs:357-366).
 TOL = 1e-4

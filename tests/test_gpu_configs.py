@@ -484,12 +484,10 @@ def test_cli_prompt_file_and_normal_init(tmp_path):
     res = subprocess.run([cli, "generate", "--checkpoint", checkpoint, "--prompt-file", str(bad), "--batch", "3"],
                          capture_output=True, text=True, timeout=60)
     assert res.returncode == 1 and "prompt file must hold one line per sequence (3), found 2" in res.stderr
-    # A synthetic model with N(0, 0.5) weights and a seeded random prompt.
-    # This process decodes it first with the persistent kernel, whose
-    # cooperative launch holds the GPU's cooperative launch resources for the
-    # rest of the process; the CLI's own cooperative launch is then refused
-    # (hipErrorIllegalState) and it must fall back to the per-phase kernels,
-    # with the same tokens.
+    # A synthetic model with N(0, 0.5) weights and a seeded random prompt,
+    # decoded first by this process with the persistent kernel, then by the
+    # CLI (a second process on the same GPU, with its own persistent
+    # launch): the same tokens.
     tiny = G.named_config("tiny")
     ot = oracle_config(tiny)
     prompt = G.random_prompts(64, 1, 16, 7)[0]

@@ -381,6 +381,39 @@ def test_persistent_decode_matches_per_phase_kernels(name, temperature, monkeypa
     assert_close(l0, l1, what="persistent vs per-phase decode logits")
 
 
+def test_persistent_decode_timeout_falls_back_to_per_phase_kernels(monkeypatch):
+    # A persistent launch whose hand-off waits time out (forced from the host
+    # with a wait limit of one 100 MHz tick, so every wait gives up after its
+    # first round of polls) ends with its abort flag set; the library then
+    # restores the decode state and runs the same steps on the per-phase
+    # kernels, so tokens and last-step logits equal a per-phase run's bit for
+    # bit.  With MG_PERSIST_STRICT=1 the same launch raises a device error.
+    config = G.named_config("mid")
+    prompts = G.random_prompts(256, 8, 20, 7)
+    runs = []
+    for env in ({"MG_DISABLE_PERSISTENT": "1"},
+                {"MG_PERSIST_WAIT_TICKS": "1", "MG_PERSIST_STRICT": "0", "MG_FORCE_PERSISTENT": "1"}):
+        for k, v in env.items():
+            monkeypatch.setenv(k, v)
+        with G.MeshGpt(0, config, 7, max_batch=8) as model:
+            model.prefill(prompts, 1.0, 11, reserve=20 + 1 + 16)
+            model.decode(16)
+            assert model.sequence_length() == 20 + 1 + 16
+            runs.append((model.read_tokens(8), model.last_logits(8)))
+        for k in env:
+            monkeypatch.delenv(k)
+    assert np.array_equal(runs[0][0], runs[1][0])
+    assert np.array_equal(runs[0][1], runs[1][1])
+    monkeypatch.setenv("MG_PERSIST_WAIT_TICKS", "1")
+    monkeypatch.setenv("MG_PERSIST_STRICT", "1")
+    monkeypatch.setenv("MG_FORCE_PERSISTENT", "1")
+    with G.MeshGpt(0, config, 7, max_batch=8) as model:
+        model.prefill(prompts, 1.0, 11, reserve=20 + 1 + 4)
+        with pytest.raises(G.MeshGptError, match="timed out waiting on a hand-off") as err:
+            model.decode(4)
+        assert err.value.status == G.MG_DEVICE_ERROR
+
+
 def test_persistent_decode_full_batch_matches_per_phase_kernels(monkeypatch):
     # 32 sequences of config 3 need more workgroups than the GPU has CUs, so
     # some share a CU and the launch maps roles to workgroups with its pairing
