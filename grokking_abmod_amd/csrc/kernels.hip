@@ -3411,10 +3411,18 @@ __device__ __forceinline__ void persistent_head_logits(const PersistArgs &a, con
     persistent_head_slice<NW, W, false>(m.xn, a.E, xc, t0, base + HB::T * NW, t1, step + 1, c.lane);
 }
 
+// A sequence's decode state at the start of the launch, loaded before the
+// XCD handshake so that the loads overlap it.
+struct PersistStart {
+    int len;       // tokens so far
+    uint32_t tok;  // the last of them
+    uint64_t rng;  // the sampler's state
+};
+
 // Mesh team `team` of sequence b.
 template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
 __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int team, const PersistLds &m,
-                                                const X &xc) {
+                                                const X &xc, const PersistStart &st0) {
     using Ctx = RowCtx<NW, CPL, GL>;
     constexpr int W = Ctx::W;
     constexpr bool FIXED = DEPTH > 0;
@@ -3422,9 +3430,9 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
     const Shape &s = a.s;
     Ctx c(m.xch, m.red);
     const int L = a.layers, V = s.V;
-    int len = a.len[b];
-    uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len - 1];
-    uint64_t rng = a.rng[b];  // the sampler's state, the same in every wave
+    int len = st0.len;
+    uint32_t tok = st0.tok;
+    uint64_t rng = st0.rng;  // the sampler's state, the same in every wave
     if constexpr (W % 256 == 0) {
         // The team's slice of E rows stays in the (otherwise unused) ring.
         const int nb = 3 + s.H;
@@ -3536,7 +3544,7 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const floa
 // them load while the inputs are awaited.
 template <int NW, int CPL, int GL, int DEPTH, int HDP, class X>
 __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b, int h, const PersistLds &m,
-                                                     const X &xc, int pair) {
+                                                     const X &xc, int pair, const PersistStart &st0) {
     using Ctx = RowCtx<NW, CPL, GL>;
     using Ring = PersistRing<NW, CPL, GL, HDP>;
     using S = AttnState<HDP, 64 * NW, Ring::UL>;
@@ -3545,12 +3553,12 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
     const KvRing<HDP, NW, U, NS> ring{m.ring};
     const Shape &s = a.s;
     constexpr int W = Ctx::W;
-    const int len0 = a.len[b], L = a.layers;
+    const int len0 = st0.len, L = a.layers;
 
     const size_t slab = size_t(b * s.H + h) * a.cap * HDP;
     static_assert(VEC % NW == 0, "lane dims must cover whole row-order columns");
-    uint32_t tok = a.tokens[size_t(b) * a.tok_stride + len0 - 1];
-    uint64_t rng = a.rng[b];
+    uint32_t tok = st0.tok;
+    uint64_t rng = st0.rng;
     for (int step = 0; step < a.steps; ++step) {
         const int pos = len0 + step - 1;  // this step's row; rows [0, pos) are cached
         for (int l = 0; l < L; ++l) {
@@ -3839,11 +3847,15 @@ persistent_decode_kernel(PersistArgs a) {
     if (b >= a.batch) return;
     const int trow = r < 3 ? 3 * b + r : 3 * a.batch + b * a.s.H + (r - 3);
     const PersistXch<false> far(a, b, trow);
+    PersistStart st0;
+    st0.len = a.len[b];
+    st0.tok = a.tokens[size_t(b) * a.tok_stride + st0.len - 1];
+    st0.rng = a.rng[b];
     auto run = [&](const auto &xc) {
         if (r < 3)
-            persistent_team<NW, CPL, GL, DEPTH, HDP>(a, b, r, m, xc);
+            persistent_team<NW, CPL, GL, DEPTH, HDP>(a, b, r, m, xc, st0);
         else
-            persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc, pair);
+            persistent_attention<NW, CPL, GL, DEPTH, HDP>(a, b, r - 3, m, xc, pair, st0);
     };
     if (!a.agent_scope && persistent_handshake(a, far, r))
         run(PersistXch<true>(a, b, trow));
