@@ -3510,8 +3510,11 @@ __device__ __forceinline__ void persistent_team(const PersistArgs &a, int b, int
 // group reduction instead of one per dim): the same sum as row_qk_rope's in
 // another order, within a few f32 roundings of it.
 // cs[e] is the (cos, sin) pair of dim d0 + e at the position (rope_pair).
+// With qs > 0 the result is scaled by qs (the query's score scale, folded
+// into the norm factor as rsqrt((ss / hd + eps) / qs^2)).
 template <int LPK, int VEC>
-__device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const float2 (&cs)[VEC], const Shape &s) {
+__device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const float2 (&cs)[VEC], const Shape &s,
+                                             float qs = 0.0f) {
     float other[VEC];
     float sq = 0.0f;
 #pragma unroll
@@ -3523,8 +3526,8 @@ __device__ __forceinline__ void lane_qk_rope(float (&x)[VEC], int d0, const floa
         if constexpr (LPK == 16) other[e] = dpp_move<0x128>(0.0f, x[e]);
         else other[e] = __shfl_xor(x[e], LPK / 2, 64);
     }
-    const float scale = 1.0f / float(s.hd);
-    const float sc = rsqrtf(ss * scale + kRmsEps);
+    const float q2 = qs > 0.0f ? 1.0f / (qs * qs) : 1.0f;  // uniform: off the chain
+    const float sc = rsqrtf(ss * ((1.0f / float(s.hd)) * q2) + kRmsEps * q2);
 #pragma unroll
     for (int e = 0; e < VEC; ++e) {
         const int d = d0 + e;
@@ -3652,7 +3655,9 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             }
             // QK-norm and RoPE of this head's query and key (the teams and
             // the layer-0 table give them before both).
-            lane_qk_rope<LPK, VEC>(qr, d0, rcs, s);
+            // The query carries the score scale (log2(e) / sqrt(hd)), so the
+            // scores below need no multiply.
+            lane_qk_rope<LPK, VEC>(qr, d0, rcs, s, a.scale_log2);
             lane_qk_rope<LPK, VEC>(kn, d0, rcs, s);
             const uint64_t t_ready = trace_time(a);
             S st;
@@ -3664,7 +3669,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 float sc = 0.0f;
 #pragma unroll
                 for (int e = 0; e < VEC; ++e) sc = fmaf(qr[e], kn[e], sc);
-                sc = group_sum<LPK>(sc) * a.scale_log2;
+                sc = group_sum<LPK>(sc);
                 const bool mine = grp == 0;
                 st.m = mine ? sc : -INFINITY;
                 st.l = mine ? 1.0f : 0.0f;
@@ -3672,9 +3677,9 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                 for (int e = 0; e < VEC; ++e) st.acc[e] = mine ? vn[e] : 0.0f;
             }
             if (ntail > 1)
-                st.add2(qr, last, nring * G * U, last2, (nring + 1) * G * U, pos, a.scale_log2);
+                st.add2(qr, last, nring * G * U, last2, (nring + 1) * G * U, pos, 1.0f);
             else if (ntail > 0)
-                st.add(qr, last, nring * G * U, pos, a.scale_log2);
+                st.add(qr, last, nring * G * U, pos, 1.0f);
             if constexpr (NS == 2) {
                 // Two rounds at a time: both slots are read, refilled and
                 // folded in together.
@@ -3686,13 +3691,13 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     ring.read(r + 1, c1, tid);
                     if (r + 2 < nring) ring.issue(kl, vl, r + 2, pos, tid, a.mall_keep);
                     if (r + 3 < nring) ring.issue(kl, vl, r + 3, pos, tid, a.mall_keep);
-                    st.add2(qr, c0, r * G * U, c1, (r + 1) * G * U, pos, a.scale_log2);
+                    st.add2(qr, c0, r * G * U, c1, (r + 1) * G * U, pos, 1.0f);
                 }
                 if (r < nring) {
                     ring.wait(0);
                     R cur;
                     ring.read(r, cur, tid);
-                    st.add(qr, cur, r * G * U, pos, a.scale_log2);
+                    st.add(qr, cur, r * G * U, pos, 1.0f);
                 }
             } else {
                 for (int r = 0; r < nring; ++r) {
@@ -3700,7 +3705,7 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
                     R cur;
                     ring.read(r, cur, tid);
                     if (r + NS < nring) ring.issue(kl, vl, r + NS, pos, tid, a.mall_keep);
-                    st.add(qr, cur, r * G * U, pos, a.scale_log2);
+                    st.add(qr, cur, r * G * U, pos, 1.0f);
                 }
             }
             // The merge borrows the LDS of the logits row and of the row
