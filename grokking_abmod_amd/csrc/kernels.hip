@@ -2566,15 +2566,23 @@ __device__ __forceinline__ int wave_sequential_pick(const float (&pc)[RMAX], int
 // caller, so that it is ready before the logits are).  Every lane returns the
 // token.  Nothing touches memory but the non-finite flag: a near-tie runs the
 // sequential f32 process on the wave's registers (wave_sequential_pick), so
-// waves of one workgroup never share scratch and need no barrier.
-template <int RMAX>
+// waves of one workgroup never share scratch and need no barrier.  VC > 0
+// compiles the choice for the vocabulary V = VC: the run length and every
+// token mask are then constants, and the uniform branches on them vanish.
+template <int RMAX, int VC = 0>
 __device__ __forceinline__ int wave_choose_token(const float (&lg)[RMAX], int V, float temperature, float u,
                                                  const uint64_t *exp_tab, int *flags) {
     static_assert(RMAX % 4 == 0, "runs are handled four tokens at a time");
-    // V is hidden from the optimiser so that the f64 constants derived from it
-    // are formed here, not hoisted out of a caller's step loop and spilled.
-    V = __builtin_amdgcn_readfirstlane(V);
-    asm volatile("" : "+s"(V));
+    static_assert(VC >= 0 && (VC + 63) / 64 <= RMAX, "a fixed vocabulary fits the runs");
+    if constexpr (VC > 0) {
+        V = VC;
+    } else {
+        // V is hidden from the optimiser so that the f64 constants derived
+        // from it are formed here, not hoisted out of a caller's step loop
+        // and spilled.
+        V = __builtin_amdgcn_readfirstlane(V);
+        asm volatile("" : "+s"(V));
+    }
     // Every per-token step below is straight-line code in blocks of four
     // tokens (a lane's tokens past V are masked by selects), so the f64
     // evaluations of neighbouring tokens overlap; only `k < R` branches, and
@@ -3331,8 +3339,12 @@ __device__ __forceinline__ uint32_t draw_token(const PersistArgs &a, const X &xc
     // A wave issues one instruction per four cycles and this code runs once
     // per step on the critical path: a vocabulary of at most 256 tokens (four
     // per lane) gets the version unrolled for four.
+    // The vocabularies of the persistent configurations (256, and 64 for
+    // the smallest) get versions compiled for them.
     if (R <= 4) {
         const float l4[4] = {lg[0], lg[1], lg[2], lg[3]};
+        if (V == 256) return uint32_t(wave_choose_token<4, 256>(l4, V, a.temperature, u, m.exp_tab, a.flags));
+        if (V == 64) return uint32_t(wave_choose_token<4, 64>(l4, V, a.temperature, u, m.exp_tab, a.flags));
         return uint32_t(wave_choose_token(l4, V, a.temperature, u, m.exp_tab, a.flags));
     }
     return uint32_t(wave_choose_token(lg, V, a.temperature, u, m.exp_tab, a.flags));
