@@ -3580,12 +3580,19 @@ __device__ __forceinline__ void persistent_attention(const PersistArgs &a, int b
             const int g = step * L + l;
             // Two workgroups sharing a CU (persistent_role's pairs: the same
             // head of two sequences) take turns at the front of the wave
-            // arbiter, layer by layer, opposite to each other while their
-            // sequences are at the same layer; by age alone the first
-            // dispatched would always win.  (Measured on config 3: 26.1 ms a
-            // 512-step launch against 26.6, alternating per step 26.3.)
+            // arbiter: by layer parity, opposite to each other while their
+            // sequences are at the same layer, and by step parity when the
+            // layer parities agree (one sequence a layer ahead), where age
+            // alone would always favour the first dispatched.  (Measured on
+            // config 3: 26.6 ms a 512-step launch by age, 26.1 with the layer
+            // parity, 25.9 with both; over the first 20 steps the sequences
+            // of the four slots of an XCD averaged 30.1-32.9 us a step by
+            // age, 31.0-32.0 and 31.1-31.4.)
             if (pair != 0) {
-                if (((g + pair) & 1) != 0) __builtin_amdgcn_s_setprio(1);
+                const int p = 2 * ((g + pair) & 1) + ((step + pair) & 1);
+                if (p == 3) __builtin_amdgcn_s_setprio(3);
+                else if (p == 2) __builtin_amdgcn_s_setprio(2);
+                else if (p == 1) __builtin_amdgcn_s_setprio(1);
                 else __builtin_amdgcn_s_setprio(0);
             }
             // Lane values are formed per layer from a thread index hidden from
