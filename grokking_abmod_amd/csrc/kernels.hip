@@ -1483,6 +1483,7 @@ __device__ __forceinline__ void rows_partner(const float (&x)[RB][CPL], float (&
     }
 }
 
+// x in and out in the log2(e)-scaled units of row_layer.
 template <int NW, int CPL, int D, int RB>
 __device__ __forceinline__ void rows_mesh_fixed(float (&x)[RB][CPL], const float2 (&w)[D][CPL], int lane, int wave,
                                                 float *xch, int &parity) {
@@ -1497,7 +1498,7 @@ __device__ __forceinline__ void rows_mesh_fixed(float (&x)[RB][CPL], const float
 #pragma unroll
             for (int j = 0; j < CPL; ++j) {
                 const float z = x[r][j] * w[u][j].x + p[r][j] * w[u][j].y;
-                x[r][j] = u + 1 == D ? z : elu(z);
+                x[r][j] = u + 1 == D ? z : elu_log2(z);
             }
     });
 }
@@ -1647,7 +1648,7 @@ row_block_rows_kernel(BlockArgs a) {
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) {
                     const float iv = rsqrtf(fmaxf(vv[r][j], kXsaFloor));
-                    y[r][j] = y[r][j] - (yv[r][j] * iv) * (v[r][j] * iv);
+                    y[r][j] = (y[r][j] - (yv[r][j] * iv) * (v[r][j] * iv)) * kLog2e;
                 }
         }
         rows_mesh_fixed<NW, CPL, D, RB>(y, wp, c.lane, c.wave, c.xch, c.parity);
@@ -1655,17 +1656,17 @@ row_block_rows_kernel(BlockArgs a) {
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) x[r][j] += y[r][j];
+            for (int j = 0; j < CPL; ++j) x[r][j] = fmaf(y[r][j], kLn2, x[r][j]);
         rows_inv_rms(c, x, 2, inv);
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) y[r][j] = x[r][j] * inv[r];
+            for (int j = 0; j < CPL; ++j) y[r][j] = x[r][j] * (inv[r] * kLog2e);
         rows_mesh_fixed<NW, CPL, D, RB>(y, wf, c.lane, c.wave, c.xch, c.parity);
 #pragma unroll
         for (int r = 0; r < RB; ++r)
 #pragma unroll
-            for (int j = 0; j < CPL; ++j) x[r][j] += y[r][j];
+            for (int j = 0; j < CPL; ++j) x[r][j] = fmaf(y[r][j], kLn2, x[r][j]);
     }
     if (team == 0 && (post || a.embed)) {
         // Into x_out, never x: the rows' other workgroups may not have read x yet.
@@ -1695,7 +1696,15 @@ row_block_rows_kernel(BlockArgs a) {
     }
     if (!pre) return;
 
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[r][j] *= kLog2e;
     rows_mesh_fixed<NW, CPL, D, RB>(x, wm, c.lane, c.wave, c.xch, c.parity);
+#pragma unroll
+    for (int r = 0; r < RB; ++r)
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) x[r][j] *= kLn2;
     if (team == 2) {
 #pragma unroll
         for (int r = 0; r < RB; ++r)
