@@ -1218,8 +1218,9 @@ struct MeshGpt::Impl {
     // launch go to drng_next and its non-finite flag to pabort[1], taken over
     // only when it completes; the token and cache rows past the old length
     // that a timed-out launch wrote are rewritten by the per-phase steps.
-    // With MG_PERSIST_STRICT=1 a timed-out launch throws instead (tests use
-    // it, so that a broken hand-off is not hidden by the fallback).
+    // With MG_PERSIST_STRICT=1 a timed-out launch throws instead, with the
+    // decode state as before (tests use it, so that a broken hand-off is not
+    // hidden by the fallback).
     // MG_PERSIST_WAIT_TICKS sets the waits' limit in 100 MHz ticks.
     bool persistent(size_t steps, uint64_t *trace = nullptr) {
         const size_t xstride = kern::persistent_exchange_words(shape);
@@ -1270,13 +1271,11 @@ struct MeshGpt::Impl {
         int status[2] = {0, 0};
         check(hipMemcpy(status, pabort.p, 8, hipMemcpyDeviceToHost), "download abort flag");
         if (status[0]) {
-            if (env_int("MG_PERSIST_STRICT", 0)) {
-                cached = kNoCache;
-                throw Error("persistent decode kernel timed out waiting on a hand-off", kDeviceError);
-            }
             // Every sequence back at the launch's starting length; the sampler
             // states in drng were not touched.
             check(hipMemsetD32Async(hipDeviceptr_t(dlen.p), int(length), batch, stream), "restore lengths");
+            if (env_int("MG_PERSIST_STRICT", 0))
+                throw Error("persistent decode kernel timed out waiting on a hand-off", kDeviceError);
             return false;
         }
         std::swap(drng.p, drng_next.p);

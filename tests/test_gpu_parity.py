@@ -383,8 +383,8 @@ def test_persistent_decode_matches_per_phase_kernels(name, temperature, monkeypa
 
 def test_persistent_decode_timeout_falls_back_to_per_phase_kernels(monkeypatch):
     # A persistent launch whose hand-off waits time out (forced from the host
-    # with a wait limit of one 100 MHz tick, so every wait gives up after its
-    # first round of polls) ends with its abort flag set; the library then
+    # with a wait limit of one 100 MHz tick, so a wait that has to poll gives
+    # up at its first unanswered poll) ends with its abort flag set; the library then
     # restores the decode state and runs the same steps on the per-phase
     # kernels, so tokens and last-step logits equal a per-phase run's bit for
     # bit.  With MG_PERSIST_STRICT=1 the same launch raises a device error.
@@ -404,14 +404,25 @@ def test_persistent_decode_timeout_falls_back_to_per_phase_kernels(monkeypatch):
             monkeypatch.delenv(k)
     assert np.array_equal(runs[0][0], runs[1][0])
     assert np.array_equal(runs[0][1], runs[1][1])
-    monkeypatch.setenv("MG_PERSIST_WAIT_TICKS", "1")
+    # Strict: the timed-out launch raises and leaves the decode state as it
+    # was, so the same steps then decode (with the default wait limit) to
+    # what a fresh model decodes.
     monkeypatch.setenv("MG_PERSIST_STRICT", "1")
     monkeypatch.setenv("MG_FORCE_PERSISTENT", "1")
     with G.MeshGpt(0, config, 7, max_batch=8) as model:
         model.prefill(prompts, 1.0, 11, reserve=20 + 1 + 4)
+        model.decode(4)
+        fresh = model.read_tokens(8)
+    with G.MeshGpt(0, config, 7, max_batch=8) as model:
+        model.prefill(prompts, 1.0, 11, reserve=20 + 1 + 4)
+        monkeypatch.setenv("MG_PERSIST_WAIT_TICKS", "1")
         with pytest.raises(G.MeshGptError, match="timed out waiting on a hand-off") as err:
             model.decode(4)
         assert err.value.status == G.MG_DEVICE_ERROR
+        assert model.sequence_length() == 20 + 1
+        monkeypatch.delenv("MG_PERSIST_WAIT_TICKS")
+        model.decode(4)
+        assert np.array_equal(model.read_tokens(8), fresh)
 
 
 def test_persistent_decode_full_batch_matches_per_phase_kernels(monkeypatch):
