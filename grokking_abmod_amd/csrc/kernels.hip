@@ -593,8 +593,10 @@ __device__ __forceinline__ float lane_read(float v, int byte_addr) {
 }
 
 // Lane l gets v of lane (l + 1) mod 64 (DPP wave_rol:1, no LDS round trip).
+// Every lane has a source, so no old value is needed (bound_ctrl), and the
+// compiler can fold the move into the instruction that uses it.
 __device__ __forceinline__ float wave_rotate1(float v) {
-    return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x134, 0xf, 0xf, false));
+    return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), 0x134, 0xf, 0xf, true));
 }
 
 // Lanes 0-31 get lanes 32-63 of a, lanes 32-63 get lanes 0-31 of b: one
@@ -1058,6 +1060,15 @@ __device__ __forceinline__ void row_partner(const float (&x)[CPL], float (&p)[CP
                 const float r = wave_rotate1(next ? x[(j + 1) % CPL] : x[j]);
                 p[j] = k == 1 ? r : wave_rotate1(r);
             });
+        } else if (k == 32 && CPL == 2) {
+            // Two swaps in place: (x0, x1) -> ([x0.lo, x1.lo], [x0.hi, x1.hi])
+            // gives p0, and swapping those back the other way round
+            // ([x0.hi, x0.lo], [x1.hi, x1.lo]) gives p1, with no copies.
+            const auto s = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(int, x[0]),
+                                                            __builtin_bit_cast(int, x[1 % CPL]), false, false);
+            p[0] = __builtin_bit_cast(float, lane < 32 ? int(s[1]) : int(s[0]));
+            const auto t = __builtin_amdgcn_permlane32_swap(int(s[1]), int(s[0]), false, false);
+            p[1 % CPL] = __builtin_bit_cast(float, lane < 32 ? int(t[1]) : int(t[0]));
         } else if (k == 32) {
             static_for<CPL>([&](auto J) {
                 constexpr int j = decltype(J)::value;
@@ -1087,11 +1098,15 @@ __device__ __forceinline__ void row_partner(const float (&x)[CPL], float (&p)[CP
 template <int NW, int CPL>
 __device__ __forceinline__ void row_layer(float (&x)[CPL], const float2 (&w)[CPL], int st, bool last, int lane,
                                           int wave, float *xch, int &parity) {
-    float p[CPL];
+    // The lane's own term first: x is then dead by the time the partner
+    // exchange runs, which may consume it (row_partner's in-place swaps).
+    float p[CPL], own[CPL];
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) own[j] = x[j] * w[j].x;
     row_partner<NW, CPL>(x, p, st, lane, wave, xch, parity);
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-        const float z = x[j] * w[j].x + p[j] * w[j].y;
+        const float z = fmaf(p[j], w[j].y, own[j]);
         x[j] = last ? z : elu_log2(z);
     }
 }
